@@ -1,0 +1,204 @@
+/*
+ * rina_hip.h — C-ABI of the MI355X (gfx950) decode hot path of the RINA
+ * engine (rina-engine).  Plain pointers and sizes; every pointer argument
+ * is device memory unless stated; `stream` is a hipStream_t (NULL = the
+ * null stream).  Every entry point is stream-ordered, never synchronizes,
+ * and returns RINA_OK (0) or a negative status.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the reference repository root).
+ */
+#ifndef RINA_HIP_H
+#define RINA_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define RINA_OK             0
+#define RINA_ERR_ARG       -1   /* null pointer, negative or zero size     */
+#define RINA_ERR_QTYPE     -2   /* quant type / KV format not supported    */
+#define RINA_ERR_SHAPE     -3   /* K % 32 != 0 for Q4 types, K too large   */
+#define RINA_ERR_RANGE     -4   /* position beyond the cache capacity      */
+#define RINA_ERR_HIP       -5   /* HIP runtime error (launch, allocation)  */
+#define RINA_ERR_WORKSPACE -6   /* caller workspace too small              */
+
+/* ---- quant type ids: rina-engine/src/core/quant.h:9-14 --------------- */
+#define RINA_QT_Q2_1      1
+#define RINA_QT_Q1_0      2
+#define RINA_QT_Q4_0      5
+#define RINA_QT_FP32      6
+#define RINA_QT_Q4_0F     7
+#define RINA_QT_GGML_Q2_K 10
+
+/* ---- KV cache modes: rina-engine/src/core/buffer.h:49 ---------------- */
+#define RINA_KV_FP32     0
+#define RINA_KV_Q8       1
+#define RINA_KV_Q4       2
+#define RINA_KV_Q4K_Q2V  3
+#define RINA_KV_Q2       4
+#define RINA_KV_Q2K_Q1V  5
+
+/* ---- KV block formats (32 values per block) -------------------------- */
+#define RINA_KVF_Q8_0  1   /* 34 B: fp16 scale + 32 x int8          */
+#define RINA_KVF_Q4_0  2   /* 18 B: fp16 scale + 16 B nibbles (q+7) */
+#define RINA_KVF_Q2_1  3   /* 10 B: fp16 amax + 8 B 2-bit (q+1)     */
+#define RINA_KVF_Q1_0  4   /*  6 B: fp16 amax + u32 sign bits       */
+
+/* ====================================================================== */
+/* Quantized matvec                                                        */
+/* ====================================================================== */
+
+/* out[M,N] = in[M,K] . W[N,K]^T with W packed along K in `quant_type`
+ * (RINA_QT_Q4_0, RINA_QT_Q4_0F, RINA_QT_GGML_Q2_K, RINA_QT_FP32).
+ * Replaces launch_linear_dispatch (rina-engine/src/ops/linear.h:7-10,
+ * ops/linear.cu:140-167): Q4_0 -> :60-95, Q4_0F -> :98-133, Q2_K -> the
+ * fused M=1 kernel :406-442 / M>1 :445-483 (flat element indexing), FP32 ->
+ * kernels/linear_fp32.cu:5-26.  Q4 types need K % 32 == 0.  input == output
+ * is allowed and computed out of place through library scratch (the
+ * reference's in-place calls race, arch/gqa/gqa_layer.cu:272). */
+int rina_hip_linear(const void* weight, int quant_type, const float* input,
+                    float* output, int M, int N, int K, void* stream);
+
+/* Fused matvec launch (no single reference counterpart: it fuses calls the
+ * reference makes back to back).  Up to 3 weight segments share one input
+ * vector and one launch:
+ *   RINA_EPI_STORE   out_s = W_s . x          (q/k/v: gqa_layer.cu:139-141)
+ *   RINA_EPI_ADD     out_s = out_s + W_s . x  (w_o/w2 + launch_add:
+ *                                              gqa_layer.cu:272-273,282-283)
+ *   RINA_EPI_SWIGLU  out_0 = silu(W_0 . x) * (W2_0 . x)
+ *                                             (w1, w3, launch_silu_mul:
+ *                                              gqa_layer.cu:278-281)
+ * All segments share quant_type and K.  input must not alias any output. */
+#define RINA_EPI_STORE  0
+#define RINA_EPI_ADD    1
+#define RINA_EPI_SWIGLU 2
+typedef struct {
+    const void* weight;    /* [N, K] packed                              */
+    const void* weight2;   /* RINA_EPI_SWIGLU: the up projection [N, K]  */
+    float* out;            /* [M, N]                                     */
+    int N;
+} rina_linear_seg;
+int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int quant_type,
+                          const float* input, int M, int K, int epilogue,
+                          void* stream);
+
+/* ====================================================================== */
+/* Weight formats                                                          */
+/* ====================================================================== */
+
+/* Pack n fp32 values (n % 32 == 0) into RINA_QT_Q4_0 (18 B blocks, fp16
+ * RNE scale) or RINA_QT_Q4_0F (20 B blocks, fp32 scale).  Replaces
+ * pack_q4_0 / pack_q4_0_f (rina-engine/tools/q4_pack.py:11-23,95-118):
+ * scale = max(amax/7, 1e-10), q = sign(y)*min(floor(|y|+0.5),7). */
+int rina_hip_pack_weights(int quant_type, const float* src, int64_t n,
+                          void* dst, void* stream);
+
+/* Dequantize n elements of a packed weight stream (flat element order) to
+ * fp32.  Q2_K replaces dequant_block_q2_K_gpu (ops/linear.cu:322-338);
+ * Q4_0/Q4_0F follow the matvec dequant rule (ops/linear.cu:77-81). */
+int rina_hip_dequant_weights(int quant_type, const void* src, int64_t n,
+                             float* dst, void* stream);
+
+/* ====================================================================== */
+/* KV cache                                                                */
+/* ====================================================================== */
+
+/* n % 32 == 0 values -> n/32 blocks of `kv_format`.  Replaces
+ * launch_quantize_kv_to_q8_0 / launch_quantize_kv_to_q4_0 /
+ * launch_quantize_k_fp32_to_q2_1 / launch_quantize_v_fp32_to_q1_0
+ * (rina-engine/src/core/kernel_api.h:42-48; kernels/quantize.cu:74-270).
+ * RINA_KVF_Q1_0 writes the documented 6-byte record [fp16][u32 LE]
+ * (core/quant.h:44), not the 8-byte CUDA struct. */
+int rina_hip_kv_quantize(int kv_format, const float* src, void* dst, int64_t n,
+                         void* stream);
+
+/* Inverse of rina_hip_kv_quantize.  Replaces launch_dequant_*
+ * (core/kernel_api.h:44-49; kernels/quantize.cu:106-295). */
+int rina_hip_kv_dequant(int kv_format, const void* src, float* dst, int64_t n,
+                        void* stream);
+
+/* Bytes of one layer's K (which_v = 0) or V (which_v = 1) cache region for
+ * `mode` at max_seq positions of kv_dim values (buffer.cpp:104-132). */
+size_t rina_hip_kv_region_bytes(int mode, int which_v, int max_seq, int kv_dim);
+
+/* RoPE + quantize-on-append for one layer (gqa_layer.cu:147-190):
+ *   q [T, H*dh] and k [T, Hkv*dh] are rotated in place with the NeoX pair
+ *   rule of ops/rope.cu:125-149 (tables [pos, dh/2]; NULL = no rotation);
+ *   K (pre-rotation when pre_rope) and V rows are written into the layer's
+ *   cache regions at position pos0 = start_pos + (d_pos ? *d_pos : 0):
+ *   mode 0: fp32 rows [max_seq, Hkv*dh]; mode 1..5: blocks of the mode's
+ *   formats at block offset pos0*Hkv*dh/32. */
+int rina_hip_rope_append(float* q, float* k, const float* v,
+                         const float* rope_q_cos, const float* rope_q_sin,
+                         const float* rope_k_cos, const float* rope_k_sin,
+                         void* cache_k, void* cache_v, int mode, int pre_rope,
+                         int T, int H, int Hkv, int dh, int start_pos,
+                         const int* d_pos, int max_seq, void* stream);
+
+/* Single-layer GQA attention for T query rows at positions
+ * pos0..pos0+T-1 (pos0 = start_pos + (d_pos ? *d_pos : 0)).  Keys/values at
+ * positions < pos0 are read from the layer's cache (fp32 or packed blocks,
+ * dequantized in registers); positions >= pos0 from kcur/vcur [T, Hkv*dh]
+ * fp32 (the current rows, post-RoPE).  Causal; query head h uses KV head
+ * h / (H/Hkv); scale 1/sqrt(dh).  out [T, H*dh].
+ * Replaces the composition of gqa_layer.cu:192-270 (cache dequant,
+ * build_qkv_fp32.cu:8-33, flash_fp32.cu:12-111, row extraction).
+ * pre_rope: cached keys are rotated with rope_k tables on read
+ * (gqa_layer.cu:236-238).  `workspace` holds split-sequence partials;
+ * rina_hip_gqa_attention_workspace() gives its size. */
+size_t rina_hip_gqa_attention_workspace(int T, int H, int dh, int max_pos);
+int rina_hip_gqa_attention(const float* q, const float* kcur, const float* vcur,
+                           const void* cache_k, const void* cache_v, int mode,
+                           int pre_rope, const float* rope_k_cos,
+                           const float* rope_k_sin, int T, int H, int Hkv, int dh,
+                           int start_pos, const int* d_pos, int max_seq,
+                           float* out, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* ====================================================================== */
+/* Per-token glue                                                          */
+/* ====================================================================== */
+
+/* x[n,d] = x * rsqrt(mean(x^2) + eps) * w — launch_rms_norm_fp32
+ * (ops/rms_norm.cu:5-34).  out may equal x. */
+int rina_hip_rms_norm(const float* x, float* out, const float* w, int n, int d,
+                      float eps, void* stream);
+/* bias-free LayerNorm — launch_pytorch_ln_kernel
+ * (kernels/pytorch_ln_kernel.cu:4-41).  out may equal x. */
+int rina_hip_layer_norm(const float* x, float* out, const float* w, int n, int d,
+                        float eps, void* stream);
+/* RoPE on x [T, H, d]: hf_pairs = 0 -> pairs (i, i+d/2) (launch_rope_fp32,
+ * ops/rope.cu:125-149); 1 -> pairs (2i, 2i+1) (launch_rope_fp32_hf,
+ * ops/rope.cu:212-234).  Row t uses table row start_pos + (d_pos?*d_pos:0) + t. */
+int rina_hip_rope(float* x, const float* cos_t, const float* sin_t, int T, int H,
+                  int d, int start_pos, const int* d_pos, int hf_pairs,
+                  void* stream);
+/* out[n,d] = dequant(W[ids[i]]) for fp32 / Q4_0 / Q4_0F / Q2_K rows —
+ * launch_embedding (ops/embedding.cu:200-230); ids are read at
+ * ids + (d_pos ? *d_pos : 0). */
+int rina_hip_embedding(const void* weight, int quant_type, const int* ids,
+                       const int* d_pos, float* out, int n, int d, void* stream);
+/* o = silu(g) * u — launch_silu_mul (ops/silu_mul.cu:5-12) */
+int rina_hip_silu_mul(float* o, const float* g, const float* u, int64_t n, void* stream);
+/* c = a + b — launch_add (ops/saxpy.cu:10-21) */
+int rina_hip_add(float* c, const float* a, const float* b, int64_t n, void* stream);
+/* d += p * s — launch_saxpy (ops/saxpy.cu:5-17) */
+int rina_hip_saxpy(float* d, const float* s, float p, int64_t n, void* stream);
+/* Greedy argmax with the strict ">" from -1e10 rule of sample()
+ * (src/main.cpp:139-146): the lowest index wins ties.  Writes the index to
+ * out_idx[0]; when d_pos is not NULL also stores it at
+ * ids_out[*d_pos + 1] and increments *d_pos (device-side decode loop). */
+int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out,
+                    int* d_pos, void* stream);
+
+/* Library version / self-description. */
+const char* rina_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

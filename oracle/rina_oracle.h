@@ -1,0 +1,159 @@
+/*
+ * rina_oracle.h — CPU restatement of the RINA engine's decode-step hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the
+ * MI355X HIP path: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it.  The product never links or calls it.
+ *
+ * Every function names the reference file:line it restates (paths are
+ * relative to the reference repository root, rina-engine/src/...).
+ * Arithmetic follows the reference's per-output loop order.  Where nvcc's
+ * default --fmad=true would contract `sum += a*b` into an FMA, the oracle
+ * writes fmaf() explicitly and is built with -ffp-contract=off, so the
+ * rounding sequence is pinned independent of the host compiler.
+ *
+ * Pinning (how each function is checked, see tests/test_oracle_*.py):
+ *   fp16 conversion        exhaustive vs numpy float16 (RNE) over all f16
+ *                          values and edge cases; truncating variant vs
+ *                          closed form.
+ *   weight packers         known answers of rina-engine/tests/test_layers.cu
+ *                          (0xEE -> 7, 0x77 -> 0), round-trip bound
+ *                          |deq - x| <= scale/2, the 0.49999997f edge.
+ *   q4 / q4f / fp32 matvec brute force in float64 (numpy) + the
+ *                          test_linear_q4.cu shapes.
+ *   Q2_K dequant           independent numpy bit-twiddling restatement of
+ *                          the three in-repo statements; exact in fp32.
+ *   KV packers             closed forms (numpy restatement), invariants.
+ *   attention              float64 textbook softmax; single-key and
+ *                          identical-keys invariants.
+ *   glue / model           float64 numpy restatement on tiny shapes.
+ */
+#ifndef RINA_ORACLE_H
+#define RINA_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* QuantType ids (rina-engine/src/core/quant.h:9-14) */
+enum {
+    ORC_Q2_1 = 1, ORC_Q1_0 = 2, ORC_Q4_0 = 5, ORC_FP32 = 6, ORC_Q4_0F = 7,
+    ORC_GGML_Q2_K = 10
+};
+
+/* KV cache modes (rina-engine/src/core/buffer.h:49, buffer.cpp:104-113) */
+enum { ORC_KV_FP32 = 0, ORC_KV_Q8 = 1, ORC_KV_Q4 = 2, ORC_KV_Q4K_Q2V = 3,
+       ORC_KV_Q2 = 4, ORC_KV_Q2K_Q1V = 5 };
+
+/* KV block formats for orc_kv_quantize / orc_kv_dequant */
+enum { ORC_KVF_Q8_0 = 1, ORC_KVF_Q4_0 = 2, ORC_KVF_Q2_1 = 3, ORC_KVF_Q1_0 = 4 };
+
+/* ---- fp16 ---------------------------------------------------------- */
+uint16_t orc_f32_to_f16(float f);        /* IEEE RNE with subnormals (__float2half) */
+uint16_t orc_f32_to_f16_trunc(float f);  /* loader_hf.cpp:208-216 truncating variant */
+float    orc_f16_to_f32(uint16_t h);
+
+/* ---- weight formats ------------------------------------------------ */
+size_t orc_quantized_size(int64_t n_elems, int qt);     /* core/quant.h:75-86 */
+void orc_pack_q4_0(const float* x, int64_t n, uint8_t* out);     /* tools/q4_pack.py:11-23,71-92 */
+void orc_pack_q4_0f(const float* x, int64_t n, uint8_t* out);    /* tools/q4_pack.py:95-118 */
+void orc_pack_q4_0_hf(const float* x, int64_t n, uint8_t* out);  /* src/loader_hf.cpp:196-230 */
+/* dequantize n elements of a weight tensor (flat element order) to fp32 */
+void orc_dequant_weights(const void* w, int qt, int64_t n, float* out);
+
+/* ---- matvec -------------------------------------------------------- */
+/* out[M,N] = in[M,K] . W[N,K]^T, the dispatch of ops/linear.cu:140-167.
+ * nthreads <= 0 picks the host core count.  Row results are independent of
+ * the thread count. */
+int orc_linear(const void* w, int qt, const float* in, float* out,
+               int M, int N, int K, int nthreads);
+
+/* ---- KV cache block formats --------------------------------------- */
+int  orc_kv_block_bytes(int fmt);   /* 34 / 18 / 10 / 6 */
+void orc_kv_quantize(int fmt, const float* in, void* out, int64_t n);
+void orc_kv_dequant(int fmt, const void* in, float* out, int64_t n);
+void orc_kv_mode_formats(int mode, int* kfmt, int* vfmt);
+
+/* ---- glue ---------------------------------------------------------- */
+void orc_rms_norm(float* x, const float* w, int n, int d, float eps);    /* ops/rms_norm.cu:5-29 */
+void orc_layer_norm(float* x, const float* w, int n, int d, float eps);  /* kernels/pytorch_ln_kernel.cu:4-35 */
+void orc_rope_neox(float* x, const float* cos_t, const float* sin_t,
+                   int T, int H, int d, int start_pos);                 /* ops/rope.cu:125-149 */
+void orc_rope_hf(float* x, const float* cos_t, const float* sin_t,
+                 int T, int H, int d, int start_pos);                   /* ops/rope.cu:212-234 */
+void orc_embedding(const void* w, int qt, const int* ids, float* out, int n, int d); /* ops/embedding.cu:6-230 */
+void orc_silu_mul(float* o, const float* g, const float* u, int n);     /* ops/silu_mul.cu:5-8 */
+void orc_add(float* c, const float* a, const float* b, int n);          /* ops/saxpy.cu:10-13 */
+void orc_saxpy(float* d, const float* s, float p, int n);               /* ops/saxpy.cu:5-8 */
+int  orc_argmax(const float* x, int n);                                 /* main.cpp:139-146 */
+
+/* ---- attention ----------------------------------------------------- */
+/* Causal single-head attention of the online form in
+ * kernels/flash_fp32.cu:12-94 for query rows [q0, q0+nq) over keys
+ * [0, q0+i] of K[T,dq] / V[T,dh] (rows of one head, row stride ldk/ldv).
+ * o receives nq rows of dh floats (row stride ldo). */
+void orc_attn_rows(const float* q, int ldq, const float* k, int ldk,
+                   const float* v, int ldv, float* o, int ldo,
+                   int q0, int nq, int dq, int dh);
+
+/* Decode/prefill attention of GQAImpl::forward (arch/gqa/gqa_layer.cu:155-270)
+ * for one layer: queries q[T, H*dh] at positions start_pos..start_pos+T-1;
+ * keys/values [0,start_pos) come from the layer's cache region (mode 0:
+ * fp32 k_cache/v_cache [max_seq, Hkv*dh]; mode>0: quantized blocks at
+ * kq/vq), keys [start_pos, start_pos+T) from kcur/vcur [T, Hkv*dh] fp32.
+ * pre_rope: cached K is stored before RoPE and rotated on read with the
+ * k tables.  out[T, H*dh]. */
+void orc_gqa_attention(const float* q, const float* kcur, const float* vcur,
+                       const float* k_cache, const float* v_cache,
+                       const uint8_t* kq, const uint8_t* vq, int mode, int pre_rope,
+                       const float* rope_k_cos, const float* rope_k_sin,
+                       int T, int start_pos, int H, int Hkv, int dh, float* out);
+
+/* ---- GQA (Llama-shaped) model -------------------------------------- */
+typedef struct {
+    const void* w_q; int qt_q;
+    const void* w_k; int qt_k;
+    const void* w_v; int qt_v;
+    const void* w_o; int qt_o;
+    const void* w1;  int qt_1;
+    const void* w2;  int qt_2;
+    const void* w3;  int qt_3;
+    const float* ln1; const float* ln2;
+    const float* rope_q_cos; const float* rope_q_sin;
+    const float* rope_k_cos; const float* rope_k_sin;
+} orc_gqa_layer_w;
+
+typedef struct {
+    int dim, n_layers, n_heads, n_kv_heads, head_dim, hidden, vocab, max_seq;
+    int use_rms_norm;   /* cfg.name contains "llama" (gqa_layer.cu:90) */
+    int kv_mode;        /* 0..5 */
+    int pre_rope;
+    int nthreads;
+    const void* wte; int qt_wte;
+    const float* ln_f;
+    const void* lm_head; int qt_lm;   /* NULL -> tied to wte */
+    const orc_gqa_layer_w* layers;
+} orc_gqa_cfg;
+
+typedef struct orc_gqa orc_gqa;
+orc_gqa* orc_gqa_create(const orc_gqa_cfg* cfg);
+void     orc_gqa_destroy(orc_gqa* m);
+/* Inference::forward of infer/infer_gqa.cpp:75-105.  logits: [T, vocab]
+ * (only the last row when last_only != 0). */
+int      orc_gqa_forward(orc_gqa* m, const int* ids, int T, int start_pos,
+                         float* logits, int last_only);
+/* raw access to the oracle's cache (mode 0: float data; mode>0: bytes) */
+void*    orc_gqa_cache(orc_gqa* m, int layer, int which_v, size_t* bytes);
+/* fp32 K/V of the last forward's tokens for one layer (post-RoPE unless pre_rope) */
+const float* orc_gqa_last_kv(orc_gqa* m, int layer, int which_v);
+/* main.cpp:666-690 greedy loop: prefill then steps-1 decodes; writes steps ids */
+int      orc_gqa_generate(orc_gqa* m, const int* prompt, int n_prompt, int steps, int* out_ids);
+
+int orc_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,50 @@
+#include "core/layer.h"
+#include <cstdio>
+#include "core/config.h"
+#include "core/tensor.h"
+
+Layer::~Layer() {
+    if (vtab && vtab->destroy_fn) vtab->destroy_fn(impl);
+}
+Layer::Layer(Layer&& o) noexcept : impl(o.impl), vtab(o.vtab) {
+    o.impl = nullptr;
+    o.vtab = nullptr;
+}
+Layer& Layer::operator=(Layer&& o) noexcept {
+    if (this != &o) {
+        if (vtab && vtab->destroy_fn) vtab->destroy_fn(impl);
+        impl = o.impl; vtab = o.vtab;
+        o.impl = nullptr; o.vtab = nullptr;
+    }
+    return *this;
+}
+bool Layer::init(const ModelConfig& cfg, const TensorMap& w, int l) { return vtab->init_fn(impl, cfg, w, l); }
+int Layer::forward(float* h, ForwardBuffers& b, int B, int T, hipStream_t s) { return vtab->forward_fn(impl, h, b, B, T, s); }
+int Layer::workspace_per_token(int d, int H, int dh) { return vtab->workspace_per_token_fn(impl, d, H, dh); }
+
+Layer create_gqa_layer();
+
+Layer* create_layer_by_type(const std::string& type) {
+    Layer* l = new Layer();
+    if (type == "standard_gqa" || type == "standard_attention" || type == "gqa") *l = create_gqa_layer();
+    else { delete l; return nullptr; }
+    return l;
+}
+
+std::vector<std::unique_ptr<Layer>> build_layers(const ModelConfig& cfg, const TensorMap& weights) {
+    std::vector<std::unique_ptr<Layer>> layers;
+    for (int l = 0; l < cfg.n_layers; l++) {
+        std::string type = l < (int)cfg.layers.size() ? cfg.layers[l].type : "standard_attention";
+        std::unique_ptr<Layer> layer(create_layer_by_type(type));
+        if (!layer) {
+            fprintf(stderr, "build_layers: unknown layer type '%s' at index %d\n", type.c_str(), l);
+            return {};
+        }
+        if (!layer->init(cfg, weights, l)) {
+            fprintf(stderr, "build_layers: init failed for layer %d type '%s'\n", l, type.c_str());
+            return {};
+        }
+        layers.push_back(std::move(layer));
+    }
+    return layers;
+}

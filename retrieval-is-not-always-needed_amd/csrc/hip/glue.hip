@@ -1,0 +1,250 @@
+// Per-token glue of the decode step (RMSNorm, LayerNorm, RoPE, embedding,
+// SiLU*up, add, saxpy, greedy argmax) and the library's runtime helpers.
+#include "rina_common.hpp"
+#include "kv_formats.hpp"
+#include <mutex>
+
+namespace {
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    const int nw = (blockDim.x + 63) >> 6;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+// ops/rms_norm.cu:5-29
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, float* out, const float* w, int d, float eps) {
+    __shared__ float red[4];
+    const float* row = x + (int64_t)blockIdx.x * d;
+    float* orow = out + (int64_t)blockIdx.x * d;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) ss = fmaf(row[i], row[i], ss);
+    ss = block_sum(ss, red);
+    float inv = 1.0f / sqrtf(ss / (float)d + eps);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) orow[i] = row[i] * inv * w[i];
+}
+
+// kernels/pytorch_ln_kernel.cu:4-35 (biased variance; two-pass form)
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float* x, float* out, const float* w, int d, float eps) {
+    __shared__ float red[4];
+    const float* row = x + (int64_t)blockIdx.x * d;
+    float* orow = out + (int64_t)blockIdx.x * d;
+    float s = 0.f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) s += row[i];
+    float mean = block_sum(s, red) / (float)d;
+    float v = 0.f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        float t = row[i] - mean;
+        v = fmaf(t, t, v);
+    }
+    float var = block_sum(v, red) / (float)d;
+    float inv = 1.0f / sqrtf(var + eps);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) orow[i] = (row[i] - mean) * inv * (w ? w[i] : 1.0f);
+}
+
+// ops/rope.cu:125-149 (pairs i, i+d/2) and :212-234 (pairs 2i, 2i+1)
+__global__ void rope_kernel(float* x, const float* ct, const float* st, int T, int H, int d, int start_pos,
+                            const int* d_pos, int hf) {
+    const int half = d / 2;
+    int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= (int64_t)T * H * half) return;
+    int i = (int)(p % half);
+    int64_t th = p / half;
+    int t = (int)(th / H);
+    int pos = read_pos(start_pos, d_pos) + t;
+    float c = ct[(int64_t)pos * half + i], s = st[(int64_t)pos * half + i];
+    float* row = x + th * d;
+    int i0 = hf ? 2 * i : i, i1 = hf ? 2 * i + 1 : i + half;
+    float x0 = row[i0], x1 = row[i1];
+    row[i0] = x0 * c - x1 * s;
+    row[i1] = x0 * s + x1 * c;
+}
+
+// ops/embedding.cu:6-230: row lookup with per-format dequant; Q2_K rows are
+// row-aligned (ceil(d/256) blocks per row, ops/embedding.cu:80-81)
+__global__ void embedding_kernel(const uint8_t* w, int qt, const int* ids, const int* d_pos, float* out, int d) {
+    const int t = blockIdx.x;
+    const int off = d_pos ? *d_pos : 0;
+    int id = ids[off + t];
+    if (id < 0) id = 0;
+    float* o = out + (int64_t)t * d;
+    const uint8_t* row;
+    if (qt == RINA_QT_Q4_0) row = w + (int64_t)id * (d / 32) * 18;
+    else if (qt == RINA_QT_Q4_0F) row = w + (int64_t)id * (d / 32) * 20;
+    else if (qt == RINA_QT_GGML_Q2_K) row = w + (int64_t)id * ((d + 255) / 256) * 84;
+    else row = w + (int64_t)id * d * 4;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) o[i] = kvq::weight_elem(qt, row, i);
+}
+
+__global__ void silu_mul_kernel(float* o, const float* g, const float* u, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+}
+__global__ void add_kernel(float* c, const float* a, const float* b, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) c[i] = a[i] + b[i];
+}
+__global__ void saxpy_kernel(float* d, const float* s, float p, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] += p * s[i];
+}
+
+// Greedy argmax (main.cpp:139-146): strict ">" from -1e10, lowest index on
+// ties.  Candidates are packed into one 64-bit key (order-preserving float
+// bits, then the complemented index) and merged with a 64-bit atomicMax;
+// the key slot is a device global that the finishing kernel clears again.
+__device__ unsigned long long g_argmax_key = 0ull;
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    uint32_t b = __float_as_uint(v);
+    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* x, int n) {
+    unsigned long long best = 0ull;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        float v = x[i];
+        if (v > -1e10f) {
+            unsigned long long k = argmax_key(v, i);
+            best = k > best ? k : best;
+        }
+    }
+    // wave max of 64-bit keys
+    for (int off = 32; off > 0; off >>= 1) {
+        unsigned long long o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0 && best) atomicMax(&g_argmax_key, best);
+}
+
+__global__ void argmax_finish_kernel(int* out_idx, int* ids_out, int* d_pos) {
+    unsigned long long k = g_argmax_key;
+    g_argmax_key = 0ull;
+    int idx = k ? (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : 0;
+    if (out_idx) *out_idx = idx;
+    if (d_pos) {
+        int p = *d_pos;
+        if (ids_out) ids_out[p + 1] = idx;
+        *d_pos = p + 1;
+    }
+}
+
+unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+struct DevState {
+    int cus = 0;
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+DevState g_dev[64];
+std::mutex g_mu;
+
+}  // namespace
+
+int rina_num_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!g_dev[dev].cus) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        g_dev[dev].cus = n;
+    }
+    return g_dev[dev].cus;
+}
+
+void* rina_scratch(size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevState& s = g_dev[dev];
+    if (s.scratch_bytes < bytes) {
+        // the previous buffer may still be read by queued work: keep it alive
+        void* p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+        s.scratch = p;
+        s.scratch_bytes = bytes;
+    }
+    return s.scratch;
+}
+
+extern "C" int rina_hip_rms_norm(const float* x, float* out, const float* w, int n, int d, float eps, void* stream) {
+    if (!x || !out || !w || n < 1 || d < 1) return RINA_ERR_ARG;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(256), 0, as_stream(stream), x, out, w, d, eps);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_layer_norm(const float* x, float* out, const float* w, int n, int d, float eps, void* stream) {
+    if (!x || !out || n < 1 || d < 1) return RINA_ERR_ARG;
+    hipLaunchKernelGGL(layer_norm_kernel, dim3(n), dim3(256), 0, as_stream(stream), x, out, w, d, eps);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_rope(float* x, const float* ct, const float* st, int T, int H, int d, int start_pos,
+                             const int* d_pos, int hf, void* stream) {
+    if (!x || !ct || !st || T < 1 || H < 1 || d < 2 || (d & 1)) return RINA_ERR_ARG;
+    int64_t n = (int64_t)T * H * (d / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), x, ct, st, T, H, d,
+                       start_pos, d_pos, hf);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_embedding(const void* w, int qt, const int* ids, const int* d_pos, float* out, int n, int d,
+                                  void* stream) {
+    if (!w || !ids || !out || n < 1 || d < 1) return RINA_ERR_ARG;
+    if (qt != RINA_QT_FP32 && qt != RINA_QT_Q4_0 && qt != RINA_QT_Q4_0F && qt != RINA_QT_GGML_Q2_K)
+        return RINA_ERR_QTYPE;
+    if ((qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && d % 32) return RINA_ERR_SHAPE;
+    hipLaunchKernelGGL(embedding_kernel, dim3(n), dim3(256), 0, as_stream(stream), (const uint8_t*)w, qt, ids, d_pos,
+                       out, d);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_silu_mul(float* o, const float* g, const float* u, int64_t n, void* stream) {
+    if (!o || !g || !u || n < 0) return RINA_ERR_ARG;
+    if (!n) return RINA_OK;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), o, g, u, n);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_add(float* c, const float* a, const float* b, int64_t n, void* stream) {
+    if (!c || !a || !b || n < 0) return RINA_ERR_ARG;
+    if (!n) return RINA_OK;
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), c, a, b, n);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_saxpy(float* d, const float* s, float p, int64_t n, void* stream) {
+    if (!d || !s || n < 0) return RINA_ERR_ARG;
+    if (!n) return RINA_OK;
+    hipLaunchKernelGGL(saxpy_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), d, s, p, n);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out, int* d_pos, void* stream) {
+    if (!x || n < 1 || (!out_idx && !d_pos)) return RINA_ERR_ARG;
+    hipStream_t st = as_stream(stream);
+    int grid = (n + 255) / 256;
+    int cap = rina_num_cus() * 2;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(grid), dim3(256), 0, st, x, n);
+    RINA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, st, out_idx, ids_out, d_pos);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" const char* rina_hip_version(void) { return "rina-mi355x hip 0.1 (gfx950)"; }

@@ -1,0 +1,115 @@
+// Shared device helpers for the gfx950 kernels of the RINA decode hot path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "rina_hip.h"
+
+#define RINA_WAVE 64
+
+// ---------------------------------------------------------------------------
+// fp16 <-> fp32
+// ---------------------------------------------------------------------------
+
+// fp32 -> fp16 bits, IEEE round-to-nearest-even, subnormals kept, overflow to
+// inf (the semantics of __float2half that the reference KV quantizers use,
+// kernels/quantize.cu:89,148,204,263).  Integer-only so the result does not
+// depend on the MODE register's rounding/denormal state.
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u)
+        return sign | (ax > 0x7f800000u ? (0x7e00u | ((ax >> 13) & 0x3ffu)) : 0x7c00u);
+    if (ax >= 0x38800000u) {                       // |f| >= 2^-14: normal f16 range
+        if (ax >= 0x47800000u) return sign | 0x7c00u;   // exponent > 15
+        uint32_t h = ((ax >> 13) - (112u << 10));       // rebias 127 -> 15
+        uint32_t rem = ax & 0x1fffu;
+        h += (rem > 0x1000u) | ((rem == 0x1000u) & (h & 1u));
+        return sign | h;                                // carry may give inf: correct
+    }
+    if (ax < 0x33000000u) return sign;             // < 2^-25: rounds to zero
+    uint32_t e = ax >> 23;                         // 102..112
+    uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    uint32_t s = 126u - e;                         // 14..24
+    uint32_t r = m >> s;
+    uint32_t rem = m & ((1u << s) - 1u);
+    uint32_t half = 1u << (s - 1u);
+    r += (rem > half) | ((rem == half) & (r & 1u));
+    return sign | r;
+}
+
+// fp16 bits -> fp32 (exact).
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    _Float16 v;
+    uint16_t b = (uint16_t)h;
+    __builtin_memcpy(&v, &b, 2);
+    return (float)v;
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions through DPP (no LDS)
+// ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each group of 8 consecutive lanes, result in every lane of the group.
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);   // row_half_mirror
+    return v;
+}
+
+// Sum over each DPP row (16 lanes), result in every lane of the row.
+__device__ __forceinline__ float sum16(float v) {
+    v = sum8(v);
+    v += dpp_f<0x140>(v);   // row_mirror
+    return v;
+}
+
+// Sum over the whole wave, result uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = sum16(v);
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// ---------------------------------------------------------------------------
+// host helpers
+// ---------------------------------------------------------------------------
+
+#define RINA_LAUNCH_CHECK()                                     \
+    do {                                                        \
+        if (hipGetLastError() != hipSuccess) return RINA_ERR_HIP; \
+    } while (0)
+
+static inline hipStream_t as_stream(void* s) { return (hipStream_t)s; }
+
+// Number of compute units of the current device (cached per device).
+int rina_num_cus();
+
+// Per-device scratch buffer owned by the library (grown on demand, never
+// shrunk).  Used only when a caller aliases input and output.
+void* rina_scratch(size_t bytes);
+
+__device__ __forceinline__ int read_pos(int start_pos, const int* d_pos) {
+    return start_pos + (d_pos ? *d_pos : 0);
+}

@@ -1,0 +1,168 @@
+"""Random-init models for the decode path (no checkpoints exist offline).
+
+Weights are fp32 ~ N(0, std) from numpy's PCG64 (one seed per tensor, so a
+tensor's values do not depend on which others are built), packed on the GPU
+by rina_hip_pack_weights (the tools/q4_pack.py rules), and registered in an
+engine model under the reference's tensor names
+(rina-engine/tools/convert_llama_to_rinn.py:97-123): transformer.wte.weight
+(fp32, tied LM head), transformer.h.{l}.attn.w_{q,k,v,o}.weight,
+transformer.h.{l}.mlp.w{1,2,3}.weight, transformer.h.{l}.ln{1,2}.weight,
+transformer.h.{l}.attn.rope_q.{cos,sin} / rope.{cos,sin}, transformer.ln_f.weight.
+"""
+import ctypes as C
+import json
+import math
+
+import numpy as np
+
+from . import QT_FP32, QT_Q4_0, QT_Q4_0F, QT_Q2_K, check, load_engine, load_hip
+
+LLAMA_1B = dict(name="llama3.2-1b", dim=2048, n_layers=16, n_heads=32, n_kv_heads=8, head_dim=64,
+                hidden_dim=8192, vocab_size=128256, rope_theta=500000.0)
+
+
+def make_rope(dim, max_pos, theta=500000.0):
+    """cos/sin tables [max_pos, dim/2] (convert_llama_to_rinn.py:19-34, no scaling)."""
+    inv = (1.0 / (np.float32(theta) ** (np.arange(0, dim, 2, dtype=np.float32) / np.float32(dim)))).astype(np.float32)
+    t = np.arange(max_pos, dtype=np.float32)
+    ang = np.outer(t, inv).astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def normal(seed, n, std):
+    return (np.random.default_rng(seed).standard_normal(n, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+def random_q2k(seed, n_elems, target_std=0.02):
+    """Random valid Q2_K blocks (84 B / 256 values): random 4-bit scale and
+    min nibbles, random 2-bit q, fp16 d / dmin sized so the values have
+    roughly target_std spread (the reference ships no Q2_K quantizer)."""
+    nb = (n_elems + 255) // 256
+    rng = np.random.default_rng(seed)
+    blk = np.zeros((nb, 84), np.uint8)
+    blk[:, 0:16] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    blk[:, 16:80] = rng.integers(0, 256, (nb, 64), dtype=np.uint8)
+    # value = d*sc*q - dmin*m, sc,m in 0..15, q in 0..3: std ~ d*7.5*1.1
+    d = np.float16(target_std / 8.0)
+    dmin = np.float16(target_std / 16.0)
+    blk[:, 80:82] = np.frombuffer(np.array([d], np.float16).tobytes(), np.uint8)
+    blk[:, 82:84] = np.frombuffer(np.array([dmin], np.float16).tobytes(), np.uint8)
+    return blk.reshape(-1)
+
+
+class DeviceArena:
+    """Keeps the torch device tensors that back borrowed engine tensors alive."""
+
+    def __init__(self):
+        self.keep = []
+
+    def put(self, t):
+        self.keep.append(t)
+        return t
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def pack_on_device(x_host, qt, stream=None):
+    """fp32 host array -> packed device tensor (uint8) via rina_hip_pack_weights."""
+    torch = _torch()
+    hip = load_hip()
+    n = x_host.size
+    x = torch.from_numpy(np.ascontiguousarray(x_host, np.float32).reshape(-1)).cuda()
+    if qt == QT_FP32:
+        return x
+    nbytes = (n // 32) * (18 if qt == QT_Q4_0 else 20)
+    out = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    check(hip.rina_hip_pack_weights(qt, x.data_ptr(), n, out.data_ptr(), s), "rina_hip_pack_weights")
+    return out
+
+
+class SynthLlama:
+    """A Llama-shaped GQA model with random weights, built on the device.
+
+    keep_host: also keep host copies of the packed tensors (for the oracle).
+    """
+
+    def __init__(self, cfg, qt=QT_Q4_0F, seed=1, max_seq=1024, std=0.02, keep_host=False, kv_mode="fp32"):
+        torch = _torch()
+        self.cfg = dict(cfg)
+        self.qt = qt
+        self.max_seq = max_seq
+        self.kv_mode = kv_mode
+        self.arena = DeviceArena()
+        self.host = {}
+        self.dev = {}
+        eng = load_engine()
+        c = self.cfg
+        d, H, Hkv, dh, hd, V, L = (c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["hidden_dim"],
+                                   c["vocab_size"], c["n_layers"])
+        header = {"name": c["name"], "dim": d, "n_layers": L, "n_heads": H, "n_kv_heads": Hkv, "head_dim": dh,
+                  "vocab_size": V, "max_seq_len": max_seq, "hidden_dim": hd, "weight_tying": True,
+                  "kv_quant_mode": kv_mode, "layers": [{"type": "standard_attention"} for _ in range(L)]}
+        self.model = eng.rina_model_create(json.dumps(header).encode())
+        if not self.model:
+            raise RuntimeError(eng.rina_engine_last_error().decode())
+        self._eng = eng
+        idx = [0]
+
+        def add(name, shape, qt_, data_dev, host=None):
+            shp = (C.c_int64 * len(shape))(*shape)
+            check(eng.rina_model_add_tensor(self.model, name.encode(), qt_, len(shape), shp, data_dev.data_ptr()),
+                  "add_tensor " + name)
+            self.arena.put(data_dev)
+            self.dev[name] = data_dev
+            if keep_host:
+                self.host[name] = host if host is not None else data_dev.cpu().numpy()
+
+        def weight(name, rows, cols):
+            idx[0] += 1
+            x = normal(seed * 1000003 + idx[0], rows * cols, std)
+            dev = pack_on_device(x, qt)
+            add(name, (rows, cols), qt, dev)
+
+        wte = normal(seed * 1000003, V * d, std)
+        add("transformer.wte.weight", (V, d), QT_FP32, torch.from_numpy(wte).cuda(), wte if keep_host else None)
+        cos, sin = make_rope(dh, max_seq, c.get("rope_theta", 500000.0))
+        cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+        ones = np.ones(d, np.float32)
+        for l in range(L):
+            p = "transformer.h.%d." % l
+            weight(p + "attn.w_q.weight", H * dh, d)
+            weight(p + "attn.w_k.weight", Hkv * dh, d)
+            weight(p + "attn.w_v.weight", Hkv * dh, d)
+            weight(p + "attn.w_o.weight", d, H * dh)
+            weight(p + "mlp.w1.weight", hd, d)
+            weight(p + "mlp.w2.weight", d, hd)
+            weight(p + "mlp.w3.weight", hd, d)
+            add(p + "ln1.weight", (d,), QT_FP32, torch.from_numpy(ones.copy()).cuda(), ones)
+            add(p + "ln2.weight", (d,), QT_FP32, torch.from_numpy(ones.copy()).cuda(), ones)
+            for nm, t, h in (("attn.rope_q.cos", cos_d, cos), ("attn.rope_q.sin", sin_d, sin),
+                             ("attn.rope.cos", cos_d, cos), ("attn.rope.sin", sin_d, sin)):
+                add(p + nm, (max_seq, dh // 2), QT_FP32, t, h)
+        add("transformer.ln_f.weight", (d,), QT_FP32, torch.from_numpy(ones.copy()).cuda(), ones)
+        self.cos, self.sin = cos, sin
+
+    def weight_bytes_per_token(self):
+        c = self.cfg
+        d, H, Hkv, dh, hd, V, L = (c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["hidden_dim"],
+                                   c["vocab_size"], c["n_layers"])
+        bpb = {QT_Q4_0: 18, QT_Q4_0F: 20}[self.qt]
+        per_layer = ((H * dh + 2 * Hkv * dh) * d + d * H * dh + 2 * hd * d + d * hd) // 32 * bpb
+        return L * per_layer + V * d * 4 + (2 * L + 1) * d * 4
+
+    def infer(self, kv_mode=None, max_seq=None):
+        eng = self._eng
+        h = eng.rina_infer_create(self.model, b"gqa", (kv_mode or self.kv_mode).encode(), max_seq or self.max_seq)
+        if not h:
+            raise RuntimeError(eng.rina_engine_last_error().decode())
+        return h
+
+    def close(self):
+        if self.model:
+            self._eng.rina_model_destroy(self.model)
+            self.model = None
+        self.arena.keep.clear()

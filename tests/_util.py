@@ -1,0 +1,65 @@
+"""Shared test helpers: device arrays through torch (plumbing only) and
+tolerance checks stated once."""
+import numpy as np
+
+# Matvec / attention tolerance of the north star: fp32 accumulate, 1e-5
+# relative, measured against the largest output magnitude of the case.
+REL_TOL = 1e-5
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = max(float(np.max(np.abs(ref))), 1e-30)
+    return float(np.max(np.abs(got - ref))) / scale
+
+
+def assert_close(got, ref, tol=REL_TOL, what=""):
+    e = rel_err(got, ref)
+    assert e <= tol, "%s: relative error %.3e > %.1e" % (what, e, tol)
+
+
+def torch():
+    import torch as t
+    return t
+
+
+def dev(a):
+    t = torch()
+    return t.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def empty(n, dtype="float32"):
+    t = torch()
+    dt = {"float32": t.float32, "uint8": t.uint8, "int32": t.int32}[dtype]
+    return t.zeros(n, dtype=dt, device="cuda")
+
+
+def host(t):
+    torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def stream():
+    return torch().cuda.current_stream().cuda_stream
+
+
+_hiprt = None
+
+
+def d2h(ptr, nbytes):
+    """Copy nbytes of device memory owned by the engine to a numpy array."""
+    global _hiprt
+    import ctypes as C
+    if _hiprt is None:
+        _hiprt = C.CDLL("libamdhip64.so")
+        _hiprt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        _hiprt.hipMemcpy.restype = C.c_int
+    torch().cuda.synchronize()
+    out = np.empty(nbytes, np.uint8)
+    assert _hiprt.hipMemcpy(out.ctypes.data, ptr, nbytes, 2) == 0   # hipMemcpyDeviceToHost
+    return out
+
+
+def rng(seed):
+    return np.random.default_rng(seed)

@@ -1,0 +1,356 @@
+"""GPU parity of every C-ABI kernel entry point against the CPU oracle.
+
+Bit-exact: weight packing, weight/KV dequant, KV quantize-on-append.
+1e-5 relative (REL_TOL, fp32 accumulate): matvec, attention, glue.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import _numpy_ref as nr
+from _util import REL_TOL, assert_close, dev, empty, host, rng, stream
+
+pytestmark = pytest.mark.gpu
+
+Q4_SHAPES = [(4, 160, 640), (2, 2048, 2048), (1, 640, 640), (8, 64, 4096),      # test_linear_q4.cu:106-124
+             (1, 8192, 2048), (1, 2048, 8192), (1, 512, 2048), (1, 100, 96), (1, 33, 160), (3, 77, 320),
+             (1, 2048, 16384)]
+
+
+def ok(rc, what=""):
+    assert rc == 0, "%s returned %d" % (what, rc)
+
+
+def q2k_blocks(seed, n):
+    nb = (n + 255) // 256
+    r = rng(seed)
+    blk = r.integers(0, 256, (nb, 84), dtype=np.uint8)
+    blk[:, 80:82] = np.frombuffer(np.float16(0.0025).tobytes() * nb, np.uint8).reshape(nb, 2)
+    blk[:, 82:84] = np.frombuffer(np.float16(0.00125).tobytes() * nb, np.uint8).reshape(nb, 2)
+    return blk.reshape(-1)
+
+
+def gpu_pack(rina, qt, x):
+    xd = dev(x)
+    out = empty((x.size // 32) * (18 if qt == 5 else 20), "uint8")
+    ok(rina.load_hip().rina_hip_pack_weights(qt, xd.data_ptr(), x.size, out.data_ptr(), stream()), "pack")
+    return out
+
+
+@pytest.mark.parametrize("qt", [5, 7])
+def test_pack_weights_bitexact(rina, orc, qt):
+    r = rng(qt)
+    x = (r.standard_normal(32 * 20000) * 0.02).astype(np.float32)
+    x[:32] = 0
+    x[32:64] = np.float32(7.0)
+    x[64:96] = 0
+    x[64] = 7.0
+    x[65] = np.float32(0.49999997)
+    x[96:128] = r.uniform(-1e-12, 1e-12, 32)
+    x[128:160] = np.float32(1e5) * r.standard_normal(32)
+    assert np.array_equal(host(gpu_pack(rina, qt, x)), orc.pack(qt, x))
+
+
+@pytest.mark.parametrize("qt", [5, 7, 10, 6])
+def test_dequant_weights_bitexact(rina, orc, qt):
+    n = 256 * 300
+    if qt == 10:
+        w = q2k_blocks(1, n)
+    elif qt == 6:
+        w = rng(2).standard_normal(n).astype(np.float32)
+    else:
+        w = orc.pack(qt, (rng(3).standard_normal(n) * 0.02).astype(np.float32))
+    out = empty(n)
+    ok(rina.load_hip().rina_hip_dequant_weights(qt, dev(w).data_ptr(), n, out.data_ptr(), stream()))
+    assert np.array_equal(host(out).view(np.uint32), orc.dequant(qt, w, n).view(np.uint32))
+
+
+def run_linear(rina, w, qt, x, N, K):
+    M = x.size // K
+    y = empty(M * N)
+    ok(rina.load_hip().rina_hip_linear(dev(w).data_ptr(), qt, dev(x).data_ptr(), y.data_ptr(), M, N, K, stream()),
+       "linear")
+    return host(y).reshape(M, N)
+
+
+@pytest.mark.parametrize("qt", [5, 7])
+@pytest.mark.parametrize("M,N,K", Q4_SHAPES)
+def test_linear_q4(rina, orc, qt, M, N, K):
+    r = rng(M + N + K + qt)
+    w = orc.pack(qt, (r.standard_normal(N * K) * 0.02).astype(np.float32))
+    x = r.standard_normal((M, K)).astype(np.float32)
+    assert_close(run_linear(rina, w, qt, x, N, K), orc.linear(w, qt, x, N, K), what="q%d %s" % (qt, (M, N, K)))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 2048), (1, 576, 2048), (1, 2048, 1408), (1, 1408, 2048),
+                                   (1, 96, 10944), (1, 4096, 512), (3, 64, 1408), (1, 77, 1408)])
+def test_linear_q2k(rina, orc, M, N, K):
+    w = q2k_blocks(N + K, N * K)
+    x = rng(K).standard_normal((M, K)).astype(np.float32)
+    assert_close(run_linear(rina, w, 10, x, N, K), orc.linear(w, 10, x, N, K), what="q2k %s" % ((M, N, K),))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 32000, 2048), (1, 1000, 640), (2, 300, 2050), (1, 64, 2048)])
+def test_linear_fp32(rina, orc, M, N, K):
+    r = rng(N)
+    w = (r.standard_normal(N * K) * 0.02).astype(np.float32)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    assert_close(run_linear(rina, w, 6, x, N, K), orc.linear(w, 6, x, N, K), what="fp32 %s" % ((M, N, K),))
+
+
+@pytest.mark.parametrize("qt", [7, 6])
+def test_linear_in_place(rina, orc, qt):
+    # input == output: defined as out of place (the reference's in-place w_o call races)
+    N = K = 2048
+    r = rng(77)
+    wf = (r.standard_normal(N * K) * 0.02).astype(np.float32)
+    w = wf if qt == 6 else orc.pack(qt, wf)
+    x = r.standard_normal(K).astype(np.float32)
+    xd = dev(x)
+    ok(rina.load_hip().rina_hip_linear(dev(w).data_ptr(), qt, xd.data_ptr(), xd.data_ptr(), 1, N, K, stream()))
+    assert_close(host(xd), orc.linear(w, qt, x, N, K)[0], what="in-place")
+
+
+@pytest.mark.parametrize("qt", [7, 5, 10, 6])
+def test_linear_fused_epilogues(rina, orc, qt):
+    hip = rina.load_hip()
+    r = rng(qt + 100)
+    K, Ns = 2048, (2048, 512, 512)
+
+    def mk(n):
+        if qt == 10:
+            return q2k_blocks(int(r.integers(1 << 30)), n * K)
+        wf = (r.standard_normal(n * K) * 0.02).astype(np.float32)
+        return wf if qt == 6 else orc.pack(qt, wf)
+
+    ws = [mk(n) for n in Ns]
+    x = r.standard_normal(K).astype(np.float32)
+    xd = dev(x)
+    wd = [dev(w) for w in ws]
+    outs = [empty(n) for n in Ns]
+    segs = (rina.LinearSeg * 3)(*[rina.LinearSeg(wd[i].data_ptr(), None, outs[i].data_ptr(), Ns[i]) for i in range(3)])
+    ok(hip.rina_hip_linear_fused(segs, 3, qt, xd.data_ptr(), 1, K, rina.EPI_STORE, stream()), "fused store")
+    for i in range(3):
+        assert_close(host(outs[i]), orc.linear(ws[i], qt, x, Ns[i], K)[0], what="seg %d" % i)
+    # residual add
+    base = r.standard_normal(2048).astype(np.float32)
+    yd = dev(base)
+    seg = rina.LinearSeg(wd[0].data_ptr(), None, yd.data_ptr(), 2048)
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, xd.data_ptr(), 1, K, rina.EPI_ADD, stream()), "fused add")
+    assert_close(host(yd), base + orc.linear(ws[0], qt, x, 2048, K)[0], what="add")
+    # SiLU(W1 x) * (W3 x)
+    w3 = mk(2048)
+    gd = empty(2048)
+    seg = rina.LinearSeg(wd[0].data_ptr(), dev(w3).data_ptr(), gd.data_ptr(), 2048)
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, xd.data_ptr(), 1, K, rina.EPI_SWIGLU, stream()), "swiglu")
+    g = orc.linear(ws[0], qt, x, 2048, K)[0]
+    u = orc.linear(w3, qt, x, 2048, K)[0]
+    ref = np.zeros(2048, np.float32)
+    orc.load().orc_silu_mul(ref.ctypes.data, g.ctypes.data, u.ctypes.data, 2048)
+    assert_close(host(gd), ref, what="swiglu")
+
+
+@pytest.mark.parametrize("fmt", [1, 2, 3, 4])
+def test_kv_quantize_bitexact(rina, orc, fmt):
+    hip = rina.load_hip()
+    r = rng(fmt)
+    x = r.standard_normal(32 * 5000).astype(np.float32)
+    x[:32] = 0
+    x[32:64] = r.uniform(-1e-11, 1e-11, 32)
+    x[64:96] = np.arange(32, dtype=np.float32) - 15.5
+    x[96:128] = np.float32(3e5) * r.standard_normal(32)
+    out = empty(x.size // 32 * nr.KV_BB[fmt], "uint8")
+    ok(hip.rina_hip_kv_quantize(fmt, dev(x).data_ptr(), out.data_ptr(), x.size, stream()))
+    got = host(out)
+    assert np.array_equal(got, orc.kv_quantize(fmt, x))
+    d = empty(x.size)
+    ok(hip.rina_hip_kv_dequant(fmt, out.data_ptr(), d.data_ptr(), x.size, stream()))
+    ref = orc.kv_dequant(fmt, got, x.size)
+    dh = host(d)
+    fin = np.isfinite(ref)
+    assert np.array_equal(dh[fin], ref[fin]) and np.array_equal(np.isfinite(dh), fin)
+
+
+def rope_tables(dh, n):
+    ang = np.outer(np.arange(n, dtype=np.float32),
+                   (1.0 / (500000.0 ** (np.arange(0, dh, 2, dtype=np.float32) / dh))).astype(np.float32))
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("pre_rope", [0, 1])
+def test_rope_append(rina, orc, mode, pre_rope):
+    hip = rina.load_hip()
+    H, Hkv, dh, T, P, max_seq = 8, 4, 64, 3, 10, 32
+    kvd = Hkv * dh
+    r = rng(mode * 2 + pre_rope)
+    q = r.standard_normal((T, H * dh)).astype(np.float32)
+    k = r.standard_normal((T, kvd)).astype(np.float32)
+    v = r.standard_normal((T, kvd)).astype(np.float32)
+    cos, sin = rope_tables(dh, max_seq)
+    nbytes = hip.rina_hip_kv_region_bytes(mode, 0, max_seq, kvd)
+    vbytes = hip.rina_hip_kv_region_bytes(mode, 1, max_seq, kvd)
+    ck, cv = empty(nbytes, "uint8"), empty(vbytes, "uint8")
+    qd, kd, vd = dev(q), dev(k), dev(v)
+    cd, sd = dev(cos), dev(sin)
+    ok(hip.rina_hip_rope_append(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), cd.data_ptr(), sd.data_ptr(),
+                                cd.data_ptr(), sd.data_ptr(), ck.data_ptr(), cv.data_ptr(), mode, pre_rope, T, H, Hkv,
+                                dh, P, None, max_seq, stream()), "rope_append")
+    qr = nr.rope_neox(q.reshape(T, H, dh), cos, sin, P).reshape(T, -1)
+    kr = nr.rope_neox(k.reshape(T, Hkv, dh), cos, sin, P).reshape(T, -1)
+    assert np.max(np.abs(host(qd) - qr)) <= 1e-5 and np.max(np.abs(host(kd) - kr)) <= 1e-5
+    kc_src = k if pre_rope else host(kd)        # what went into the cache, in fp32
+    if mode == 0:
+        got_k = host(ck).view(np.float32).reshape(max_seq, kvd)[P:P + T]
+        got_v = host(cv).view(np.float32).reshape(max_seq, kvd)[P:P + T]
+        assert np.array_equal(got_k, kc_src) and np.array_equal(got_v, v)
+    else:
+        kf, vf = orc.kv_mode_formats(mode)
+        kb, vb = nr.KV_BB[kf], nr.KV_BB[vf]
+        nbp = kvd // 32
+        got_k = host(ck)[P * nbp * kb:(P + T) * nbp * kb]
+        got_v = host(cv)[P * nbp * vb:(P + T) * nbp * vb]
+        assert np.array_equal(got_k, orc.kv_quantize(kf, kc_src))
+        assert np.array_equal(got_v, orc.kv_quantize(vf, v))
+        assert not host(ck)[: P * nbp * kb].any()        # nothing written outside the rows
+
+
+def attention_case(rina, orc, mode, P, T, H=32, Hkv=8, dh=64, pre_rope=0, use_dpos=False, seed=0):
+    hip = rina.load_hip()
+    L = orc.load()
+    kvd = Hkv * dh
+    max_seq = max(P + T, 8)
+    r = rng(seed * 1000 + mode * 31 + P + T)
+    kc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    vc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    q = r.standard_normal((T, H * dh)).astype(np.float32)
+    kcur = r.standard_normal((T, kvd)).astype(np.float32)
+    vcur = r.standard_normal((T, kvd)).astype(np.float32)
+    cos, sin = rope_tables(dh, max_seq)
+    if mode == 0:
+        ckb, cvb = kc.view(np.uint8).reshape(-1), vc.view(np.uint8).reshape(-1)
+    else:
+        kf, vf = orc.kv_mode_formats(mode)
+        ckb, cvb = orc.kv_quantize(kf, kc), orc.kv_quantize(vf, vc)
+    out = np.zeros((T, H * dh), np.float32)
+    if mode == 0:
+        L.orc_gqa_attention(q.ctypes.data, kcur.ctypes.data, vcur.ctypes.data, kc.ctypes.data, vc.ctypes.data, None,
+                            None, 0, pre_rope, cos.ctypes.data, sin.ctypes.data, T, P, H, Hkv, dh, out.ctypes.data)
+    else:
+        L.orc_gqa_attention(q.ctypes.data, kcur.ctypes.data, vcur.ctypes.data, None, None, ckb.ctypes.data,
+                            cvb.ctypes.data, mode, pre_rope, cos.ctypes.data, sin.ctypes.data, T, P, H, Hkv, dh,
+                            out.ctypes.data)
+    ws_bytes = hip.rina_hip_gqa_attention_workspace(T, H, dh, max_seq)
+    ws = empty(ws_bytes, "uint8")
+    od = empty(T * H * dh)
+    cd, sd = dev(cos), dev(sin)
+    pos = dev(np.array([P], np.int32)) if use_dpos else None
+    ok(hip.rina_hip_gqa_attention(dev(q).data_ptr(), dev(kcur).data_ptr(), dev(vcur).data_ptr(), dev(ckb).data_ptr(),
+                                  dev(cvb).data_ptr(), mode, pre_rope, cd.data_ptr(), sd.data_ptr(), T, H, Hkv, dh,
+                                  0 if use_dpos else P, pos.data_ptr() if use_dpos else None, max_seq, od.data_ptr(),
+                                  ws.data_ptr(), ws_bytes, stream()), "attention")
+    return host(od).reshape(T, -1), out
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("P", [0, 1, 31, 32, 33, 100, 543])
+def test_attention_decode(rina, orc, mode, P):
+    got, ref = attention_case(rina, orc, mode, P, 1)
+    assert_close(got, ref, what="decode mode %d pos %d" % (mode, P))
+
+
+@pytest.mark.parametrize("mode", [0, 1, 5])
+def test_attention_decode_device_pos(rina, orc, mode):
+    got, ref = attention_case(rina, orc, mode, 70, 1, use_dpos=True)
+    assert_close(got, ref, what="d_pos mode %d" % mode)
+
+
+@pytest.mark.parametrize("mode,P,T", [(0, 0, 7), (0, 5, 4), (2, 9, 3), (5, 0, 33), (1, 40, 2)])
+def test_attention_multi_row(rina, orc, mode, P, T):
+    got, ref = attention_case(rina, orc, mode, P, T)
+    assert_close(got, ref, what="rows mode %d P %d T %d" % (mode, P, T))
+
+
+@pytest.mark.parametrize("H,Hkv,dh", [(10, 5, 64), (16, 16, 128), (4, 2, 32)])
+def test_attention_other_shapes(rina, orc, H, Hkv, dh):
+    got, ref = attention_case(rina, orc, 0, 20, 1, H=H, Hkv=Hkv, dh=dh)
+    assert_close(got, ref, what="shape %s" % ((H, Hkv, dh),))
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_attention_pre_rope(rina, orc, mode):
+    got, ref = attention_case(rina, orc, mode, 12, 1, pre_rope=1)
+    assert_close(got, ref, what="pre_rope mode %d" % mode)
+
+
+def test_glue(rina, orc):
+    hip = rina.load_hip()
+    L = orc.load()
+    r = rng(5)
+    n, d = 3, 2048
+    x = r.standard_normal((n, d)).astype(np.float32)
+    w = r.uniform(0.5, 1.5, d).astype(np.float32)
+    for fn_h, fn_o in ((hip.rina_hip_rms_norm, L.orc_rms_norm), (hip.rina_hip_layer_norm, L.orc_layer_norm)):
+        xd, od = dev(x), empty(n * d)
+        ok(fn_h(xd.data_ptr(), od.data_ptr(), dev(w).data_ptr(), n, d, np.float32(1e-5), stream()))
+        ref = x.copy()
+        fn_o(ref.ctypes.data, w.ctypes.data, n, d, np.float32(1e-5))
+        assert_close(host(od).reshape(n, d), ref, what="norm")
+    T, H, hd = 3, 4, 64
+    cos, sin = rope_tables(hd, 64)
+    xr = r.standard_normal((T, H, hd)).astype(np.float32)
+    for hf, fn in ((0, L.orc_rope_neox), (1, L.orc_rope_hf)):
+        xd = dev(xr)
+        ok(hip.rina_hip_rope(xd.data_ptr(), dev(cos).data_ptr(), dev(sin).data_ptr(), T, H, hd, 9, None, hf, stream()))
+        ref = xr.copy()
+        fn(ref.ctypes.data, cos.ctypes.data, sin.ctypes.data, T, H, hd, 9)
+        assert np.max(np.abs(host(xd) - ref)) <= 1e-6
+    g = r.standard_normal(5000).astype(np.float32)
+    u = r.standard_normal(5000).astype(np.float32)
+    od = empty(5000)
+    ok(hip.rina_hip_silu_mul(od.data_ptr(), dev(g).data_ptr(), dev(u).data_ptr(), 5000, stream()))
+    ref = np.zeros(5000, np.float32)
+    L.orc_silu_mul(ref.ctypes.data, g.ctypes.data, u.ctypes.data, 5000)
+    assert_close(host(od), ref, what="silu")
+    ok(hip.rina_hip_add(od.data_ptr(), dev(g).data_ptr(), dev(u).data_ptr(), 5000, stream()))
+    assert np.array_equal(host(od), g + u)
+    dd = dev(g)
+    ok(hip.rina_hip_saxpy(dd.data_ptr(), dev(u).data_ptr(), np.float32(0.5), 5000, stream()))
+    assert_close(host(dd), g + np.float32(0.5) * u, what="saxpy")
+
+
+@pytest.mark.parametrize("qt", [6, 5, 7, 10])
+def test_embedding(rina, orc, qt):
+    hip = rina.load_hip()
+    V, d = 300, 512
+    if qt == 10:
+        w = q2k_blocks(9, V * d)
+    else:
+        wf = (rng(qt).standard_normal(V * d) * 0.02).astype(np.float32)
+        w = wf if qt == 6 else orc.pack(qt, wf)
+    ids = np.array([0, 299, -4, 17, 150], np.int32)
+    od = empty(5 * d)
+    ok(hip.rina_hip_embedding(dev(w).data_ptr(), qt, dev(ids).data_ptr(), None, od.data_ptr(), 5, d, stream()))
+    ref = np.zeros((5, d), np.float32)
+    orc.load().orc_embedding(w.ctypes.data, qt, ids.ctypes.data, ref.ctypes.data, 5, d)
+    assert np.array_equal(host(od).reshape(5, d), ref)
+
+
+def test_argmax(rina, orc):
+    hip = rina.load_hip()
+    cases = [np.array([-1e11, 3.0, 5.0, 5.0, np.nan, 1.0], np.float32),
+             np.full(7, -2e10, np.float32),
+             rng(1).standard_normal(128256).astype(np.float32)]
+    c3 = cases[2].copy()
+    c3[[100, 90000, 128255]] = 50.0
+    cases.append(c3)
+    for a in cases:
+        out = empty(1, "int32")
+        ok(hip.rina_hip_argmax(dev(a).data_ptr(), a.size, out.data_ptr(), None, None, stream()))
+        assert int(host(out)[0]) == orc.load().orc_argmax(a.ctypes.data, a.size)
+    # device-loop form: ids[pos+1] = argmax, pos += 1
+    ids = empty(16, "int32")
+    pos = dev(np.array([4], np.int32))
+    ok(hip.rina_hip_argmax(dev(c3).data_ptr(), c3.size, None, ids.data_ptr(), pos.data_ptr(), stream()))
+    assert int(host(pos)[0]) == 5 and int(host(ids)[5]) == 100
