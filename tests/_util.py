@@ -24,15 +24,26 @@ def torch():
     return t
 
 
+# Device tensors created by dev()/empty() stay referenced until the next
+# test starts (conftest clears the list): a temporary whose only use is
+# .data_ptr() would otherwise return its block to torch's caching allocator
+# before the kernel runs, and the next upload would alias it.
+LIVE = []
+
+
 def dev(a):
     t = torch()
-    return t.from_numpy(np.ascontiguousarray(a)).cuda()
+    x = t.from_numpy(np.ascontiguousarray(a)).cuda()
+    LIVE.append(x)
+    return x
 
 
 def empty(n, dtype="float32"):
     t = torch()
     dt = {"float32": t.float32, "uint8": t.uint8, "int32": t.int32}[dtype]
-    return t.zeros(n, dtype=dt, device="cuda")
+    x = t.zeros(n, dtype=dt, device="cuda")
+    LIVE.append(x)
+    return x
 
 
 def host(t):

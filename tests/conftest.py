@@ -30,6 +30,15 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: full-size shapes")
 
 
+@pytest.fixture(autouse=True)
+def _release_device_tensors():
+    yield
+    import _util
+    if _util.LIVE:
+        _util.torch().cuda.synchronize()
+        _util.LIVE.clear()
+
+
 @pytest.fixture(scope="session")
 def rina():
     return load_pkg()
