@@ -137,7 +137,7 @@ def main():
 
     def swiglu(i=0):
         return hip.rina_hip_linear_fused(C.byref(segs[i % nl]), 1, rina.QT_Q4_0F, x.data_ptr(), 1, d,
-                                         rina.EPI_SWIGLU, st)
+                                         rina.EPI_SWIGLU, rina.PRO_NONE, None, 0.0, st)
     t_sw = time_kernel(torch, swiglu, args.kernel_iters)
     sw_bytes = 2 * hd * d // 32 * 20 + d * 4 + hd * 4
     sw_roof = roofline(sw_bytes, t_sw)

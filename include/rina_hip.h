@@ -72,10 +72,20 @@ int rina_hip_linear(const void* weight, int quant_type, const float* input,
  *   RINA_EPI_SWIGLU  out_0 = silu(W_0 . x) * (W2_0 . x)
  *                                             (w1, w3, launch_silu_mul:
  *                                              gqa_layer.cu:278-281)
- * All segments share quant_type and K.  input must not alias any output. */
+ * All segments share quant_type and K.  input must not alias any output.
+ * prologue normalizes each input row before the product, fusing the
+ * norm launch that precedes these matvecs in the reference:
+ *   RINA_PRO_NONE       x used as is
+ *   RINA_PRO_RMSNORM    x * rsqrt(mean(x^2) + eps) * norm_w
+ *                       (ops/rms_norm.cu:5-29, gqa_layer.cu:136,277)
+ *   RINA_PRO_LAYERNORM  (x - mean) * rsqrt(var + eps) * norm_w
+ *                       (kernels/pytorch_ln_kernel.cu:4-35) */
 #define RINA_EPI_STORE  0
 #define RINA_EPI_ADD    1
 #define RINA_EPI_SWIGLU 2
+#define RINA_PRO_NONE      0
+#define RINA_PRO_RMSNORM   1
+#define RINA_PRO_LAYERNORM 2
 typedef struct {
     const void* weight;    /* [N, K] packed                              */
     const void* weight2;   /* RINA_EPI_SWIGLU: the up projection [N, K]  */
@@ -84,6 +94,7 @@ typedef struct {
 } rina_linear_seg;
 int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int quant_type,
                           const float* input, int M, int K, int epilogue,
+                          int prologue, const float* norm_w, float eps,
                           void* stream);
 
 /* ====================================================================== */

@@ -17,6 +17,7 @@ QT_Q4_0, QT_FP32, QT_Q4_0F, QT_Q2_K = 5, 6, 7, 10
 KV_MODES = {"fp32": 0, "q8": 1, "q4": 2, "q4k_q2v": 3, "q2": 4, "q2k_q1v": 5}
 KVF_Q8_0, KVF_Q4_0, KVF_Q2_1, KVF_Q1_0 = 1, 2, 3, 4
 EPI_STORE, EPI_ADD, EPI_SWIGLU = 0, 1, 2
+PRO_NONE, PRO_RMSNORM, PRO_LAYERNORM = 0, 1, 2
 STATUS = {0: "OK", -1: "ERR_ARG", -2: "ERR_QTYPE", -3: "ERR_SHAPE", -4: "ERR_RANGE", -5: "ERR_HIP",
           -6: "ERR_WORKSPACE"}
 
@@ -32,7 +33,7 @@ class LinearSeg(C.Structure):
 
 _HIP_SIGS = {
     "rina_hip_linear": (I32, [VP, I32, VP, VP, I32, I32, I32, VP]),
-    "rina_hip_linear_fused": (I32, [C.POINTER(LinearSeg), I32, I32, VP, I32, I32, I32, VP]),
+    "rina_hip_linear_fused": (I32, [C.POINTER(LinearSeg), I32, I32, VP, I32, I32, I32, I32, VP, F32, VP]),
     "rina_hip_pack_weights": (I32, [I32, VP, I64, VP, VP]),
     "rina_hip_dequant_weights": (I32, [I32, VP, I64, VP, VP]),
     "rina_hip_kv_quantize": (I32, [I32, VP, VP, I64, VP]),

@@ -4,8 +4,9 @@
 //   fp32); o = attention over cache + current rows; h += W_o o;
 //   a = norm(h, ln2); h += W2 (silu(W1 a) * (W3 a)).
 // The launches are fused where the reference runs back-to-back kernels on
-// the same data (q/k/v in one matvec launch, RoPE + append in one kernel,
-// W_o and W2 with the residual add as epilogue, W1/W3 with SiLU*up), and
+// the same data (norm as the matvec prologue, q/k/v in one matvec launch,
+// RoPE + append in one kernel, W_o and W2 with the residual add as
+// epilogue, W1/W3 with SiLU*up), and
 // W_o is computed out of place (the reference's in-place call races,
 // gqa_layer.cu:272).
 #include <cstdio>
@@ -62,20 +63,16 @@ struct GQAImpl {
         return ok;
     }
 
-    int norm(const float* x, float* out, const float* w, int n, hipStream_t s) {
-        return use_rms_norm ? rina_hip_rms_norm(x, out, w, n, d, 1e-5f, s) : rina_hip_layer_norm(x, out, w, n, d, 1e-5f, s);
-    }
-
     int forward(float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
         const int n = B * T, kvd = Hkv * dh;
         const int start_pos = b.kv_cache.start_pos;
         int rc;
 #define CK(x) do { if ((rc = (x)) != RINA_OK) return rc; } while (0)
-        CK(norm(h, b.a, ln1, n, s));
+        const int pro = use_rms_norm ? RINA_PRO_RMSNORM : RINA_PRO_LAYERNORM;
         rina_linear_seg qkv[3] = {{w_q.data, nullptr, b.q, H * dh},
                                   {w_k.data, nullptr, b.k, kvd},
                                   {w_v.data, nullptr, b.v, kvd}};
-        CK(rina_hip_linear_fused(qkv, 3, (int)w_q.qt, b.a, n, d, RINA_EPI_STORE, s));
+        CK(rina_hip_linear_fused(qkv, 3, (int)w_q.qt, h, n, d, RINA_EPI_STORE, pro, ln1, 1e-5f, s));
         const int mode = b.kv_cache_quant.mode;
         void* ck;
         void* cv;
@@ -99,12 +96,11 @@ struct GQAImpl {
         CK(rina_hip_gqa_attention(b.q, b.k, b.v, ck, cv, mode, pre_rope, rk_cos, rk_sin, n, H, Hkv, dh, start_pos,
                                   b.d_pos, max_seq, b.a, b.attn_ws, b.attn_ws_bytes, s));
         rina_linear_seg o{w_o.data, nullptr, h, d};
-        CK(rina_hip_linear_fused(&o, 1, (int)w_o.qt, b.a, n, H * dh, RINA_EPI_ADD, s));
-        CK(norm(h, b.a, ln2, n, s));
+        CK(rina_hip_linear_fused(&o, 1, (int)w_o.qt, b.a, n, H * dh, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
         rina_linear_seg up{w1.data, w3.data, b.g, hd};
-        CK(rina_hip_linear_fused(&up, 1, (int)w1.qt, b.a, n, d, RINA_EPI_SWIGLU, s));
+        CK(rina_hip_linear_fused(&up, 1, (int)w1.qt, h, n, d, RINA_EPI_SWIGLU, pro, ln2, 1e-5f, s));
         rina_linear_seg down{w2.data, nullptr, h, d};
-        CK(rina_hip_linear_fused(&down, 1, (int)w2.qt, b.g, n, hd, RINA_EPI_ADD, s));
+        CK(rina_hip_linear_fused(&down, 1, (int)w2.qt, b.g, n, hd, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
 #undef CK
         return RINA_OK;
     }

@@ -94,12 +94,6 @@ struct GQAInference : Inference {
         return RINA_OK;
     }
 
-    int norm_f(float* x, int n, hipStream_t s) {
-        if (!ln_f) return RINA_OK;
-        const float* w = (const float*)ln_f->data;
-        return use_rms ? rina_hip_rms_norm(x, x, w, n, cfg.dim, 1e-5f, s) : rina_hip_layer_norm(x, x, w, n, cfg.dim, 1e-5f, s);
-    }
-
     const WeightTensor* head() const {
         return (lm_head && lm_head->quant_type != QuantType::GGML_Q6_K) ? lm_head : wte;   // infer_gqa.cpp:97-100
     }
@@ -118,8 +112,11 @@ struct GQAInference : Inference {
         const float* x = f.h;
         int M = T;
         if (last_only) { x = f.h + (size_t)(T - 1) * cfg.dim; M = 1; }
-        if ((rc = norm_f((float*)x, M, s))) return rc;
-        return rina_hip_linear(hw->data, (int)hw->quant_type, x, logits, M, cfg.vocab_size, cfg.dim, s);
+        // ln_f fused as the LM head's prologue (infer_gqa.cpp:90-100)
+        rina_linear_seg seg{hw->data, nullptr, logits, cfg.vocab_size};
+        int pro = ln_f ? (use_rms ? RINA_PRO_RMSNORM : RINA_PRO_LAYERNORM) : RINA_PRO_NONE;
+        return rina_hip_linear_fused(&seg, 1, (int)hw->quant_type, x, M, cfg.dim, RINA_EPI_STORE, pro,
+                                     ln_f ? (const float*)ln_f->data : nullptr, 1e-5f, s);
     }
 
     int forward(const int* ids, float* logits, int B, int T, int start_pos, hipStream_t s) override {

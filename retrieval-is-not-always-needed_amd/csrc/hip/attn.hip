@@ -8,19 +8,32 @@
 // reads KV head h / (H/Hkv); score = (q.k) / sqrt(dh).
 //
 // Decode (T == 1, dh == 64): split-sequence.  A workgroup takes a chunk of
-// kChunk positions and a group of HG KV heads whose records are contiguous
+// positions and a group of HG KV heads whose records are contiguous
 // in every cache layout (position-major, heads inside), so each position's
 // bytes are consumed whole.  8 lanes cover one head's 64 dims (8 values per
 // lane, dequantized in registers), the REP query heads of that KV head are
 // reduced with DPP inside the 8-lane group.  Scores go to LDS, the chunk's
 // softmax is formed there, V is accumulated in registers and the chunk
-// writes (max, sum, O) partials; a combine kernel merges the chunks.
+// writes (max, sum, O) partials; the last chunk to finish merges them.
 #include "rina_common.hpp"
 #include "kv_formats.hpp"
 
 namespace {
 
-constexpr int kChunk = 32;   // positions per decode workgroup
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSub = 32;     // chunk granularity (a multiple of every sub-step)
+constexpr int kMaxChunks = 64;  // chunk partials per head (chunk size adapts)
+
+// Chunk length for a cache of max_pos positions: at most kMaxChunks
+// partials per head, each a multiple of the kSub sub-step.
+int chunk_len(int max_pos, int gran) {
+    int per = (max_pos + kMaxChunks - 1) / kMaxChunks;
+    per = (per + gran - 1) / gran * gran;
+    return per < gran ? gran : per;
+}
+
+constexpr size_t kCounterBytes = 256;   // per-head-group completion counters
 
 struct AttnArgs {
     const float* q;
@@ -34,8 +47,11 @@ struct AttnArgs {
     float* ws_m;
     float* ws_l;
     float* ws_o;
-    int mode, pre_rope, T, H, Hkv, dh, start_pos, max_seq, nchunk_max;
+    int mode, pre_rope, T, H, Hkv, dh, start_pos, max_seq, nchunk_max, chunk;
     const int* d_pos;
+    int* counters;   // per head group, in the workspace; zero between calls
+    void* ws;
+    size_t ws_bytes;
     float scale;
 };
 
@@ -43,8 +59,8 @@ struct AttnArgs {
 template <int FMT>
 __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o)[8]) {
     if (FMT == 0) {
-        const float4* p = (const float4*)((const float*)base + v0);
-        float4 a = p[0], b = p[1];
+        const f32x4* p = (const f32x4*)((const float*)base + v0);
+        f32x4 a = gld(p), b = gld(p + 1);
         o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
         o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
         return;
@@ -52,52 +68,65 @@ __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o
     constexpr int BB = kvq::block_bytes_c(FMT);
     const uint8_t* blk = base + (v0 >> 5) * BB;
     const int w = (int)(v0 & 31);
-    float s = f16_to_f32(kvq::ld16(blk));
+    float s = f16_to_f32(gld((const uint16_t*)blk));
     if (FMT == RINA_KVF_Q8_0) {
         const uint8_t* d = blk + 2 + w;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
-            uint32_t two = kvq::ld16(d + i);
+            uint32_t two = gld((const uint16_t*)(d + i));
             o[i] = (float)(int8_t)(two & 0xFF) * s;
             o[i + 1] = (float)(int8_t)(two >> 8) * s;
         }
     } else if (FMT == RINA_KVF_Q4_0) {
-        uint32_t n = kvq::ld16(blk + 2 + w / 2) | (kvq::ld16(blk + 4 + w / 2) << 16);
+        uint32_t n = (uint32_t)gld((const uint16_t*)(blk + 2 + w / 2)) |
+                     ((uint32_t)gld((const uint16_t*)(blk + 4 + w / 2)) << 16);
 #pragma unroll
         for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (4 * i)) & 0xF) - 7) * s;
     } else if (FMT == RINA_KVF_Q2_1) {
-        uint32_t n = kvq::ld16(blk + 2 + w / 4);
+        uint32_t n = gld((const uint16_t*)(blk + 2 + w / 4));
 #pragma unroll
         for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (2 * i)) & 3) - 1) * s;
     } else {
-        uint32_t bits = (kvq::ld16(blk + 2) | (kvq::ld16(blk + 4) << 16)) >> w;
+        uint32_t bits = ((uint32_t)gld((const uint16_t*)(blk + 2)) | ((uint32_t)gld((const uint16_t*)(blk + 4)) << 16)) >> w;
 #pragma unroll
         for (int i = 0; i < 8; i++) o[i] = ((bits >> i) & 1u) ? s : -s;
     }
 }
 
+// Chunk c of a head group covers positions [c*CS, c*CS+CS) in sub-steps of
+// kSub positions; K and V of a sub-step are loaded together (one HBM round
+// trip), scores are reduced in LDS and the chunk keeps an online softmax
+// across sub-steps.  The last workgroup of a head group to finish (counter in
+// the workspace, reset by that workgroup) merges the chunk partials, so no
+// second launch and no memset node is needed.
 template <int KF, int VF, int HG, int REP>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     constexpr int DH = 64;
     constexpr int LPP = 8 * HG;          // lanes per position record
     constexpr int PPW = 64 / LPP;        // positions per wave step
     constexpr int GS = 4 * PPW;          // positions per workgroup step
+    constexpr int SUB = GS > 16 ? GS : 16;   // positions per sub-step (divides kSub)
+    constexpr int NST = SUB / GS;            // steps per sub-step
     constexpr int QH = HG * REP;         // query heads in the group
     constexpr int KBB = kvq::block_bytes_c(KF), VBB = kvq::block_bytes_c(VF);
-    __shared__ float s_lds[QH][kChunk];
-    __shared__ float o_red[GS][QH * DH];
+    static_assert(NST >= 1 && kSub % SUB == 0, "sub-step");
+    __shared__ float s_lds[QH][SUB];
+    __shared__ float s_alpha[QH];
+    __shared__ float o_red[GS * QH * DH];
+    __shared__ float s_hm[QH], s_hl[QH];
+    __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;     // capacity guard (host checks host-known positions)
     const int L = pos0 + 1;
+    const int CS = a.chunk;
     const int c = blockIdx.x;
-    const int j0 = c * kChunk;
+    const int j0 = c * CS;
     if (j0 >= L) return;
-    const int nvalid = min(kChunk, L - j0);
+    const int ncv = min(CS, L - j0);
     const int kvd = a.Hkv * DH;
     const int hg0 = blockIdx.y * HG;
-    // bytes of one position record (all KV heads) in each cache region
     const int64_t KREC = KF ? (int64_t)(kvd / 32) * KBB : (int64_t)kvd * 4;
     const int64_t VREC = VF ? (int64_t)(kvd / 32) * VBB : (int64_t)kvd * 4;
 
@@ -106,105 +135,166 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     const int dim0 = (lig & 7) * 8;
     const int kvh = hg0 + kvl;
     const int64_t voff = (int64_t)kvh * DH + dim0;  // value offset inside a position record
+    const int wslot = wave * PPW + slot;
 
-    float qv[REP][8];
+    float qv[REP][8], ov[REP][8];
+    float m_run = -INFINITY, l_run = 0.f;           // owned by threads tid < QH
+    bool first = true;
+    for (int sub = 0; sub < ncv; sub += SUB) {
+        float kv[NST][8], vv[NST][8];
 #pragma unroll
-    for (int r = 0; r < REP; r++) {
-        const float4* qp = (const float4*)(a.q + (int64_t)(kvh * REP + r) * DH + dim0);
-        float4 x0 = qp[0], x1 = qp[1];
-        qv[r][0] = x0.x; qv[r][1] = x0.y; qv[r][2] = x0.z; qv[r][3] = x0.w;
-        qv[r][4] = x1.x; qv[r][5] = x1.y; qv[r][6] = x1.z; qv[r][7] = x1.w;
-    }
-
-    // ---- scores
-    for (int st = 0; st < kChunk; st += GS) {
-        const int jl = st + wave * PPW + slot;
-        const int j = j0 + jl;
-        const bool valid = jl < nvalid;
-        float kv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (valid) {
-            if (j == pos0) load8<0>((const uint8_t*)a.kcur, voff, kv);
-            else load8<KF>(a.ck + (int64_t)j * KREC, voff, kv);
-        }
+        for (int st = 0; st < NST; st++) {
+            const int jl = sub + st * GS + wslot;
+            const int j = j0 + jl;
 #pragma unroll
-        for (int r = 0; r < REP; r++) {
-            float p = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) p = fmaf(qv[r][i], kv[i], p);
-            p = sum8(p);
-            if (valid && (lig & 7) == 0) s_lds[kvl * REP + r][jl] = p * a.scale;
-        }
-    }
-    __syncthreads();
-    // ---- chunk softmax: one thread per query head
-    if (tid < QH) {
-        float m = -INFINITY;
-        for (int jl = 0; jl < nvalid; jl++) m = fmaxf(m, s_lds[tid][jl]);
-        float l = 0.f;
-        for (int jl = 0; jl < nvalid; jl++) {
-            float p = expf(s_lds[tid][jl] - m);
-            s_lds[tid][jl] = p;
-            l += p;
-        }
-        const int h = hg0 * REP + tid;
-        a.ws_m[(int64_t)c * a.H + h] = m;
-        a.ws_l[(int64_t)c * a.H + h] = l;
-    }
-    __syncthreads();
-    // ---- P.V
-    float ov[REP][8];
-#pragma unroll
-    for (int r = 0; r < REP; r++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) ov[r][i] = 0.f;
-    for (int st = 0; st < kChunk; st += GS) {
-        const int jl = st + wave * PPW + slot;
-        const int j = j0 + jl;
-        if (jl < nvalid) {
-            float vv[8];
-            if (j == pos0) load8<0>((const uint8_t*)a.vcur, voff, vv);
-            else load8<VF>(a.cv + (int64_t)j * VREC, voff, vv);
-#pragma unroll
-            for (int r = 0; r < REP; r++) {
-                float p = s_lds[kvl * REP + r][jl];
-#pragma unroll
-                for (int i = 0; i < 8; i++) ov[r][i] = fmaf(p, vv[i], ov[r][i]);
+            for (int i = 0; i < 8; i++) kv[st][i] = vv[st][i] = 0.f;
+            if (jl < ncv) {
+                if (j == pos0) {
+                    load8<0>((const uint8_t*)a.kcur, voff, kv[st]);
+                    load8<0>((const uint8_t*)a.vcur, voff, vv[st]);
+                } else {
+                    load8<KF>(a.ck + (int64_t)j * KREC, voff, kv[st]);
+                    load8<VF>(a.cv + (int64_t)j * VREC, voff, vv[st]);
+                }
             }
         }
+        if (first) {
+#pragma unroll
+            for (int r = 0; r < REP; r++) {
+                const f32x4* qp = (const f32x4*)(a.q + (int64_t)(kvh * REP + r) * DH + dim0);
+                f32x4 x0 = gld(qp), x1 = gld(qp + 1);
+                qv[r][0] = x0.x; qv[r][1] = x0.y; qv[r][2] = x0.z; qv[r][3] = x0.w;
+                qv[r][4] = x1.x; qv[r][5] = x1.y; qv[r][6] = x1.z; qv[r][7] = x1.w;
+#pragma unroll
+                for (int i = 0; i < 8; i++) ov[r][i] = 0.f;
+            }
+            first = false;
+        }
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            const int jl = sub + st * GS + wslot;
+#pragma unroll
+            for (int r = 0; r < REP; r++) {
+                float p = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) p = fmaf(qv[r][i], kv[st][i], p);
+                p = sum8(p);
+                if (jl < ncv && (lig & 7) == 0) s_lds[kvl * REP + r][st * GS + wslot] = p * a.scale;
+            }
+        }
+        __syncthreads();
+        if (tid < QH) {
+            const int nv = min(SUB, ncv - sub);
+            float mx = -INFINITY;
+            for (int jl = 0; jl < nv; jl++) mx = fmaxf(mx, s_lds[tid][jl]);
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = expf(m_run - m_new);      // 0 on the first sub-step
+            float sum = 0.f;
+            for (int jl = 0; jl < nv; jl++) {
+                float p = expf(s_lds[tid][jl] - m_new);
+                s_lds[tid][jl] = p;
+                sum += p;
+            }
+            l_run = l_run * alpha + sum;
+            m_run = m_new;
+            s_alpha[tid] = alpha;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < REP; r++) {
+            const float al = s_alpha[kvl * REP + r];
+#pragma unroll
+            for (int i = 0; i < 8; i++) ov[r][i] *= al;
+#pragma unroll
+            for (int st = 0; st < NST; st++) {
+                if (sub + st * GS + wslot < ncv) {
+                    const float p = s_lds[kvl * REP + r][st * GS + wslot];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) ov[r][i] = fmaf(p, vv[st][i], ov[r][i]);
+                }
+            }
+        }
+        __syncthreads();
     }
-    const int gslot = wave * PPW + slot;
+    // chunk partials
+    if (tid < QH) {
+        const int h = hg0 * REP + tid;
+        a.ws_m[(int64_t)c * a.H + h] = m_run;
+        a.ws_l[(int64_t)c * a.H + h] = l_run;
+    }
 #pragma unroll
     for (int r = 0; r < REP; r++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) o_red[gslot][(kvl * REP + r) * DH + dim0 + i] = ov[r][i];
+        for (int i = 0; i < 8; i++) o_red[wslot * QH * DH + (kvl * REP + r) * DH + dim0 + i] = ov[r][i];
     __syncthreads();
     for (int e = tid; e < QH * DH; e += 256) {
         float acc = 0.f;
 #pragma unroll
-        for (int g = 0; g < GS; g++) acc += o_red[g][e];
+        for (int g = 0; g < GS; g++) acc += o_red[g * QH * DH + e];
         const int h = hg0 * REP + e / DH;
         a.ws_o[((int64_t)c * a.H + h) * DH + (e % DH)] = acc;
     }
-}
-
-__global__ void attn_combine_kernel(AttnArgs a) {
-    const int h = blockIdx.x;
-    const int pos0 = read_pos(a.start_pos, a.d_pos);
-    if (pos0 < 0 || pos0 >= a.max_seq) {
-        for (int d = threadIdx.x; d < a.dh; d += blockDim.x) a.out[(int64_t)h * a.dh + d] = 0.f;
-        return;
+    // ---- completion: the last chunk of this head group merges the partials
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    const int nch = (L + CS - 1) / CS;
+    if (tid == 0) {
+        int prev = __hip_atomic_fetch_add(a.counters + blockIdx.y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == nch - 1);
     }
-    const int nch = min((pos0 + 1 + kChunk - 1) / kChunk, a.nchunk_max);
-    float M = -INFINITY;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, a.ws_m[(int64_t)c * a.H + h]);
-    float Lsum = 0.f;
-    for (int c = 0; c < nch; c++) Lsum += a.ws_l[(int64_t)c * a.H + h] * expf(a.ws_m[(int64_t)c * a.H + h] - M);
-    for (int d = threadIdx.x; d < a.dh; d += blockDim.x) {
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // per-head max and sum over chunks: QH heads x (256/QH) chunk lanes
+    constexpr int CL = 256 / QH;
+    float* wts = o_red;                                   // [nch][QH] softmax weights
+    {
+        const int hq = tid / CL, cl = tid % CL;
+        const int h = hg0 * REP + hq;
+        float mx = -INFINITY;
+        for (int cc = cl; cc < nch; cc += CL) mx = fmaxf(mx, gld(a.ws_m + (int64_t)cc * a.H + h));
+        o_red[GS * QH * DH - 256 + tid] = mx;
+        __syncthreads();
+        if (cl == 0) {
+            float m = -INFINITY;
+            for (int k = 0; k < CL; k++) m = fmaxf(m, o_red[GS * QH * DH - 256 + hq * CL + k]);
+            s_hm[hq] = m;
+        }
+        __syncthreads();
+        const float M = s_hm[hq];
+        float ls = 0.f;
+        for (int cc = cl; cc < nch; cc += CL) {
+            float w = expf(gld(a.ws_m + (int64_t)cc * a.H + h) - M);
+            wts[cc * QH + hq] = w;
+            ls = fmaf(gld(a.ws_l + (int64_t)cc * a.H + h), w, ls);
+        }
+        o_red[GS * QH * DH - 256 + tid] = ls;
+        __syncthreads();
+        if (cl == 0) {
+            float t = 0.f;
+            for (int k = 0; k < CL; k++) t += o_red[GS * QH * DH - 256 + hq * CL + k];
+            s_hl[hq] = 1.0f / t;
+        }
+        __syncthreads();
+    }
+    const int64_t cstride = (int64_t)a.H * DH;
+    for (int e = tid; e < QH * DH; e += 256) {
+        const int hq = e / DH, d = e % DH;
+        const int h = hg0 * REP + hq;
+        const float* op = a.ws_o + (int64_t)h * DH + d;
         float acc = 0.f;
-        for (int c = 0; c < nch; c++)
-            acc = fmaf(a.ws_o[((int64_t)c * a.H + h) * a.dh + d], expf(a.ws_m[(int64_t)c * a.H + h] - M), acc);
-        a.out[(int64_t)h * a.dh + d] = acc / Lsum;
+        int cc = 0;
+        for (; cc + 8 <= nch; cc += 8) {       // 8 independent loads in flight
+            float o[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) o[k] = gld(op + (cc + k) * cstride);
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc = fmaf(o[k], wts[(cc + k) * QH + hq], acc);
+        }
+        for (; cc < nch; cc++) acc = fmaf(gld(op + cc * cstride), wts[cc * QH + hq], acc);
+        gst(a.out + (int64_t)h * DH + d, acc * s_hl[hq]);
     }
+    if (tid == 0) __hip_atomic_store(a.counters + blockIdx.y, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -277,7 +367,18 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs a, int kf, in
 }
 
 template <int KF, int VF, int HG>
-int launch_decode_rep(const AttnArgs& a, int rep, hipStream_t st) {
+int launch_decode_rep(AttnArgs a, int rep, hipStream_t st) {
+    // sub-step of this head-group size: 16 positions, 32 for single heads
+    const int gran = HG >= 2 ? 16 : 32;
+    a.chunk = chunk_len(a.max_seq, gran);
+    const int max_pos = a.d_pos ? a.max_seq : a.start_pos + 1;
+    a.nchunk_max = (max_pos + a.chunk - 1) / a.chunk;
+    const size_t need = kCounterBytes + (size_t)a.nchunk_max * a.H * (2 + (size_t)a.dh) * sizeof(float);
+    if (!a.ws || a.ws_bytes < need) return RINA_ERR_WORKSPACE;
+    a.counters = (int*)a.ws;
+    a.ws_m = (float*)((char*)a.ws + kCounterBytes);
+    a.ws_l = a.ws_m + (size_t)a.nchunk_max * a.H;
+    a.ws_o = a.ws_l + (size_t)a.nchunk_max * a.H;
     dim3 grid(a.nchunk_max, a.Hkv / HG);
     switch (rep) {
         case 1: hipLaunchKernelGGL((attn_decode_kernel<KF, VF, HG, 1>), grid, dim3(256), 0, st, a); break;
@@ -286,8 +387,6 @@ int launch_decode_rep(const AttnArgs& a, int rep, hipStream_t st) {
         case 8: hipLaunchKernelGGL((attn_decode_kernel<KF, VF, HG, 8>), grid, dim3(256), 0, st, a); break;
         default: return RINA_ERR_SHAPE;
     }
-    if (hipGetLastError() != hipSuccess) return RINA_ERR_HIP;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.H), dim3(64), 0, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 
@@ -302,12 +401,14 @@ int launch_decode(const AttnArgs& a, int rep, hipStream_t st) {
     return launch_decode_rep<KF, VF, 1>(a, rep, st);
 }
 
+
 }  // namespace
 
 extern "C" size_t rina_hip_gqa_attention_workspace(int T, int H, int dh, int max_pos) {
     (void)T;
-    size_t nch = (size_t)(max_pos + kChunk - 1) / kChunk + 1;
-    return nch * H * (2 + (size_t)dh) * sizeof(float);
+    // granularity 16 gives the most chunks, an upper bound for every kernel shape
+    size_t nch = (size_t)(max_pos + chunk_len(max_pos, 16) - 1) / chunk_len(max_pos, 16);
+    return kCounterBytes + nch * H * (2 + (size_t)dh) * sizeof(float);
 }
 
 extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const float* vcur, const void* cache_k,
@@ -336,13 +437,8 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
                 ((uintptr_t)q % 16 == 0) && ((uintptr_t)kcur % 16 == 0) && ((uintptr_t)vcur % 16 == 0) &&
                 (mode != RINA_KV_FP32 || (((uintptr_t)cache_k | (uintptr_t)cache_v) % 16 == 0));
     if (fast) {
-        int max_pos = d_pos ? max_seq : start_pos + 1;
-        a.nchunk_max = (max_pos + kChunk - 1) / kChunk;
-        size_t need = (size_t)a.nchunk_max * H * (2 + (size_t)dh) * sizeof(float);
-        if (!workspace || ws_bytes < need) return RINA_ERR_WORKSPACE;
-        a.ws_m = (float*)workspace;
-        a.ws_l = a.ws_m + (size_t)a.nchunk_max * H;
-        a.ws_o = a.ws_l + (size_t)a.nchunk_max * H;
+        a.ws = workspace;
+        a.ws_bytes = ws_bytes;
         switch (mode) {
             case RINA_KV_FP32: return launch_decode<0, 0>(a, rep, st);
             case RINA_KV_Q8: return launch_decode<RINA_KVF_Q8_0, RINA_KVF_Q8_0>(a, rep, st);

@@ -46,6 +46,8 @@ struct GemvArgs {
     int epi;
     int rowbytes;     // Q4 formats: bytes per row
     int slot;         // LDS bytes per matrix slot (16-byte multiple)
+    const float* nw;  // prologue norm weight
+    float eps;
 };
 
 __device__ __forceinline__ void tile_of(const GemvArgs& a, int t, int& s, int& n0, int& rows) {
@@ -70,15 +72,14 @@ __device__ __forceinline__ void tile_bytes(const GemvArgs& a, int n0, int rows, 
     }
 }
 
+// Thread tid loads chunks tid + k*kWG (k < kMaxChunks/NMAT) of each matrix's
+// 16-byte-aligned byte window; the chunk -> matrix mapping is static.
 template <int FMT, int NMAT>
-__device__ __forceinline__ void tile_load(const GemvArgs& a, int t, u32x4 (&pre)[kMaxChunks]) {
+__device__ __forceinline__ void tile_windows(const GemvArgs& a, int t, const uint8_t* (&base)[2], int (&nch)[2]) {
     int s, n0, rows;
     tile_of(a, t, s, n0, rows);
     int64_t start, len;
     tile_bytes<FMT>(a, n0, rows, start, len);
-    const int tid = threadIdx.x;
-    int nch[2];
-    const uint8_t* base[2];
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {
         const uint8_t* g = (m == 0 ? a.seg[s].w : a.seg[s].w2) + start;
@@ -86,34 +87,32 @@ __device__ __forceinline__ void tile_load(const GemvArgs& a, int t, u32x4 (&pre)
         base[m] = g - lead;
         nch[m] = (int)((lead + len + 15) >> 4);
     }
+}
+
+template <int FMT, int NMAT>
+__device__ __forceinline__ void tile_load(const GemvArgs& a, int t, u32x4 (&pre)[kMaxChunks]) {
+    constexpr int CPM = kMaxChunks / NMAT;
+    const uint8_t* base[2];
+    int nch[2];
+    tile_windows<FMT, NMAT>(a, t, base, nch);
+    const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < kMaxChunks; i++) {
-        int c = tid + i * kWG;
-        int m = 0;
-        if (NMAT == 2 && c >= nch[0]) { c -= nch[0]; m = 1; }
-        if (c < nch[m]) pre[i] = __builtin_nontemporal_load((const u32x4*)(base[m]) + c);
+        const int m = i / CPM, c = tid + (i % CPM) * kWG;
+        if (c < nch[m]) pre[i] = gld_nt((const u32x4*)(base[m]) + c);
     }
 }
 
 template <int FMT, int NMAT>
 __device__ __forceinline__ void tile_store(const GemvArgs& a, int t, const u32x4 (&pre)[kMaxChunks], uint8_t* buf) {
-    int s, n0, rows;
-    tile_of(a, t, s, n0, rows);
-    int64_t start, len;
-    tile_bytes<FMT>(a, n0, rows, start, len);
-    const int tid = threadIdx.x;
+    constexpr int CPM = kMaxChunks / NMAT;
+    const uint8_t* base[2];
     int nch[2];
-#pragma unroll
-    for (int m = 0; m < NMAT; m++) {
-        const uint8_t* g = (m == 0 ? a.seg[s].w : a.seg[s].w2) + start;
-        int lead = (int)((uintptr_t)g & 15);
-        nch[m] = (int)((lead + len + 15) >> 4);
-    }
+    tile_windows<FMT, NMAT>(a, t, base, nch);
+    const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < kMaxChunks; i++) {
-        int c = tid + i * kWG;
-        int m = 0;
-        if (NMAT == 2 && c >= nch[0]) { c -= nch[0]; m = 1; }
+        const int m = i / CPM, c = tid + (i % CPM) * kWG;
         if (c < nch[m]) *(u32x4*)(buf + m * a.slot + c * 16) = pre[i];
     }
 }
@@ -125,36 +124,92 @@ __device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t sh
     return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
 }
 
-// sum_i q_i x_i over one 32-value block whose 16 nibble bytes are nib[0..3]
-__device__ __forceinline__ float q4_dot(const uint32_t (&nib)[4], const float* x) {
-    float a0 = 0.f, a1 = 0.f;
+// Activation columns owned by one lane, as block floating point: the column's
+// values x_i = X_i * 2^(e-22) with integers |X_i| < 2^22 (e: exponent of the
+// column's max |x|), and X_i split into three signed 8-bit digit planes
+// X = d0 + 256 d1 + 65536 d2.  A weight block then needs only integer dot
+// products (v_dot4c_i32_i8, 4 MACs per instruction, exact) and one fp32
+// scale per block: the error is that of rounding x to 22 significant bits of
+// its column maximum, below the fp32 accumulation error of the reference loop.
+// Plane dword t of a Q4 column holds the digits of values 8(t/2)+2b+(t%2),
+// b = 0..3: the order of the nibble bytes after the low/high split.
+template <int FMT, int CPL>
+struct XCols {
+    static constexpr int UNIT = (FMT == FMT_Q2_K) ? 16 : 32;
+    static constexpr int ND = UNIT / 4;   // dwords per digit plane
+    int32_t dg[CPL][3][ND];
+    float tt[CPL][3];   // 7 * (sum of plane digits): the -7 nibble offset
+    float xe[CPL];      // 2^(e-22)
+    float xs[CPL];      // fp32 sum of the column (Q2_K min term)
+};
+
+template <int FMT, int CPL>
+__device__ __forceinline__ void digitize(XCols<FMT, CPL>& xc, int j, const float (&x)[XCols<FMT, CPL>::UNIT]) {
+    constexpr int UNIT = XCols<FMT, CPL>::UNIT;
+    float mx = 0.f, sum = 0.f;
 #pragma unroll
-    for (int d = 0; d < 4; d++) {
-        uint32_t lo = nib[d] & 0x0F0F0F0Fu, hi = (nib[d] >> 4) & 0x0F0F0F0Fu;
-        a0 = fmaf((float)(lo & 0xFF), x[8 * d + 0], a0);
-        a1 = fmaf((float)(hi & 0xFF), x[8 * d + 1], a1);
-        a0 = fmaf((float)((lo >> 8) & 0xFF), x[8 * d + 2], a0);
-        a1 = fmaf((float)((hi >> 8) & 0xFF), x[8 * d + 3], a1);
-        a0 = fmaf((float)((lo >> 16) & 0xFF), x[8 * d + 4], a0);
-        a1 = fmaf((float)((hi >> 16) & 0xFF), x[8 * d + 5], a1);
-        a0 = fmaf((float)(lo >> 24), x[8 * d + 6], a0);
-        a1 = fmaf((float)(hi >> 24), x[8 * d + 7], a1);
+    for (int i = 0; i < UNIT; i++) { mx = fmaxf(mx, fabsf(x[i])); sum += x[i]; }
+    int e = 0;
+    if (mx > 0.f) (void)frexpf(mx, &e);            // mx < 2^e
+    const float up = ldexpf(1.0f, 22 - e);
+    xc.xe[j] = ldexpf(1.0f, e - 22);
+    xc.xs[j] = sum;
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int t = 0; t < XCols<FMT, CPL>::ND; t++) {
+        uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int k = (FMT == FMT_Q2_K) ? 4 * t + b : 8 * (t >> 1) + 2 * b + (t & 1);
+            int X = (int)rintf(x[k] * up);
+            int d0 = ((X + 128) & 255) - 128;
+            int X1 = (X - d0) >> 8;
+            int d1 = ((X1 + 128) & 255) - 128;
+            int d2 = (X1 - d1) >> 8;
+            s0 += d0; s1 += d1; s2 += d2;
+            p0 |= (uint32_t)(d0 & 255) << (8 * b);
+            p1 |= (uint32_t)(d1 & 255) << (8 * b);
+            p2 |= (uint32_t)(d2 & 255) << (8 * b);
+        }
+        xc.dg[j][0][t] = (int32_t)p0;
+        xc.dg[j][1][t] = (int32_t)p1;
+        xc.dg[j][2][t] = (int32_t)p2;
     }
-    return a0 + a1;
+    xc.tt[j][0] = 7.0f * (float)s0;
+    xc.tt[j][1] = 7.0f * (float)s1;
+    xc.tt[j][2] = 7.0f * (float)s2;
 }
 
-// sum_i q_i x_i over a 16-value Q2_K unit: qs bytes q[0..3], shift 2g
-__device__ __forceinline__ float q2_dot(const uint32_t (&q)[4], uint32_t sh, const float* x) {
-    float a0 = 0.f, a1 = 0.f;
+// exact integer sum_i (q_i - 7) X_i of one Q4 block (nib: its 16 nibble bytes), as float
+template <int FMT, int CPL>
+__device__ __forceinline__ float q4_dot(const uint32_t (&nib)[4], const XCols<FMT, CPL>& xc, int j) {
+    int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
     for (int d = 0; d < 4; d++) {
-        uint32_t t = (q[d] >> sh) & 0x03030303u;
-        a0 = fmaf((float)(t & 0xFF), x[4 * d + 0], a0);
-        a1 = fmaf((float)((t >> 8) & 0xFF), x[4 * d + 1], a1);
-        a0 = fmaf((float)((t >> 16) & 0xFF), x[4 * d + 2], a0);
-        a1 = fmaf((float)(t >> 24), x[4 * d + 3], a1);
+        const int lo = (int)and_opaque(nib[d], 0x0F0F0F0Fu), hi = (int)and_opaque(nib[d] >> 4, 0x0F0F0F0Fu);
+        a0 = __builtin_amdgcn_sdot4(lo, xc.dg[j][0][2 * d], a0, false);
+        a1 = __builtin_amdgcn_sdot4(lo, xc.dg[j][1][2 * d], a1, false);
+        a2 = __builtin_amdgcn_sdot4(lo, xc.dg[j][2][2 * d], a2, false);
+        a0 = __builtin_amdgcn_sdot4(hi, xc.dg[j][0][2 * d + 1], a0, false);
+        a1 = __builtin_amdgcn_sdot4(hi, xc.dg[j][1][2 * d + 1], a1, false);
+        a2 = __builtin_amdgcn_sdot4(hi, xc.dg[j][2][2 * d + 1], a2, false);
     }
-    return a0 + a1;
+    const float f0 = (float)a0 - xc.tt[j][0], f1 = (float)a1 - xc.tt[j][1], f2 = (float)a2 - xc.tt[j][2];
+    return fmaf(65536.0f, f2, fmaf(256.0f, f1, f0));
+}
+
+// exact integer sum_i q_i X_i of one 16-value Q2_K unit (qs bytes q[0..3], shift 2g), as float
+template <int CPL>
+__device__ __forceinline__ float q2_dot(const uint32_t (&q)[4], uint32_t sh, const XCols<FMT_Q2_K, CPL>& xc, int j) {
+    int a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const int t = (int)and_opaque(q[d] >> sh, 0x03030303u);
+        a0 = __builtin_amdgcn_sdot4(t, xc.dg[j][0][d], a0, false);
+        a1 = __builtin_amdgcn_sdot4(t, xc.dg[j][1][d], a1, false);
+        a2 = __builtin_amdgcn_sdot4(t, xc.dg[j][2][d], a2, false);
+    }
+    return fmaf(65536.0f, (float)a2, fmaf(256.0f, (float)a1, (float)a0));
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
@@ -162,140 +217,430 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f 
 template <int NMAT>
 __device__ __forceinline__ void epilogue(const GemvArgs& a, int s, int n, const float (&v)[2]) {
     float* y = a.seg[s].y + n;
-    if (NMAT == 2) *y = silu_mul(v[0], v[1]);
-    else if (a.epi == RINA_EPI_ADD) *y = *y + v[0];
-    else *y = v[0];
+    if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
+    else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
+    else gst(y, v[0]);
 }
 
-// UNIT: values per lane work unit (32 for Q4 blocks, 16 for Q2_K units)
+// One tile of R rows from LDS: lane owns units (cp*CPL+j)*64+lane of each row.
 template <int FMT, int WPR, int CPL, int NMAT>
-__global__ __launch_bounds__(kWG) void gemv_quant_kernel(GemvArgs a) {
+__device__ __forceinline__ void compute_tile(const GemvArgs& a, int t, const uint8_t* buf, const uint8_t* smem,
+                                             const XCols<FMT, CPL>& xc, float* red) {
     constexpr int UNIT = (FMT == FMT_Q2_K) ? 16 : 32;
     constexpr int RPI = 4 / WPR;
-    extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rs = wave / WPR, cp = wave % WPR;
     const int K = a.K;
     const int nunits = K / UNIT;
+    int s, n0, rows;
+    tile_of(a, t, s, n0, rows);
+    int64_t start, len;
+    tile_bytes<FMT>(a, n0, rows, start, len);
+    int lead[2];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) lead[m] = (int)((uintptr_t)((m == 0 ? a.seg[s].w : a.seg[s].w2) + start) & 15);
 
-    // activation columns owned by this lane
-    float xr[CPL][UNIT];
-    float xs[CPL];
+    for (int r = rs; r < rows; r += RPI) {
+        float v[2] = {0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            const uint8_t* sl = buf + m * a.slot + lead[m];
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; j++) {
+                int u = (cp * CPL + j) * 64 + lane;
+                if (u >= nunits) continue;
+                if constexpr (FMT == FMT_Q4_0F) {
+                    const uint8_t* bp = sl + r * a.rowbytes + u * 20;
+                    float sc = __uint_as_float(lds_u32(bp));
+                    uint32_t nib[4];
+#pragma unroll
+                    for (int d = 0; d < 4; d++) nib[d] = lds_u32(bp + 4 + 4 * d);
+                    part = fmaf(sc * xc.xe[j], q4_dot(nib, xc, j), part);
+                } else if constexpr (FMT == FMT_Q4_0) {
+                    int off = (int)((uintptr_t)(sl + r * a.rowbytes + u * 18) - (uintptr_t)smem);
+                    float sc = f16_to_f32(lds_u16(smem + off));
+                    int an = (off + 2) & ~3;
+                    uint32_t sh = (uint32_t)((off + 2) & 3) * 8;
+                    uint32_t dw[5];
+#pragma unroll
+                    for (int d = 0; d < 5; d++) dw[d] = lds_u32(smem + an + 4 * d);
+                    uint32_t nib[4];
+#pragma unroll
+                    for (int d = 0; d < 4; d++) nib[d] = funnel(dw[d], dw[d + 1], sh);
+                    part = fmaf(sc * xc.xe[j], q4_dot(nib, xc, j), part);
+                } else {
+                    // Q2_K unit u of row n0+r: flat element e = (n0+r)K + 16u
+                    int64_t e = (int64_t)(n0 + r) * K + (int64_t)u * 16;
+                    int lb = (int)((e >> 8) - (((int64_t)n0 * K) >> 8));
+                    int inb = (int)(e & 255);
+                    int page = inb >> 7, g = (inb >> 5) & 3, h2 = (inb >> 4) & 1;
+                    const uint8_t* bp = sl + lb * 84;
+                    uint32_t dd = lds_u32(bp + 80);
+                    float dall = f16_to_f32(dd & 0xFFFF), dmin = f16_to_f32(dd >> 16);
+                    uint32_t scb = bp[8 * page + 2 * g + h2];
+                    uint32_t q[4];
+#pragma unroll
+                    for (int d = 0; d < 4; d++) q[d] = lds_u32(bp + 16 + 32 * page + 16 * h2 + 4 * d);
+                    float dl = dall * (float)(scb & 0xF), ml = dmin * (float)(scb >> 4);
+                    part = fmaf(dl * xc.xe[j], q2_dot(q, 2u * g, xc, j), fmaf(-ml, xc.xs[j], part));
+                }
+            }
+            v[m] = wave_sum(part);
+        }
+        if (WPR == 1) {
+            if (lane == 0) epilogue<NMAT>(a, s, n0 + r, v);
+        } else if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) red[(m * a.R + r) * WPR + cp] = v[m];
+        }
+    }
+    if (WPR > 1) {
+        __syncthreads();
+        if (tid < rows) {
+            float v[2] = {0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                float acc = 0.f;
+#pragma unroll
+                for (int c = 0; c < WPR; c++) acc += red[(m * a.R + tid) * WPR + c];
+                v[m] = acc;
+            }
+            epilogue<NMAT>(a, s, n0 + tid, v);
+        }
+    }
+}
+
+// Lane-owned activation columns (and prologue norm weights), raw.
+template <int FMT, int WPR, int CPL, int PRO>
+struct XRaw {
+    static constexpr int UNIT = (FMT == FMT_Q2_K) ? 16 : 32;
+    float x[CPL][UNIT];
+    float w[PRO != RINA_PRO_NONE ? CPL : 1][PRO != RINA_PRO_NONE ? UNIT : 1];
+};
+
+template <int FMT, int WPR, int CPL, int PRO>
+__device__ __forceinline__ void load_x_raw(const GemvArgs& a, XRaw<FMT, WPR, CPL, PRO>& r) {
+    constexpr int UNIT = XRaw<FMT, WPR, CPL, PRO>::UNIT;
+    const int lane = threadIdx.x & 63, cp = (threadIdx.x >> 6) % WPR;
+    const int nunits = a.K / UNIT;
 #pragma unroll
     for (int j = 0; j < CPL; j++) {
         int u = (cp * CPL + j) * 64 + lane;
-        xs[j] = 0.f;
         if (u < nunits) {
             const f32x4* xp = (const f32x4*)(a.x + (int64_t)u * UNIT);
 #pragma unroll
             for (int i = 0; i < UNIT / 4; i++) {
-                f32x4 v = xp[i];
-                xr[j][4 * i + 0] = v.x; xr[j][4 * i + 1] = v.y;
-                xr[j][4 * i + 2] = v.z; xr[j][4 * i + 3] = v.w;
+                f32x4 v = gld(xp + i);
+                r.x[j][4 * i + 0] = v.x; r.x[j][4 * i + 1] = v.y;
+                r.x[j][4 * i + 2] = v.z; r.x[j][4 * i + 3] = v.w;
             }
+            if constexpr (PRO != RINA_PRO_NONE) {
+                const f32x4* wp = (const f32x4*)(a.nw + (int64_t)u * UNIT);
 #pragma unroll
-            for (int i = 0; i < UNIT; i++) xs[j] += xr[j][i];
+                for (int i = 0; i < UNIT / 4; i++) {
+                    f32x4 v = gld(wp + i);
+                    r.w[j][4 * i + 0] = v.x; r.w[j][4 * i + 1] = v.y;
+                    r.w[j][4 * i + 2] = v.z; r.w[j][4 * i + 3] = v.w;
+                }
+            }
         } else {
 #pragma unroll
-            for (int i = 0; i < UNIT; i++) xr[j][i] = 0.f;
+            for (int i = 0; i < UNIT; i++) r.x[j][i] = 0.f;
+            if constexpr (PRO != RINA_PRO_NONE) {
+#pragma unroll
+                for (int i = 0; i < UNIT; i++) r.w[j][i] = 0.f;
+            }
         }
     }
+}
 
+// Normalize (PRO: 0 none, 1 RMSNorm, 2 LayerNorm; needs WPR == 1 so every
+// wave holds the whole row) and digitize the lane's columns.
+template <int FMT, int WPR, int CPL, int PRO>
+__device__ __forceinline__ void prep_x(const GemvArgs& a, XRaw<FMT, WPR, CPL, PRO>& r, XCols<FMT, CPL>& xc) {
+    constexpr int UNIT = XRaw<FMT, WPR, CPL, PRO>::UNIT;
+    if constexpr (PRO != RINA_PRO_NONE) {
+        const int lane = threadIdx.x & 63, cp = (threadIdx.x >> 6) % WPR;
+        const int nunits = a.K / UNIT;
+        const float d = (float)a.K;
+        float mean = 0.f;
+        if (PRO == RINA_PRO_LAYERNORM) {
+            float sm = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; j++)
+#pragma unroll
+                for (int i = 0; i < UNIT; i++) sm += r.x[j][i];
+            mean = wave_sum(sm) / d;
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            int u = (cp * CPL + j) * 64 + lane;
+            if (u >= nunits) continue;
+#pragma unroll
+            for (int i = 0; i < UNIT; i++) {
+                float t = r.x[j][i] - mean;
+                ss = fmaf(t, t, ss);
+            }
+        }
+        const float inv = 1.0f / sqrtf(wave_sum(ss) / d + a.eps);
+#pragma unroll
+        for (int j = 0; j < CPL; j++)
+#pragma unroll
+            for (int i = 0; i < UNIT; i++) r.x[j][i] = (r.x[j][i] - mean) * inv * r.w[j][i];
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; j++) digitize<FMT, CPL>(xc, j, r.x[j]);
+}
+
+template <int FMT, int WPR, int CPL, int PRO>
+__device__ __forceinline__ void load_x(const GemvArgs& a, XCols<FMT, CPL>& xc) {
+    XRaw<FMT, WPR, CPL, PRO> r;
+    load_x_raw<FMT, WPR, CPL, PRO>(a, r);
+    prep_x<FMT, WPR, CPL, PRO>(a, r, xc);
+}
+
+// Tiles are dealt round-robin to the workgroups; two tiles ahead are kept in
+// flight in registers (sets A and B) while the LDS copy of the current one is
+// consumed, and the first loads go out before the activation vector is read.
+template <int FMT, int WPR, int CPL, int NMAT, int PRO>
+__global__ __launch_bounds__(kWG) void gemv_quant_kernel(GemvArgs a) {
+    constexpr int UNIT = (FMT == FMT_Q2_K) ? 16 : 32;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int T = a.total_tiles, G = gridDim.x;
     const int bufbytes = NMAT * a.slot;
+    uint8_t* buf0 = smem;
+    uint8_t* buf1 = smem + bufbytes;
     float* red = (float*)(smem + 2 * bufbytes);   // [NMAT][R][WPR]
 
-    u32x4 pre[kMaxChunks];
+    u32x4 pA[kMaxChunks], pB[kMaxChunks];
     int t = blockIdx.x;
-    if (t < a.total_tiles) tile_load<FMT, NMAT>(a, t, pre);
-    int b = 0;
-    for (; t < a.total_tiles; t += gridDim.x, b ^= 1) {
-        uint8_t* buf = smem + b * bufbytes;
-        tile_store<FMT, NMAT>(a, t, pre, buf);
-        __syncthreads();
-        int tn = t + gridDim.x;
-        if (tn < a.total_tiles) tile_load<FMT, NMAT>(a, tn, pre);
+    if (t < T) tile_load<FMT, NMAT>(a, t, pA);
+    if (t + G < T) tile_load<FMT, NMAT>(a, t + G, pB);
 
-        int s, n0, rows;
-        tile_of(a, t, s, n0, rows);
-        int64_t start, len;
-        tile_bytes<FMT>(a, n0, rows, start, len);
-        int lead[2];
+    XCols<FMT, CPL> xc;
+    load_x<FMT, WPR, CPL, PRO>(a, xc);
+
+    for (; t < T; t += 2 * G) {
+        tile_store<FMT, NMAT>(a, t, pA, buf0);
+        __syncthreads();
+        if (t + 2 * G < T) tile_load<FMT, NMAT>(a, t + 2 * G, pA);
+        compute_tile<FMT, WPR, CPL, NMAT>(a, t, buf0, smem, xc, red);
+        if (t + G >= T) break;
+        tile_store<FMT, NMAT>(a, t + G, pB, buf1);
+        __syncthreads();
+        if (t + 3 * G < T) tile_load<FMT, NMAT>(a, t + 3 * G, pB);
+        compute_tile<FMT, WPR, CPL, NMAT>(a, t + G, buf1, smem, xc, red);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Direct-load Q4 matvec (M = 1).  Lane l owns block column cp*64+l of every
+// row; a wave takes RB rows at a time and loads each of its blocks straight
+// from HBM (one 16-byte + one 4-byte load per block at 4-byte alignment, the
+// 18/20-byte block layout needs no staging), so every lane keeps RB*NMAT
+// blocks in flight and the RB*NMAT row sums reduce as independent DPP
+// chains.  No LDS and no barrier unless a row spans several waves (WPR > 1,
+// one LDS exchange per row group).
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// 16-byte streaming load from a 4-byte aligned global address
+__device__ __forceinline__ u32x4_a4 gld_nt_a4(const uint8_t* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_a4*)p);
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_q4_block(const uint8_t* p, float& sc, uint32_t (&nib)[4]) {
+    if constexpr (FMT == FMT_Q4_0F) {
+        const u32x4_a4 v = gld_nt_a4(p);
+        const uint32_t t = gld_nt((const uint32_t*)(p + 16));
+        sc = __uint_as_float(v.x);
+        nib[0] = v.y; nib[1] = v.z; nib[2] = v.w; nib[3] = t;
+    } else {
+        // 18-byte block: 20-byte window from the dword at or below its start
+        const uintptr_t al = (uintptr_t)p & ~(uintptr_t)3;
+        const uint32_t sh = (uint32_t)((uintptr_t)p & 3) * 8;        // 0 or 16
+        const u32x4_a4 v = gld_nt_a4((const uint8_t*)al);
+        const uint32_t t = gld_nt((const uint32_t*)(al + 16));
+        const uint32_t d[5] = {v.x, v.y, v.z, v.w, t};
+        sc = f16_to_f32(sh ? (d[0] >> 16) : (d[0] & 0xFFFF));
+#pragma unroll
+        for (int k = 0; k < 4; k++) nib[k] = (uint32_t)((((uint64_t)d[k + 1] << 32) | d[k]) >> (16 + sh));
+    }
+}
+
+// Blocks of one row group held in registers: RB rows x NMAT matrices.
+template <int RB>
+struct DirectBlk {
+    float sc[RB][2];
+    uint32_t nib[RB][2][4];
+    int seg[RB], row[RB];
+    bool ok[RB];
+};
+
+__device__ __forceinline__ uint64_t uni64(const void* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Segment table as wave-uniform values read once at kernel entry.  A field
+// of segment sg is picked with integer arithmetic on these values: indexing
+// the argument struct (or any array) with a run-time segment number makes
+// the compiler copy it to scratch memory.
+struct DirectSegs {
+    uint64_t w0, w1, w2, v0, v1, v2, y0, y1, y2;
+    int t1, t2, nseg;
+    __device__ __forceinline__ explicit DirectSegs(const GemvArgs& a) {
+        w0 = uni64(a.seg[0].w); w1 = uni64(a.seg[1].w); w2 = uni64(a.seg[2].w);
+        v0 = uni64(a.seg[0].w2); v1 = uni64(a.seg[1].w2); v2 = uni64(a.seg[2].w2);
+        y0 = uni64(a.seg[0].y); y1 = uni64(a.seg[1].y); y2 = uni64(a.seg[2].y);
+        t1 = __builtin_amdgcn_readfirstlane(a.seg[1].tile0);
+        t2 = __builtin_amdgcn_readfirstlane(a.seg[2].tile0);
+        nseg = __builtin_amdgcn_readfirstlane(a.nseg);
+    }
+    __device__ __forceinline__ int seg_of(int vr) const {
+        return (nseg > 2 && vr >= t2) ? 2 : (nseg > 1 && vr >= t1) ? 1 : 0;
+    }
+    __device__ __forceinline__ static uint64_t sel(int sg, uint64_t f0, uint64_t f1, uint64_t f2) {
+        const uint64_t m1 = (uint64_t)0 - (uint64_t)(sg == 1), m2 = (uint64_t)0 - (uint64_t)(sg == 2);
+        const uint64_t m0 = ~(m1 | m2);
+        return (f0 & m0) | (f1 & m1) | (f2 & m2);
+    }
+    __device__ __forceinline__ int t0(int sg) const { return (int)sel(sg, 0, (uint64_t)t1, (uint64_t)t2); }
+    __device__ __forceinline__ const uint8_t* wt(int sg, int m) const {
+        return (const uint8_t*)(m == 0 ? sel(sg, w0, w1, w2) : sel(sg, v0, v1, v2));
+    }
+    __device__ __forceinline__ float* out(int sg) const { return (float*)sel(sg, y0, y1, y2); }
+};
+
+// Issue the loads of row group grp (virtual rows grp*RB ..) for block column u.
+template <int FMT, int NMAT, int RB>
+__device__ __forceinline__ void direct_issue(const GemvArgs& a, const DirectSegs& S, int grp, int u, bool active,
+                                             DirectBlk<RB>& b) {
+    constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
+#pragma unroll
+    for (int i = 0; i < RB; i++) {
+        const int vr = grp * RB + i;
+        const int sg = S.seg_of(vr);
+        b.seg[i] = sg;
+        b.row[i] = (grp < a.total_tiles && vr < a.R) ? vr - S.t0(sg) : -1;
+        // Loads are unconditional (a branch around them costs the waitcnt
+        // pass its count and it then waits for every load): lanes past the
+        // row's end or rows past the matrix read block 0 of the segment and
+        // get scale 0.
+        const bool ok = active && b.row[i] >= 0;
+        const int64_t off = ok ? (int64_t)b.row[i] * a.rowbytes + (int64_t)u * BB : 0;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) load_q4_block<FMT>(S.wt(sg, m) + off, b.sc[i][m], b.nib[i][m]);
+        b.ok[i] = ok;   // applied where the scale is used, so nothing waits here
+    }
+}
+
+template <int NMAT>
+__device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const DirectSegs& S, int sg, int n,
+                                                const float (&v)[2]) {
+    float* y = S.out(sg) + n;
+    if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
+    else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
+    else gst(y, v[0]);
+}
+
+// Row sums of one row group and their epilogue.
+template <int FMT, int WPR, int NMAT, int RB>
+__device__ __forceinline__ void direct_consume(const GemvArgs& a, const DirectSegs& S, const XCols<FMT, 1>& xc,
+                                               const DirectBlk<RB>& cur, int it, int rs, int cp,
+                                               float (*red)[RB * NMAT][WPR]) {
+    constexpr int RPI = 4 / WPR;
+    const int tid = threadIdx.x, lane = tid & 63;
+    float part[RB][2];
+#pragma unroll
+    for (int i = 0; i < RB; i++)
 #pragma unroll
         for (int m = 0; m < NMAT; m++)
-            lead[m] = (int)((uintptr_t)((m == 0 ? a.seg[s].w : a.seg[s].w2) + start) & 15);
-
-        for (int r = rs; r < rows; r += RPI) {
-            float v[2] = {0.f, 0.f};
+            part[i][m] = wave_sum((cur.ok[i] ? cur.sc[i][m] : 0.f) * xc.xe[0] * q4_dot(cur.nib[i][m], xc, 0));
+    if (WPR == 1) {
+        if (lane == 0) {
 #pragma unroll
-            for (int m = 0; m < NMAT; m++) {
-                const uint8_t* sl = buf + m * a.slot + lead[m];
-                float part = 0.f;
-#pragma unroll
-                for (int j = 0; j < CPL; j++) {
-                    int u = (cp * CPL + j) * 64 + lane;
-                    if (u >= nunits) continue;
-                    if (FMT == FMT_Q4_0F) {
-                        const uint8_t* bp = sl + r * a.rowbytes + u * 20;
-                        float sc = __uint_as_float(lds_u32(bp));
-                        uint32_t nib[4];
-#pragma unroll
-                        for (int d = 0; d < 4; d++) nib[d] = lds_u32(bp + 4 + 4 * d);
-                        float qx = q4_dot(nib, xr[j]);
-                        part = fmaf(sc, fmaf(-7.0f, xs[j], qx), part);
-                    } else if (FMT == FMT_Q4_0) {
-                        int off = (int)((uintptr_t)(sl + r * a.rowbytes + u * 18) - (uintptr_t)smem);
-                        float sc = f16_to_f32(lds_u16(smem + off));
-                        int an = (off + 2) & ~3;
-                        uint32_t sh = (uint32_t)((off + 2) & 3) * 8;
-                        uint32_t dw[5];
-#pragma unroll
-                        for (int d = 0; d < 5; d++) dw[d] = lds_u32(smem + an + 4 * d);
-                        uint32_t nib[4];
-#pragma unroll
-                        for (int d = 0; d < 4; d++) nib[d] = funnel(dw[d], dw[d + 1], sh);
-                        float qx = q4_dot(nib, xr[j]);
-                        part = fmaf(sc, fmaf(-7.0f, xs[j], qx), part);
-                    } else {
-                        // Q2_K unit u of row n0+r: flat element e = (n0+r)K + 16u
-                        int64_t e = (int64_t)(n0 + r) * K + (int64_t)u * 16;
-                        int lb = (int)((e >> 8) - (((int64_t)n0 * K) >> 8));
-                        int inb = (int)(e & 255);
-                        int page = inb >> 7, g = (inb >> 5) & 3, h2 = (inb >> 4) & 1;
-                        const uint8_t* bp = sl + lb * 84;
-                        uint32_t dd = lds_u32(bp + 80);
-                        float dall = f16_to_f32(dd & 0xFFFF), dmin = f16_to_f32(dd >> 16);
-                        uint32_t scb = bp[8 * page + 2 * g + h2];
-                        uint32_t q[4];
-#pragma unroll
-                        for (int d = 0; d < 4; d++) q[d] = lds_u32(bp + 16 + 32 * page + 16 * h2 + 4 * d);
-                        float qx = q2_dot(q, 2u * g, xr[j]);
-                        float dl = dall * (float)(scb & 0xF), ml = dmin * (float)(scb >> 4);
-                        part = fmaf(dl, qx, fmaf(-ml, xs[j], part));
-                    }
+            for (int i = 0; i < RB; i++)
+                if (cur.row[i] >= 0) {
+                    float v[2] = {part[i][0], NMAT == 2 ? part[i][1] : 0.f};
+                    direct_epilogue<NMAT>(a, S, cur.seg[i], cur.row[i], v);
                 }
-                v[m] = wave_sum(part);
-            }
-            if (WPR == 1) {
-                if (lane == 0) epilogue<NMAT>(a, s, n0 + r, v);
-            } else if (lane == 0) {
-#pragma unroll
-                for (int m = 0; m < NMAT; m++) red[(m * a.R + r) * WPR + cp] = v[m];
-            }
         }
-        if (WPR > 1) {
-            __syncthreads();
-            if (tid < rows) {
+    } else {
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < RB; i++)
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) red[rs][i * NMAT + m][cp] = part[i][m];
+        }
+        __syncthreads();
+        if (tid < RPI * RB) {
+            const int r2 = tid / RB, i = tid % RB;
+            const int grp = it * RPI + r2, vr = grp * RB + i;
+            if (grp < a.total_tiles && vr < a.R) {
+                const int sg = S.seg_of(vr);
                 float v[2] = {0.f, 0.f};
 #pragma unroll
-                for (int m = 0; m < NMAT; m++) {
-                    float acc = 0.f;
+                for (int m = 0; m < NMAT; m++)
 #pragma unroll
-                    for (int c = 0; c < WPR; c++) acc += red[(m * a.R + tid) * WPR + c];
-                    v[m] = acc;
-                }
-                epilogue<NMAT>(a, s, n0 + tid, v);
+                    for (int c = 0; c < WPR; c++) v[m] += red[r2][i * NMAT + m][c];
+                direct_epilogue<NMAT>(a, S, sg, vr - S.t0(sg), v);
             }
         }
+        __syncthreads();
+    }
+}
+
+// GemvArgs reuse for this kernel: total_tiles = number of row groups,
+// R = number of virtual rows, seg[s].tile0 = first virtual row of segment s.
+// Workgroup iterations alternate between two register sets (A, B): the next
+// group's loads are issued before the current group is reduced, and each
+// path has its own straight-line code so the load counters stay exact.
+template <int FMT, int WPR, int NMAT, int PRO, int RB>
+__global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
+    constexpr int RPI = 4 / WPR;                 // row groups per workgroup iteration
+    __shared__ float red[RPI][RB * NMAT][WPR];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rs = wave / WPR, cp = wave % WPR;
+    const int u = cp * 64 + lane;                // this lane's block column
+    const bool active = u < a.K / 32;
+    const int G = gridDim.x;
+    const int ngrp = a.total_tiles;
+    const DirectSegs S(a);
+
+    // activation loads first (cache hits) so that digitizing them overlaps
+    // the weight loads: vmcnt retires loads in issue order
+    XRaw<FMT, WPR, 1, PRO> xr;
+    load_x_raw<FMT, WPR, 1, PRO>(a, xr);
+    int it = blockIdx.x;
+    DirectBlk<RB> A, B;
+    direct_issue<FMT, NMAT, RB>(a, S, it * RPI + rs, u, active, A);
+    XCols<FMT, 1> xc;
+    prep_x<FMT, WPR, 1, PRO>(a, xr, xc);
+
+    for (;;) {
+        if ((it + G) * RPI < ngrp) {
+            direct_issue<FMT, NMAT, RB>(a, S, (it + G) * RPI + rs, u, active, B);
+            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, A, it, rs, cp, red);
+        } else {
+            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, A, it, rs, cp, red);
+            break;
+        }
+        it += G;
+        if ((it + G) * RPI < ngrp) {
+            direct_issue<FMT, NMAT, RB>(a, S, (it + G) * RPI + rs, u, active, A);
+            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, B, it, rs, cp, red);
+        } else {
+            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, B, it, rs, cp, red);
+            break;
+        }
+        it += G;
     }
 }
 
@@ -310,6 +655,9 @@ struct F32Args {
     int K;
     int total_rows;
     int epi;
+    int pro;
+    const float* nw;
+    float eps;
 };
 
 // dot of one fp32 row with the LDS copy of x; 4 independent 16-byte loads
@@ -323,10 +671,10 @@ __device__ __forceinline__ float f32_row_dot(const float* w, const float* xl, in
         const int n4 = K >> 2;
         int k = lane;
         for (; k + 192 < n4; k += 256) {
-            f32x4 a0 = __builtin_nontemporal_load(w4 + k);
-            f32x4 a1 = __builtin_nontemporal_load(w4 + k + 64);
-            f32x4 a2 = __builtin_nontemporal_load(w4 + k + 128);
-            f32x4 a3 = __builtin_nontemporal_load(w4 + k + 192);
+            f32x4 a0 = gld_nt(w4 + k);
+            f32x4 a1 = gld_nt(w4 + k + 64);
+            f32x4 a2 = gld_nt(w4 + k + 128);
+            f32x4 a3 = gld_nt(w4 + k + 192);
             f32x4 b0 = x4[k], b1 = x4[k + 64], b2 = x4[k + 128], b3 = x4[k + 192];
             s0 = fmaf(b0.x, a0.x, s0); s0 = fmaf(b0.y, a0.y, s0); s0 = fmaf(b0.z, a0.z, s0); s0 = fmaf(b0.w, a0.w, s0);
             s1 = fmaf(b1.x, a1.x, s1); s1 = fmaf(b1.y, a1.y, s1); s1 = fmaf(b1.z, a1.z, s1); s1 = fmaf(b1.w, a1.w, s1);
@@ -334,12 +682,12 @@ __device__ __forceinline__ float f32_row_dot(const float* w, const float* xl, in
             s3 = fmaf(b3.x, a3.x, s3); s3 = fmaf(b3.y, a3.y, s3); s3 = fmaf(b3.z, a3.z, s3); s3 = fmaf(b3.w, a3.w, s3);
         }
         for (; k < n4; k += 64) {
-            f32x4 a0 = __builtin_nontemporal_load(w4 + k);
+            f32x4 a0 = gld_nt(w4 + k);
             f32x4 b0 = x4[k];
             s0 = fmaf(b0.x, a0.x, s0); s0 = fmaf(b0.y, a0.y, s0); s0 = fmaf(b0.z, a0.z, s0); s0 = fmaf(b0.w, a0.w, s0);
         }
     } else {
-        for (int k = lane; k < K; k += 64) s0 = fmaf(xl[k], w[k], s0);
+        for (int k = lane; k < K; k += 64) s0 = fmaf(xl[k], gld(w + k), s0);
     }
     return (s0 + s1) + (s2 + s3);
 }
@@ -347,9 +695,33 @@ __device__ __forceinline__ float f32_row_dot(const float* w, const float* xl, in
 template <int NMAT, bool VEC>
 __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     extern __shared__ __align__(16) float xs_lds[];
+    __shared__ float red[8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K;
-    for (int i = tid; i < K; i += kWG) xs_lds[i] = a.x[i];
+    for (int i = tid; i < K; i += kWG) xs_lds[i] = gld(a.x + i);
+    if (a.pro != RINA_PRO_NONE) {   // RMSNorm / LayerNorm of x, in LDS
+        __syncthreads();
+        float mean = 0.f;
+        if (a.pro == RINA_PRO_LAYERNORM) {
+            float sm = 0.f;
+            for (int i = tid; i < K; i += kWG) sm += xs_lds[i];
+            sm = wave_sum(sm);
+            if (lane == 0) red[wave] = sm;
+            __syncthreads();
+            mean = (red[0] + red[1] + red[2] + red[3]) / (float)K;
+            __syncthreads();
+        }
+        float ss = 0.f;
+        for (int i = tid; i < K; i += kWG) {
+            float t = xs_lds[i] - mean;
+            ss = fmaf(t, t, ss);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[4 + wave] = ss;
+        __syncthreads();
+        float inv = 1.0f / sqrtf((red[4] + red[5] + red[6] + red[7]) / (float)K + a.eps);
+        for (int i = tid; i < K; i += kWG) xs_lds[i] = (xs_lds[i] - mean) * inv * gld(a.nw + i);
+    }
     __syncthreads();
     const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
     for (int vr = gw; vr < a.total_rows; vr += nw) {
@@ -365,9 +737,9 @@ __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
         }
         if (lane == 0) {
             float* y = a.seg[s].y + row;
-            if (NMAT == 2) *y = silu_mul(v[0], v[1]);
-            else if (a.epi == RINA_EPI_ADD) *y = *y + v[0];
-            else *y = v[0];
+            if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
+            else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
+            else gst(y, v[0]);
         }
     }
 }
@@ -471,47 +843,112 @@ int fmt_of(int qt) {
     }
 }
 
-template <int FMT, int WPR, int CPL, int NMAT>
+template <int FMT, int WPR, int CPL, int NMAT, int PRO>
 int launch_quant(GemvArgs& a, hipStream_t st) {
     int cus = rina_num_cus();
     int grid = a.total_tiles < cus * 4 ? a.total_tiles : cus * 4;
     size_t lds = 2 * (size_t)NMAT * a.slot + (size_t)NMAT * a.R * WPR * 4;
-    hipLaunchKernelGGL((gemv_quant_kernel<FMT, WPR, CPL, NMAT>), dim3(grid), dim3(kWG), lds, st, a);
+    hipLaunchKernelGGL((gemv_quant_kernel<FMT, WPR, CPL, NMAT, PRO>), dim3(grid), dim3(kWG), lds, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 
 template <int FMT, int NMAT>
-int dispatch_wpr(GemvArgs& a, int wpr, int cpl, hipStream_t st) {
-    if (wpr == 1) return cpl == 1 ? launch_quant<FMT, 1, 1, NMAT>(a, st) : RINA_ERR_SHAPE;
-    if (wpr == 2) return cpl == 1 ? launch_quant<FMT, 2, 1, NMAT>(a, st) : RINA_ERR_SHAPE;
+int dispatch_wpr(GemvArgs& a, int wpr, int cpl, int pro, hipStream_t st) {
+    if (wpr == 1 && cpl == 1) {
+        if (pro == RINA_PRO_RMSNORM) return launch_quant<FMT, 1, 1, NMAT, RINA_PRO_RMSNORM>(a, st);
+        if (pro == RINA_PRO_LAYERNORM) return launch_quant<FMT, 1, 1, NMAT, RINA_PRO_LAYERNORM>(a, st);
+        return launch_quant<FMT, 1, 1, NMAT, 0>(a, st);
+    }
+    if (pro != RINA_PRO_NONE) return RINA_ERR_SHAPE;
+    if (wpr == 2) return cpl == 1 ? launch_quant<FMT, 2, 1, NMAT, 0>(a, st) : RINA_ERR_SHAPE;
     switch (cpl) {
-        case 1: return launch_quant<FMT, 4, 1, NMAT>(a, st);
-        case 2: return launch_quant<FMT, 4, 2, NMAT>(a, st);
-        case 3: return launch_quant<FMT, 4, 3, NMAT>(a, st);
-        case 4: return launch_quant<FMT, 4, 4, NMAT>(a, st);
+        case 1: return launch_quant<FMT, 4, 1, NMAT, 0>(a, st);
+        case 2: return launch_quant<FMT, 4, 2, NMAT, 0>(a, st);
+        case 3: return launch_quant<FMT, 4, 3, NMAT, 0>(a, st);
+        case 4: return launch_quant<FMT, 4, 4, NMAT, 0>(a, st);
         default: return RINA_ERR_SHAPE;
     }
 }
 
-int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, int K, int epi, hipStream_t st) {
+template <int FMT, int WPR, int NMAT, int PRO, int RB>
+int launch_direct(GemvArgs& a, hipStream_t st) {
+    constexpr int RPI = 4 / WPR;
+    int cus = rina_num_cus();
+    int wgs = (a.total_tiles + RPI - 1) / RPI;
+    int per_cu = RB == 4 ? 3 : 4;   // workgroups resident per CU at this register count
+    int grid = wgs < cus * per_cu ? wgs : cus * per_cu;
+    hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB>), dim3(grid), dim3(kWG), 0, st, a);
+    return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
+}
+
+template <int FMT, int WPR, int NMAT, int PRO>
+int direct_rb(GemvArgs& a, int rb, hipStream_t st) {
+    switch (rb) {
+        case 1: return launch_direct<FMT, WPR, NMAT, PRO, 1>(a, st);
+        case 2: return launch_direct<FMT, WPR, NMAT, PRO, 2>(a, st);
+        default: return launch_direct<FMT, WPR, NMAT, PRO, 4>(a, st);
+    }
+}
+
+template <int FMT, int NMAT>
+int dispatch_direct(GemvArgs& a, int wpr, int rb, int pro, hipStream_t st) {
+    if (wpr == 1) {
+        if (pro == RINA_PRO_RMSNORM) return direct_rb<FMT, 1, NMAT, RINA_PRO_RMSNORM>(a, rb, st);
+        if (pro == RINA_PRO_LAYERNORM) return direct_rb<FMT, 1, NMAT, RINA_PRO_LAYERNORM>(a, rb, st);
+        return direct_rb<FMT, 1, NMAT, 0>(a, rb, st);
+    }
+    if (pro != RINA_PRO_NONE) return RINA_ERR_SHAPE;
+    if (wpr == 2) return direct_rb<FMT, 2, NMAT, 0>(a, rb, st);
+    return direct_rb<FMT, 4, NMAT, 0>(a, rb, st);
+}
+
+// waves per row / units per lane for a row of `nunits` work units
+void split_row(int nunits, int& wpr, int& cpl) {
+    if (nunits <= 64) { wpr = 1; cpl = 1; }
+    else if (nunits <= 128) { wpr = 2; cpl = 1; }
+    else { wpr = 4; cpl = (nunits + 255) / 256; }
+}
+
+int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, int K, int epi, int pro,
+               const float* nw, float eps, hipStream_t st) {
     int fmt = fmt_of(qt);
     int nmat = (epi == RINA_EPI_SWIGLU) ? 2 : 1;
     int unit = fmt == FMT_Q2_K ? 16 : 32;
     if (K % unit) return RINA_ERR_SHAPE;
-    int nunits = K / unit;
     int wpr, cpl;
-    if (nunits <= 64) { wpr = 1; cpl = 1; }
-    else if (nunits <= 128) { wpr = 2; cpl = 1; }
-    else { wpr = 4; cpl = (nunits + 255) / 256; }
+    split_row(K / unit, wpr, cpl);
     if (cpl > 4) return RINA_ERR_SHAPE;
-    int rpi = 4 / wpr;
     GemvArgs a{};
     a.nseg = nseg;
     a.x = x;
     a.K = K;
     a.epi = epi;
+    a.nw = nw;
+    a.eps = eps;
     int64_t rowbytes = fmt == FMT_Q4_0 ? (int64_t)(K / 32) * 18 : fmt == FMT_Q4_0F ? (int64_t)(K / 32) * 20 : 0;
     a.rowbytes = (int)rowbytes;
+    if (fmt != FMT_Q2_K && cpl == 1) {
+        // direct-load kernel: virtual rows over all segments, RB rows per wave
+        int rows = 0;
+        for (int s = 0; s < nseg; s++) {
+            a.seg[s].w = (const uint8_t*)segs[s].weight;
+            a.seg[s].w2 = (const uint8_t*)segs[s].weight2;
+            a.seg[s].y = segs[s].out;
+            a.seg[s].N = segs[s].N;
+            a.seg[s].tile0 = rows;
+            rows += segs[s].N;
+        }
+        // enough row groups to give every wave of a full wave-slot load
+        // (4 workgroups of 4 waves per CU) one group, then more rows per wave
+        int64_t waves = (int64_t)rina_num_cus() * 16;
+        int64_t want = ((int64_t)rows * wpr + waves - 1) / waves;
+        int rb = want <= 1 ? 1 : want <= 2 ? 2 : 4;
+        a.R = rows;
+        a.total_tiles = (rows + rb - 1) / rb;
+        if (fmt == FMT_Q4_0)
+            return nmat == 2 ? dispatch_direct<FMT_Q4_0, 2>(a, wpr, rb, pro, st) : dispatch_direct<FMT_Q4_0, 1>(a, wpr, rb, pro, st);
+        return nmat == 2 ? dispatch_direct<FMT_Q4_0F, 2>(a, wpr, rb, pro, st) : dispatch_direct<FMT_Q4_0F, 1>(a, wpr, rb, pro, st);
+    }
     // LDS bytes of one matrix slot for R rows: the rows' byte range, a
     // 16-byte alignment lead, read slack, and for Q2_K one extra block
     // (a tile's rows may straddle 256-value blocks at both ends).
@@ -519,12 +956,11 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
         int64_t b = fmt == FMT_Q2_K ? (((int64_t)R * K + 255) / 256 + 1) * 84 : (int64_t)R * rowbytes;
         return (b + 32 + 15) & ~15LL;
     };
-    int R = (64 / rpi) * rpi;
-    while (R > rpi && slot_for(R) * nmat > kTileBytes) R -= rpi;
+    int R = 64;
+    while (R > 1 && slot_for(R) * nmat > kTileBytes) R--;
     if (slot_for(R) * nmat > kTileBytes) return RINA_ERR_SHAPE;
-    int64_t slot_bytes = slot_for(R);
     a.R = R;
-    a.slot = (int)slot_bytes;
+    a.slot = (int)slot_for(R);
     int tiles = 0;
     for (int s = 0; s < nseg; s++) {
         a.seg[s].w = (const uint8_t*)segs[s].weight;
@@ -536,14 +972,21 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
     }
     a.total_tiles = tiles;
     switch (fmt) {
-        case FMT_Q4_0: return nmat == 2 ? dispatch_wpr<FMT_Q4_0, 2>(a, wpr, cpl, st) : dispatch_wpr<FMT_Q4_0, 1>(a, wpr, cpl, st);
-        case FMT_Q4_0F: return nmat == 2 ? dispatch_wpr<FMT_Q4_0F, 2>(a, wpr, cpl, st) : dispatch_wpr<FMT_Q4_0F, 1>(a, wpr, cpl, st);
-        default: return nmat == 2 ? dispatch_wpr<FMT_Q2_K, 2>(a, wpr, cpl, st) : dispatch_wpr<FMT_Q2_K, 1>(a, wpr, cpl, st);
+        case FMT_Q4_0:
+            return nmat == 2 ? dispatch_wpr<FMT_Q4_0, 2>(a, wpr, cpl, pro, st) : dispatch_wpr<FMT_Q4_0, 1>(a, wpr, cpl, pro, st);
+        case FMT_Q4_0F:
+            return nmat == 2 ? dispatch_wpr<FMT_Q4_0F, 2>(a, wpr, cpl, pro, st) : dispatch_wpr<FMT_Q4_0F, 1>(a, wpr, cpl, pro, st);
+        default:
+            return nmat == 2 ? dispatch_wpr<FMT_Q2_K, 2>(a, wpr, cpl, pro, st) : dispatch_wpr<FMT_Q2_K, 1>(a, wpr, cpl, pro, st);
     }
 }
 
-int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int epi, hipStream_t st) {
+int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int epi, int pro, const float* nw,
+             float eps, hipStream_t st) {
     F32Args a{};
+    a.pro = pro;
+    a.nw = nw;
+    a.eps = eps;
     a.nseg = nseg;
     a.x = x;
     a.K = K;
@@ -591,10 +1034,11 @@ bool qt_supported(int qt) {
 }  // namespace
 
 extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int qt, const float* input,
-                                     int M, int K, int epi, void* stream) {
+                                     int M, int K, int epi, int pro, const float* nw, float eps, void* stream) {
     if (!segs || nseg < 1 || nseg > 3 || !input || M < 1 || K < 1) return RINA_ERR_ARG;
     if (!qt_supported(qt)) return RINA_ERR_QTYPE;
     if (epi < RINA_EPI_STORE || epi > RINA_EPI_SWIGLU) return RINA_ERR_ARG;
+    if (pro < RINA_PRO_NONE || pro > RINA_PRO_LAYERNORM || (pro != RINA_PRO_NONE && !nw)) return RINA_ERR_ARG;
     if (epi == RINA_EPI_SWIGLU && nseg != 1) return RINA_ERR_ARG;
     if ((qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && (K % 32)) return RINA_ERR_SHAPE;
     for (int s = 0; s < nseg; s++) {
@@ -603,6 +1047,22 @@ extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int 
         if ((uintptr_t)segs[s].weight % 4 || (segs[s].weight2 && (uintptr_t)segs[s].weight2 % 4)) return RINA_ERR_ARG;
     }
     hipStream_t st = as_stream(stream);
+    int unit = qt == RINA_QT_GGML_Q2_K ? 16 : 32;
+    int wpr = 1, cpl = 1;
+    if (qt != RINA_QT_FP32 && K % unit == 0) split_row(K / unit, wpr, cpl);
+    bool fused_pro = M == 1 && ((qt == RINA_QT_FP32 && K <= 16384) ||
+                                (qt != RINA_QT_FP32 && wpr == 1 && cpl == 1 && (uintptr_t)input % 16 == 0 &&
+                                 (uintptr_t)nw % 16 == 0));
+    if (pro != RINA_PRO_NONE && !fused_pro) {
+        // normalize into library scratch first (prompt rows, unusual shapes)
+        float* tmp = (float*)rina_scratch((size_t)M * K * 4);
+        if (!tmp) return RINA_ERR_HIP;
+        int rc = pro == RINA_PRO_RMSNORM ? rina_hip_rms_norm(input, tmp, nw, M, K, eps, stream)
+                                         : rina_hip_layer_norm(input, tmp, nw, M, K, eps, stream);
+        if (rc) return rc;
+        input = tmp;
+        pro = RINA_PRO_NONE;
+    }
     if (M > 1) {
         for (int s = 0; s < nseg; s++) {
             int rc = gemm_tiled(segs[s], qt, input, M, K, epi, st);
@@ -610,7 +1070,7 @@ extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int 
         }
         return RINA_OK;
     }
-    if (qt == RINA_QT_FP32) return gemv_f32(segs, nseg, input, K, epi, st);
+    if (qt == RINA_QT_FP32) return gemv_f32(segs, nseg, input, K, epi, pro, nw, eps, st);
     if ((uintptr_t)input % 16) {   // register staging of x uses 16-byte loads
         for (int s = 0; s < nseg; s++) {
             int rc = gemm_tiled(segs[s], qt, input, M, K, epi, st);
@@ -618,7 +1078,7 @@ extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int 
         }
         return RINA_OK;
     }
-    return gemv_quant(segs, nseg, qt, input, K, epi, st);
+    return gemv_quant(segs, nseg, qt, input, K, epi, pro, nw, eps, st);
 }
 
 extern "C" int rina_hip_linear(const void* weight, int qt, const float* input, float* output, int M, int N, int K,
@@ -639,7 +1099,7 @@ extern "C" int rina_hip_linear(const void* weight, int qt, const float* input, f
         if (!dst) return RINA_ERR_HIP;
     }
     rina_linear_seg seg{weight, nullptr, dst, N};
-    int rc = rina_hip_linear_fused(&seg, 1, qt, input, M, K, RINA_EPI_STORE, stream);
+    int rc = rina_hip_linear_fused(&seg, 1, qt, input, M, K, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, stream);
     if (rc) return rc;
     if (alias && hipMemcpyAsync(output, dst, (size_t)M * N * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
         return RINA_ERR_HIP;

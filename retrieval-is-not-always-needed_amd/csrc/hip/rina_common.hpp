@@ -47,6 +47,34 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
 }
 
 // ---------------------------------------------------------------------------
+// global-memory loads
+// ---------------------------------------------------------------------------
+// Pointers that reach a kernel inside an argument struct are generic; loads
+// through them become FLAT instructions, which also count in LGKM_CNT, so any
+// later LDS access waits for every outstanding weight prefetch.  These
+// helpers cast to the global address space so the loads stay GLOBAL_LOAD.
+template <typename T>
+__device__ __forceinline__ T gld(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ T gld_nt(const T* p) {   // streaming (non-temporal) load
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) T*)p);
+}
+template <typename T>
+__device__ __forceinline__ void gst(T* p, T v) {
+    *(__attribute__((address_space(1))) T*)p = v;
+}
+
+// v_and_b32 the compiler cannot fold into per-field extracts, so the four
+// bytes of the result feed v_cvt_f32_ubyte0..3 directly.
+__device__ __forceinline__ uint32_t and_opaque(uint32_t a, uint32_t m) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(m));
+    return r;
+}
+
+// ---------------------------------------------------------------------------
 // wave64 reductions through DPP (no LDS)
 // ---------------------------------------------------------------------------
 

@@ -15,7 +15,10 @@ pytestmark = pytest.mark.gpu
 
 Q4_SHAPES = [(4, 160, 640), (2, 2048, 2048), (1, 640, 640), (8, 64, 4096),      # test_linear_q4.cu:106-124
              (1, 8192, 2048), (1, 2048, 8192), (1, 512, 2048), (1, 100, 96), (1, 33, 160), (3, 77, 320),
-             (1, 2048, 16384)]
+             (1, 2048, 16384),
+             # direct-load matvec: 2 waves per row with several row groups per
+             # workgroup, and a ragged 4-row-group shape that loops
+             (1, 12289, 4096), (1, 70001, 2048)]
 
 
 def ok(rc, what=""):
@@ -130,20 +133,23 @@ def test_linear_fused_epilogues(rina, orc, qt):
     wd = [dev(w) for w in ws]
     outs = [empty(n) for n in Ns]
     segs = (rina.LinearSeg * 3)(*[rina.LinearSeg(wd[i].data_ptr(), None, outs[i].data_ptr(), Ns[i]) for i in range(3)])
-    ok(hip.rina_hip_linear_fused(segs, 3, qt, xd.data_ptr(), 1, K, rina.EPI_STORE, stream()), "fused store")
+    ok(hip.rina_hip_linear_fused(segs, 3, qt, xd.data_ptr(), 1, K, rina.EPI_STORE, 0, None, 0.0, stream()),
+       "fused store")
     for i in range(3):
         assert_close(host(outs[i]), orc.linear(ws[i], qt, x, Ns[i], K)[0], what="seg %d" % i)
     # residual add
     base = r.standard_normal(2048).astype(np.float32)
     yd = dev(base)
     seg = rina.LinearSeg(wd[0].data_ptr(), None, yd.data_ptr(), 2048)
-    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, xd.data_ptr(), 1, K, rina.EPI_ADD, stream()), "fused add")
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, xd.data_ptr(), 1, K, rina.EPI_ADD, 0, None, 0.0, stream()),
+       "fused add")
     assert_close(host(yd), base + orc.linear(ws[0], qt, x, 2048, K)[0], what="add")
     # SiLU(W1 x) * (W3 x)
     w3 = mk(2048)
     gd = empty(2048)
     seg = rina.LinearSeg(wd[0].data_ptr(), dev(w3).data_ptr(), gd.data_ptr(), 2048)
-    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, xd.data_ptr(), 1, K, rina.EPI_SWIGLU, stream()), "swiglu")
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, xd.data_ptr(), 1, K, rina.EPI_SWIGLU, 0, None, 0.0,
+                                 stream()), "swiglu")
     g = orc.linear(ws[0], qt, x, 2048, K)[0]
     u = orc.linear(w3, qt, x, 2048, K)[0]
     ref = np.zeros(2048, np.float32)
@@ -354,3 +360,30 @@ def test_argmax(rina, orc):
     pos = dev(np.array([4], np.int32))
     ok(hip.rina_hip_argmax(dev(c3).data_ptr(), c3.size, None, ids.data_ptr(), pos.data_ptr(), stream()))
     assert int(host(pos)[0]) == 5 and int(host(ids)[5]) == 100
+
+
+@pytest.mark.parametrize("qt", [7, 5, 10, 6])
+@pytest.mark.parametrize("pro", [1, 2])
+@pytest.mark.parametrize("M,K", [(1, 2048), (1, 640), (2, 2048), (1, 8192)])
+def test_linear_norm_prologue(rina, orc, qt, pro, M, K):
+    """norm(x) fused into the matvec == oracle norm followed by oracle matvec"""
+    hip = rina.load_hip()
+    L = orc.load()
+    r = rng(qt * 10 + pro + K)
+    N = 256
+    if qt == 10:
+        if K % 256:
+            pytest.skip("Q2_K rows of 640 are not 16-value aligned")
+        w = q2k_blocks(K, N * K)
+    else:
+        wf = (r.standard_normal(N * K) * 0.02).astype(np.float32)
+        w = wf if qt == 6 else orc.pack(qt, wf)
+    x = (r.standard_normal((M, K)) * 3 + 0.5).astype(np.float32)
+    nw = r.uniform(0.5, 1.5, K).astype(np.float32)
+    y = empty(M * N)
+    seg = rina.LinearSeg(dev(w).data_ptr(), None, y.data_ptr(), N)
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, dev(x).data_ptr(), M, K, rina.EPI_STORE, pro,
+                                 dev(nw).data_ptr(), np.float32(1e-5), stream()), "prologue")
+    xn = x.copy()
+    (L.orc_rms_norm if pro == 1 else L.orc_layer_norm)(xn.ctypes.data, nw.ctypes.data, M, K, np.float32(1e-5))
+    assert_close(host(y).reshape(M, N), orc.linear(w, qt, xn, N, K), what="prologue %d qt %d" % (pro, qt))
