@@ -170,6 +170,24 @@ int rina_hip_gqa_attention(const float* q, const float* kcur, const float* vcur,
                            float* out, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* Decode step (T == 1, dh == 64) of one layer's attention with RoPE and the
+ * cache append fused in: the result equals rina_hip_rope_append (pre_rope 0)
+ * followed by rina_hip_gqa_attention, except that q and k are read raw and
+ * left unmodified.  q [H*dh], k/v [Hkv*dh] are the current rows before RoPE;
+ * K (rotated) and V are appended at pos0 = start_pos + (d_pos ? *d_pos : 0).
+ * k_rot_out (optional, [Hkv*dh]) receives the rotated K row.  Same
+ * workspace as rina_hip_gqa_attention.  Fuses gqa_layer.cu:147-270 for the
+ * decode step (no counterpart as one reference call); RINA_ERR_SHAPE for
+ * shapes it does not cover (the caller then uses the two-call form). */
+int rina_hip_gqa_decode_attention(const float* q, const float* k, const float* v,
+                                  const float* rope_q_cos, const float* rope_q_sin,
+                                  const float* rope_k_cos, const float* rope_k_sin,
+                                  void* cache_k, void* cache_v, int mode, int H,
+                                  int Hkv, int dh, int start_pos, const int* d_pos,
+                                  int max_seq, float* out, float* k_rot_out,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* ====================================================================== */
 /* Per-token glue                                                          */
 /* ====================================================================== */

@@ -83,6 +83,19 @@ struct GQAImpl {
         float* tap_k = nullptr;
         if (b.kv_tap && !b.d_pos) tap_k = b.kv_tap + ((size_t)layer * 2 * max_seq + start_pos) * kvd;
         const size_t rows_bytes = (size_t)n * kvd * sizeof(float);
+        if (n == 1 && !pre_rope) {
+            // decode step: RoPE, append and attention in one call
+            rc = rina_hip_gqa_decode_attention(b.q, b.k, b.v, rq_cos, rq_sin, rk_cos, rk_sin, ck, cv, mode, H, Hkv,
+                                               dh, start_pos, b.d_pos, max_seq, b.a, tap_k, b.attn_ws,
+                                               b.attn_ws_bytes, s);
+            if (rc == RINA_OK) {
+                if (tap_k && hipMemcpyAsync(tap_k + (size_t)max_seq * kvd, b.v, rows_bytes, hipMemcpyDeviceToDevice,
+                                            s) != hipSuccess)
+                    return RINA_ERR_HIP;
+                return finish(h, b, n, s);
+            }
+            if (rc != RINA_ERR_SHAPE) return rc;
+        }
         if (tap_k && pre_rope && hipMemcpyAsync(tap_k, b.k, rows_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
             return RINA_ERR_HIP;
         CK(rina_hip_rope_append(b.q, b.k, b.v, rq_cos, rq_sin, rk_cos, rk_sin, ck, cv, mode, pre_rope, n, H, Hkv, dh,
@@ -95,6 +108,15 @@ struct GQAImpl {
         }
         CK(rina_hip_gqa_attention(b.q, b.k, b.v, ck, cv, mode, pre_rope, rk_cos, rk_sin, n, H, Hkv, dh, start_pos,
                                   b.d_pos, max_seq, b.a, b.attn_ws, b.attn_ws_bytes, s));
+        return finish(h, b, n, s);
+#undef CK
+    }
+
+    // W_o + residual, then the SwiGLU MLP + residual
+    int finish(float* h, ForwardBuffers& b, int n, hipStream_t s) {
+        int rc;
+#define CK(x) do { if ((rc = (x)) != RINA_OK) return rc; } while (0)
+        const int pro = use_rms_norm ? RINA_PRO_RMSNORM : RINA_PRO_LAYERNORM;
         rina_linear_seg o{w_o.data, nullptr, h, d};
         CK(rina_hip_linear_fused(&o, 1, (int)w_o.qt, b.a, n, H * dh, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
         rina_linear_seg up{w1.data, w3.data, b.g, hd};

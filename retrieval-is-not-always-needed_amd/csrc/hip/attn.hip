@@ -7,14 +7,18 @@
 // kernels/quantize.cu), the others from the current fp32 rows; query head h
 // reads KV head h / (H/Hkv); score = (q.k) / sqrt(dh).
 //
-// Decode (T == 1, dh == 64): split-sequence.  A workgroup takes a chunk of
-// positions and a group of HG KV heads whose records are contiguous
-// in every cache layout (position-major, heads inside), so each position's
-// bytes are consumed whole.  8 lanes cover one head's 64 dims (8 values per
-// lane, dequantized in registers), the REP query heads of that KV head are
-// reduced with DPP inside the 8-lane group.  Scores go to LDS, the chunk's
-// softmax is formed there, V is accumulated in registers and the chunk
-// writes (max, sum, O) partials; the last chunk to finish merges them.
+// Decode (T == 1, dh == 64): split-sequence in two launches.  The split
+// kernel gives each workgroup a chunk of positions of HG KV heads (records of
+// a position are contiguous: position-major, heads inside); 8 lanes cover one
+// head's 64 dims (8 values per lane, dequantized in registers) and the REP
+// query heads of that KV head are reduced with DPP inside the 8-lane group.
+// Every 8-lane slot keeps its own online softmax over the positions it takes
+// (no barrier in the loop; the next positions' K/V loads are in flight while
+// the current ones are consumed); slots merge through cross-lane shuffles and
+// one LDS exchange, and the chunk writes (max, sum, O) partials.  The combine
+// kernel merges the chunks of each head.  Optionally the split kernel also
+// applies RoPE to q and the current k and appends K/V at the current position
+// (the workgroup holding that position), replacing the separate append launch.
 #include "rina_common.hpp"
 #include "kv_formats.hpp"
 
@@ -22,18 +26,15 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSub = 32;     // chunk granularity (a multiple of every sub-step)
-constexpr int kMaxChunks = 64;  // chunk partials per head (chunk size adapts)
+constexpr int kMaxChunks = 64;  // chunk partials per head (chunk length adapts)
 
 // Chunk length for a cache of max_pos positions: at most kMaxChunks
-// partials per head, each a multiple of the kSub sub-step.
+// partials per head, each a multiple of the workgroup step `gran`.
 int chunk_len(int max_pos, int gran) {
     int per = (max_pos + kMaxChunks - 1) / kMaxChunks;
     per = (per + gran - 1) / gran * gran;
     return per < gran ? gran : per;
 }
-
-constexpr size_t kCounterBytes = 256;   // per-head-group completion counters
 
 struct AttnArgs {
     const float* q;
@@ -44,14 +45,25 @@ struct AttnArgs {
     const float* rkc;
     const float* rks;
     float* out;
-    float* ws_m;
-    float* ws_l;
-    float* ws_o;
-    int mode, pre_rope, T, H, Hkv, dh, start_pos, max_seq, nchunk_max, chunk;
+    int mode, pre_rope, T, H, Hkv, dh, start_pos, max_seq;
     const int* d_pos;
-    int* counters;   // per head group, in the workspace; zero between calls
-    void* ws;
-    size_t ws_bytes;
+    float scale;
+};
+
+struct SplitArgs {
+    const float* q;        // [H*64]; raw when the kernel applies RoPE
+    const float* kcur;     // [Hkv*64]; raw when the kernel applies RoPE
+    const float* vcur;     // [Hkv*64]
+    const float *qc, *qs, *kc, *ks;   // RoPE tables [max_seq][32] (NULL: no rotation)
+    uint8_t* ck;           // caches; written at pos0 when the kernel appends
+    uint8_t* cv;
+    float* k_rot_out;      // optional copy of the appended (rotated) fp32 K row
+    float* ws_m;           // [nchunk][H]
+    float* ws_l;           // [nchunk][H]
+    float* ws_o;           // [nchunk][H][64]
+    float* out;            // [H*64]
+    int mode, H, Hkv, start_pos, max_seq, chunk;
+    const int* d_pos;
     float scale;
 };
 
@@ -93,28 +105,39 @@ __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o
     }
 }
 
-// Chunk c of a head group covers positions [c*CS, c*CS+CS) in sub-steps of
-// kSub positions; K and V of a sub-step are loaded together (one HBM round
-// trip), scores are reduced in LDS and the chunk keeps an online softmax
-// across sub-steps.  The last workgroup of a head group to finish (counter in
-// the workspace, reset by that workgroup) merges the chunk partials, so no
-// second launch and no memset node is needed.
-template <int KF, int VF, int HG, int REP>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+__device__ __forceinline__ void ld8f(const float* p, float (&o)[8]) {
+    const f32x4* v = (const f32x4*)p;
+    f32x4 a = gld(v), b = gld(v + 1);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+
+// Dims [dim0, dim0+8) of a 64-dim head row after the NeoX rotation with
+// table row (c, s) (ops/rope.cu:125-149, same fused-multiply form as the
+// reference's compiled kernel: x0*c - x1*s and x0*s + x1*c with one rounding
+// of the x1 product inside each fma).  own: the row's values at these dims;
+// pair: the values 32 dims away.
+__device__ __forceinline__ void rope8(int dim0, const float (&own)[8], const float (&pair)[8], const float (&c)[8],
+                                      const float (&s)[8], float (&o)[8]) {
+    if (dim0 < 32) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = fmaf(own[i], c[i], -(pair[i] * s[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = fmaf(pair[i], s[i], own[i] * c[i]);
+    }
+}
+
+template <int KF, int VF, int HG, int REP, bool FUSED>
+__global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     constexpr int DH = 64;
     constexpr int LPP = 8 * HG;          // lanes per position record
-    constexpr int PPW = 64 / LPP;        // positions per wave step
+    constexpr int PPW = 64 / LPP;        // positions per wave step (slots)
     constexpr int GS = 4 * PPW;          // positions per workgroup step
-    constexpr int SUB = GS > 16 ? GS : 16;   // positions per sub-step (divides kSub)
-    constexpr int NST = SUB / GS;            // steps per sub-step
     constexpr int QH = HG * REP;         // query heads in the group
-    constexpr int KBB = kvq::block_bytes_c(KF), VBB = kvq::block_bytes_c(VF);
-    static_assert(NST >= 1 && kSub % SUB == 0, "sub-step");
-    __shared__ float s_lds[QH][SUB];
-    __shared__ float s_alpha[QH];
-    __shared__ float o_red[GS * QH * DH];
-    __shared__ float s_hm[QH], s_hl[QH];
-    __shared__ int s_last;
+    __shared__ float s_o[4][QH][DH];
+    __shared__ float s_m[4][QH], s_l[4][QH];
+    __shared__ float s_k[FUSED ? HG * DH : 1], s_v[FUSED ? HG * DH : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
@@ -125,8 +148,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     const int j0 = c * CS;
     if (j0 >= L) return;
     const int ncv = min(CS, L - j0);
+    const bool has_cur = pos0 < j0 + CS;            // this chunk holds the current position
     const int kvd = a.Hkv * DH;
     const int hg0 = blockIdx.y * HG;
+    constexpr int KBB = kvq::block_bytes_c(KF), VBB = kvq::block_bytes_c(VF);
     const int64_t KREC = KF ? (int64_t)(kvd / 32) * KBB : (int64_t)kvd * 4;
     const int64_t VREC = VF ? (int64_t)(kvd / 32) * VBB : (int64_t)kvd * 4;
 
@@ -137,164 +162,226 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     const int64_t voff = (int64_t)kvh * DH + dim0;  // value offset inside a position record
     const int wslot = wave * PPW + slot;
 
-    float qv[REP][8], ov[REP][8];
-    float m_run = -INFINITY, l_run = 0.f;           // owned by threads tid < QH
-    bool first = true;
-    for (int sub = 0; sub < ncv; sub += SUB) {
-        float kv[NST][8], vv[NST][8];
+    // query rows (and the current K/V row) first: cache hits, consumed while
+    // the chunk's K/V loads are in flight
+    float qraw[REP][8], qpair[REP][8], tc[8], ts[8];
+    float kown[8], kpair[8], kc8[8], ks8[8], vcur[8];
 #pragma unroll
-        for (int st = 0; st < NST; st++) {
-            const int jl = sub + st * GS + wslot;
-            const int j = j0 + jl;
+    for (int i = 0; i < 8; i++) kown[i] = vcur[i] = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) kv[st][i] = vv[st][i] = 0.f;
-            if (jl < ncv) {
-                if (j == pos0) {
-                    load8<0>((const uint8_t*)a.kcur, voff, kv[st]);
-                    load8<0>((const uint8_t*)a.vcur, voff, vv[st]);
-                } else {
-                    load8<KF>(a.ck + (int64_t)j * KREC, voff, kv[st]);
-                    load8<VF>(a.cv + (int64_t)j * VREC, voff, vv[st]);
-                }
-            }
+    for (int r = 0; r < REP; r++) {
+        const float* qh = a.q + (int64_t)(kvh * REP + r) * DH;
+        ld8f(qh + dim0, qraw[r]);
+        if (FUSED && a.qc) ld8f(qh + (dim0 ^ 32), qpair[r]);
+    }
+    if (FUSED && a.qc) {
+        ld8f(a.qc + (int64_t)pos0 * 32 + (dim0 & 31), tc);
+        ld8f(a.qs + (int64_t)pos0 * 32 + (dim0 & 31), ts);
+    }
+    if (has_cur) {
+        ld8f(a.kcur + voff, kown);
+        ld8f(a.vcur + voff, vcur);
+        if (FUSED && a.kc) {
+            ld8f(a.kcur + (int64_t)kvh * DH + (dim0 ^ 32), kpair);
+            ld8f(a.kc + (int64_t)pos0 * 32 + (dim0 & 31), kc8);
+            ld8f(a.ks + (int64_t)pos0 * 32 + (dim0 & 31), ks8);
         }
-        if (first) {
+    }
+
+    // K/V of step st: every lane loads (positions past the chunk end read
+    // the chunk's first position and are masked), so the load counters stay
+    // exact across the pipelined steps
+    const int nsteps = (ncv + GS - 1) / GS;
+    auto issue = [&](int st, float (&kk)[8], float (&vv)[8]) {
+        const int jl = st * GS + wslot;
+        const int j = j0 + (jl < ncv ? jl : 0);
+        load8<KF>(a.ck + (int64_t)j * KREC, voff, kk);
+        load8<VF>(a.cv + (int64_t)j * VREC, voff, vv);
+    };
+    float kA[8], vA[8], kB[8], vB[8];
+    issue(0, kA, vA);
+
+    float qv[REP][8];
 #pragma unroll
-            for (int r = 0; r < REP; r++) {
-                const f32x4* qp = (const f32x4*)(a.q + (int64_t)(kvh * REP + r) * DH + dim0);
-                f32x4 x0 = gld(qp), x1 = gld(qp + 1);
-                qv[r][0] = x0.x; qv[r][1] = x0.y; qv[r][2] = x0.z; qv[r][3] = x0.w;
-                qv[r][4] = x1.x; qv[r][5] = x1.y; qv[r][6] = x1.z; qv[r][7] = x1.w;
+    for (int r = 0; r < REP; r++) {
+        if (FUSED && a.qc) rope8(dim0, qraw[r], qpair[r], tc, ts, qv[r]);
+        else {
 #pragma unroll
-                for (int i = 0; i < 8; i++) ov[r][i] = 0.f;
-            }
-            first = false;
+            for (int i = 0; i < 8; i++) qv[r][i] = qraw[r][i];
         }
+    }
+    float kcur[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (has_cur) {
+        if (FUSED && a.kc) rope8(dim0, kown, kpair, kc8, ks8, kcur);
+        else {
 #pragma unroll
-        for (int st = 0; st < NST; st++) {
-            const int jl = sub + st * GS + wslot;
-#pragma unroll
-            for (int r = 0; r < REP; r++) {
-                float p = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; i++) p = fmaf(qv[r][i], kv[st][i], p);
-                p = sum8(p);
-                if (jl < ncv && (lig & 7) == 0) s_lds[kvl * REP + r][st * GS + wslot] = p * a.scale;
-            }
+            for (int i = 0; i < 8; i++) kcur[i] = kown[i];
         }
-        __syncthreads();
-        if (tid < QH) {
-            const int nv = min(SUB, ncv - sub);
-            float mx = -INFINITY;
-            for (int jl = 0; jl < nv; jl++) mx = fmaxf(mx, s_lds[tid][jl]);
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = expf(m_run - m_new);      // 0 on the first sub-step
-            float sum = 0.f;
-            for (int jl = 0; jl < nv; jl++) {
-                float p = expf(s_lds[tid][jl] - m_new);
-                s_lds[tid][jl] = p;
-                sum += p;
-            }
-            l_run = l_run * alpha + sum;
-            m_run = m_new;
-            s_alpha[tid] = alpha;
+    }
+
+    float ov[REP][8], m_run[REP], l_run[REP];
+#pragma unroll
+    for (int r = 0; r < REP; r++) {
+        m_run[r] = -INFINITY;
+        l_run[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) ov[r][i] = 0.f;
+    }
+    auto consume = [&](int st, const float (&kk)[8], const float (&vv)[8]) {
+        const int jl = st * GS + wslot;
+        const bool valid = jl < ncv;
+        const bool cur = has_cur && (j0 + jl == pos0);
+        float kx[8], vx[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            kx[i] = cur ? kcur[i] : kk[i];
+            vx[i] = cur ? vcur[i] : vv[i];
         }
-        __syncthreads();
 #pragma unroll
         for (int r = 0; r < REP; r++) {
-            const float al = s_alpha[kvl * REP + r];
+            float p = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) ov[r][i] *= al;
+            for (int i = 0; i < 8; i++) p = fmaf(qv[r][i], kx[i], p);
+            const float sc = sum8(p) * a.scale;
+            if (valid) {
+                const float mn = fmaxf(m_run[r], sc);
+                const float al = expf(m_run[r] - mn);   // 0 while nothing is accumulated
+                const float pe = expf(sc - mn);
+                l_run[r] = fmaf(l_run[r], al, pe);
 #pragma unroll
-            for (int st = 0; st < NST; st++) {
-                if (sub + st * GS + wslot < ncv) {
-                    const float p = s_lds[kvl * REP + r][st * GS + wslot];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) ov[r][i] = fmaf(p, vv[st][i], ov[r][i]);
-                }
+                for (int i = 0; i < 8; i++) ov[r][i] = fmaf(ov[r][i], al, pe * vx[i]);
+                m_run[r] = mn;
             }
         }
-        __syncthreads();
+    };
+    for (int st = 0;;) {
+        if (st + 1 < nsteps) {
+            issue(st + 1, kB, vB);
+            consume(st, kA, vA);
+        } else {
+            consume(st, kA, vA);
+            break;
+        }
+        st++;
+        if (st + 1 < nsteps) {
+            issue(st + 1, kA, vA);
+            consume(st, kB, vB);
+        } else {
+            consume(st, kB, vB);
+            break;
+        }
+        st++;
     }
-    // chunk partials
-    if (tid < QH) {
-        const int h = hg0 * REP + tid;
-        a.ws_m[(int64_t)c * a.H + h] = m_run;
-        a.ws_l[(int64_t)c * a.H + h] = l_run;
+
+    // merge the wave's slots (lanes lig, lig+LPP, ...) by shuffles
+#pragma unroll
+    for (int off = LPP; off < 64; off <<= 1) {
+#pragma unroll
+        for (int r = 0; r < REP; r++) {
+            const float mo = __shfl_xor(m_run[r], off), lo = __shfl_xor(l_run[r], off);
+            const float mn = fmaxf(m_run[r], mo);
+            const float a1 = m_run[r] == -INFINITY ? 0.f : expf(m_run[r] - mn);
+            const float a2 = mo == -INFINITY ? 0.f : expf(mo - mn);
+            l_run[r] = l_run[r] * a1 + lo * a2;
+#pragma unroll
+            for (int i = 0; i < 8; i++) ov[r][i] = ov[r][i] * a1 + __shfl_xor(ov[r][i], off) * a2;
+            m_run[r] = mn;
+        }
     }
+    if (lane < LPP) {
 #pragma unroll
-    for (int r = 0; r < REP; r++)
+        for (int r = 0; r < REP; r++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) o_red[wslot * QH * DH + (kvl * REP + r) * DH + dim0 + i] = ov[r][i];
+            for (int i = 0; i < 8; i++) s_o[wave][kvl * REP + r][dim0 + i] = ov[r][i];
+            if ((lig & 7) == 0) {
+                s_m[wave][kvl * REP + r] = m_run[r];
+                s_l[wave][kvl * REP + r] = l_run[r];
+            }
+        }
+        if (FUSED && has_cur && wave == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                s_k[kvl * DH + dim0 + i] = kcur[i];
+                s_v[kvl * DH + dim0 + i] = vcur[i];
+            }
+        }
+    }
     __syncthreads();
     for (int e = tid; e < QH * DH; e += 256) {
-        float acc = 0.f;
+        const int qh = e / DH, d = e % DH;
+        float M = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < GS; g++) acc += o_red[g * QH * DH + e];
-        const int h = hg0 * REP + e / DH;
-        a.ws_o[((int64_t)c * a.H + h) * DH + (e % DH)] = acc;
+        for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w][qh]);
+        float o = 0.f, l = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float mw = s_m[w][qh];
+            const float aw = mw == -INFINITY ? 0.f : expf(mw - M);
+            o = fmaf(s_o[w][qh][d], aw, o);
+            l = fmaf(s_l[w][qh], aw, l);
+        }
+        const int h = hg0 * REP + qh;
+        gst(a.ws_o + ((int64_t)c * a.H + h) * DH + d, o);
+        if (d == 0) {
+            gst(a.ws_m + (int64_t)c * a.H + h, M);
+            gst(a.ws_l + (int64_t)c * a.H + h, l);
+        }
     }
-    // ---- completion: the last chunk of this head group merges the partials
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // K/V append at pos0 (positions < pos0 are the only cache rows read by
+    // this launch, so the write races with nothing)
+    if (FUSED && has_cur) {
+        const int64_t row = (int64_t)pos0 * kvd + (int64_t)hg0 * DH;
+        if (a.mode == RINA_KV_FP32) {
+            if (tid < HG * DH) {
+                gst((float*)a.ck + row + tid, s_k[tid]);
+                gst((float*)a.cv + row + tid, s_v[tid]);
+            }
+        } else if (tid < 4 * HG) {              // HG heads x 2 blocks x {K, V}
+            const bool isv = tid >= 2 * HG;
+            const int b = isv ? tid - 2 * HG : tid;
+            float vals[32];
+            const float* src = (isv ? s_v : s_k) + b * 32;
+#pragma unroll
+            for (int i = 0; i < 32; i++) vals[i] = src[i];
+            const int64_t blk = row / 32 + b;
+            if (isv) kvq::quantize_block(VF, vals, a.cv + blk * VBB);
+            else kvq::quantize_block(KF, vals, a.ck + blk * KBB);
+        }
+        if (a.k_rot_out && tid < HG * DH) gst(a.k_rot_out + (int64_t)hg0 * DH + tid, s_k[tid]);
+    }
+}
+
+// out[h] = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c over the chunks that
+// hold positions 0..pos0 (at most kMaxChunks = 64).  One workgroup per query
+// head.  Every wave reads all chunk maxima and sums at once (lane c: chunk c)
+// and each thread (chunk group g, dim d) issues its 16 O loads together, so
+// the kernel costs one memory round trip.
+__global__ __launch_bounds__(256) void attn_combine_kernel(SplitArgs a) {
+    constexpr int DH = 64;
+    constexpr int PER = kMaxChunks / 4;
+    __shared__ float s_o[4][DH];
+    const int pos0 = read_pos(a.start_pos, a.d_pos);
+    if (pos0 < 0 || pos0 >= a.max_seq) return;
+    const int nch = (pos0 + a.chunk) / a.chunk;     // chunks holding positions 0..pos0
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+    const int cl = lane < nch ? lane : nch - 1;
+    const float mr = gld(a.ws_m + (int64_t)cl * a.H + h), lr = gld(a.ws_l + (int64_t)cl * a.H + h);
+    float ov[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int cc = min(g + 4 * k, nch - 1);
+        ov[k] = gld(a.ws_o + ((int64_t)cc * a.H + h) * DH + lane);
+    }
+    const float ml = lane < nch ? mr : -INFINITY;
+    const float M = wave_max(ml);
+    const float wl = lane < nch ? expf(ml - M) : 0.f;
+    const float lt = wave_sum(wl * lr);
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) o = fmaf(ov[k], __shfl(wl, g + 4 * k), o);   // wl is 0 past nch
+    s_o[g][lane] = o;
     __syncthreads();
-    const int nch = (L + CS - 1) / CS;
-    if (tid == 0) {
-        int prev = __hip_atomic_fetch_add(a.counters + blockIdx.y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == nch - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // per-head max and sum over chunks: QH heads x (256/QH) chunk lanes
-    constexpr int CL = 256 / QH;
-    float* wts = o_red;                                   // [nch][QH] softmax weights
-    {
-        const int hq = tid / CL, cl = tid % CL;
-        const int h = hg0 * REP + hq;
-        float mx = -INFINITY;
-        for (int cc = cl; cc < nch; cc += CL) mx = fmaxf(mx, gld(a.ws_m + (int64_t)cc * a.H + h));
-        o_red[GS * QH * DH - 256 + tid] = mx;
-        __syncthreads();
-        if (cl == 0) {
-            float m = -INFINITY;
-            for (int k = 0; k < CL; k++) m = fmaxf(m, o_red[GS * QH * DH - 256 + hq * CL + k]);
-            s_hm[hq] = m;
-        }
-        __syncthreads();
-        const float M = s_hm[hq];
-        float ls = 0.f;
-        for (int cc = cl; cc < nch; cc += CL) {
-            float w = expf(gld(a.ws_m + (int64_t)cc * a.H + h) - M);
-            wts[cc * QH + hq] = w;
-            ls = fmaf(gld(a.ws_l + (int64_t)cc * a.H + h), w, ls);
-        }
-        o_red[GS * QH * DH - 256 + tid] = ls;
-        __syncthreads();
-        if (cl == 0) {
-            float t = 0.f;
-            for (int k = 0; k < CL; k++) t += o_red[GS * QH * DH - 256 + hq * CL + k];
-            s_hl[hq] = 1.0f / t;
-        }
-        __syncthreads();
-    }
-    const int64_t cstride = (int64_t)a.H * DH;
-    for (int e = tid; e < QH * DH; e += 256) {
-        const int hq = e / DH, d = e % DH;
-        const int h = hg0 * REP + hq;
-        const float* op = a.ws_o + (int64_t)h * DH + d;
-        float acc = 0.f;
-        int cc = 0;
-        for (; cc + 8 <= nch; cc += 8) {       // 8 independent loads in flight
-            float o[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) o[k] = gld(op + (cc + k) * cstride);
-#pragma unroll
-            for (int k = 0; k < 8; k++) acc = fmaf(o[k], wts[(cc + k) * QH + hq], acc);
-        }
-        for (; cc < nch; cc++) acc = fmaf(gld(op + cc * cstride), wts[cc * QH + hq], acc);
-        gst(a.out + (int64_t)h * DH + d, acc * s_hl[hq]);
-    }
-    if (tid == 0) __hip_atomic_store(a.counters + blockIdx.y, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (g == 0) gst(a.out + (int64_t)h * DH + lane, ((s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane])) / lt);
 }
 
 // ---------------------------------------------------------------------------
@@ -366,49 +453,65 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs a, int kf, in
     }
 }
 
-template <int KF, int VF, int HG>
-int launch_decode_rep(AttnArgs a, int rep, hipStream_t st) {
-    // sub-step of this head-group size: 16 positions, 32 for single heads
-    const int gran = HG >= 2 ? 16 : 32;
-    a.chunk = chunk_len(a.max_seq, gran);
+// head-group size: 2 KV heads when the count allows (a position's slice of
+// the record is then >= 2 heads wide), else 1
+inline int head_group(int Hkv) { return Hkv % 2 == 0 ? 2 : 1; }
+
+size_t split_ws_bytes(int H, int nchunk) { return (size_t)nchunk * H * (2 + 64) * sizeof(float); }
+
+template <int KF, int VF, int HG, bool FUSED>
+int launch_split(SplitArgs a, int rep, size_t ws_bytes, void* ws, hipStream_t st) {
+    constexpr int GS = 4 * (64 / (8 * HG));
+    a.chunk = chunk_len(a.max_seq, GS);
     const int max_pos = a.d_pos ? a.max_seq : a.start_pos + 1;
-    a.nchunk_max = (max_pos + a.chunk - 1) / a.chunk;
-    const size_t need = kCounterBytes + (size_t)a.nchunk_max * a.H * (2 + (size_t)a.dh) * sizeof(float);
-    if (!a.ws || a.ws_bytes < need) return RINA_ERR_WORKSPACE;
-    a.counters = (int*)a.ws;
-    a.ws_m = (float*)((char*)a.ws + kCounterBytes);
-    a.ws_l = a.ws_m + (size_t)a.nchunk_max * a.H;
-    a.ws_o = a.ws_l + (size_t)a.nchunk_max * a.H;
-    dim3 grid(a.nchunk_max, a.Hkv / HG);
+    const int nchunk = (max_pos + a.chunk - 1) / a.chunk;
+    if (!ws || ws_bytes < split_ws_bytes(a.H, nchunk)) return RINA_ERR_WORKSPACE;
+    a.ws_m = (float*)ws;
+    a.ws_l = a.ws_m + (size_t)nchunk * a.H;
+    a.ws_o = a.ws_l + (size_t)nchunk * a.H;
+    dim3 grid(nchunk, a.Hkv / HG);
     switch (rep) {
-        case 1: hipLaunchKernelGGL((attn_decode_kernel<KF, VF, HG, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((attn_decode_kernel<KF, VF, HG, 2>), grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((attn_decode_kernel<KF, VF, HG, 4>), grid, dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((attn_decode_kernel<KF, VF, HG, 8>), grid, dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 1, FUSED>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 2, FUSED>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 4, FUSED>), grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 8, FUSED>), grid, dim3(256), 0, st, a); break;
         default: return RINA_ERR_SHAPE;
     }
+    if (hipGetLastError() != hipSuccess) return RINA_ERR_HIP;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.H), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 
-// head-group size per mode: enough heads that a position's K record slice
-// spans >= ~128 contiguous bytes
-template <int KF, int VF>
-int launch_decode(const AttnArgs& a, int rep, hipStream_t st) {
-    constexpr int HGP = KF == 0 ? 2 : KF == RINA_KVF_Q8_0 ? 4 : 8;
-    if (a.Hkv % HGP == 0) return launch_decode_rep<KF, VF, HGP>(a, rep, st);
-    if (a.Hkv % 4 == 0 && HGP > 4) return launch_decode_rep<KF, VF, 4>(a, rep, st);
-    if (a.Hkv % 2 == 0 && HGP > 2) return launch_decode_rep<KF, VF, 2>(a, rep, st);
-    return launch_decode_rep<KF, VF, 1>(a, rep, st);
+template <int KF, int VF, bool FUSED>
+int launch_split_hg(const SplitArgs& a, int rep, size_t ws_bytes, void* ws, hipStream_t st) {
+    if (head_group(a.Hkv) == 2) return launch_split<KF, VF, 2, FUSED>(a, rep, ws_bytes, ws, st);
+    return launch_split<KF, VF, 1, FUSED>(a, rep, ws_bytes, ws, st);
 }
 
+template <bool FUSED>
+int launch_split_mode(const SplitArgs& a, int rep, size_t ws_bytes, void* ws, hipStream_t st) {
+    switch (a.mode) {
+        case RINA_KV_FP32: return launch_split_hg<0, 0, FUSED>(a, rep, ws_bytes, ws, st);
+        case RINA_KV_Q8: return launch_split_hg<RINA_KVF_Q8_0, RINA_KVF_Q8_0, FUSED>(a, rep, ws_bytes, ws, st);
+        case RINA_KV_Q4: return launch_split_hg<RINA_KVF_Q4_0, RINA_KVF_Q4_0, FUSED>(a, rep, ws_bytes, ws, st);
+        case RINA_KV_Q4K_Q2V: return launch_split_hg<RINA_KVF_Q4_0, RINA_KVF_Q2_1, FUSED>(a, rep, ws_bytes, ws, st);
+        case RINA_KV_Q2: return launch_split_hg<RINA_KVF_Q2_1, RINA_KVF_Q2_1, FUSED>(a, rep, ws_bytes, ws, st);
+        default: return launch_split_hg<RINA_KVF_Q2_1, RINA_KVF_Q1_0, FUSED>(a, rep, ws_bytes, ws, st);
+    }
+}
+
+bool rep_ok(int rep) { return rep == 1 || rep == 2 || rep == 4 || rep == 8; }
 
 }  // namespace
 
 extern "C" size_t rina_hip_gqa_attention_workspace(int T, int H, int dh, int max_pos) {
     (void)T;
-    // granularity 16 gives the most chunks, an upper bound for every kernel shape
-    size_t nch = (size_t)(max_pos + chunk_len(max_pos, 16) - 1) / chunk_len(max_pos, 16);
-    return kCounterBytes + nch * H * (2 + (size_t)dh) * sizeof(float);
+    (void)dh;
+    if (H < 1 || max_pos < 1) return 0;
+    // the smallest workgroup step (16 positions) gives the most chunks: an
+    // upper bound for every head-group size
+    const int cs = chunk_len(max_pos, 16);
+    return split_ws_bytes(H, (max_pos + cs - 1) / cs);
 }
 
 extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const float* vcur, const void* cache_k,
@@ -425,6 +528,19 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
     hipStream_t st = as_stream(stream);
     int kf = 0, vf = 0;
     if (mode != RINA_KV_FP32) kvq::mode_formats_host(mode, kf, vf);
+    int rep = H / Hkv;
+    bool fast = T == 1 && dh == 64 && !pre_rope && rep_ok(rep) && cache_k && cache_v &&
+                ((uintptr_t)q % 16 == 0) && ((uintptr_t)kcur % 16 == 0) && ((uintptr_t)vcur % 16 == 0) &&
+                (mode != RINA_KV_FP32 || (((uintptr_t)cache_k | (uintptr_t)cache_v) % 16 == 0));
+    if (fast) {
+        SplitArgs sa{};
+        sa.q = q; sa.kcur = kcur; sa.vcur = vcur;
+        sa.ck = (uint8_t*)cache_k; sa.cv = (uint8_t*)cache_v;
+        sa.out = out;
+        sa.mode = mode; sa.H = H; sa.Hkv = Hkv; sa.start_pos = start_pos; sa.max_seq = max_seq; sa.d_pos = d_pos;
+        sa.scale = 1.0f / sqrtf((float)dh);
+        return launch_split_mode<false>(sa, rep, ws_bytes, workspace, st);
+    }
     AttnArgs a{};
     a.q = q; a.kcur = kcur; a.vcur = vcur;
     a.ck = (const uint8_t*)cache_k; a.cv = (const uint8_t*)cache_v;
@@ -432,23 +548,33 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
     a.mode = mode; a.pre_rope = pre_rope; a.T = T; a.H = H; a.Hkv = Hkv; a.dh = dh;
     a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos;
     a.scale = 1.0f / sqrtf((float)dh);
-    int rep = H / Hkv;
-    bool fast = T == 1 && dh == 64 && !pre_rope && (rep == 1 || rep == 2 || rep == 4 || rep == 8) &&
-                ((uintptr_t)q % 16 == 0) && ((uintptr_t)kcur % 16 == 0) && ((uintptr_t)vcur % 16 == 0) &&
-                (mode != RINA_KV_FP32 || (((uintptr_t)cache_k | (uintptr_t)cache_v) % 16 == 0));
-    if (fast) {
-        a.ws = workspace;
-        a.ws_bytes = ws_bytes;
-        switch (mode) {
-            case RINA_KV_FP32: return launch_decode<0, 0>(a, rep, st);
-            case RINA_KV_Q8: return launch_decode<RINA_KVF_Q8_0, RINA_KVF_Q8_0>(a, rep, st);
-            case RINA_KV_Q4: return launch_decode<RINA_KVF_Q4_0, RINA_KVF_Q4_0>(a, rep, st);
-            case RINA_KV_Q4K_Q2V: return launch_decode<RINA_KVF_Q4_0, RINA_KVF_Q2_1>(a, rep, st);
-            case RINA_KV_Q2: return launch_decode<RINA_KVF_Q2_1, RINA_KVF_Q2_1>(a, rep, st);
-            default: return launch_decode<RINA_KVF_Q2_1, RINA_KVF_Q1_0>(a, rep, st);
-        }
-    }
     hipLaunchKernelGGL(attn_generic_kernel, dim3(H, T), dim3(64), 0, st, a, kf, vf);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
+}
+
+extern "C" int rina_hip_gqa_decode_attention(const float* q, const float* k, const float* v, const float* rope_q_cos,
+                                             const float* rope_q_sin, const float* rope_k_cos,
+                                             const float* rope_k_sin, void* cache_k, void* cache_v, int mode, int H,
+                                             int Hkv, int dh, int start_pos, const int* d_pos, int max_seq,
+                                             float* out, float* k_rot_out, void* workspace, size_t ws_bytes,
+                                             void* stream) {
+    if (!q || !k || !v || !out || !cache_k || !cache_v || H < 1 || Hkv < 1 || max_seq < 1) return RINA_ERR_ARG;
+    if (mode < RINA_KV_FP32 || mode > RINA_KV_Q2K_Q1V) return RINA_ERR_QTYPE;
+    if (H % Hkv || dh != 64 || !rep_ok(H / Hkv)) return RINA_ERR_SHAPE;
+    if ((!rope_q_cos) != (!rope_q_sin) || (!rope_k_cos) != (!rope_k_sin)) return RINA_ERR_ARG;
+    if (!d_pos && (start_pos < 0 || start_pos + 1 > max_seq)) return RINA_ERR_RANGE;
+    const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)rope_q_cos | (uintptr_t)rope_q_sin |
+                         (uintptr_t)rope_k_cos | (uintptr_t)rope_k_sin | (uintptr_t)k_rot_out;
+    if (al % 16 || (mode == RINA_KV_FP32 && ((uintptr_t)cache_k | (uintptr_t)cache_v) % 16) ||
+        (mode != RINA_KV_FP32 && ((uintptr_t)cache_k | (uintptr_t)cache_v) % 2))
+        return RINA_ERR_SHAPE;
+    SplitArgs sa{};
+    sa.q = q; sa.kcur = k; sa.vcur = v;
+    sa.qc = rope_q_cos; sa.qs = rope_q_sin; sa.kc = rope_k_cos; sa.ks = rope_k_sin;
+    sa.ck = (uint8_t*)cache_k; sa.cv = (uint8_t*)cache_v; sa.k_rot_out = k_rot_out;
+    sa.out = out;
+    sa.mode = mode; sa.H = H; sa.Hkv = Hkv; sa.start_pos = start_pos; sa.max_seq = max_seq; sa.d_pos = d_pos;
+    sa.scale = 1.0f / sqrtf((float)dh);
+    return launch_split_mode<true>(sa, H / Hkv, ws_bytes, workspace, as_stream(stream));
 }

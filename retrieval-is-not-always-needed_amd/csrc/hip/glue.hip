@@ -6,6 +6,8 @@
 
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -107,21 +109,32 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
     return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
 }
 
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
+__device__ __forceinline__ unsigned long long cand(float v, int i) { return v > -1e10f ? argmax_key(v, i) : 0ull; }
+
+// A few workgroups (one 64-bit atomic each, after a wave + LDS reduction)
+// cover x with 16-byte loads; many same-address atomics serialize.
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* x, int n) {
+    __shared__ unsigned long long red[4];
     unsigned long long best = 0ull;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        float v = x[i];
-        if (v > -1e10f) {
-            unsigned long long k = argmax_key(v, i);
-            best = k > best ? k : best;
-        }
+    const int tid = threadIdx.x;
+    const int stride = gridDim.x * blockDim.x;
+    const int n4 = ((uintptr_t)x % 16 == 0) ? n / 4 : 0;
+    const f32x4* x4 = (const f32x4*)x;
+    for (int i = blockIdx.x * blockDim.x + tid; i < n4; i += stride) {
+        const f32x4 v = gld(x4 + i);
+        best = umax64(best, umax64(umax64(cand(v.x, 4 * i), cand(v.y, 4 * i + 1)),
+                                   umax64(cand(v.z, 4 * i + 2), cand(v.w, 4 * i + 3))));
     }
-    // wave max of 64-bit keys
-    for (int off = 32; off > 0; off >>= 1) {
-        unsigned long long o = __shfl_xor(best, off);
-        best = o > best ? o : best;
+    for (int i = 4 * n4 + blockIdx.x * blockDim.x + tid; i < n; i += stride) best = umax64(best, cand(gld(x + i), i));
+    for (int off = 32; off > 0; off >>= 1) best = umax64(best, __shfl_xor(best, off));
+    if ((tid & 63) == 0) red[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        best = umax64(umax64(red[0], red[1]), umax64(red[2], red[3]));
+        if (best) atomicMax(&g_argmax_key, best);
     }
-    if ((threadIdx.x & 63) == 0 && best) atomicMax(&g_argmax_key, best);
 }
 
 __global__ void argmax_finish_kernel(int* out_idx, int* ids_out, int* d_pos) {
@@ -237,9 +250,8 @@ extern "C" int rina_hip_saxpy(float* d, const float* s, float p, int64_t n, void
 extern "C" int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out, int* d_pos, void* stream) {
     if (!x || n < 1 || (!out_idx && !d_pos)) return RINA_ERR_ARG;
     hipStream_t st = as_stream(stream);
-    int grid = (n + 255) / 256;
-    int cap = rina_num_cus() * 2;
-    if (grid > cap) grid = cap;
+    int grid = (n + 1023) / 1024;
+    if (grid > 64) grid = 64;
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(grid), dim3(256), 0, st, x, n);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, st, out_idx, ids_out, d_pos);

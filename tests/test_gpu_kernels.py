@@ -284,6 +284,66 @@ def test_attention_other_shapes(rina, orc, H, Hkv, dh):
     assert_close(got, ref, what="shape %s" % ((H, Hkv, dh),))
 
 
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("P,H,Hkv,use_dpos", [(0, 32, 8, False), (37, 32, 8, False), (543, 32, 8, True),
+                                              (1500, 32, 8, False), (70, 10, 5, False), (16, 8, 8, True)])
+def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
+    """RoPE + K/V append + attention in one call == rope_append then attention
+    (oracle): the rotated K row and the appended cache bytes bit-exact, the
+    output within tolerance, and no other cache row touched."""
+    hip = rina.load_hip()
+    L = orc.load()
+    dh = 64
+    kvd = Hkv * dh
+    max_seq = P + 9
+    r = rng(mode * 7 + P + H)
+    kc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    vc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    q = r.standard_normal(H * dh).astype(np.float32)
+    k = r.standard_normal(kvd).astype(np.float32)
+    v = r.standard_normal(kvd).astype(np.float32)
+    cos, sin = rope_tables(dh, max_seq)
+    qr, kr = q.copy(), k.copy()
+    L.orc_rope_neox(qr.ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, H, dh, P)
+    L.orc_rope_neox(kr.ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, Hkv, dh, P)
+    if mode == 0:
+        ckb, cvb = kc.view(np.uint8).reshape(-1).copy(), vc.view(np.uint8).reshape(-1).copy()
+    else:
+        kf, vf = orc.kv_mode_formats(mode)
+        ckb, cvb = orc.kv_quantize(kf, kc), orc.kv_quantize(vf, vc)
+    ref = np.zeros(H * dh, np.float32)
+    if mode == 0:
+        L.orc_gqa_attention(qr.ctypes.data, kr.ctypes.data, v.ctypes.data, kc.ctypes.data, vc.ctypes.data, None,
+                            None, 0, 0, None, None, 1, P, H, Hkv, dh, ref.ctypes.data)
+    else:
+        L.orc_gqa_attention(qr.ctypes.data, kr.ctypes.data, v.ctypes.data, None, None, ckb.ctypes.data,
+                            cvb.ctypes.data, mode, 0, None, None, 1, P, H, Hkv, dh, ref.ctypes.data)
+    ws_bytes = hip.rina_hip_gqa_attention_workspace(1, H, dh, max_seq)
+    ws = empty(ws_bytes, "uint8")
+    ckd, cvd = dev(ckb), dev(cvb)
+    od, krot = empty(H * dh), empty(kvd)
+    cd, sd = dev(cos), dev(sin)
+    pos = dev(np.array([P], np.int32)) if use_dpos else None
+    ok(hip.rina_hip_gqa_decode_attention(dev(q).data_ptr(), dev(k).data_ptr(), dev(v).data_ptr(), cd.data_ptr(),
+                                         sd.data_ptr(), cd.data_ptr(), sd.data_ptr(), ckd.data_ptr(), cvd.data_ptr(),
+                                         mode, H, Hkv, dh, 0 if use_dpos else P,
+                                         pos.data_ptr() if use_dpos else None, max_seq, od.data_ptr(),
+                                         krot.data_ptr(), ws.data_ptr(), ws_bytes, stream()), "decode attention")
+    assert np.array_equal(host(krot).view(np.uint32), kr.view(np.uint32))
+    assert_close(host(od), ref, what="fused decode mode %d P %d" % (mode, P))
+    gk, gv = host(ckd), host(cvd)
+    if mode == 0:
+        want_k = kc.copy(); want_k[P] = kr
+        want_v = vc.copy(); want_v[P] = v
+        assert np.array_equal(gk.view(np.float32).reshape(max_seq, kvd), want_k)
+        assert np.array_equal(gv.view(np.float32).reshape(max_seq, kvd), want_v)
+    else:
+        want_k = kc.copy(); want_k[P] = kr
+        want_v = vc.copy(); want_v[P] = v
+        assert np.array_equal(gk, orc.kv_quantize(kf, want_k))
+        assert np.array_equal(gv, orc.kv_quantize(vf, want_v))
+
+
 @pytest.mark.parametrize("mode", [0, 2])
 def test_attention_pre_rope(rina, orc, mode):
     got, ref = attention_case(rina, orc, mode, 12, 1, pre_rope=1)
@@ -355,6 +415,14 @@ def test_argmax(rina, orc):
         out = empty(1, "int32")
         ok(hip.rina_hip_argmax(dev(a).data_ptr(), a.size, out.data_ptr(), None, None, stream()))
         assert int(host(out)[0]) == orc.load().orc_argmax(a.ctypes.data, a.size)
+    # ragged length (scalar tail) and an unaligned start (scalar path)
+    c4 = rng(2).standard_normal(100003).astype(np.float32)
+    c4[100002] = 9.0
+    d4 = dev(np.concatenate([np.zeros(1, np.float32), c4]))
+    for ptr, arr in ((d4.data_ptr() + 4, c4), (d4.data_ptr(), np.concatenate([np.zeros(1, np.float32), c4]))):
+        out = empty(1, "int32")
+        ok(hip.rina_hip_argmax(ptr, arr.size, out.data_ptr(), None, None, stream()))
+        assert int(host(out)[0]) == orc.load().orc_argmax(arr.ctypes.data, arr.size)
     # device-loop form: ids[pos+1] = argmax, pos += 1
     ids = empty(16, "int32")
     pos = dev(np.array([4], np.int32))
