@@ -549,6 +549,164 @@ __device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const DirectS
     else gst(y, v[0]);
 }
 
+// Workgroup-cooperative activation prep for the direct kernel: the K values
+// are split over the 256 threads (TPC threads per 32-value column, 8..32
+// values each) instead of every wave digitizing the whole row; the optional
+// norm prologue reduces over the workgroup.  Digit planes, offsets and
+// exponents go to LDS as [plane][dword][column] so each consumer lane then
+// reads its column conflict-free.
+struct PrepLds {
+    int32_t dg[3][8][256];
+    float tt[3][256];
+    float xe[256];
+    float red[8];
+};
+
+__device__ __forceinline__ float block_sum4(float v, float* red, int slot) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[slot * 4 + (threadIdx.x >> 6)] = v;
+    __syncthreads();
+    return (red[slot * 4 + 0] + red[slot * 4 + 1]) + (red[slot * 4 + 2] + red[slot * 4 + 3]);
+}
+
+// sum / max over groups of TPC consecutive lanes (TPC 1, 2 or 4)
+template <int TPC>
+__device__ __forceinline__ float grp_max(float v) {
+    if (TPC >= 2) v = fmaxf(v, dpp_f<0xB1>(v));
+    if (TPC >= 4) v = fmaxf(v, dpp_f<0x4E>(v));
+    return v;
+}
+template <int TPC>
+__device__ __forceinline__ int grp_sum_i(int v) {
+    if (TPC >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
+    if (TPC >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
+    return v;
+}
+
+template <int TPC, int PRO>
+struct PrepRaw {
+    static constexpr int VPC = 32 / TPC;           // values per thread
+    float x[VPC];
+    float w[PRO != RINA_PRO_NONE ? VPC : 1];
+};
+
+// issued before the weight loads: vmcnt retires loads in issue order
+template <int TPC, int PRO>
+__device__ __forceinline__ void wg_prep_load(const GemvArgs& a, PrepRaw<TPC, PRO>& r) {
+    constexpr int VPC = 32 / TPC;
+    const int tid = threadIdx.x;
+    const int u = tid / TPC, j = tid % TPC;
+    const bool on = u < a.K / 32;
+    float (&x)[VPC] = r.x;
+    auto& w = r.w;
+    {
+        const int uu = on ? u : 0;
+        const f32x4* xp = (const f32x4*)(a.x + (int64_t)uu * 32 + j * VPC);
+#pragma unroll
+        for (int i = 0; i < VPC / 4; i++) {
+            f32x4 v = gld(xp + i);
+            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+        }
+        if constexpr (PRO != RINA_PRO_NONE) {
+            const f32x4* wp = (const f32x4*)(a.nw + (int64_t)uu * 32 + j * VPC);
+#pragma unroll
+            for (int i = 0; i < VPC / 4; i++) {
+                f32x4 v = gld(wp + i);
+                w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+            }
+        }
+    }
+}
+
+template <int TPC, int PRO>
+__device__ __forceinline__ void wg_prep_x(const GemvArgs& a, PrepRaw<TPC, PRO>& r, PrepLds& L) {
+    constexpr int VPC = 32 / TPC;
+    const int tid = threadIdx.x;
+    const int u = tid / TPC, j = tid % TPC;
+    const bool on = u < a.K / 32;
+    float (&x)[VPC] = r.x;
+    auto& w = r.w;
+    if (!on) {
+#pragma unroll
+        for (int i = 0; i < VPC; i++) x[i] = 0.f;
+    }
+    if constexpr (PRO != RINA_PRO_NONE) {
+        const float d = (float)a.K;
+        float mean = 0.f;
+        if (PRO == RINA_PRO_LAYERNORM) {
+            float sm = 0.f;
+#pragma unroll
+            for (int i = 0; i < VPC; i++) sm += x[i];
+            mean = block_sum4(sm, L.red, 0) / d;
+        }
+        float ss = 0.f;
+        if (on) {
+#pragma unroll
+            for (int i = 0; i < VPC; i++) {
+                const float t = x[i] - mean;
+                ss = fmaf(t, t, ss);
+            }
+        }
+        const float inv = 1.0f / sqrtf(block_sum4(ss, L.red, 1) / d + a.eps);
+#pragma unroll
+        for (int i = 0; i < VPC; i++) x[i] = on ? (x[i] - mean) * inv * w[i] : 0.f;
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPC; i++) mx = fmaxf(mx, fabsf(x[i]));
+    mx = grp_max<TPC>(mx);
+    int e = 0;
+    if (mx > 0.f) (void)frexpf(mx, &e);            // mx < 2^e
+    const float up = ldexpf(1.0f, 22 - e);
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int tl = 0; tl < VPC / 4; tl++) {         // local dword pair index tl/2, parity tl%2
+        uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int k = 8 * (tl >> 1) + 2 * b + (tl & 1);
+            const int X = (int)rintf(x[k] * up);
+            const int d0 = ((X + 128) & 255) - 128;
+            const int X1 = (X - d0) >> 8;
+            const int d1 = ((X1 + 128) & 255) - 128;
+            const int d2 = (X1 - d1) >> 8;
+            s0 += d0; s1 += d1; s2 += d2;
+            p0 |= (uint32_t)(d0 & 255) << (8 * b);
+            p1 |= (uint32_t)(d1 & 255) << (8 * b);
+            p2 |= (uint32_t)(d2 & 255) << (8 * b);
+        }
+        if (on) {
+            const int t = j * (VPC / 4) + tl;
+            L.dg[0][t][u] = (int32_t)p0;
+            L.dg[1][t][u] = (int32_t)p1;
+            L.dg[2][t][u] = (int32_t)p2;
+        }
+    }
+    s0 = grp_sum_i<TPC>(s0);
+    s1 = grp_sum_i<TPC>(s1);
+    s2 = grp_sum_i<TPC>(s2);
+    if (on && j == 0) {
+        L.tt[0][u] = 7.0f * (float)s0;
+        L.tt[1][u] = 7.0f * (float)s1;
+        L.tt[2][u] = 7.0f * (float)s2;
+        L.xe[u] = ldexpf(1.0f, e - 22);
+    }
+    __syncthreads();
+}
+
+template <int FMT>
+__device__ __forceinline__ void read_cols(const PrepLds& L, int u, bool active, XCols<FMT, 1>& xc) {
+    const int uu = active ? u : 0;
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+#pragma unroll
+        for (int t = 0; t < 8; t++) xc.dg[0][p][t] = L.dg[p][t][uu];
+        xc.tt[0][p] = L.tt[p][uu];
+    }
+    xc.xe[0] = L.xe[uu];
+    xc.xs[0] = 0.f;
+}
+
 // Row sums of one row group and their epilogue.
 template <int FMT, int WPR, int NMAT, int RB>
 __device__ __forceinline__ void direct_consume(const GemvArgs& a, const DirectSegs& S, const XCols<FMT, 1>& xc,
@@ -614,15 +772,18 @@ __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
     const int ngrp = a.total_tiles;
     const DirectSegs S(a);
 
-    // activation loads first (cache hits) so that digitizing them overlaps
-    // the weight loads: vmcnt retires loads in issue order
-    XRaw<FMT, WPR, 1, PRO> xr;
-    load_x_raw<FMT, WPR, 1, PRO>(a, xr);
+    // activation loads, then the first row group's weight loads, then the
+    // activation prep (overlapping the weight loads)
+    __shared__ PrepLds prep;
+    constexpr int TPC = WPR == 1 ? 4 : WPR == 2 ? 2 : 1;
+    PrepRaw<TPC, PRO> raw;
+    wg_prep_load<TPC, PRO>(a, raw);
     int it = blockIdx.x;
     DirectBlk<RB> A, B;
     direct_issue<FMT, NMAT, RB>(a, S, it * RPI + rs, u, active, A);
+    wg_prep_x<TPC, PRO>(a, raw, prep);
     XCols<FMT, 1> xc;
-    prep_x<FMT, WPR, 1, PRO>(a, xr, xc);
+    read_cols<FMT>(prep, u, active, xc);
 
     for (;;) {
         if ((it + G) * RPI < ngrp) {
@@ -875,7 +1036,7 @@ int launch_direct(GemvArgs& a, hipStream_t st) {
     constexpr int RPI = 4 / WPR;
     int cus = rina_num_cus();
     int wgs = (a.total_tiles + RPI - 1) / RPI;
-    int per_cu = RB == 4 ? 3 : 4;   // workgroups resident per CU at this register count
+    int per_cu = RB >= 8 ? 2 : RB == 4 ? 3 : 4;   // workgroups resident per CU at this register count
     int grid = wgs < cus * per_cu ? wgs : cus * per_cu;
     hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB>), dim3(grid), dim3(kWG), 0, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
@@ -886,20 +1047,23 @@ int direct_rb(GemvArgs& a, int rb, hipStream_t st) {
     switch (rb) {
         case 1: return launch_direct<FMT, WPR, NMAT, PRO, 1>(a, st);
         case 2: return launch_direct<FMT, WPR, NMAT, PRO, 2>(a, st);
-        default: return launch_direct<FMT, WPR, NMAT, PRO, 4>(a, st);
+        case 4: return launch_direct<FMT, WPR, NMAT, PRO, 4>(a, st);
+        default: return launch_direct<FMT, WPR, NMAT, PRO, 8>(a, st);
     }
+}
+
+template <int FMT, int WPR, int NMAT>
+int direct_pro(GemvArgs& a, int rb, int pro, hipStream_t st) {
+    if (pro == RINA_PRO_RMSNORM) return direct_rb<FMT, WPR, NMAT, RINA_PRO_RMSNORM>(a, rb, st);
+    if (pro == RINA_PRO_LAYERNORM) return direct_rb<FMT, WPR, NMAT, RINA_PRO_LAYERNORM>(a, rb, st);
+    return direct_rb<FMT, WPR, NMAT, 0>(a, rb, st);
 }
 
 template <int FMT, int NMAT>
 int dispatch_direct(GemvArgs& a, int wpr, int rb, int pro, hipStream_t st) {
-    if (wpr == 1) {
-        if (pro == RINA_PRO_RMSNORM) return direct_rb<FMT, 1, NMAT, RINA_PRO_RMSNORM>(a, rb, st);
-        if (pro == RINA_PRO_LAYERNORM) return direct_rb<FMT, 1, NMAT, RINA_PRO_LAYERNORM>(a, rb, st);
-        return direct_rb<FMT, 1, NMAT, 0>(a, rb, st);
-    }
-    if (pro != RINA_PRO_NONE) return RINA_ERR_SHAPE;
-    if (wpr == 2) return direct_rb<FMT, 2, NMAT, 0>(a, rb, st);
-    return direct_rb<FMT, 4, NMAT, 0>(a, rb, st);
+    if (wpr == 1) return direct_pro<FMT, 1, NMAT>(a, rb, pro, st);
+    if (wpr == 2) return direct_pro<FMT, 2, NMAT>(a, rb, pro, st);
+    return direct_pro<FMT, 4, NMAT>(a, rb, pro, st);
 }
 
 // waves per row / units per lane for a row of `nunits` work units
@@ -938,11 +1102,11 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
             a.seg[s].tile0 = rows;
             rows += segs[s].N;
         }
-        // enough row groups to give every wave of a full wave-slot load
-        // (4 workgroups of 4 waves per CU) one group, then more rows per wave
-        int64_t waves = (int64_t)rina_num_cus() * 16;
+        // rows per wave: about two workgroups per CU (each preps the
+        // activation once), up to 8 rows per wave
+        int64_t waves = (int64_t)rina_num_cus() * 8;
         int64_t want = ((int64_t)rows * wpr + waves - 1) / waves;
-        int rb = want <= 1 ? 1 : want <= 2 ? 2 : 4;
+        int rb = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : 8;
         a.R = rows;
         a.total_tiles = (rows + rb - 1) / rb;
         if (fmt == FMT_Q4_0)
@@ -1050,8 +1214,10 @@ extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int 
     int unit = qt == RINA_QT_GGML_Q2_K ? 16 : 32;
     int wpr = 1, cpl = 1;
     if (qt != RINA_QT_FP32 && K % unit == 0) split_row(K / unit, wpr, cpl);
+    // direct Q4 kernel: any waves-per-row; Q2_K tile kernel: one wave per row
+    const bool q4 = qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F;
     bool fused_pro = M == 1 && ((qt == RINA_QT_FP32 && K <= 16384) ||
-                                (qt != RINA_QT_FP32 && wpr == 1 && cpl == 1 && (uintptr_t)input % 16 == 0 &&
+                                (qt != RINA_QT_FP32 && (wpr == 1 || q4) && cpl == 1 && (uintptr_t)input % 16 == 0 &&
                                  (uintptr_t)nw % 16 == 0));
     if (pro != RINA_PRO_NONE && !fused_pro) {
         // normalize into library scratch first (prompt rows, unusual shapes)

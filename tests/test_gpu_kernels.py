@@ -432,7 +432,7 @@ def test_argmax(rina, orc):
 
 @pytest.mark.parametrize("qt", [7, 5, 10, 6])
 @pytest.mark.parametrize("pro", [1, 2])
-@pytest.mark.parametrize("M,K", [(1, 2048), (1, 640), (2, 2048), (1, 8192)])
+@pytest.mark.parametrize("M,K", [(1, 2048), (1, 640), (2, 2048), (1, 8192), (1, 4096)])
 def test_linear_norm_prologue(rina, orc, qt, pro, M, K):
     """norm(x) fused into the matvec == oracle norm followed by oracle matvec"""
     hip = rina.load_hip()
