@@ -189,6 +189,50 @@ int rina_hip_gqa_decode_attention(const float* q, const float* k, const float* v
                                   void* stream);
 
 /* ====================================================================== */
+/* DeepSeek MLA (latent cache) and MoE                                     */
+/* ====================================================================== */
+
+/* Decode attention of one DeepseekMLAImpl layer at position
+ * pos0 = start_pos + (d_pos ? *d_pos : 0), the intended math of
+ * arch/mla/deepseek_mla_layer.cu:180-269 (the reference's start_pos > 0
+ * branch is broken).  q [H*(nope+rope)] = W_q output ([H*nope | H*rope]);
+ * kva [dc+rope] = W_kv_a output ([c_kv | k_pe]).  Appends the latent record
+ * [RMSNorm(c_kv)*k_norm | RoPE(k_pe)] at pos0 of `cache` ([max_seq][dc+rope]
+ * fp32) and writes out [H*v] = per head W_vb softmax-weighted latent, with
+ * scores (q_nope.W_kb c + RoPE(q_rope).k_pe) / sqrt(nope+rope); W_kv_b
+ * [H*(nope+v), dc] in flat element order (Q2_K, Q4_0, Q4_0F or fp32).
+ * RoPE tables [max_seq][rope/2] (NULL: none).  dc % 64 == 0, dc <= 512,
+ * dc + rope <= 640. */
+size_t rina_hip_mla_attention_workspace(int H, int dc, int rope, int max_pos);
+size_t rina_hip_mla_cache_bytes(int dc, int rope, int max_seq);
+int rina_hip_mla_decode_attention(const float* q, const float* kva, const float* k_norm,
+                                  float eps, const float* rope_cos, const float* rope_sin,
+                                  const void* w_kv_b, int qt_kv_b, float* cache, int H,
+                                  int nope, int rope, int v_dim, int dc, int start_pos,
+                                  const int* d_pos, int max_seq, float* out,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Router top-k of deepseek_mla_layer.cu:310-326 on the device: softmax of
+ * the E logits, insertion top-k kept ascending (strict ">", the earlier
+ * expert wins ties).  ids/probs [k] in that order.  E <= 256, k <= 16. */
+int rina_hip_moe_topk(const float* logits, int n_experts, int k, int* ids,
+                      float* probs, void* stream);
+
+/* Routed experts of forward_moe (deepseek_mla_layer.cu:328-349) for one
+ * token: for j < k (ascending): y_j = W_down[e_j] (SiLU(W_gate[e_j] x) *
+ * (W_up[e_j] x)); h[i] += shared_out[i] + sum_j probs[j] y_j[i] (the sum
+ * accumulated onto shared_out in j order, as the reference's saxpy chain).
+ * Expert e's matrices start e*stride bytes into the stacked tensors of
+ * n_experts experts; ids outside [0, n_experts) are skipped.  workspace: rina_hip_moe_workspace(k, ffn) bytes. */
+size_t rina_hip_moe_workspace(int k, int ffn);
+int rina_hip_moe_ffn(const float* x, const void* gate_exps, const void* up_exps,
+                     const void* down_exps, int quant_type, int64_t stride_gate_up,
+                     int64_t stride_down, int n_experts, const int* ids,
+                     const float* probs, int k,
+                     int d, int ffn, const float* shared_out, float* h, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* ====================================================================== */
 /* Per-token glue                                                          */
 /* ====================================================================== */
 

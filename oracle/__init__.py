@@ -33,6 +33,24 @@ class GQACfg(C.Structure):
                 ("lm_head", VP), ("qt_lm", I32), ("layers", C.POINTER(GQALayerW))]
 
 
+class MLALayerW(C.Structure):
+    _fields_ = [("w_q", VP), ("qt_q", I32), ("w_kv_a", VP), ("qt_kv_a", I32), ("k_norm", VP),
+                ("w_kv_b", VP), ("qt_kv_b", I32), ("w_o", VP), ("qt_o", I32), ("ln1", VP), ("ln2", VP),
+                ("rope_cos", VP), ("rope_sin", VP), ("is_moe", I32),
+                ("w1", VP), ("qt_1", I32), ("w2", VP), ("qt_2", I32), ("w3", VP), ("qt_3", I32), ("hidden", I32),
+                ("gate_inp", VP), ("qt_gate_inp", I32), ("gate_exps", VP), ("up_exps", VP), ("qt_gu", I32),
+                ("down_exps", VP), ("qt_dn", I32), ("stride_gu", I64), ("stride_dn", I64),
+                ("gate_sh", VP), ("up_sh", VP), ("qt_sh_gu", I32), ("down_sh", VP), ("qt_sh_dn", I32),
+                ("shared_hidden", I32)]
+
+
+class MLACfg(C.Structure):
+    _fields_ = [("dim", I32), ("n_layers", I32), ("n_heads", I32), ("nope", I32), ("rope", I32), ("v_dim", I32),
+                ("dc", I32), ("vocab", I32), ("max_seq", I32), ("n_experts", I32), ("top_k", I32),
+                ("expert_ffn", I32), ("nthreads", I32), ("wte", VP), ("qt_wte", I32), ("ln_f", VP),
+                ("lm_head", VP), ("qt_lm", I32), ("layers", C.POINTER(MLALayerW))]
+
+
 _lib = None
 
 
@@ -72,6 +90,12 @@ def load(build=True):
         "orc_gqa_last_kv": (VP, [VP, I32, I32]),
         "orc_gqa_generate": (I32, [VP, VP, I32, I32, VP]),
         "orc_num_threads": (I32, []),
+        "orc_moe_topk": (None, [VP, I32, I32, VP, VP]),
+        "orc_mla_create": (VP, [C.POINTER(MLACfg)]),
+        "orc_mla_destroy": (None, [VP]),
+        "orc_mla_forward": (I32, [VP, VP, I32, I32, VP, I32]),
+        "orc_mla_generate": (I32, [VP, VP, I32, I32, VP]),
+        "orc_mla_cache": (VP, [VP, I32, I32]),
     }
     for n, (r, a) in sigs.items():
         f = getattr(L, n)
@@ -185,5 +209,77 @@ def gqa_generate(m, prompt, steps):
     p = np.ascontiguousarray(prompt, np.int32)
     out = np.zeros(steps, np.int32)
     rc = load().orc_gqa_generate(m, p.ctypes.data, p.size, steps, out.ctypes.data)
+    assert rc == 0, rc
+    return [int(v) for v in out]
+
+
+def moe_topk(logits, k):
+    lg = np.ascontiguousarray(logits, np.float32)
+    ids = np.zeros(k, np.int32)
+    pr = np.zeros(k, np.float32)
+    load().orc_moe_topk(lg.ctypes.data, lg.size, k, ids.ctypes.data, pr.ctypes.data)
+    return ids, pr
+
+
+def mla_from_tensors(cfg, tensors, qts, max_seq, nthreads=0):
+    """Oracle DeepSeek MLA + MoE model over host copies of an engine model's
+    tensors.  cfg: dict with dim, n_layers, n_heads, nope, rope, v_dim, dc,
+    vocab_size, n_experts, top_k, expert_ffn; tensors: name -> numpy array
+    (packed bytes or fp32) under the reference names; qts: name -> quant
+    type.  Returns (handle, keepalive)."""
+    hold = []
+
+    def h(name):
+        if name not in tensors:
+            return None
+        a = np.ascontiguousarray(tensors[name])
+        hold.append(a)
+        return a.ctypes.data
+
+    def q(name):
+        return qts.get(name, FP32)
+
+    nl = cfg["n_layers"]
+    lw = (MLALayerW * nl)()
+    for l in range(nl):
+        p = "transformer.h.%d." % l
+        o = lw[l]
+        for f, nm in (("w_q", "attn.w_q"), ("w_kv_a", "attn.w_kv_a"), ("w_kv_b", "attn.w_kv_b"), ("w_o", "attn.w_o")):
+            setattr(o, f, h(p + nm + ".weight"))
+            setattr(o, "qt_" + f[2:], q(p + nm + ".weight"))
+        o.k_norm = h(p + "attn.k_norm.weight")
+        o.ln1, o.ln2 = h(p + "ln1.weight"), h(p + "ln2.weight")
+        o.rope_cos, o.rope_sin = h(p + "attn.rope_q.cos"), h(p + "attn.rope_q.sin")
+        if (p + "mlp.gate_inp.weight") in tensors:
+            o.is_moe = 1
+            o.gate_inp, o.qt_gate_inp = h(p + "mlp.gate_inp.weight"), q(p + "mlp.gate_inp.weight")
+            o.gate_exps, o.up_exps = h(p + "mlp.gate_exps.weight"), h(p + "mlp.up_exps.weight")
+            o.qt_gu = q(p + "mlp.gate_exps.weight")
+            o.down_exps, o.qt_dn = h(p + "mlp.down_exps.weight"), q(p + "mlp.down_exps.weight")
+            o.stride_gu = tensors[p + "mlp.gate_exps.weight"].nbytes // cfg["n_experts"]
+            o.stride_dn = tensors[p + "mlp.down_exps.weight"].nbytes // cfg["n_experts"]
+            o.gate_sh, o.up_sh = h(p + "mlp.gate_shexp.weight"), h(p + "mlp.up_shexp.weight")
+            o.qt_sh_gu = q(p + "mlp.gate_shexp.weight")
+            o.down_sh, o.qt_sh_dn = h(p + "mlp.down_shexp.weight"), q(p + "mlp.down_shexp.weight")
+            o.shared_hidden = cfg["shared_ffn"]
+        else:
+            o.w1, o.qt_1 = h(p + "mlp.w1.weight"), q(p + "mlp.w1.weight")
+            o.w2, o.qt_2 = h(p + "mlp.w2.weight"), q(p + "mlp.w2.weight")
+            o.w3, o.qt_3 = h(p + "mlp.w3.weight"), q(p + "mlp.w3.weight")
+            o.hidden = cfg["dense_ffn"]
+    c = MLACfg(dim=cfg["dim"], n_layers=nl, n_heads=cfg["n_heads"], nope=cfg["nope"], rope=cfg["rope"],
+               v_dim=cfg["v_dim"], dc=cfg["dc"], vocab=cfg["vocab_size"], max_seq=max_seq,
+               n_experts=cfg.get("n_experts", 0), top_k=cfg.get("top_k", 0), expert_ffn=cfg.get("expert_ffn", 0),
+               nthreads=nthreads, wte=h("transformer.wte.weight"), qt_wte=q("transformer.wte.weight"),
+               ln_f=h("transformer.ln_f.weight"), lm_head=h("lm_head.weight"), qt_lm=q("lm_head.weight"),
+               layers=lw)
+    m = load().orc_mla_create(C.byref(c))
+    return m, (hold, lw, c)
+
+
+def mla_generate(m, prompt, steps):
+    p = np.ascontiguousarray(prompt, np.int32)
+    out = np.zeros(steps, np.int32)
+    rc = load().orc_mla_generate(m, p.ctypes.data, p.size, steps, out.ctypes.data)
     assert rc == 0, rc
     return [int(v) for v in out]

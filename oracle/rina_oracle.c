@@ -777,3 +777,195 @@ int orc_gqa_generate(orc_gqa* m, const int* prompt, int n_prompt, int steps, int
     free(logits);
     return rc;
 }
+
+/* ------------------------------------------------------------------ */
+/* DeepSeek MLA + MoE (arch/mla/deepseek_mla_layer.cu, infer_mla.cpp)   */
+/* ------------------------------------------------------------------ */
+
+/* deepseek_mla_layer.cu:310-326 generalized to E experts, top k */
+void orc_moe_topk(const float* lp, int E, int k, int* topk, float* topw) {
+    float max_lp = lp[0];
+    for (int e = 1; e < E; e++) if (lp[e] > max_lp) max_lp = lp[e];   /* std::max_element */
+    float sum_exp = 0.0f;
+    for (int e = 0; e < E; e++) sum_exp += expf(lp[e] - max_lp);
+    float inv_sum = 1.0f / sum_exp;
+    for (int j = 0; j < k; j++) { topk[j] = -1; topw[j] = -1e10f; }
+    for (int e = 0; e < E; e++) {
+        float w = expf(lp[e] - max_lp) * inv_sum;
+        if (w > topw[0]) {
+            topw[0] = w; topk[0] = e;
+            for (int j = 0; j < k - 1 && topw[j] > topw[j + 1]; j++) {
+                float tw = topw[j]; topw[j] = topw[j + 1]; topw[j + 1] = tw;
+                int ti = topk[j]; topk[j] = topk[j + 1]; topk[j + 1] = ti;
+            }
+        }
+    }
+}
+
+struct orc_mla {
+    orc_mla_cfg c;
+    orc_mla_layer_w* layers;
+    float* cache;      /* [L][max_seq*(rope + H*nope + H*v)] */
+    size_t per_layer;
+};
+
+orc_mla* orc_mla_create(const orc_mla_cfg* cfg) {
+    orc_mla* m = (orc_mla*)calloc(1, sizeof(orc_mla));
+    m->c = *cfg;
+    m->layers = (orc_mla_layer_w*)malloc(sizeof(orc_mla_layer_w) * cfg->n_layers);
+    memcpy(m->layers, cfg->layers, sizeof(orc_mla_layer_w) * cfg->n_layers);
+    m->c.layers = m->layers;
+    int H = cfg->n_heads;
+    m->per_layer = (size_t)cfg->max_seq * (cfg->rope + (size_t)H * cfg->nope + (size_t)H * cfg->v_dim);
+    m->cache = (float*)calloc((size_t)cfg->n_layers * m->per_layer, 4);
+    return m;
+}
+
+void orc_mla_destroy(orc_mla* m) {
+    if (!m) return;
+    free(m->layers); free(m->cache);
+    free(m);
+}
+
+const float* orc_mla_cache(orc_mla* m, int layer, int which) {
+    const orc_mla_cfg* c = &m->c;
+    float* base = m->cache + (size_t)layer * m->per_layer;
+    if (which == 0) return base;
+    base += (size_t)c->max_seq * c->rope;
+    if (which == 1) return base;
+    return base + (size_t)c->max_seq * c->n_heads * c->nope;
+}
+
+/* SwiGLU block: out[d] = W_down(silu(W_gate x) * (W_up x)) */
+static void swiglu_rows(const void* wg, const void* wu, int qt_gu, const void* wd, int qt_d,
+                        const float* x, float* out, int T, int d, int hid, int nt) {
+    float* g = (float*)malloc((size_t)T * hid * 4);
+    float* u = (float*)malloc((size_t)T * hid * 4);
+    orc_linear(wg, qt_gu, x, g, T, hid, d, nt);
+    orc_linear(wu, qt_gu, x, u, T, hid, d, nt);
+    orc_silu_mul(g, g, u, T * hid);
+    orc_linear(wd, qt_d, g, out, T, d, hid, nt);
+    free(g); free(u);
+}
+
+int orc_mla_forward(orc_mla* m, const int* ids, int T, int start_pos, float* logits, int last_only) {
+    const orc_mla_cfg* c = &m->c;
+    const int d = c->dim, H = c->n_heads, nope = c->nope, rope = c->rope, vd = c->v_dim, dc = c->dc;
+    const int dq = nope + rope, nt = c->nthreads, ms = c->max_seq;
+    if (start_pos < 0 || start_pos + T > ms) return -3;
+    float* h = (float*)malloc((size_t)T * d * 4);
+    float* a = (float*)malloc((size_t)T * d * 4);
+    float* Q = (float*)malloc((size_t)T * H * dq * 4);
+    float* KVA = (float*)malloc((size_t)T * (dc + rope) * 4);
+    float* Cn = (float*)malloc((size_t)T * dc * 4);
+    float* KVB = (float*)malloc((size_t)T * H * (nope + vd) * 4);
+    float* att = (float*)malloc((size_t)T * H * vd * 4);
+    float* tmp = (float*)malloc((size_t)T * d * 4);
+    float* Kh = (float*)malloc((size_t)ms * dq * 4);
+    float* Vh = (float*)malloc((size_t)ms * vd * 4);
+    float qv[1024];
+    orc_embedding(c->wte, c->qt_wte, ids, h, T, d);
+    for (int l = 0; l < c->n_layers; l++) {
+        const orc_mla_layer_w* L = &c->layers[l];
+        float* kpe_c = (float*)orc_mla_cache(m, l, 0);
+        float* kn_c = (float*)orc_mla_cache(m, l, 1);
+        float* v_c = (float*)orc_mla_cache(m, l, 2);
+        memcpy(a, h, (size_t)T * d * 4);
+        orc_rms_norm(a, L->ln1, T, d, 1e-5f);                                  /* :180-181 */
+        orc_linear(L->w_q, L->qt_q, a, Q, T, H * dq, d, nt);                  /* :184 */
+        orc_linear(L->w_kv_a, L->qt_kv_a, a, KVA, T, dc + rope, d, nt);       /* :187 */
+        for (int t = 0; t < T; t++) memcpy(Cn + (size_t)t * dc, KVA + (size_t)t * (dc + rope), (size_t)dc * 4);
+        orc_rms_norm(Cn, L->k_norm, T, dc, 1e-5f);                             /* :192 */
+        orc_linear(L->w_kv_b, L->qt_kv_b, Cn, KVB, T, H * (nope + vd), dc, nt);  /* :196 */
+        for (int t = 0; t < T; t++) {
+            const int pos = start_pos + t;
+            float* qr = Q + (size_t)t * H * dq + (size_t)H * nope;             /* [H*rope] of this row */
+            float* kpe = KVA + (size_t)t * (dc + rope) + dc;
+            if (L->rope_cos) {                                                 /* :202-203 */
+                orc_rope_neox(qr, L->rope_cos, L->rope_sin, 1, H, rope, pos);
+                orc_rope_neox(kpe, L->rope_cos, L->rope_sin, 1, 1, rope, pos);
+            }
+            memcpy(kpe_c + (size_t)pos * rope, kpe, (size_t)rope * 4);
+            memcpy(kn_c + (size_t)pos * H * nope, KVB + (size_t)t * H * (nope + vd), (size_t)H * nope * 4);
+            memcpy(v_c + (size_t)pos * H * vd, KVB + (size_t)t * H * (nope + vd) + (size_t)H * nope,
+                   (size_t)H * vd * 4);
+        }
+        /* attention per head over keys 0..pos: K = [K_nope | k_pe], V, scale rsqrt(dq) */
+        for (int hh = 0; hh < H; hh++) {
+            const int last = start_pos + T;
+            for (int j = 0; j < last; j++) {
+                memcpy(Kh + (size_t)j * dq, kn_c + (size_t)j * H * nope + (size_t)hh * nope, (size_t)nope * 4);
+                memcpy(Kh + (size_t)j * dq + nope, kpe_c + (size_t)j * rope, (size_t)rope * 4);
+                memcpy(Vh + (size_t)j * vd, v_c + (size_t)j * H * vd + (size_t)hh * vd, (size_t)vd * 4);
+            }
+            for (int t = 0; t < T; t++) {
+                const float* qrow = Q + (size_t)t * H * dq;
+                memcpy(qv, qrow + (size_t)hh * nope, (size_t)nope * 4);
+                memcpy(qv + nope, qrow + (size_t)H * nope + (size_t)hh * rope, (size_t)rope * 4);
+                orc_attn_rows(qv, dq, Kh, dq, Vh, vd, att + (size_t)t * H * vd + (size_t)hh * vd, vd,
+                              start_pos + t, 1, dq, vd);
+            }
+        }
+        orc_linear(L->w_o, L->qt_o, att, tmp, T, d, H * vd, nt);               /* :271 (out of place) */
+        orc_add(h, h, tmp, T * d);
+        memcpy(a, h, (size_t)T * d * 4);
+        orc_rms_norm(a, L->ln2, T, d, 1e-5f);                                  /* :276 */
+        if (!L->is_moe) {
+            swiglu_rows(L->w1, L->w3, L->qt_1, L->w2, L->qt_2, a, tmp, T, d, L->hidden, nt);   /* :281-286 */
+            orc_add(h, h, tmp, T * d);
+            continue;
+        }
+        /* forward_moe (:291-350), per token */
+        const int E = c->n_experts, K = c->top_k, F = c->expert_ffn;
+        float* lg = (float*)malloc((size_t)E * 4);
+        float* acc = (float*)malloc((size_t)d * 4);
+        float* eo = (float*)malloc((size_t)d * 4);
+        int topk[64];
+        float topw[64];
+        for (int t = 0; t < T; t++) {
+            const float* at = a + (size_t)t * d;
+            swiglu_rows(L->gate_sh, L->up_sh, L->qt_sh_gu, L->down_sh, L->qt_sh_dn, at, acc, 1, d,
+                        L->shared_hidden, nt);                                 /* :297-302 */
+            orc_linear(L->gate_inp, L->qt_gate_inp, at, lg, 1, E, d, nt);      /* :305 */
+            orc_moe_topk(lg, E, K, topk, topw);
+            for (int j = 0; j < K; j++) {
+                const int e = topk[j];
+                if (e < 0) continue;
+                swiglu_rows((const uint8_t*)L->gate_exps + (int64_t)e * L->stride_gu,
+                            (const uint8_t*)L->up_exps + (int64_t)e * L->stride_gu, L->qt_gu,
+                            (const uint8_t*)L->down_exps + (int64_t)e * L->stride_dn, L->qt_dn, at, eo, 1, d, F,
+                            nt);                                               /* :332-343 */
+                orc_saxpy(acc, eo, topw[j], d);                                /* :345 */
+            }
+            orc_add(h + (size_t)t * d, h + (size_t)t * d, acc, d);            /* :349 */
+        }
+        free(lg); free(acc); free(eo);
+    }
+    if (c->ln_f) orc_rms_norm(h, c->ln_f, T, d, 1e-5f);
+    const void* lm = c->lm_head ? c->lm_head : c->wte;
+    int qlm = c->lm_head ? c->qt_lm : c->qt_wte;
+    if (last_only) orc_linear(lm, qlm, h + (size_t)(T - 1) * d, logits, 1, c->vocab, d, nt);
+    else orc_linear(lm, qlm, h, logits, T, c->vocab, d, nt);
+    free(h); free(a); free(Q); free(KVA); free(Cn); free(KVB); free(att); free(tmp); free(Kh); free(Vh);
+    return 0;
+}
+
+int orc_mla_generate(orc_mla* m, const int* prompt, int n_prompt, int steps, int* out_ids) {
+    int V = m->c.vocab;
+    int* gen = (int*)malloc(sizeof(int) * (n_prompt + steps));
+    memcpy(gen, prompt, sizeof(int) * n_prompt);
+    float* logits = (float*)malloc((size_t)V * 4);
+    int len = n_prompt, rc = 0;
+    for (int step = 0; step < steps; step++) {
+        int T = step == 0 ? len : 1;
+        int sp = step == 0 ? 0 : len - 1;
+        rc = orc_mla_forward(m, gen + sp, T, sp, logits, 1);
+        if (rc) break;
+        int nx = orc_argmax(logits, V);
+        gen[len++] = nx;
+        out_ids[step] = nx;
+    }
+    free(gen);
+    free(logits);
+    return rc;
+}

@@ -151,6 +151,59 @@ const float* orc_gqa_last_kv(orc_gqa* m, int layer, int which_v);
 /* main.cpp:666-690 greedy loop: prefill then steps-1 decodes; writes steps ids */
 int      orc_gqa_generate(orc_gqa* m, const int* prompt, int n_prompt, int steps, int* out_ids);
 
+/* ---- DeepSeek MLA + MoE model ---------------------------------------- */
+/* Router top-k of deepseek_mla_layer.cu:310-326: softmax over E logits
+ * (max-subtracted expf, serial fp32 sum, one reciprocal), then insertion
+ * top-k keeping topw ascending (strict ">": the earlier expert wins ties).
+ * ids/probs in that ascending order; unfilled slots get id -1. */
+void orc_moe_topk(const float* logits, int E, int k, int* ids, float* probs);
+
+typedef struct {
+    const void* w_q; int qt_q;          /* [H*(nope+rope), d]; row order [H*nope | H*rope] */
+    const void* w_kv_a; int qt_kv_a;    /* [dc+rope, d]; row order [c_kv | k_pe] */
+    const float* k_norm;                /* [dc] */
+    const void* w_kv_b; int qt_kv_b;    /* [H*(nope+v), dc]; row order [H*nope | H*v] */
+    const void* w_o; int qt_o;          /* [d, H*v] */
+    const float* ln1; const float* ln2;
+    const float* rope_cos; const float* rope_sin;   /* [max_pos][rope/2] (attn.rope_q) */
+    int is_moe;
+    const void* w1; int qt_1;           /* dense SwiGLU [hidden, d] */
+    const void* w2; int qt_2;           /* [d, hidden] */
+    const void* w3; int qt_3;
+    int hidden;
+    const void* gate_inp; int qt_gate_inp;             /* router [E, d] */
+    const void* gate_exps; const void* up_exps; int qt_gu;   /* [E] x [ffn, d] */
+    const void* down_exps; int qt_dn;                        /* [E] x [d, ffn] */
+    int64_t stride_gu, stride_dn;                            /* bytes per expert */
+    const void* gate_sh; const void* up_sh; int qt_sh_gu;    /* [shared, d] */
+    const void* down_sh; int qt_sh_dn;                       /* [d, shared] */
+    int shared_hidden;
+} orc_mla_layer_w;
+
+typedef struct {
+    int dim, n_layers, n_heads, nope, rope, v_dim, dc, vocab, max_seq;
+    int n_experts, top_k, expert_ffn;
+    int nthreads;
+    const void* wte; int qt_wte;
+    const float* ln_f;
+    const void* lm_head; int qt_lm;     /* NULL -> tied to wte */
+    const orc_mla_layer_w* layers;
+} orc_mla_cfg;
+
+typedef struct orc_mla orc_mla;
+orc_mla* orc_mla_create(const orc_mla_cfg* cfg);
+void     orc_mla_destroy(orc_mla* m);
+/* MLAInference::forward (infer/infer_mla.cpp:66-106) with
+ * DeepseekMLAImpl::forward / forward_moe (deepseek_mla_layer.cu:171-350)
+ * as intended at any start_pos: keys/values of positions < start_pos come
+ * from the expanded per-layer cache (k_pe rotated, K_nope, V per head;
+ * core/buffer.h:70-92 layout).  logits [T, vocab] or the last row. */
+int      orc_mla_forward(orc_mla* m, const int* ids, int T, int start_pos, float* logits, int last_only);
+int      orc_mla_generate(orc_mla* m, const int* prompt, int n_prompt, int steps, int* out_ids);
+/* the expanded cache of one layer: k_pe [max_seq][rope], k_nope
+ * [max_seq][H*nope], v [max_seq][H*v] (which: 0, 1, 2) */
+const float* orc_mla_cache(orc_mla* m, int layer, int which);
+
 int orc_num_threads(void);
 
 #ifdef __cplusplus

@@ -46,6 +46,13 @@ _HIP_SIGS = {
                                      VP, SZ, VP]),
     "rina_hip_gqa_decode_attention": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, I32, I32, VP, I32,
                                             VP, VP, VP, SZ, VP]),
+    "rina_hip_mla_attention_workspace": (SZ, [I32, I32, I32, I32]),
+    "rina_hip_mla_cache_bytes": (SZ, [I32, I32, I32]),
+    "rina_hip_mla_decode_attention": (I32, [VP, VP, VP, F32, VP, VP, VP, I32, VP, I32, I32, I32, I32, I32, I32, VP,
+                                            I32, VP, VP, SZ, VP]),
+    "rina_hip_moe_topk": (I32, [VP, I32, I32, VP, VP, VP]),
+    "rina_hip_moe_workspace": (SZ, [I32, I32]),
+    "rina_hip_moe_ffn": (I32, [VP, VP, VP, VP, I32, I64, I64, I32, VP, VP, I32, I32, I32, VP, VP, VP, SZ, VP]),
     "rina_hip_rms_norm": (I32, [VP, VP, VP, I32, I32, F32, VP]),
     "rina_hip_layer_norm": (I32, [VP, VP, VP, I32, I32, F32, VP]),
     "rina_hip_rope": (I32, [VP, VP, VP, I32, I32, I32, I32, VP, I32, VP]),

@@ -50,6 +50,7 @@ struct ForwardBuffers {
     struct {
         float* data = nullptr;
         int max_seq = 0, n_layers = 0, rank = 0, rope = 0;
+        int start_pos = 0;
         float* layer(int l) const { return data + (size_t)l * max_seq * (rank + rope); }
     } mla_cache;
 

@@ -23,10 +23,12 @@ int Layer::forward(float* h, ForwardBuffers& b, int B, int T, hipStream_t s) { r
 int Layer::workspace_per_token(int d, int H, int dh) { return vtab->workspace_per_token_fn(impl, d, H, dh); }
 
 Layer create_gqa_layer();
+Layer create_mla_layer();
 
 Layer* create_layer_by_type(const std::string& type) {
     Layer* l = new Layer();
     if (type == "standard_gqa" || type == "standard_attention" || type == "gqa") *l = create_gqa_layer();
+    else if (type == "deepseek_mla_dense" || type == "deepseek_mla_moe") *l = create_mla_layer();
     else { delete l; return nullptr; }
     return l;
 }

@@ -1,0 +1,109 @@
+// Device-side greedy decode loop shared by the Inference orchestrators
+// (the loop of rina-engine/src/main.cpp:666-690, moved onto the GPU): the
+// argmax kernel writes the next id into the device id buffer and advances a
+// device position, so one decode step is position-independent and is
+// captured once as a HIP graph and replayed.
+#pragma once
+#include <hip/hip_runtime_api.h>
+#include <string>
+#include "infer/infer_base.h"
+#include "rina_hip.h"
+
+struct DeviceGreedyInference : Inference {
+    int* d_ids = nullptr;      // [max_seq + 1]
+    int* d_pos = nullptr;      // device position of the last id
+    int max_seq = 0;
+    int vocab = 0;
+    int gen_len = 0;           // ids valid in d_ids after the last generate / decode_more
+    hipGraphExec_t graph = nullptr;
+    hipStream_t graph_stream = nullptr;
+    std::string tag = "infer";
+
+    ~DeviceGreedyInference() override {
+        if (graph) (void)hipGraphExecDestroy(graph);
+        if (d_ids) (void)hipFree(d_ids);
+        if (d_pos) (void)hipFree(d_pos);
+    }
+
+    // embedding -> layers -> final norm -> LM head for T ids at start_pos
+    // (pos_dev: device position instead, T == 1); logits of the last row
+    // only when last_only.
+    virtual int run(const int* ids, const int* pos_dev, int T, int start_pos, float* logits, bool last_only,
+                    hipStream_t s) = 0;
+    // grow the activation buffers to n rows (caches are kept)
+    virtual int ensure_cap(int n) = 0;
+    // last-row logits buffer of the device loop
+    virtual float* lm_buffer() = 0;
+
+    bool alloc_ids() {
+        return hipMalloc(&d_ids, sizeof(int) * (max_seq + 1)) == hipSuccess &&
+               hipMalloc(&d_pos, sizeof(int)) == hipSuccess;
+    }
+
+    int decode_step(hipStream_t s) {
+        int rc = run(d_ids, d_pos, 1, 0, lm_buffer(), true, s);
+        if (rc) return rc;
+        return rina_hip_argmax(lm_buffer(), vocab, nullptr, d_ids, d_pos, s);
+    }
+
+    int generate(const int* prompt, int n, int steps, int* out, bool use_graph, hipStream_t s,
+                 float* decode_ms) override {
+        if (n < 1 || steps < 1 || n + steps - 1 > max_seq) { err_ = tag + ": prompt + steps exceed max_seq"; return RINA_ERR_RANGE; }
+        int rc = ensure_cap(n);
+        if (rc) return rc;
+        if (hipMemcpyAsync(d_ids, prompt, sizeof(int) * n, hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
+        int p0 = n - 1;
+        if (hipMemcpyAsync(d_pos, &p0, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
+        if ((rc = run(d_ids, nullptr, n, 0, lm_buffer(), true, s))) return rc;
+        if ((rc = rina_hip_argmax(lm_buffer(), vocab, nullptr, d_ids, d_pos, s))) return rc;
+        if (hipStreamSynchronize(s) != hipSuccess) return RINA_ERR_HIP;
+        gen_len = n + 1;
+        if (hipMemcpyAsync(out, d_ids + n, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return RINA_ERR_HIP;
+        if (steps == 1) {
+            if (decode_ms) *decode_ms = 0.f;
+            return hipStreamSynchronize(s) == hipSuccess ? RINA_OK : RINA_ERR_HIP;
+        }
+        return decode_more(steps - 1, out + 1, use_graph, s, decode_ms);
+    }
+
+    int decode_more(int steps, int* out, bool use_graph, hipStream_t s, float* decode_ms) override {
+        if (gen_len < 1) { err_ = tag + ": decode_more before generate"; return RINA_ERR_ARG; }
+        if (steps < 1 || gen_len + steps - 1 > max_seq) { err_ = tag + ": decode exceeds max_seq"; return RINA_ERR_RANGE; }
+        int rc;
+        if (use_graph && (!graph || graph_stream != s)) {
+            if (graph) { (void)hipGraphExecDestroy(graph); graph = nullptr; }
+            hipGraph_t g = nullptr;
+            if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return RINA_ERR_HIP;
+            int crc = decode_step(s);
+            hipError_t ce = hipStreamEndCapture(s, &g);
+            if (crc) { if (g) (void)hipGraphDestroy(g); return crc; }
+            if (ce != hipSuccess) return RINA_ERR_HIP;
+            hipError_t ie = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ie != hipSuccess) { graph = nullptr; return RINA_ERR_HIP; }
+            graph_stream = s;
+        }
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        (void)hipEventCreate(&e0);
+        (void)hipEventCreate(&e1);
+        (void)hipEventRecord(e0, s);
+        rc = RINA_OK;
+        for (int i = 0; i < steps && rc == RINA_OK; i++) {
+            if (use_graph) rc = hipGraphLaunch(graph, s) == hipSuccess ? RINA_OK : RINA_ERR_HIP;
+            else rc = decode_step(s);
+        }
+        (void)hipEventRecord(e1, s);
+        if (rc == RINA_OK && hipMemcpyAsync(out, d_ids + gen_len, sizeof(int) * steps, hipMemcpyDeviceToHost, s) != hipSuccess)
+            rc = RINA_ERR_HIP;
+        if (hipStreamSynchronize(s) != hipSuccess && rc == RINA_OK) rc = RINA_ERR_HIP;
+        float ms = 0.f;
+        if (rc == RINA_OK) {
+            gen_len += steps;
+            (void)hipEventElapsedTime(&ms, e0, e1);
+        }
+        if (decode_ms) *decode_ms = ms;
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        return rc;
+    }
+};

@@ -12,6 +12,7 @@
 #include <vector>
 #include "core/buffer.h"
 #include "core/layer.h"
+#include "infer/greedy.h"
 #include "infer/infer_base.h"
 #include "rina_hip.h"
 
@@ -19,30 +20,21 @@ int gqa_layer_hidden(const Layer& l);
 
 namespace {
 
-struct GQAInference : Inference {
+struct GQAInference : DeviceGreedyInference {
     std::vector<std::unique_ptr<Layer>> layers;
     BufferManager bufs;
     ModelConfig cfg;
     const WeightTensor* wte = nullptr;
     const WeightTensor* ln_f = nullptr;
     const WeightTensor* lm_head = nullptr;
-    int hd = 0, max_seq = 0, kvd = 0;
+    int hd = 0, kvd = 0;
     bool use_rms = false;
-    int* d_ids = nullptr;      // [max_seq + 1]
-    int* d_pos = nullptr;      // device position for graph decode
-    hipGraphExec_t graph = nullptr;
-    hipStream_t graph_stream = nullptr;
-
-    ~GQAInference() override {
-        if (graph) (void)hipGraphExecDestroy(graph);
-        if (d_ids) (void)hipFree(d_ids);
-        if (d_pos) (void)hipFree(d_pos);
-    }
 
     bool fail(const std::string& m) { err_ = m; return false; }
 
     bool init(ModelConfig& c, const TensorMap& w) override {
         cfg = c;
+        tag = "gqa";
         if (cfg.dim <= 0 || cfg.n_heads <= 0 || cfg.n_kv_heads <= 0 || cfg.head_dim <= 0 || cfg.vocab_size <= 0)
             return fail("gqa: incomplete config");
         layers = build_layers(cfg, w);
@@ -50,6 +42,7 @@ struct GQAInference : Inference {
         hd = gqa_layer_hidden(*layers[0]);
         for (auto& l : layers) hd = std::max(hd, gqa_layer_hidden(*l));
         max_seq = cfg.max_seq_len > 0 ? cfg.max_seq_len : 512;
+        vocab = cfg.vocab_size;
         kvd = cfg.n_kv_heads * cfg.head_dim;
         use_rms = cfg.name.find("llama") != std::string::npos;
         int cap = std::min(max_seq, 512);
@@ -68,8 +61,7 @@ struct GQAInference : Inference {
         bufs.fwd.kv_cache_quant.pre_rope = cfg.use_pre_rope_k;
         if (!bufs.alloc_attn_ws(rina_hip_gqa_attention_workspace(1, cfg.n_heads, cfg.head_dim, max_seq)))
             return fail("gqa: attention workspace allocation failed");
-        if (hipMalloc(&d_ids, sizeof(int) * (max_seq + 1)) != hipSuccess || hipMalloc(&d_pos, sizeof(int)) != hipSuccess)
-            return fail("gqa: id buffer allocation failed");
+        if (!alloc_ids()) return fail("gqa: id buffer allocation failed");
         wte = w.get("transformer.wte.weight");
         ln_f = w.get("transformer.ln_f.weight");
         lm_head = w.get("lm_head.weight");
@@ -77,7 +69,7 @@ struct GQAInference : Inference {
         return true;
     }
 
-    int ensure_cap(int n) {
+    int ensure_cap(int n) override {
         if (n <= bufs.fwd.cap) return RINA_OK;
         ForwardBuffers keep = bufs.fwd;   // caches survive the re-allocation
         bufs.fwd.kv_cache.data = nullptr;
@@ -90,16 +82,19 @@ struct GQAInference : Inference {
         bufs.fwd.mla_cache = keep.mla_cache;
         bufs.fwd.attn_ws = keep.attn_ws;
         bufs.fwd.attn_ws_bytes = keep.attn_ws_bytes;
+        bufs.fwd.kv_tap = keep.kv_tap;
         if (!bufs.alloc_fwd(n, cfg.dim, cfg.n_heads * cfg.head_dim, kvd, hd, cfg.vocab_size, 0)) return RINA_ERR_HIP;
         return RINA_OK;
     }
+
+    float* lm_buffer() override { return bufs.fwd.lm; }
 
     const WeightTensor* head() const {
         return (lm_head && lm_head->quant_type != QuantType::GGML_Q6_K) ? lm_head : wte;   // infer_gqa.cpp:97-100
     }
 
-    // embedding -> layers -> ln_f -> lm_head (rows [row0, T) of the chunk)
-    int run(const int* ids, const int* pos_dev, int T, int start_pos, float* logits, bool last_only, hipStream_t s) {
+    int run(const int* ids, const int* pos_dev, int T, int start_pos, float* logits, bool last_only,
+            hipStream_t s) override {
         int rc;
         ForwardBuffers& f = bufs.fwd;
         f.kv_cache.start_pos = start_pos;
@@ -125,71 +120,6 @@ struct GQAInference : Inference {
         int rc = ensure_cap(T);
         if (rc) return rc;
         return run(ids, nullptr, T, start_pos, logits, false, s);
-    }
-
-    int decode_step(hipStream_t s) {
-        int rc = run(d_ids, d_pos, 1, 0, bufs.fwd.lm, true, s);
-        if (rc) return rc;
-        return rina_hip_argmax(bufs.fwd.lm, cfg.vocab_size, nullptr, d_ids, d_pos, s);
-    }
-
-    int generate(const int* prompt, int n, int steps, int* out, bool use_graph, hipStream_t s, float* decode_ms) override {
-        if (n < 1 || steps < 1 || n + steps - 1 > max_seq) { err_ = "gqa: prompt + steps exceed max_seq"; return RINA_ERR_RANGE; }
-        int rc = ensure_cap(n);
-        if (rc) return rc;
-        if (hipMemcpyAsync(d_ids, prompt, sizeof(int) * n, hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
-        int p0 = n - 1;
-        if (hipMemcpyAsync(d_pos, &p0, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
-        if ((rc = run(d_ids, nullptr, n, 0, bufs.fwd.lm, true, s))) return rc;
-        if ((rc = rina_hip_argmax(bufs.fwd.lm, cfg.vocab_size, nullptr, d_ids, d_pos, s))) return rc;
-        if (hipStreamSynchronize(s) != hipSuccess) return RINA_ERR_HIP;
-        gen_len = n + 1;
-        if (hipMemcpyAsync(out, d_ids + n, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return RINA_ERR_HIP;
-        if (steps == 1) {
-            if (decode_ms) *decode_ms = 0.f;
-            return hipStreamSynchronize(s) == hipSuccess ? RINA_OK : RINA_ERR_HIP;
-        }
-        return decode_more(steps - 1, out + 1, use_graph, s, decode_ms);
-    }
-
-    int gen_len = 0;   // ids valid in d_ids after the last generate / decode_more
-
-    int decode_more(int steps, int* out, bool use_graph, hipStream_t s, float* decode_ms) override {
-        if (gen_len < 1) { err_ = "gqa: decode_more before generate"; return RINA_ERR_ARG; }
-        if (steps < 1 || gen_len + steps - 1 > max_seq) { err_ = "gqa: decode exceeds max_seq"; return RINA_ERR_RANGE; }
-        int rc;
-        hipEvent_t e0 = nullptr, e1 = nullptr;
-        (void)hipEventCreate(&e0);
-        (void)hipEventCreate(&e1);
-        if (use_graph && (!graph || graph_stream != s)) {
-            if (graph) { (void)hipGraphExecDestroy(graph); graph = nullptr; }
-            hipGraph_t g = nullptr;
-            if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return RINA_ERR_HIP;
-            int crc = decode_step(s);
-            hipError_t ce = hipStreamEndCapture(s, &g);
-            if (crc) { if (g) (void)hipGraphDestroy(g); return crc; }
-            if (ce != hipSuccess) return RINA_ERR_HIP;
-            hipError_t ie = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(g);
-            if (ie != hipSuccess) { graph = nullptr; return RINA_ERR_HIP; }
-            graph_stream = s;
-        }
-        (void)hipEventRecord(e0, s);
-        for (int i = 0; i < steps; i++) {
-            if (use_graph) { if (hipGraphLaunch(graph, s) != hipSuccess) return RINA_ERR_HIP; }
-            else if ((rc = decode_step(s))) return rc;
-        }
-        (void)hipEventRecord(e1, s);
-        if (hipMemcpyAsync(out, d_ids + gen_len, sizeof(int) * steps, hipMemcpyDeviceToHost, s) != hipSuccess)
-            return RINA_ERR_HIP;
-        if (hipStreamSynchronize(s) != hipSuccess) return RINA_ERR_HIP;
-        gen_len += steps;
-        float ms = 0.f;
-        (void)hipEventElapsedTime(&ms, e0, e1);
-        if (decode_ms) *decode_ms = ms;
-        (void)hipEventDestroy(e0);
-        (void)hipEventDestroy(e1);
-        return RINA_OK;
     }
 
     int set_kv_tap(float* tap) override {

@@ -4,6 +4,7 @@
 #include "infer/infer_base.h"
 
 Inference* create_gqa_inference();
+Inference* create_mla_inference();
 
 namespace {
 std::unordered_map<std::string, InferenceFactory>& factories() {
@@ -26,4 +27,5 @@ Inference* create_inference(const std::string& name) {
 
 void register_all_inferences() {
     register_inference("gqa", create_gqa_inference);
+    register_inference("mla", create_mla_inference);
 }

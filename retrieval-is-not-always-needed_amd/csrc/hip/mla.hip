@@ -1,0 +1,467 @@
+// DeepSeek MLA decode attention over a latent KV cache, and the MoE router
+// and expert FFN (arch/mla/deepseek_mla_layer.cu:171-350), for gfx950.
+//
+// Attention math (the reference's intended decode semantics, as the CPU
+// oracle restates it in expanded form): per head h,
+//   q = [q_nope_h | RoPE(q_rope_h)],  K_j = [W_kb_h c_j | RoPE(k_pe_j)],
+//   V_j = W_vb_h c_j,  c_j = RMSNorm(c_kv_j) * k_norm,  scale 1/sqrt(nope+rope).
+// This build caches the latent record [c_j | RoPE(k_pe_j)] (dc + rope floats
+// per position, 2304 B at the DeepSeek-V2-Lite shape, instead of 16 KB of
+// expanded K/V) and folds W_kb into the query and W_vb after the softmax:
+//   q_lat_h = W_kb_h^T q_nope_h,  s_j = (q_lat_h . c_j + q_rope_h . kpe_j) scale,
+//   o_h = W_vb_h (sum_j p_j c_j).
+// Three launches: prep (q_lat, rotated q_rope, latent append at pos0),
+// split (chunk partials over positions, one workgroup per chunk and head),
+// out (chunk merge and W_vb per head).
+//
+// MoE: device top-k (no host round trip), a gathered SiLU*up matvec over the
+// selected experts, and the down projection that accumulates the experts in
+// the reference's ascending order onto the shared-expert output and adds the
+// residual.
+#include "rina_common.hpp"
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16 consecutive values [e0, e0+16) of a weight stream in flat element
+// order (e0 % 16 == 0): Q2_K (ops/linear.cu:322-338 indexing), Q4_0 / Q4_0F
+// (half a block) or fp32.
+__device__ __forceinline__ void load_unit16(const uint8_t* w, int qt, int64_t e0, float (&v)[16]) {
+    if (qt == RINA_QT_GGML_Q2_K) {
+        const uint8_t* bp = w + (e0 >> 8) * 84;
+        const int inb = (int)(e0 & 255);
+        const int page = inb >> 7, g = (inb >> 5) & 3, h2 = (inb >> 4) & 1;
+        const uint32_t dd = gld((const uint32_t*)(bp + 80));
+        const uint32_t scb = gld(bp + 8 * page + 2 * g + h2);
+        const float dl = f16_to_f32(dd & 0xFFFF) * (float)(scb & 0xF);
+        const float ml = f16_to_f32(dd >> 16) * (float)(scb >> 4);
+        const uint32_t* qp = (const uint32_t*)(bp + 16 + 32 * page + 16 * h2);
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t q = gld(qp + d) >> (2 * g);
+#pragma unroll
+            for (int b = 0; b < 4; b++) v[4 * d + b] = fmaf(dl, (float)((q >> (8 * b)) & 3), -ml);
+        }
+    } else if (qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) {
+        const int bb = qt == RINA_QT_Q4_0 ? 18 : 20, so = qt == RINA_QT_Q4_0 ? 2 : 4;
+        const uint8_t* bp = w + (e0 >> 5) * bb;
+        const int half = (int)((e0 >> 4) & 1);
+        float sc;
+        if (qt == RINA_QT_Q4_0) sc = f16_to_f32(gld((const uint16_t*)bp));
+        else sc = __uint_as_float(gld((const uint32_t*)bp));
+        const uint8_t* np = bp + so + 8 * half;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t byte = gld(np + j);
+            v[2 * j] = (float)((int)(byte & 0xF) - 7) * sc;
+            v[2 * j + 1] = (float)((int)(byte >> 4) - 7) * sc;
+        }
+    } else {
+        const f32x4* p = (const f32x4*)((const float*)w + e0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f32x4 x = gld(p + i);
+            v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+        }
+    }
+}
+
+// dot of row `row` of an [N, K] weight (flat element order) with x (LDS),
+// lanes over 16-value units; result in every lane
+__device__ __forceinline__ float row_dot(const uint8_t* w, int qt, int64_t row, int K, const float* x, int lane) {
+    float acc = 0.f;
+    for (int u = lane; u < K / 16; u += 64) {
+        float v[16];
+        load_unit16(w, qt, row * K + 16 * u, v);
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = fmaf(v[i], x[16 * u + i], acc);
+    }
+    return wave_sum(acc);
+}
+
+struct MlaArgs {
+    const float* q;        // [H*(nope+rope)]: [H*nope | H*rope]
+    const float* kva;      // [dc+rope]: [c_kv | k_pe], raw
+    const float* k_norm;   // [dc]
+    float eps;
+    const float* rc;       // RoPE tables [max_seq][rope/2] (NULL: none)
+    const float* rs;
+    const uint8_t* wkvb;   // [H*(nope+v), dc]
+    int qt;
+    float* cache;          // [max_seq][dc+rope] latent records
+    float* out;            // [H*v]
+    float* ws_q;           // [H][dc+rope]: q_lat | rotated q_rope
+    float* ws_m;           // [nchunk][H]
+    float* ws_l;
+    float* ws_o;           // [nchunk][H][dc]
+    int H, nope, rope, v, dc, start_pos, max_seq, chunk;
+    const int* d_pos;
+    float scale;
+};
+
+constexpr int kMlaChunk = 32;          // positions per split workgroup (8 per wave)
+constexpr int kMaxRecLanes = 10;       // record floats per lane: dc + rope <= 640
+constexpr int kMaxOutLanes = 8;        // latent dims per lane: dc <= 512
+
+// NeoX rotation of pair (i, i+rope/2) at table row pos, reference fma form
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& o0, float& o1) {
+    o0 = fmaf(x0, c, -(x1 * s));
+    o1 = fmaf(x0, s, x1 * c);
+}
+
+// grid H + 1: workgroup h < H builds q_lat_h and the rotated q_rope_h;
+// workgroup H appends the latent record of position pos0.
+__global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
+    __shared__ float s_q[512];
+    __shared__ float s_part[4096];
+    __shared__ float s_red[4];
+    const int tid = threadIdx.x;
+    const int pos = read_pos(a.start_pos, a.d_pos);
+    if (pos < 0 || pos >= a.max_seq) return;
+    const int R = a.dc + a.rope, hr = a.rope / 2;
+    if (blockIdx.x == (unsigned)a.H) {
+        float ss = 0.f;
+        for (int k = tid; k < a.dc; k += 256) {
+            const float x = gld(a.kva + k);
+            ss = fmaf(x, x, ss);
+        }
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+        __syncthreads();
+        const float inv = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)a.dc + a.eps);
+        float* rec = a.cache + (int64_t)pos * R;
+        for (int k = tid; k < a.dc; k += 256) gst(rec + k, gld(a.kva + k) * inv * gld(a.k_norm + k));
+        for (int j = tid; j < hr; j += 256) {
+            float x0 = gld(a.kva + a.dc + j), x1 = gld(a.kva + a.dc + j + hr);
+            if (a.rc) rope_pair(x0, x1, gld(a.rc + (int64_t)pos * hr + j), gld(a.rs + (int64_t)pos * hr + j), x0, x1);
+            gst(rec + a.dc + j, x0);
+            gst(rec + a.dc + j + hr, x1);
+        }
+        return;
+    }
+    const int h = blockIdx.x;
+    float* qo = a.ws_q + (int64_t)h * R;
+    for (int i = tid; i < a.nope; i += 256) s_q[i] = gld(a.q + (int64_t)h * a.nope + i);
+    for (int j = tid; j < hr; j += 256) {
+        const float* qr = a.q + (int64_t)a.H * a.nope + (int64_t)h * a.rope;
+        float x0 = gld(qr + j), x1 = gld(qr + j + hr);
+        if (a.rc) rope_pair(x0, x1, gld(a.rc + (int64_t)pos * hr + j), gld(a.rs + (int64_t)pos * hr + j), x0, x1);
+        gst(qo + a.dc + j, x0);
+        gst(qo + a.dc + j + hr, x1);
+    }
+    __syncthreads();
+    // q_lat[k] = sum_i q_nope[i] W[h*nope + i][k]: thread = (row slice, 16-column unit)
+    const int ncu = a.dc / 16;
+    const int RS = 256 / ncu;
+    const int cu = tid % ncu, rsl = tid / ncu;
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) acc[j] = 0.f;
+    for (int i = rsl; i < a.nope; i += RS) {
+        float w[16];
+        load_unit16(a.wkvb, a.qt, ((int64_t)h * a.nope + i) * a.dc + 16 * cu, w);
+        const float qi = s_q[i];
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[j] = fmaf(qi, w[j], acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++) s_part[rsl * a.dc + 16 * cu + j] = acc[j];
+    __syncthreads();
+    for (int k = tid; k < a.dc; k += 256) {
+        float t = 0.f;
+        for (int r = 0; r < RS; r++) t += s_part[r * a.dc + k];
+        gst(qo + k, t);
+    }
+}
+
+// grid (nchunk, H): each wave takes 8 positions of the chunk (loads issued
+// together), lanes cover the record's dims; online softmax per wave, waves
+// merged in LDS, chunk partials (m, l, sum p c) written.
+__global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
+    __shared__ float s_o[4][512];
+    __shared__ float s_m[4], s_l[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos0 = read_pos(a.start_pos, a.d_pos);
+    if (pos0 < 0 || pos0 >= a.max_seq) return;
+    const int L = pos0 + 1, c = blockIdx.x, h = blockIdx.y;
+    const int j0 = c * kMlaChunk;
+    if (j0 >= L) return;
+    const int ncv = min(kMlaChunk, L - j0);
+    const int R = a.dc + a.rope;
+    const float* qh = a.ws_q + (int64_t)h * R;
+    float qv[kMaxRecLanes];
+#pragma unroll
+    for (int j = 0; j < kMaxRecLanes; j++) qv[j] = (lane + 64 * j < R) ? gld(qh + lane + 64 * j) : 0.f;
+    // this wave's positions: j0 + wave + 4 i (past the chunk end: the chunk's
+    // first position, masked below)
+    constexpr int PW = kMlaChunk / 4;
+    float kv[PW][kMaxRecLanes];
+#pragma unroll
+    for (int i = 0; i < PW; i++) {
+        const int p = wave + 4 * i;
+        const float* rec = a.cache + (int64_t)(j0 + (p < ncv ? p : 0)) * R;
+#pragma unroll
+        for (int j = 0; j < kMaxRecLanes; j++) kv[i][j] = (lane + 64 * j < R) ? gld(rec + lane + 64 * j) : 0.f;
+    }
+    float m = -INFINITY, l = 0.f, o[kMaxOutLanes];
+#pragma unroll
+    for (int j = 0; j < kMaxOutLanes; j++) o[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < PW; i++) {
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxRecLanes; j++) dot = fmaf(qv[j], kv[i][j], dot);
+        const float s = wave_sum(dot) * a.scale;
+        if (wave + 4 * i < ncv) {
+            const float mn = fmaxf(m, s);
+            const float al = expf(m - mn), pe = expf(s - mn);
+            l = fmaf(l, al, pe);
+#pragma unroll
+            for (int j = 0; j < kMaxOutLanes; j++) o[j] = fmaf(o[j], al, pe * kv[i][j]);
+            m = mn;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxOutLanes; j++)
+        if (lane + 64 * j < a.dc) s_o[wave][lane + 64 * j] = o[j];
+    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w]);
+    float aw[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) aw[w] = s_m[w] == -INFINITY ? 0.f : expf(s_m[w] - M);
+    float* wo = a.ws_o + ((int64_t)c * a.H + h) * a.dc;
+    for (int k = tid; k < a.dc; k += 256)
+        gst(wo + k, ((s_o[0][k] * aw[0] + s_o[1][k] * aw[1]) + (s_o[2][k] * aw[2] + s_o[3][k] * aw[3])));
+    if (tid == 0) {
+        gst(a.ws_m + (int64_t)c * a.H + h, M);
+        gst(a.ws_l + (int64_t)c * a.H + h, (s_l[0] * aw[0] + s_l[1] * aw[1]) + (s_l[2] * aw[2] + s_l[3] * aw[3]));
+    }
+}
+
+// grid H: merge the chunks of head h into o_lat, then out_h = W_vb_h o_lat
+__global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
+    __shared__ float s_w[256];
+    __shared__ float s_lat[512];
+    __shared__ float s_red[8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos0 = read_pos(a.start_pos, a.d_pos);
+    if (pos0 < 0 || pos0 >= a.max_seq) return;
+    const int nch = pos0 / kMlaChunk + 1;
+    const int h = blockIdx.x;
+    const float mc = tid < nch ? gld(a.ws_m + (int64_t)tid * a.H + h) : -INFINITY;
+    const float lc = tid < nch ? gld(a.ws_l + (int64_t)tid * a.H + h) : 0.f;
+    const float mw = wave_max(mc);
+    if (lane == 0) s_red[wave] = mw;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float w = tid < nch ? expf(mc - M) : 0.f;
+    s_w[tid] = w;
+    const float lw = wave_sum(w * lc);
+    __syncthreads();
+    if (lane == 0) s_red[4 + wave] = lw;
+    __syncthreads();
+    const float inv_l = 1.0f / ((s_red[4] + s_red[5]) + (s_red[6] + s_red[7]));
+    for (int k = tid; k < a.dc; k += 256) {
+        float acc = 0.f;
+        for (int cc = 0; cc < nch; cc++) acc = fmaf(gld(a.ws_o + ((int64_t)cc * a.H + h) * a.dc + k), s_w[cc], acc);
+        s_lat[k] = acc * inv_l;
+    }
+    __syncthreads();
+    const int64_t row0 = (int64_t)a.H * a.nope + (int64_t)h * a.v;
+    for (int i = wave; i < a.v; i += 4) {
+        const float r = row_dot(a.wkvb, a.qt, row0 + i, a.dc, s_lat, lane);
+        if (lane == 0) gst(a.out + (int64_t)h * a.v + i, r);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MoE
+// ---------------------------------------------------------------------------
+
+// deepseek_mla_layer.cu:310-326: softmax over E logits, insertion top-k
+// kept ascending with strict ">" (the earlier expert wins ties).
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float* lg, int E, int k, int* ids, float* probs) {
+    __shared__ float s_e[256];
+    __shared__ float s_mx;
+    const int tid = threadIdx.x;
+    const float x = tid < E ? gld(lg + tid) : -INFINITY;
+    if (tid == 0) {
+        float mx = gld(lg);
+        for (int e = 1; e < E; e++) mx = fmaxf(mx, gld(lg + e));   // max_element: value only
+        s_mx = mx;
+    }
+    __syncthreads();
+    if (tid < E) s_e[tid] = expf(x - s_mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.f;
+        for (int e = 0; e < E; e++) sum += s_e[e];
+        const float inv = 1.0f / sum;
+        int tk[16];
+        float tw[16];
+        for (int j = 0; j < k; j++) { tk[j] = -1; tw[j] = -1e10f; }
+        for (int e = 0; e < E; e++) {
+            const float p = s_e[e] * inv;
+            if (p > tw[0]) {
+                tw[0] = p; tk[0] = e;
+                for (int j = 0; j < k - 1 && tw[j] > tw[j + 1]; j++) {
+                    const float t = tw[j]; tw[j] = tw[j + 1]; tw[j + 1] = t;
+                    const int ti = tk[j]; tk[j] = tk[j + 1]; tk[j + 1] = ti;
+                }
+            }
+        }
+        for (int j = 0; j < k; j++) { gst(ids + j, tk[j]); gst(probs + j, tw[j]); }
+    }
+}
+
+struct MoeArgs {
+    const float* x;        // [d] (post-norm activation)
+    const uint8_t* wg;     // gate experts [E] x [ffn, d]
+    const uint8_t* wu;     // up experts
+    const uint8_t* wd;     // down experts [E] x [d, ffn]
+    int qt;
+    int64_t stride_gu, stride_dn;
+    const int* ids;        // [k] ascending by probability, -1 = none
+    const float* probs;    // [k]
+    int k, d, ffn, E;
+    float* G;              // [k][ffn] SiLU(gate) * up
+    const float* shared;   // [d] shared-expert output
+    float* h;              // [d] residual stream: h += shared + sum_k p_k y_k
+};
+
+// one wave per (slot, row) of the selected experts' gate/up
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
+    extern __shared__ float s_x[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < a.d; i += 256) s_x[i] = gld(a.x + i);
+    __syncthreads();
+    const int rows = a.k * a.ffn;
+    for (int r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {
+        const int slot = r / a.ffn, i = r % a.ffn;
+        const int e = gld(a.ids + slot);
+        float v = 0.f;
+        if (e >= 0 && e < a.E) {
+            const float g = row_dot(a.wg + (int64_t)e * a.stride_gu, a.qt, i, a.d, s_x, lane);
+            const float u = row_dot(a.wu + (int64_t)e * a.stride_gu, a.qt, i, a.d, s_x, lane);
+            v = (g / (1.0f + expf(-g))) * u;
+        }
+        if (lane == 0) gst(a.G + r, v);
+    }
+}
+
+// one wave per output row i: acc = shared[i]; acc += p_j y_j (ascending j); h[i] += acc
+__global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
+    extern __shared__ float s_g[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < a.k * a.ffn; i += 256) s_g[i] = gld(a.G + i);
+    __syncthreads();
+    for (int i = blockIdx.x * 4 + wave; i < a.d; i += gridDim.x * 4) {
+        float acc = gld(a.shared + i);
+        for (int j = 0; j < a.k; j++) {
+            const int e = gld(a.ids + j);
+            if (e < 0 || e >= a.E) continue;
+            const float y = row_dot(a.wd + (int64_t)e * a.stride_dn, a.qt, i, a.ffn, s_g + j * a.ffn, lane);
+            acc = fmaf(gld(a.probs + j), y, acc);
+        }
+        if (lane == 0) gst(a.h + i, gld(a.h + i) + acc);
+    }
+}
+
+bool unit_qt(int qt) {
+    return qt == RINA_QT_GGML_Q2_K || qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F || qt == RINA_QT_FP32;
+}
+
+int mla_nchunk(int max_pos) { return (max_pos + kMlaChunk - 1) / kMlaChunk; }
+
+}  // namespace
+
+extern "C" size_t rina_hip_mla_attention_workspace(int H, int dc, int rope, int max_pos) {
+    if (H < 1 || dc < 1 || max_pos < 1) return 0;
+    const size_t nch = (size_t)mla_nchunk(max_pos);
+    return ((size_t)H * (dc + rope) + nch * H * (2 + (size_t)dc)) * sizeof(float);
+}
+
+extern "C" size_t rina_hip_mla_cache_bytes(int dc, int rope, int max_seq) {
+    return (size_t)max_seq * (dc + rope) * sizeof(float);
+}
+
+extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, const float* k_norm, float eps,
+                                             const float* rope_cos, const float* rope_sin, const void* w_kv_b,
+                                             int qt_kv_b, float* cache, int H, int nope, int rope, int v_dim, int dc,
+                                             int start_pos, const int* d_pos, int max_seq, float* out,
+                                             void* workspace, size_t ws_bytes, void* stream) {
+    if (!q || !kva || !k_norm || !w_kv_b || !cache || !out || H < 1 || nope < 1 || v_dim < 1 || max_seq < 1)
+        return RINA_ERR_ARG;
+    if (!unit_qt(qt_kv_b)) return RINA_ERR_QTYPE;
+    if ((!rope_cos) != (!rope_sin)) return RINA_ERR_ARG;
+    if (dc % 64 || dc > 512 || rope % 2 || rope < 0 || dc + rope > 64 * kMaxRecLanes || nope > 512 ||
+        mla_nchunk(max_seq) > 256 || (256 % (dc / 16)))
+        return RINA_ERR_SHAPE;
+    if (!d_pos && (start_pos < 0 || start_pos >= max_seq)) return RINA_ERR_RANGE;
+    if (((uintptr_t)w_kv_b | (uintptr_t)q | (uintptr_t)cache) % 16 || (uintptr_t)w_kv_b % 4) return RINA_ERR_SHAPE;
+    const int max_pos = d_pos ? max_seq : start_pos + 1;
+    const size_t need = rina_hip_mla_attention_workspace(H, dc, rope, max_pos);
+    if (!workspace || ws_bytes < need) return RINA_ERR_WORKSPACE;
+    MlaArgs a{};
+    a.q = q; a.kva = kva; a.k_norm = k_norm; a.eps = eps; a.rc = rope_cos; a.rs = rope_sin;
+    a.wkvb = (const uint8_t*)w_kv_b; a.qt = qt_kv_b; a.cache = cache; a.out = out;
+    a.H = H; a.nope = nope; a.rope = rope; a.v = v_dim; a.dc = dc;
+    a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos; a.chunk = kMlaChunk;
+    a.scale = 1.0f / sqrtf((float)(nope + rope));
+    const int nch = mla_nchunk(max_pos);
+    a.ws_q = (float*)workspace;
+    a.ws_m = a.ws_q + (size_t)H * (dc + rope);
+    a.ws_l = a.ws_m + (size_t)nch * H;
+    a.ws_o = a.ws_l + (size_t)nch * H;
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(mla_prep_kernel, dim3(H + 1), dim3(256), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(mla_split_kernel, dim3(nch, H), dim3(256), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(mla_out_kernel, dim3(H), dim3(256), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_moe_topk(const float* logits, int n_experts, int k, int* ids, float* probs, void* stream) {
+    if (!logits || !ids || !probs || n_experts < 1 || n_experts > 256 || k < 1 || k > 16 || k > n_experts)
+        return RINA_ERR_ARG;
+    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(256), 0, as_stream(stream), logits, n_experts, k, ids, probs);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" size_t rina_hip_moe_workspace(int k, int ffn) { return (size_t)k * ffn * sizeof(float); }
+
+extern "C" int rina_hip_moe_ffn(const float* x, const void* gate_exps, const void* up_exps, const void* down_exps,
+                                int qt, int64_t stride_gu, int64_t stride_dn, int n_experts, const int* ids,
+                                const float* probs, int k, int d, int ffn, const float* shared_out, float* h,
+                                void* workspace, size_t ws_bytes, void* stream) {
+    if (!x || !gate_exps || !up_exps || !down_exps || !ids || !probs || !shared_out || !h || k < 1 || d < 1 ||
+        ffn < 1 || n_experts < 1)
+        return RINA_ERR_ARG;
+    if (!unit_qt(qt)) return RINA_ERR_QTYPE;
+    if (d % 16 || ffn % 16 || (size_t)k * ffn * 4 > 64 * 1024 || (size_t)d * 4 > 64 * 1024) return RINA_ERR_SHAPE;
+    if (!workspace || ws_bytes < rina_hip_moe_workspace(k, ffn)) return RINA_ERR_WORKSPACE;
+    if (((uintptr_t)gate_exps | (uintptr_t)up_exps | (uintptr_t)down_exps) % 4 || stride_gu % 4 || stride_dn % 4)
+        return RINA_ERR_SHAPE;
+    MoeArgs a{};
+    a.x = x; a.wg = (const uint8_t*)gate_exps; a.wu = (const uint8_t*)up_exps; a.wd = (const uint8_t*)down_exps;
+    a.qt = qt; a.stride_gu = stride_gu; a.stride_dn = stride_dn; a.ids = ids; a.probs = probs;
+    a.k = k; a.d = d; a.ffn = ffn; a.E = n_experts; a.G = (float*)workspace; a.shared = shared_out; a.h = h;
+    hipStream_t st = as_stream(stream);
+    const int cus = rina_num_cus();
+    int g1 = (k * ffn + 3) / 4;
+    if (g1 > cus * 4) g1 = cus * 4;
+    hipLaunchKernelGGL(moe_gate_up_kernel, dim3(g1), dim3(256), (size_t)d * 4, st, a);
+    RINA_LAUNCH_CHECK();
+    int g2 = (d + 3) / 4;
+    if (g2 > cus * 4) g2 = cus * 4;
+    hipLaunchKernelGGL(moe_down_kernel, dim3(g2), dim3(256), (size_t)k * ffn * 4, st, a);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}

@@ -166,3 +166,39 @@ class SynthLlama:
             self._eng.rina_model_destroy(self.model)
             self.model = None
         self.arena.keep.clear()
+
+
+class HostModel:
+    """An engine model uploaded from host tensors: header is the config
+    dict (JSON keys of the engine's ModelConfig), tensors maps reference
+    names to (quant_type, shape, ndarray of packed bytes or fp32)."""
+
+    def __init__(self, header, tensors):
+        torch = _torch()
+        self.header = dict(header)
+        self.arena = DeviceArena()
+        self.dev = {}
+        eng = load_engine()
+        self._eng = eng
+        self.model = eng.rina_model_create(json.dumps(self.header).encode())
+        if not self.model:
+            raise RuntimeError(eng.rina_engine_last_error().decode())
+        for name, (qt, shape, arr) in tensors.items():
+            t = torch.from_numpy(np.ascontiguousarray(arr)).cuda()
+            shp = (C.c_int64 * len(shape))(*shape)
+            check(eng.rina_model_add_tensor(self.model, name.encode(), qt, len(shape), shp, t.data_ptr()),
+                  "add_tensor " + name)
+            self.arena.put(t)
+            self.dev[name] = t
+
+    def infer(self, arch, kv_mode=None, max_seq=0):
+        h = self._eng.rina_infer_create(self.model, arch.encode(), kv_mode.encode() if kv_mode else None, max_seq)
+        if not h:
+            raise RuntimeError(self._eng.rina_engine_last_error().decode())
+        return h
+
+    def close(self):
+        if self.model:
+            self._eng.rina_model_destroy(self.model)
+            self.model = None
+        self.arena.keep.clear()

@@ -74,3 +74,7 @@ def d2h(ptr, nbytes):
 
 def rng(seed):
     return np.random.default_rng(seed)
+
+
+def ok(rc, what=""):
+    assert rc == 0, "%s returned %d" % (what, rc)

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import _numpy_ref as nr
-from _util import REL_TOL, assert_close, dev, empty, host, rng, stream
+from _util import REL_TOL, assert_close, dev, empty, host, ok, rng, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -19,10 +19,6 @@ Q4_SHAPES = [(4, 160, 640), (2, 2048, 2048), (1, 640, 640), (8, 64, 4096),      
              # direct-load matvec: 2 waves per row with several row groups per
              # workgroup, and a ragged 4-row-group shape that loops
              (1, 12289, 4096), (1, 70001, 2048)]
-
-
-def ok(rc, what=""):
-    assert rc == 0, "%s returned %d" % (what, rc)
 
 
 def q2k_blocks(seed, n):

@@ -1,0 +1,239 @@
+"""DeepSeek MLA + MoE on the GPU: the latent decode attention and the MoE
+kernels against float64 restatements of the intended math, the router
+top-k against the oracle, and the engine's "mla" Inference (logits and
+greedy tokens) against the CPU oracle model."""
+import ctypes as C
+import importlib
+
+import numpy as np
+import pytest
+
+import _mla_tiny as mt
+import _numpy_ref as nr
+from _util import assert_close, dev, empty, host, ok, rng, stream
+
+pytestmark = pytest.mark.gpu
+
+Q2K, Q4F, FP32 = 10, 7, 6
+
+
+def rope_tables(rope, n, theta=10000.0):
+    ang = np.outer(np.arange(n), 1.0 / theta ** (np.arange(0, rope, 2) / rope)).astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def weight(orc, qt, rows, cols, r):
+    """packed weight + its float64 matrix (numpy restatement dequant)"""
+    if qt == Q2K:
+        w = mt.q2k_random(r, rows * cols)
+        return w, nr.dequant_q2k_blocks(w)[: rows * cols].reshape(rows, cols).astype(np.float64)
+    wf = (r.standard_normal(rows * cols) * 0.05).astype(np.float32)
+    if qt == FP32:
+        return wf, wf.reshape(rows, cols).astype(np.float64)
+    w = orc.pack(qt, wf)
+    return w, nr.dequant_q4(w, rows * cols, qt == Q4F).reshape(rows, cols).astype(np.float64)
+
+
+@pytest.mark.parametrize("shape", ["tiny", "dsv2lite"])
+@pytest.mark.parametrize("qt", [Q2K, Q4F])
+@pytest.mark.parametrize("P,use_dpos", [(0, False), (5, False), (40, True), (100, False)])
+def test_mla_decode_attention(rina, orc, shape, qt, P, use_dpos):
+    hip = rina.load_hip()
+    L = orc.load()
+    H, nope, rope, vd, dc = (4, 32, 16, 32, 64) if shape == "tiny" else (16, 128, 64, 128, 512)
+    R = dc + rope
+    max_seq = P + 7
+    r = rng(P * 3 + H + qt)
+    wkvb, W = weight(orc, qt, H * (nope + vd), dc, r)
+    q = r.standard_normal(H * (nope + rope)).astype(np.float32)
+    kva = r.standard_normal(R).astype(np.float32)
+    knorm = r.uniform(0.8, 1.2, dc).astype(np.float32)
+    cos, sin = rope_tables(rope, max_seq)
+    cache = r.standard_normal((max_seq, R)).astype(np.float32)     # records of earlier positions
+    # expected record at P: RMSNorm(c)*k_norm (oracle fp32 rule), RoPE(k_pe) (oracle, bit-exact)
+    rec = np.zeros(R, np.float32)
+    c = kva[:dc].copy()
+    L.orc_rms_norm(c.ctypes.data, knorm.ctypes.data, 1, dc, np.float32(1e-5))
+    kpe = kva[dc:].copy()
+    L.orc_rope_neox(kpe.ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, 1, rope, P)
+    rec[:dc], rec[dc:] = c, kpe
+    # float64 reference over the expanded form
+    qr = q.copy()
+    L.orc_rope_neox(qr[H * nope:].ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, H, rope, P)
+    allc = cache.astype(np.float64).copy()
+    allc[P] = rec
+    ref = np.zeros(H * vd)
+    for hh in range(H):
+        Kn = allc[: P + 1, :dc] @ W[hh * nope:(hh + 1) * nope].T            # [P+1, nope]
+        K = np.concatenate([Kn, allc[: P + 1, dc:]], axis=1)
+        V = allc[: P + 1, :dc] @ W[H * nope + hh * vd: H * nope + (hh + 1) * vd].T
+        qh = np.concatenate([qr[hh * nope:(hh + 1) * nope], qr[H * nope + hh * rope: H * nope + (hh + 1) * rope]])
+        ref[hh * vd:(hh + 1) * vd] = nr.softmax_attn(qh.astype(np.float64), K, V, 1 / np.sqrt(nope + rope))
+    ws_bytes = hip.rina_hip_mla_attention_workspace(H, dc, rope, max_seq)
+    ws = empty(ws_bytes, "uint8")
+    cd = dev(cache)
+    od = empty(H * vd)
+    pos = dev(np.array([P], np.int32)) if use_dpos else None
+    ok(hip.rina_hip_mla_decode_attention(dev(q).data_ptr(), dev(kva).data_ptr(), dev(knorm).data_ptr(),
+                                         np.float32(1e-5), dev(cos).data_ptr(), dev(sin).data_ptr(),
+                                         dev(wkvb).data_ptr(), qt, cd.data_ptr(), H, nope, rope, vd, dc,
+                                         0 if use_dpos else P, pos.data_ptr() if use_dpos else None, max_seq,
+                                         od.data_ptr(), ws.data_ptr(), ws_bytes, stream()), "mla attention")
+    assert_close(host(od), ref, what="mla %s qt %d P %d" % (shape, qt, P))
+    gc = host(cd).reshape(max_seq, R)
+    assert np.array_equal(gc[P, dc:].view(np.uint32), kpe.view(np.uint32))     # RoPE: same fma form
+    assert np.max(np.abs(gc[P, :dc] - c)) <= 1e-6 * np.max(np.abs(c))          # norm: sum order differs
+    others = np.ones(max_seq, bool)
+    others[P] = False
+    assert np.array_equal(gc[others], cache[others])
+
+
+def test_moe_topk_matches_oracle(rina, orc):
+    hip = rina.load_hip()
+    r = rng(77)
+    checked = 0
+    for trial in range(40):
+        E, k = (64, 6) if trial % 2 == 0 else (8, 3)
+        lg = (r.standard_normal(E) * 1.5).astype(np.float32)
+        p = np.sort(np.exp(lg - lg.max()) / np.exp(lg - lg.max()).sum())[::-1]
+        if p[k - 1] - p[k] < 1e-5:
+            continue
+        ids_o, pr_o = orc.moe_topk(lg, k)
+        ids, pr = empty(k, "int32"), empty(k)
+        ok(hip.rina_hip_moe_topk(dev(lg).data_ptr(), E, k, ids.data_ptr(), pr.data_ptr(), stream()), "topk")
+        assert host(ids).tolist() == ids_o.tolist()
+        assert np.allclose(host(pr), pr_o, rtol=2e-6, atol=0)
+        checked += 1
+    assert checked >= 30
+
+
+def packed_only(orc, qt, rows, cols, r):
+    if qt == Q2K:
+        return mt.q2k_random(r, rows * cols)
+    return orc.pack(qt, (r.standard_normal(rows * cols) * 0.05).astype(np.float32))
+
+
+def as_f64(qt, w, rows, cols):
+    if qt == Q2K:
+        return nr.dequant_q2k_blocks(w)[: rows * cols].reshape(rows, cols).astype(np.float64)
+    return nr.dequant_q4(w, rows * cols, qt == Q4F).reshape(rows, cols).astype(np.float64)
+
+
+@pytest.mark.parametrize("d,F,E,k,qt", [(256, 48, 8, 3, Q2K), (2048, 1408, 64, 6, Q2K), (512, 96, 4, 2, Q4F)])
+def test_moe_ffn_vs_float64(rina, orc, d, F, E, k, qt):
+    hip = rina.load_hip()
+    r = rng(d + F + k)
+    parts = {nm: [packed_only(orc, qt, *shp, r) for _ in range(E)] for nm, shp in
+             (("g", (F, d)), ("u", (F, d)), ("dn", (d, F)))}
+    gate, up, down = (np.concatenate(parts[nm]) for nm in ("g", "u", "dn"))
+    sgu, sdn = gate.nbytes // E, down.nbytes // E
+    x = r.standard_normal(d).astype(np.float32)
+    ids = np.sort(r.choice(E, k, replace=False)).astype(np.int32)
+    ids[0] = -1 if k > 2 else ids[0]                                    # a skipped slot
+    probs = np.sort(r.uniform(0.05, 0.3, k)).astype(np.float32)
+    shared = r.standard_normal(d).astype(np.float32)
+    h0 = r.standard_normal(d).astype(np.float32)
+    acc = shared.astype(np.float64).copy()
+    for j in range(k):
+        e = ids[j]
+        if e < 0:
+            continue
+        g = as_f64(qt, parts["g"][e], F, d) @ x
+        u = as_f64(qt, parts["u"][e], F, d) @ x
+        acc += probs[j] * (as_f64(qt, parts["dn"][e], d, F) @ (g / (1 + np.exp(-g)) * u))
+    ref = h0 + acc
+    hd = dev(h0)
+    wsb = hip.rina_hip_moe_workspace(k, F)
+    ws = empty(wsb, "uint8")
+    ok(hip.rina_hip_moe_ffn(dev(x).data_ptr(), dev(gate).data_ptr(), dev(up).data_ptr(), dev(down).data_ptr(), qt,
+                            sgu, sdn, E, dev(ids).data_ptr(), dev(probs).data_ptr(), k, d, F, dev(shared).data_ptr(),
+                            hd.data_ptr(), ws.data_ptr(), wsb, stream()), "moe ffn")
+    assert_close(host(hd), ref, what="moe d %d F %d" % (d, F))
+
+
+# ---- engine ---------------------------------------------------------------
+
+def header(max_seq):
+    c = mt.CFG
+    return {"name": c["name"], "dim": c["dim"], "n_layers": c["n_layers"], "n_heads": c["n_heads"],
+            "n_kv_heads": c["n_heads"], "head_dim": c["nope"], "qk_nope_head_dim": c["nope"],
+            "qk_rope_head_dim": c["rope"], "v_head_dim": c["v_dim"], "kv_lora_rank": c["dc"],
+            "vocab_size": c["vocab_size"], "max_seq_len": max_seq, "n_routed_experts": c["n_experts"],
+            "num_experts_per_tok": c["top_k"], "moe_intermediate_size": c["expert_ffn"],
+            "layers": [{"type": "deepseek_mla_dense"}] + [{"type": "deepseek_mla_moe"}] * (c["n_layers"] - 1)}
+
+
+def shape_of(name, arr, qt):
+    c = mt.CFG
+    if qt == FP32:
+        return arr.shape if arr.ndim > 1 else (arr.size,)
+    rows = {"w_q": c["n_heads"] * (c["nope"] + c["rope"]), "w_kv_a": c["dc"] + c["rope"],
+            "w_kv_b": c["n_heads"] * (c["nope"] + c["v_dim"]), "w_o": c["dim"], "w1": c["dense_ffn"],
+            "w3": c["dense_ffn"], "w2": c["dim"], "gate_exps": c["expert_ffn"], "up_exps": c["expert_ffn"],
+            "down_exps": c["dim"], "gate_shexp": c["shared_ffn"], "up_shexp": c["shared_ffn"],
+            "down_shexp": c["dim"], "wte": c["vocab_size"], "lm_head": c["vocab_size"]}
+    key = name.split(".")[-2]
+    n = rows[key]
+    if key.endswith("exps"):
+        return (c["n_experts"], n, -1)
+    return (n, -1)
+
+
+@pytest.fixture(scope="module")
+def tiny_mla(rina):
+    synth = importlib.import_module("rina_amd.synth")
+    max_seq = 48
+    tensors, qts, mats = mt.build(seed=11, max_pos=max_seq)
+    up = {}
+    for nm, arr in tensors.items():
+        shp = list(shape_of(nm, arr, qts[nm]))
+        if shp[-1] == -1:       # cols of a packed matrix
+            c = mt.CFG
+            cols = {"w_kv_b": c["dc"], "w_o": c["n_heads"] * c["v_dim"], "w2": c["dense_ffn"],
+                    "down_exps": c["expert_ffn"], "down_shexp": c["shared_ffn"]}.get(nm.split(".")[-2], c["dim"])
+            shp[-1] = cols
+        up[nm] = (qts[nm], tuple(shp), arr)
+    hm = synth.HostModel(header(max_seq), up)
+    yield hm, tensors, qts, max_seq
+    hm.close()
+
+
+def test_mla_engine_forward_logits(rina, orc, tiny_mla):
+    import torch
+    hm, tensors, qts, max_seq = tiny_mla
+    eng = rina.load_engine()
+    inf = hm.infer("mla", max_seq=max_seq)
+    V = mt.CFG["vocab_size"]
+    ids = np.array([5, 17, 3, 90, 42, 7], np.int32)
+    lg = empty(len(ids) * V)
+    rina.check(eng.rina_infer_forward(inf, torch.from_numpy(ids).cuda().data_ptr(), lg.data_ptr(), 1, len(ids), 0,
+                                      stream()), "forward")
+    m, hold = orc.mla_from_tensors(mt.CFG, tensors, qts, max_seq)
+    ref = np.zeros((len(ids), V), np.float32)
+    assert orc.load().orc_mla_forward(m, ids.ctypes.data, len(ids), 0, ref.ctypes.data, 0) == 0
+    assert_close(host(lg).reshape(len(ids), V), ref, what="mla prefill logits")
+    nxt = np.array([11], np.int32)
+    rina.check(eng.rina_infer_forward(inf, torch.from_numpy(nxt).cuda().data_ptr(), lg.data_ptr(), 1, 1, 6,
+                                      stream()), "decode")
+    ref1 = np.zeros(V, np.float32)
+    orc.load().orc_mla_forward(m, nxt.ctypes.data, 1, 6, ref1.ctypes.data, 0)
+    assert_close(host(lg)[:V], ref1, what="mla decode logits")
+    orc.load().orc_mla_destroy(m)
+    eng.rina_infer_destroy(inf)
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_mla_engine_greedy_identical(rina, orc, tiny_mla, use_graph):
+    hm, tensors, qts, max_seq = tiny_mla
+    eng = rina.load_engine()
+    inf = hm.infer("mla", max_seq=max_seq)
+    prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+    steps = 20
+    out = (C.c_int * steps)()
+    rina.check(eng.rina_infer_generate(inf, (C.c_int * len(prompt))(*prompt), len(prompt), steps, out,
+                                       1 if use_graph else 0, stream(), None), "generate")
+    eng.rina_infer_destroy(inf)
+    m, hold = orc.mla_from_tensors(mt.CFG, tensors, qts, max_seq)
+    ref = orc.mla_generate(m, prompt, steps)
+    orc.load().orc_mla_destroy(m)
+    assert list(out) == ref
