@@ -74,6 +74,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-steps", type=int, default=6)
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--no-config4", action="store_true", help="skip the DeepSeek MLA + MoE (config 4) decode line")
+    ap.add_argument("--config4-steps", type=int, default=32)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X in this build "
@@ -158,6 +160,37 @@ def main():
     log("config-1 Q4_0 GEMV: %.2f us, %.0f GB/s" % (t_q4 * 1e6, q4_bytes / t_q4 / 1e9))
     del ring
 
+    # ---- config 4: DeepSeek-V2-Lite-shaped MLA + MoE decode, random Q2_K weights
+    cfg4 = None
+    if not args.no_config4:
+        t4 = time.time()
+        p4, s4 = 32, args.config4_steps
+        ds = synth.SynthDeepSeek(seed=1, max_seq=p4 + s4 + 8)
+        log("config 4 model built in %.1fs" % (time.time() - t4))
+        inf4 = ds.infer()
+        pr4 = np.random.default_rng(4).integers(0, ds.cfg["vocab_size"], p4).astype(np.int32)
+        first4 = (C.c_int * 2)()
+        rina.check(eng.rina_infer_generate(inf4, pr4.ctypes.data_as(C.POINTER(C.c_int)), p4, 2, first4, 1, st, None),
+                   "config 4 prefill")
+        out4 = (C.c_int * s4)()
+        torch.cuda.synchronize()
+        tq = time.perf_counter()
+        rina.check(eng.rina_infer_decode(inf4, s4, out4, 1, st, None), "config 4 decode")
+        torch.cuda.synchronize()
+        w4 = time.perf_counter() - tq
+        eng.rina_infer_destroy(inf4)
+        b4 = ds.bytes_per_token(p4 + 1 + s4 // 2)
+        cfg4 = {"workload": "DeepSeek-V2-Lite-shaped MLA + MoE decode: 27 layers (1 dense + 26 MoE, 64 experts top-6 "
+                            "of 1408, 2 shared), d 2048, 16 heads, kv_lora_rank 512, rope 64, vocab 102400, random "
+                            "Q2_K weights, latent fp32 cache, %d-token prompt, greedy" % p4,
+                "tokens_per_s": round(s4 / w4, 2), "ms_per_step": round(w4 * 1e3 / s4, 4), "steps": s4,
+                "bytes_per_token": b4, "hbm_gbps": round(b4 * s4 / w4 / 1e9, 1),
+                "hbm_frac": round(b4 * s4 / w4 / HBM_PEAK, 4), "tokens_head": list(first4) + list(out4)[:6]}
+        log("config 4: %.3f ms/step, %.1f tok/s" % (w4 * 1e3 / s4, s4 / w4))
+        ds.close()
+        del ds
+        torch.cuda.empty_cache()
+
     # ---- CPU baseline: the oracle (scalar C restatement) decoding the same model
     cpu = None
     if want_cpu:
@@ -209,6 +242,7 @@ def main():
         },
         "decode_hbm_gbps": round(per_token * tok_s / 1e9, 1),
         "decode_hbm_frac": round(per_token * tok_s / HBM_PEAK, 4),
+        "config4_deepseek_mla_moe": cfg4,
         "cpu_baseline": cpu,
         "tokens_head": tokens[:8],
     }

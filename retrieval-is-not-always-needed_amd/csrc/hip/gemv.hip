@@ -859,7 +859,7 @@ __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     __shared__ float red[8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K;
-    for (int i = tid; i < K; i += kWG) xs_lds[i] = gld(a.x + i);
+    stage_lds(xs_lds, a.x, K);
     if (a.pro != RINA_PRO_NONE) {   // RMSNorm / LayerNorm of x, in LDS
         __syncthreads();
         float mean = 0.f;

@@ -80,6 +80,37 @@ __device__ __forceinline__ float row_dot(const uint8_t* w, int qt, int64_t row, 
     return wave_sum(acc);
 }
 
+// N row dots at once (loads of all N rows issued before the FMAs):
+// out[r] = W_r[row_r] . x_r, rows of K values in flat element order.
+template <int N>
+__device__ __forceinline__ void rows_dot(const uint8_t* const (&w)[N], int qt, const int64_t (&row)[N], int K,
+                                         const float* const (&x)[N], int lane, float (&out)[N]) {
+    float acc[N];
+#pragma unroll
+    for (int r = 0; r < N; r++) acc[r] = 0.f;
+    for (int u = lane; u < K / 16; u += 64) {
+        float v[N][16];
+#pragma unroll
+        for (int r = 0; r < N; r++) load_unit16(w[r], qt, row[r] * K + 16 * u, v[r]);
+#pragma unroll
+        for (int r = 0; r < N; r++) {
+            // 16-byte LDS reads (x 16-byte aligned): scalar reads of a
+            // 16-float slice per lane conflict 16 ways across the banks
+            const f32x4* xr = (const f32x4*)(x[r] + 16 * u);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 xv = xr[q];
+                acc[r] = fmaf(v[r][4 * q], xv.x, acc[r]);
+                acc[r] = fmaf(v[r][4 * q + 1], xv.y, acc[r]);
+                acc[r] = fmaf(v[r][4 * q + 2], xv.z, acc[r]);
+                acc[r] = fmaf(v[r][4 * q + 3], xv.w, acc[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < N; r++) out[r] = wave_sum(acc[r]);
+}
+
 struct MlaArgs {
     const float* q;        // [H*(nope+rope)]: [H*nope | H*rope]
     const float* kva;      // [dc+rope]: [c_kv | k_pe], raw
@@ -113,7 +144,7 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
 // grid H + 1: workgroup h < H builds q_lat_h and the rotated q_rope_h;
 // workgroup H appends the latent record of position pos0.
 __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
-    __shared__ float s_q[512];
+    __shared__ __align__(16) float s_q[512];
     __shared__ float s_part[4096];
     __shared__ float s_red[4];
     const int tid = threadIdx.x;
@@ -121,6 +152,7 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
     if (pos < 0 || pos >= a.max_seq) return;
     const int R = a.dc + a.rope, hr = a.rope / 2;
     if (blockIdx.x == (unsigned)a.H) {
+        if (blockIdx.y) return;
         float ss = 0.f;
         for (int k = tid; k < a.dc; k += 256) {
             const float x = gld(a.kva + k);
@@ -142,8 +174,8 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
     }
     const int h = blockIdx.x;
     float* qo = a.ws_q + (int64_t)h * R;
-    for (int i = tid; i < a.nope; i += 256) s_q[i] = gld(a.q + (int64_t)h * a.nope + i);
-    for (int j = tid; j < hr; j += 256) {
+    stage_lds(s_q, a.q + (int64_t)h * a.nope, a.nope);
+    for (int j = tid; j < hr && blockIdx.y == 0; j += 256) {
         const float* qr = a.q + (int64_t)a.H * a.nope + (int64_t)h * a.rope;
         float x0 = gld(qr + j), x1 = gld(qr + j + hr);
         if (a.rc) rope_pair(x0, x1, gld(a.rc + (int64_t)pos * hr + j), gld(a.rs + (int64_t)pos * hr + j), x0, x1);
@@ -151,13 +183,15 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
         gst(qo + a.dc + j + hr, x1);
     }
     __syncthreads();
-    // q_lat[k] = sum_i q_nope[i] W[h*nope + i][k]: thread = (row slice, 16-column unit)
-    const int ncu = a.dc / 16;
+    // q_lat[k] = sum_i q_nope[i] W[h*nope + i][k] for this workgroup's column
+    // quarter: thread = (row slice, 16-column unit)
+    const int ncu = a.dc / 64;
     const int RS = 256 / ncu;
-    const int cu = tid % ncu, rsl = tid / ncu;
+    const int cu = blockIdx.y * ncu + tid % ncu, rsl = tid / ncu;
     float acc[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) acc[j] = 0.f;
+#pragma unroll 4
     for (int i = rsl; i < a.nope; i += RS) {
         float w[16];
         load_unit16(a.wkvb, a.qt, ((int64_t)h * a.nope + i) * a.dc + 16 * cu, w);
@@ -165,13 +199,14 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; j++) acc[j] = fmaf(qi, w[j], acc[j]);
     }
+    const int cw = a.dc / 4;                      // columns of this workgroup
 #pragma unroll
-    for (int j = 0; j < 16; j++) s_part[rsl * a.dc + 16 * cu + j] = acc[j];
+    for (int j = 0; j < 16; j++) s_part[rsl * cw + 16 * (tid % ncu) + j] = acc[j];
     __syncthreads();
-    for (int k = tid; k < a.dc; k += 256) {
+    for (int k = tid; k < cw; k += 256) {
         float t = 0.f;
-        for (int r = 0; r < RS; r++) t += s_part[r * a.dc + k];
-        gst(qo + k, t);
+        for (int r = 0; r < RS; r++) t += s_part[r * cw + k];
+        gst(qo + blockIdx.y * cw + k, t);
     }
 }
 
@@ -242,10 +277,11 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
     }
 }
 
-// grid H: merge the chunks of head h into o_lat, then out_h = W_vb_h o_lat
+// grid (H, v/16): merge the chunks of head h into o_lat (every workgroup of
+// the head repeats this small merge), then 16 rows of out_h = W_vb_h o_lat
 __global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
     __shared__ float s_w[256];
-    __shared__ float s_lat[512];
+    __shared__ __align__(16) float s_lat[512];
     __shared__ float s_red[8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
@@ -267,14 +303,20 @@ __global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
     const float inv_l = 1.0f / ((s_red[4] + s_red[5]) + (s_red[6] + s_red[7]));
     for (int k = tid; k < a.dc; k += 256) {
         float acc = 0.f;
+#pragma unroll 8
         for (int cc = 0; cc < nch; cc++) acc = fmaf(gld(a.ws_o + ((int64_t)cc * a.H + h) * a.dc + k), s_w[cc], acc);
         s_lat[k] = acc * inv_l;
     }
     __syncthreads();
+    // out rows: 4 per wave at a time (v % 4 == 0)
     const int64_t row0 = (int64_t)a.H * a.nope + (int64_t)h * a.v;
-    for (int i = wave; i < a.v; i += 4) {
-        const float r = row_dot(a.wkvb, a.qt, row0 + i, a.dc, s_lat, lane);
-        if (lane == 0) gst(a.out + (int64_t)h * a.v + i, r);
+    for (int i = 16 * blockIdx.y + 4 * wave; i < min(a.v, 16 * (int)blockIdx.y + 16); i += 16) {
+        const uint8_t* const w4[4] = {a.wkvb, a.wkvb, a.wkvb, a.wkvb};
+        const int64_t r4[4] = {row0 + i, row0 + i + 1, row0 + i + 2, row0 + i + 3};
+        const float* const x4[4] = {s_lat, s_lat, s_lat, s_lat};
+        float o4[4];
+        rows_dot<4>(w4, a.qt, r4, a.dc, x4, lane, o4);
+        if (lane < 4) gst(a.out + (int64_t)h * a.v + i + lane, lane == 0 ? o4[0] : lane == 1 ? o4[1] : lane == 2 ? o4[2] : o4[3]);
     }
 }
 
@@ -282,39 +324,45 @@ __global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
 // MoE
 // ---------------------------------------------------------------------------
 
-// deepseek_mla_layer.cu:310-326: softmax over E logits, insertion top-k
-// kept ascending with strict ">" (the earlier expert wins ties).
+// deepseek_mla_layer.cu:310-326: softmax over E logits (serial fp32 sum of
+// the exponentials in expert order), then the top-k of the reference's
+// insertion loop.  That loop keeps the k largest probabilities with strict
+// ">" (of equal values the earlier expert stays) in ascending order, equal
+// values ending up later-expert first.  Here every expert computes its rank
+// against the others in parallel, which gives the same set and order.
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float* lg, int E, int k, int* ids, float* probs) {
-    __shared__ float s_e[256];
-    __shared__ float s_mx;
-    const int tid = threadIdx.x;
+    __shared__ float s_p[256];
+    __shared__ float s_red[4];
+    __shared__ float s_inv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float x = tid < E ? gld(lg + tid) : -INFINITY;
-    if (tid == 0) {
-        float mx = gld(lg);
-        for (int e = 1; e < E; e++) mx = fmaxf(mx, gld(lg + e));   // max_element: value only
-        s_mx = mx;
-    }
+    const float wm = wave_max(x);
+    if (lane == 0) s_red[wave] = wm;
     __syncthreads();
-    if (tid < E) s_e[tid] = expf(x - s_mx);
+    const float mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float ex = tid < E ? expf(x - mx) : 0.f;
+    s_p[tid] = ex;
     __syncthreads();
     if (tid == 0) {
         float sum = 0.f;
-        for (int e = 0; e < E; e++) sum += s_e[e];
-        const float inv = 1.0f / sum;
-        int tk[16];
-        float tw[16];
-        for (int j = 0; j < k; j++) { tk[j] = -1; tw[j] = -1e10f; }
+        for (int e = 0; e < E; e++) sum += s_p[e];
+        s_inv = 1.0f / sum;
+    }
+    __syncthreads();
+    const float p = ex * s_inv;
+    __syncthreads();
+    s_p[tid] = p;
+    __syncthreads();
+    if (tid < E) {
+        int above = 0;
         for (int e = 0; e < E; e++) {
-            const float p = s_e[e] * inv;
-            if (p > tw[0]) {
-                tw[0] = p; tk[0] = e;
-                for (int j = 0; j < k - 1 && tw[j] > tw[j + 1]; j++) {
-                    const float t = tw[j]; tw[j] = tw[j + 1]; tw[j + 1] = t;
-                    const int ti = tk[j]; tk[j] = tk[j + 1]; tk[j + 1] = ti;
-                }
-            }
+            const float q = s_p[e];
+            above += (q > p) || (q == p && e < tid);
         }
-        for (int j = 0; j < k; j++) { gst(ids + j, tk[j]); gst(probs + j, tw[j]); }
+        if (above < k) {
+            gst(ids + (k - 1 - above), tid);
+            gst(probs + (k - 1 - above), p);
+        }
     }
 }
 
@@ -335,37 +383,68 @@ struct MoeArgs {
 
 // one wave per (slot, row) of the selected experts' gate/up
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
-    extern __shared__ float s_x[];
+    extern __shared__ __align__(16) float s_x[];
+    __shared__ int s_ids[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < a.d; i += 256) s_x[i] = gld(a.x + i);
+    stage_lds(s_x, a.x, a.d);
+    if (tid < a.k) s_ids[tid] = gld(a.ids + tid);
     __syncthreads();
-    const int rows = a.k * a.ffn;
-    for (int r = blockIdx.x * 4 + wave; r < rows; r += gridDim.x * 4) {
-        const int slot = r / a.ffn, i = r % a.ffn;
-        const int e = gld(a.ids + slot);
-        float v = 0.f;
-        if (e >= 0 && e < a.E) {
-            const float g = row_dot(a.wg + (int64_t)e * a.stride_gu, a.qt, i, a.d, s_x, lane);
-            const float u = row_dot(a.wu + (int64_t)e * a.stride_gu, a.qt, i, a.d, s_x, lane);
-            v = (g / (1.0f + expf(-g))) * u;
+    const int rows = a.k * a.ffn;                 // even: ffn % 16 == 0
+    for (int r = 2 * (blockIdx.x * 4 + wave); r < rows; r += 2 * gridDim.x * 4) {
+        int e2[2];
+        int64_t i2[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int e = s_ids[(r + t) / a.ffn];
+            e2[t] = (e >= 0 && e < a.E) ? e : -1;
+            i2[t] = (r + t) % a.ffn;
         }
-        if (lane == 0) gst(a.G + r, v);
+        const uint8_t* const w4[4] = {a.wg + (int64_t)max(e2[0], 0) * a.stride_gu, a.wu + (int64_t)max(e2[0], 0) * a.stride_gu,
+                                      a.wg + (int64_t)max(e2[1], 0) * a.stride_gu, a.wu + (int64_t)max(e2[1], 0) * a.stride_gu};
+        const int64_t r4[4] = {i2[0], i2[0], i2[1], i2[1]};
+        const float* const x4[4] = {s_x, s_x, s_x, s_x};
+        float o4[4];
+        rows_dot<4>(w4, a.qt, r4, a.d, x4, lane, o4);
+        if (lane < 2) {
+            const float g = lane == 0 ? o4[0] : o4[2], u = lane == 0 ? o4[1] : o4[3];
+            gst(a.G + r + lane, e2[lane] >= 0 ? (g / (1.0f + expf(-g))) * u : 0.f);
+        }
     }
 }
 
 // one wave per output row i: acc = shared[i]; acc += p_j y_j (ascending j); h[i] += acc
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
-    extern __shared__ float s_g[];
+    extern __shared__ __align__(16) float s_g[];
+    __shared__ int s_ids[16];
+    __shared__ float s_p[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < a.k * a.ffn; i += 256) s_g[i] = gld(a.G + i);
+    stage_lds(s_g, a.G, a.k * a.ffn);
+    if (tid < a.k) { s_ids[tid] = gld(a.ids + tid); s_p[tid] = gld(a.probs + tid); }
     __syncthreads();
     for (int i = blockIdx.x * 4 + wave; i < a.d; i += gridDim.x * 4) {
         float acc = gld(a.shared + i);
-        for (int j = 0; j < a.k; j++) {
-            const int e = gld(a.ids + j);
-            if (e < 0 || e >= a.E) continue;
-            const float y = row_dot(a.wd + (int64_t)e * a.stride_dn, a.qt, i, a.ffn, s_g + j * a.ffn, lane);
-            acc = fmaf(gld(a.probs + j), y, acc);
+        for (int j0 = 0; j0 < a.k; j0 += 6) {
+            const uint8_t* w4[6];
+            int64_t r4[6];
+            const float* x4[6];
+#pragma unroll
+            for (int t = 0; t < 6; t++) {
+                const int j = min(j0 + t, a.k - 1);
+                const int e = s_ids[j];
+                w4[t] = a.wd + (int64_t)((e >= 0 && e < a.E) ? e : 0) * a.stride_dn;
+                r4[t] = i;
+                x4[t] = s_g + j * a.ffn;
+            }
+            float y4[6];
+            rows_dot<6>(w4, a.qt, r4, a.ffn, x4, lane, y4);
+#pragma unroll
+            for (int t = 0; t < 6; t++) {
+                const int j = j0 + t;
+                if (j < a.k) {
+                    const int e = s_ids[j];
+                    if (e >= 0 && e < a.E) acc = fmaf(s_p[j], y4[t], acc);   // ascending j, as the saxpy chain
+                }
+            }
         }
         if (lane == 0) gst(a.h + i, gld(a.h + i) + acc);
     }
@@ -398,8 +477,8 @@ extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, c
         return RINA_ERR_ARG;
     if (!unit_qt(qt_kv_b)) return RINA_ERR_QTYPE;
     if ((!rope_cos) != (!rope_sin)) return RINA_ERR_ARG;
-    if (dc % 64 || dc > 512 || rope % 2 || rope < 0 || dc + rope > 64 * kMaxRecLanes || nope > 512 ||
-        mla_nchunk(max_seq) > 256 || (256 % (dc / 16)))
+    if (dc % 64 || dc > 512 || rope % 2 || rope < 0 || dc + rope > 64 * kMaxRecLanes || nope > 512 || v_dim % 4 ||
+        mla_nchunk(max_seq) > 256 || (256 % (dc / 64)))
         return RINA_ERR_SHAPE;
     if (!d_pos && (start_pos < 0 || start_pos >= max_seq)) return RINA_ERR_RANGE;
     if (((uintptr_t)w_kv_b | (uintptr_t)q | (uintptr_t)cache) % 16 || (uintptr_t)w_kv_b % 4) return RINA_ERR_SHAPE;
@@ -418,11 +497,11 @@ extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, c
     a.ws_l = a.ws_m + (size_t)nch * H;
     a.ws_o = a.ws_l + (size_t)nch * H;
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(mla_prep_kernel, dim3(H + 1), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(mla_prep_kernel, dim3(H + 1, 4), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(mla_split_kernel, dim3(nch, H), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
-    hipLaunchKernelGGL(mla_out_kernel, dim3(H), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(mla_out_kernel, dim3(H, (v_dim + 15) / 16), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }
@@ -445,7 +524,8 @@ extern "C" int rina_hip_moe_ffn(const float* x, const void* gate_exps, const voi
         ffn < 1 || n_experts < 1)
         return RINA_ERR_ARG;
     if (!unit_qt(qt)) return RINA_ERR_QTYPE;
-    if (d % 16 || ffn % 16 || (size_t)k * ffn * 4 > 64 * 1024 || (size_t)d * 4 > 64 * 1024) return RINA_ERR_SHAPE;
+    if (d % 16 || ffn % 16 || k > 16 || (size_t)k * ffn * 4 > 64 * 1024 || (size_t)d * 4 > 64 * 1024)
+        return RINA_ERR_SHAPE;
     if (!workspace || ws_bytes < rina_hip_moe_workspace(k, ffn)) return RINA_ERR_WORKSPACE;
     if (((uintptr_t)gate_exps | (uintptr_t)up_exps | (uintptr_t)down_exps) % 4 || stride_gu % 4 || stride_dn % 4)
         return RINA_ERR_SHAPE;
@@ -455,12 +535,12 @@ extern "C" int rina_hip_moe_ffn(const float* x, const void* gate_exps, const voi
     a.k = k; a.d = d; a.ffn = ffn; a.E = n_experts; a.G = (float*)workspace; a.shared = shared_out; a.h = h;
     hipStream_t st = as_stream(stream);
     const int cus = rina_num_cus();
-    int g1 = (k * ffn + 3) / 4;
+    int g1 = (k * ffn / 2 + 3) / 4;
     if (g1 > cus * 4) g1 = cus * 4;
     hipLaunchKernelGGL(moe_gate_up_kernel, dim3(g1), dim3(256), (size_t)d * 4, st, a);
     RINA_LAUNCH_CHECK();
-    int g2 = (d + 3) / 4;
-    if (g2 > cus * 4) g2 = cus * 4;
+    int g2 = (d + 7) / 8;          // two rows per wave: the activations are staged once per 8 rows
+    if (g2 > cus) g2 = cus;
     hipLaunchKernelGGL(moe_down_kernel, dim3(g2), dim3(256), (size_t)k * ffn * 4, st, a);
     RINA_LAUNCH_CHECK();
     return RINA_OK;

@@ -120,6 +120,26 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Copy n floats from global memory to LDS with the whole workgroup, 16-byte
+// loads when both ends allow, unrolled so the loads of several iterations
+// are in flight together (a plain strided loop issues one load per round
+// trip).
+__device__ __forceinline__ void stage_lds(float* dst, const float* src, int n) {
+    typedef float f32x4_s __attribute__((ext_vector_type(4)));
+    const int tid = threadIdx.x, nt = blockDim.x;
+    if (((uintptr_t)src % 16) == 0 && ((uintptr_t)dst % 16) == 0) {
+        const int n4 = n >> 2;
+        const f32x4_s* s4 = (const f32x4_s*)src;
+        f32x4_s* d4 = (f32x4_s*)dst;
+#pragma unroll 4
+        for (int i = tid; i < n4; i += nt) d4[i] = gld(s4 + i);
+        for (int i = 4 * n4 + tid; i < n; i += nt) dst[i] = gld(src + i);
+    } else {
+#pragma unroll 8
+        for (int i = tid; i < n; i += nt) dst[i] = gld(src + i);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // host helpers
 // ---------------------------------------------------------------------------

@@ -202,3 +202,125 @@ class HostModel:
             self._eng.rina_model_destroy(self.model)
             self.model = None
         self.arena.keep.clear()
+
+
+DSV2_LITE = dict(name="deepseek-v2-lite", dim=2048, n_layers=27, n_heads=16, nope=128, rope=64, v_dim=128, dc=512,
+                 vocab_size=102400, dense_ffn=10944, n_experts=64, top_k=6, expert_ffn=1408, shared_ffn=2816,
+                 rope_theta=10000.0)
+
+
+def q2k_device(n_elems, seed, std=0.02):
+    """Random valid Q2_K blocks generated on the device (see random_q2k)."""
+    torch = _torch()
+    nb = (n_elems + 255) // 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    blk = torch.randint(0, 256, (nb, 84), dtype=torch.uint8, device="cuda", generator=g)
+    dd = np.frombuffer(np.array([std / 8.0, std / 16.0], np.float16).tobytes(), np.uint8)
+    blk[:, 80:84] = torch.from_numpy(dd.copy()).cuda()
+    return blk.reshape(-1)
+
+
+class SynthDeepSeek:
+    """DeepSeek-V2-Lite-shaped MLA + MoE model with random Q2_K weights
+    (fp32 router, norms 1, NeoX RoPE tables), built on the device.  Layer 0
+    is dense, the rest MoE (config 4 of the benchmark set)."""
+
+    def __init__(self, cfg=DSV2_LITE, seed=1, max_seq=2048, keep_host=False, n_layers=None):
+        torch = _torch()
+        c = self.cfg = dict(cfg)
+        if n_layers is not None:
+            c["n_layers"] = n_layers
+        self.max_seq = max_seq
+        self.host, self.qts, self.dev = {}, {}, {}
+        d, H, nope, rope, vd, dc = c["dim"], c["n_heads"], c["nope"], c["rope"], c["v_dim"], c["dc"]
+        E, F, S, hd, V, L = c["n_experts"], c["expert_ffn"], c["shared_ffn"], c["dense_ffn"], c["vocab_size"], c["n_layers"]
+        header = {"name": c["name"], "dim": d, "n_layers": L, "n_heads": H, "n_kv_heads": H, "head_dim": nope,
+                  "qk_nope_head_dim": nope, "qk_rope_head_dim": rope, "v_head_dim": vd, "kv_lora_rank": dc,
+                  "vocab_size": V, "max_seq_len": max_seq, "n_routed_experts": E, "num_experts_per_tok": c["top_k"],
+                  "moe_intermediate_size": F,
+                  "layers": [{"type": "deepseek_mla_dense"}] + [{"type": "deepseek_mla_moe"}] * (L - 1)}
+        eng = load_engine()
+        self._eng = eng
+        self.arena = DeviceArena()
+        self.model = eng.rina_model_create(json.dumps(header).encode())
+        if not self.model:
+            raise RuntimeError(eng.rina_engine_last_error().decode())
+        idx = [0]
+
+        def add(name, shape, qt, t):
+            shp = (C.c_int64 * len(shape))(*shape)
+            check(eng.rina_model_add_tensor(self.model, name.encode(), qt, len(shape), shp, t.data_ptr()),
+                  "add_tensor " + name)
+            self.arena.put(t)
+            self.dev[name] = t
+            self.qts[name] = qt
+            if keep_host:
+                self.host[name] = t.cpu().numpy()
+
+        def q2(name, shape):
+            idx[0] += 1
+            n = int(np.prod(shape))
+            if len(shape) == 3:   # stacked experts: whole blocks per expert
+                per = (shape[1] * shape[2] + 255) // 256 * 256
+                t = q2k_device(shape[0] * per, seed * 7919 + idx[0])
+            else:
+                t = q2k_device(n, seed * 7919 + idx[0])
+            add(name, shape, QT_Q2_K, t)
+
+        def f32(name, a):
+            add(name, a.shape, QT_FP32, torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda())
+
+        cos, sin = make_rope(rope, max_seq, c.get("rope_theta", 10000.0))
+        ones = np.ones(d, np.float32)
+        for l in range(L):
+            p = "transformer.h.%d." % l
+            q2(p + "attn.w_q.weight", (H * (nope + rope), d))
+            q2(p + "attn.w_kv_a.weight", (dc + rope, d))
+            f32(p + "attn.k_norm.weight", np.ones(dc, np.float32))
+            q2(p + "attn.w_kv_b.weight", (H * (nope + vd), dc))
+            q2(p + "attn.w_o.weight", (d, H * vd))
+            f32(p + "ln1.weight", ones)
+            f32(p + "ln2.weight", ones)
+            f32(p + "attn.rope_q.cos", cos)
+            f32(p + "attn.rope_q.sin", sin)
+            if l == 0:
+                q2(p + "mlp.w1.weight", (hd, d))
+                q2(p + "mlp.w2.weight", (d, hd))
+                q2(p + "mlp.w3.weight", (hd, d))
+            else:
+                f32(p + "mlp.gate_inp.weight", normal(seed * 31 + l, E * d, 0.02).reshape(E, d))
+                q2(p + "mlp.gate_exps.weight", (E, F, d))
+                q2(p + "mlp.up_exps.weight", (E, F, d))
+                q2(p + "mlp.down_exps.weight", (E, d, F))
+                q2(p + "mlp.gate_shexp.weight", (S, d))
+                q2(p + "mlp.up_shexp.weight", (S, d))
+                q2(p + "mlp.down_shexp.weight", (d, S))
+        q2("transformer.wte.weight", (V, d))
+        f32("transformer.ln_f.weight", ones)
+        q2("lm_head.weight", (V, d))
+
+    def bytes_per_token(self, pos):
+        """HBM bytes one decode step reads at cache position pos: all
+        attention / dense / shared weights, top_k experts per MoE layer, the
+        router, the LM head row block, and the latent cache."""
+        c = self.cfg
+        d, H, nope, rope, vd, dc = c["dim"], c["n_heads"], c["nope"], c["rope"], c["v_dim"], c["dc"]
+        q2 = lambda n: (n + 255) // 256 * 84
+        attn = q2(H * (nope + rope) * d) + q2((dc + rope) * d) + q2(H * (nope + vd) * dc) + q2(d * H * vd)
+        dense = 3 * q2(c["dense_ffn"] * d)
+        moe = c["top_k"] * 3 * q2(c["expert_ffn"] * d) + 3 * q2(c["shared_ffn"] * d) + c["n_experts"] * d * 4
+        L = c["n_layers"]
+        return (L * attn + dense + (L - 1) * moe + q2(c["vocab_size"] * d) + L * (pos + 1) * (dc + rope) * 4)
+
+    def infer(self, max_seq=None):
+        h = self._eng.rina_infer_create(self.model, b"mla", None, max_seq or self.max_seq)
+        if not h:
+            raise RuntimeError(self._eng.rina_engine_last_error().decode())
+        return h
+
+    def close(self):
+        if self.model:
+            self._eng.rina_model_destroy(self.model)
+            self.model = None
+        self.arena.keep.clear()

@@ -237,3 +237,25 @@ def test_mla_engine_greedy_identical(rina, orc, tiny_mla, use_graph):
     ref = orc.mla_generate(m, prompt, steps)
     orc.load().orc_mla_destroy(m)
     assert list(out) == ref
+
+
+def test_mla_engine_full_width_greedy(rina, orc):
+    """DeepSeek-V2-Lite widths (3 layers: dense + 2 MoE, vocab 102400, 64
+    experts of 1408): greedy tokens identical to the oracle."""
+    synth = importlib.import_module("rina_amd.synth")
+    sm = synth.SynthDeepSeek(seed=5, max_seq=64, keep_host=True, n_layers=3)
+    try:
+        eng = rina.load_engine()
+        inf = sm.infer()
+        prompt = [101, 2047, 9, 55555, 3, 777]
+        steps = 5
+        out = (C.c_int * steps)()
+        rina.check(eng.rina_infer_generate(inf, (C.c_int * len(prompt))(*prompt), len(prompt), steps, out, 1,
+                                           stream(), None), "generate")
+        eng.rina_infer_destroy(inf)
+        m, hold = orc.mla_from_tensors(sm.cfg, sm.host, sm.qts, 64)
+        ref = orc.mla_generate(m, prompt, steps)
+        orc.load().orc_mla_destroy(m)
+        assert list(out) == ref
+    finally:
+        sm.close()
