@@ -233,6 +233,39 @@ int rina_hip_moe_ffn(const float* x, const void* gate_exps, const void* up_exps,
                      size_t workspace_bytes, void* stream);
 
 /* ====================================================================== */
+/* RINA Jamba hybrid (SSM and RINA-MLA layers)                             */
+/* ====================================================================== */
+
+/* One position of the InertiaWave SSM (arch/ssm/rina_ssm_layer.cu:98-109,
+ * kernels/ssm_kernels_fp32.cu:6-47): dec_raw [steps][H] are the pre-sigmoid
+ * decay projections, mem [steps][H*dh] the memory projections (steps <= 3,
+ * missing steps act as decay 1, memory 0).  Per (h, d): da = d0 d1 d2,
+ * ma = m0 d1 d2 + m1 d2 + m2, lcs += log(max(da, 1e-38)), ca = exp(lcs),
+ * wcs += ma / max(ca, 1e-30), sf_out = ca wcs.  lcs / wcs [H*dh] carry the
+ * scan across calls (reset != 0 starts it from zero), which reproduces the
+ * reference's scan over the whole sequence. */
+int rina_hip_ssm_step(const float* mem, const float* dec_raw, int steps, int H, int dh,
+                      float* lcs, float* wcs, float* sf_out, int reset, void* stream);
+
+/* Decode attention of RinaMLAImpl (arch/mla/rina_mla_layer.cu:78-86) at
+ * pos0 = start_pos + (d_pos ? *d_pos : 0): query [qa | RoPE_hf(qb)] per head
+ * (qa [H*da], qb [H*db]), key [ka | RoPE_hf(kb)] and value v per KV head
+ * (ka [Hkv*da], kb [Hkv*db], v [Hkv*dv]) appended at pos0 into fp32 caches
+ * cache_k [max_seq][Hkv][da+db], cache_v [max_seq][Hkv][dv]; causal over
+ * positions 0..pos0, head h uses KV head h / (H/Hkv), scale 1/sqrt(da+db);
+ * out [H*dv].  HF RoPE pairs (2i, 2i+1) with tables [max_seq][db/2]
+ * (ops/rope.cu:212-227; NULL: none).  dv == 64, 64 <= da + db <= 128,
+ * contexts up to 2048 positions. */
+size_t rina_hip_dq_attention_workspace(int H, int dq, int max_pos);
+int rina_hip_dq_decode_attention(const float* qa, const float* qb, const float* ka,
+                                 const float* kb, const float* v, const float* rope_q_cos,
+                                 const float* rope_q_sin, const float* rope_k_cos,
+                                 const float* rope_k_sin, float* cache_k, float* cache_v,
+                                 int H, int Hkv, int da, int db, int dv, int start_pos,
+                                 const int* d_pos, int max_seq, float* out, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* ====================================================================== */
 /* Per-token glue                                                          */
 /* ====================================================================== */
 

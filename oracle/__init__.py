@@ -51,6 +51,20 @@ class MLACfg(C.Structure):
                 ("lm_head", VP), ("qt_lm", I32), ("layers", C.POINTER(MLALayerW))]
 
 
+class JambaLayerW(C.Structure):
+    _fields_ = [("type", I32), ("qt", I32), ("ln1", VP), ("ln2", VP), ("w_dq", VP), ("q_norm", VP),
+                ("w_mem", VP * 3), ("w_decay", VP * 3), ("w_out", VP), ("w_uq", VP), ("w_uk", VP),
+                ("w_k2v", VP), ("w_qr", VP), ("w_kr", VP), ("c_proj", VP), ("rope_q_cos", VP),
+                ("rope_q_sin", VP), ("rope_k_cos", VP), ("rope_k_sin", VP), ("w1", VP), ("w2", VP), ("w3", VP)]
+
+
+class JambaCfg(C.Structure):
+    _fields_ = [("dim", I32), ("n_layers", I32), ("n_heads", I32), ("n_kv_heads", I32), ("head_dim", I32),
+                ("dhr", I32), ("dc", I32), ("ssm_steps", I32), ("hidden", I32), ("vocab", I32), ("max_seq", I32),
+                ("nthreads", I32), ("wte", VP), ("qt_wte", I32), ("ln_f", VP), ("lm_head", VP), ("qt_lm", I32),
+                ("layers", C.POINTER(JambaLayerW))]
+
+
 _lib = None
 
 
@@ -91,6 +105,11 @@ def load(build=True):
         "orc_gqa_generate": (I32, [VP, VP, I32, I32, VP]),
         "orc_num_threads": (I32, []),
         "orc_moe_topk": (None, [VP, I32, I32, VP, VP]),
+        "orc_jamba_create": (VP, [C.POINTER(JambaCfg)]),
+        "orc_jamba_destroy": (None, [VP]),
+        "orc_jamba_forward": (I32, [VP, VP, I32, I32, VP, I32]),
+        "orc_jamba_generate": (I32, [VP, VP, I32, I32, VP]),
+        "orc_jamba_generate_recompute": (I32, [VP, VP, I32, I32, VP]),
         "orc_mla_create": (VP, [C.POINTER(MLACfg)]),
         "orc_mla_destroy": (None, [VP]),
         "orc_mla_forward": (I32, [VP, VP, I32, I32, VP, I32]),
@@ -281,5 +300,63 @@ def mla_generate(m, prompt, steps):
     p = np.ascontiguousarray(prompt, np.int32)
     out = np.zeros(steps, np.int32)
     rc = load().orc_mla_generate(m, p.ctypes.data, p.size, steps, out.ctypes.data)
+    assert rc == 0, rc
+    return [int(v) for v in out]
+
+
+JAMBA_SSM_TYPES = ("inertia_wave_ssm", "ssm")
+
+
+def jamba_from_tensors(cfg, tensors, layer_types, qt, max_seq, nthreads=0):
+    """Oracle RINA Jamba model over host tensors (reference names).  cfg:
+    dim, n_layers, n_heads, n_kv_heads, head_dim, d_h_r, d_c, ssm_steps,
+    hidden_dim, vocab_size; layer_types: per-layer type strings; qt: quant
+    type of every linear.  Returns (handle, keepalive)."""
+    hold = []
+
+    def h(name):
+        if name not in tensors:
+            return None
+        a = np.ascontiguousarray(tensors[name])
+        hold.append(a)
+        return a.ctypes.data
+
+    nl = cfg["n_layers"]
+    lw = (JambaLayerW * nl)()
+    for l in range(nl):
+        p = "transformer.h.%d." % l
+        o = lw[l]
+        o.qt = qt
+        o.ln1, o.ln2 = h(p + "ln1.weight"), h(p + "ln2.weight")
+        o.w1, o.w2, o.w3 = (h(p + "mlp.w%d.weight" % i) for i in (1, 2, 3))
+        o.q_norm = h(p + "path.q_norm.weight")
+        if layer_types[l] in JAMBA_SSM_TYPES:
+            o.type = 0
+            o.w_dq = h(p + "path.w_dq.weight")
+            for k in range(3):
+                o.w_mem[k] = h(p + "path.w_mem.%d.weight" % k)
+                o.w_decay[k] = h(p + "path.w_decay.%d.weight" % k)
+            o.w_out = h(p + "path.w_out.weight")
+        else:
+            o.type = 1
+            o.w_dq = h(p + "path.w_dqkv.weight")
+            for f in ("w_uq", "w_uk", "w_k2v", "w_qr", "w_kr", "c_proj"):
+                setattr(o, f, h(p + "path.%s.weight" % f))
+            o.rope_q_cos, o.rope_q_sin = h(p + "path.rope_q.cos"), h(p + "path.rope_q.sin")
+            o.rope_k_cos, o.rope_k_sin = h(p + "path.rope.cos"), h(p + "path.rope.sin")
+    c = JambaCfg(dim=cfg["dim"], n_layers=nl, n_heads=cfg["n_heads"], n_kv_heads=cfg["n_kv_heads"],
+                 head_dim=cfg["head_dim"], dhr=cfg["d_h_r"], dc=cfg["d_c"], ssm_steps=cfg["ssm_steps"],
+                 hidden=cfg["hidden_dim"], vocab=cfg["vocab_size"], max_seq=max_seq, nthreads=nthreads,
+                 wte=h("transformer.wte.weight"), qt_wte=FP32, ln_f=h("transformer.ln_f.weight"),
+                 lm_head=h("lm_head.weight"), qt_lm=FP32, layers=lw)
+    m = load().orc_jamba_create(C.byref(c))
+    return m, (hold, lw, c)
+
+
+def jamba_generate(m, prompt, steps, recompute=False):
+    p = np.ascontiguousarray(prompt, np.int32)
+    out = np.zeros(steps, np.int32)
+    f = load().orc_jamba_generate_recompute if recompute else load().orc_jamba_generate
+    rc = f(m, p.ctypes.data, p.size, steps, out.ctypes.data)
     assert rc == 0, rc
     return [int(v) for v in out]

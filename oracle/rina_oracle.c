@@ -969,3 +969,226 @@ int orc_mla_generate(orc_mla* m, const int* prompt, int n_prompt, int steps, int
     free(logits);
     return rc;
 }
+
+/* ------------------------------------------------------------------ */
+/* RINA Jamba hybrid (rina_ssm_layer.cu, rina_mla_layer.cu)            */
+/* ------------------------------------------------------------------ */
+
+struct orc_jamba {
+    orc_jamba_cfg c;
+    orc_jamba_layer_w* layers;
+    float** lcs;     /* SSM layers: [H*dh] log cumulative decay (one per scan thread) */
+    float** wcs;     /* SSM layers: [H*dh] weighted cumulative memory */
+    float** kc;      /* RMLA layers: [max_seq][Hkv*(dh+dhr)] */
+    float** vc;      /* RMLA layers: [max_seq][Hkv*dh] */
+};
+
+orc_jamba* orc_jamba_create(const orc_jamba_cfg* cfg) {
+    orc_jamba* m = (orc_jamba*)calloc(1, sizeof(orc_jamba));
+    m->c = *cfg;
+    int L = cfg->n_layers;
+    m->layers = (orc_jamba_layer_w*)malloc(sizeof(orc_jamba_layer_w) * L);
+    memcpy(m->layers, cfg->layers, sizeof(orc_jamba_layer_w) * L);
+    m->c.layers = m->layers;
+    m->lcs = (float**)calloc(L, sizeof(float*));
+    m->wcs = (float**)calloc(L, sizeof(float*));
+    m->kc = (float**)calloc(L, sizeof(float*));
+    m->vc = (float**)calloc(L, sizeof(float*));
+    const int H = cfg->n_heads, Hkv = cfg->n_kv_heads, dh = cfg->head_dim, dhr = cfg->dhr;
+    for (int l = 0; l < L; l++) {
+        if (m->layers[l].type == ORC_JAMBA_SSM) {
+            m->lcs[l] = (float*)calloc((size_t)H * dh, 4);
+            m->wcs[l] = (float*)calloc((size_t)H * dh, 4);
+        } else {
+            m->kc[l] = (float*)calloc((size_t)cfg->max_seq * Hkv * (dh + dhr), 4);
+            m->vc[l] = (float*)calloc((size_t)cfg->max_seq * Hkv * dh, 4);
+        }
+    }
+    return m;
+}
+
+void orc_jamba_destroy(orc_jamba* m) {
+    if (!m) return;
+    for (int l = 0; l < m->c.n_layers; l++) { free(m->lcs[l]); free(m->wcs[l]); free(m->kc[l]); free(m->vc[l]); }
+    free(m->lcs); free(m->wcs); free(m->kc); free(m->vc); free(m->layers);
+    free(m);
+}
+
+static float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }   /* ssm_kernels_fp32.cu:6-8 */
+
+/* one SSM layer on token rows [T, d] (rina_ssm_layer.cu:90-126) */
+static void jamba_ssm(orc_jamba* m, int l, float* h, int T) {
+    const orc_jamba_cfg* c = &m->c;
+    const orc_jamba_layer_w* L = &c->layers[l];
+    const int d = c->dim, H = c->n_heads, dh = c->head_dim, dc = c->dc, S = c->ssm_steps, nt = c->nthreads;
+    const int d2 = d + H * dh;
+    float* x2 = (float*)malloc((size_t)T * d2 * 4);
+    float* a = (float*)malloc((size_t)T * d * 4);
+    float* cq = (float*)malloc((size_t)T * dc * 4);
+    float* mem = (float*)malloc((size_t)3 * T * H * dh * 4);
+    float* dec = (float*)malloc((size_t)3 * T * H * 4);
+    float* tmp = (float*)malloc((size_t)T * d * 4);
+    memcpy(a, h, (size_t)T * d * 4);
+    orc_layer_norm(a, L->ln1, T, d, 1e-5f);                                    /* :93-95 */
+    orc_linear(L->w_dq, L->qt, a, cq, T, dc, d, nt);                            /* :96 */
+    orc_layer_norm(cq, L->q_norm, T, dc, 1e-5f);                                /* :97 */
+    for (int k = 0; k < 3; k++) {
+        if (k < S) {
+            orc_linear(L->w_mem[k], L->qt, cq, mem + (size_t)k * T * H * dh, T, H * dh, dc, nt);   /* :100 */
+            orc_linear(L->w_decay[k], L->qt, cq, dec + (size_t)k * T * H, T, H, dc, nt);           /* :101 */
+            for (int i = 0; i < T * H; i++) dec[(size_t)k * T * H + i] = orc_sigmoid(dec[(size_t)k * T * H + i]);
+        } else {   /* fewer steps: neutral factors */
+            memset(mem + (size_t)k * T * H * dh, 0, (size_t)T * H * dh * 4);
+            for (int i = 0; i < T * H; i++) dec[(size_t)k * T * H + i] = 1.0f;
+        }
+    }
+    /* ssm_agg (ssm_kernels_fp32.cu:14-22) then ssm_scan (:30-42), per (h, d) thread over t */
+    for (int t = 0; t < T; t++) {
+        for (int hh = 0; hh < H; hh++) {
+            const size_t i = (size_t)t * H + hh;
+            const float dd0 = dec[i], dd1 = dec[(size_t)T * H + i], dd2 = dec[(size_t)2 * T * H + i];
+            float da = dd0 * dd1 * dd2;
+            if (da <= 1e-38f) da = 1e-38f;
+            for (int dd = 0; dd < dh; dd++) {
+                const size_t j = i * dh + dd;
+                const float m0 = mem[j], m1 = mem[(size_t)T * H * dh + j], m2 = mem[(size_t)2 * T * H * dh + j];
+                const float ma = fmaf(m0 * dd1, dd2, m1 * dd2) + m2;
+                float* lcs = &m->lcs[l][hh * dh + dd];
+                float* wcs = &m->wcs[l][hh * dh + dd];
+                *lcs += logf(da);
+                const float ca = expf(*lcs);
+                *wcs += ma / fmaxf(ca, 1e-30f);
+                x2[(size_t)t * d2 + d + hh * dh + dd] = ca * *wcs;
+            }
+        }
+        memcpy(x2 + (size_t)t * d2, a + (size_t)t * d, (size_t)d * 4);          /* :110-113 [x_ln | sf] */
+    }
+    orc_linear(L->w_out, L->qt, x2, tmp, T, d, d2, nt);                         /* :114 */
+    orc_add(h, h, tmp, T * d);
+    free(x2); free(a); free(cq); free(mem); free(dec); free(tmp);
+}
+
+/* HF RoPE pairs (2i, 2i+1) of one head row at position pos (ops/rope.cu:212-227) */
+static void rope_hf_row(float* row, const float* ct, const float* st, int d, int pos) {
+    const int half = d / 2;
+    for (int i = 0; i < half; i++) {
+        const float cc = ct[(int64_t)pos * half + i], ss = st[(int64_t)pos * half + i];
+        const float x0 = row[2 * i], x1 = row[2 * i + 1];
+        row[2 * i] = fmaf(x0, cc, -(x1 * ss));
+        row[2 * i + 1] = fmaf(x0, ss, x1 * cc);
+    }
+}
+
+/* one RINA-MLA layer on token rows [T, d] at positions start_pos.. (rina_mla_layer.cu:65-98) */
+static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
+    const orc_jamba_cfg* c = &m->c;
+    const orc_jamba_layer_w* L = &c->layers[l];
+    const int d = c->dim, H = c->n_heads, Hkv = c->n_kv_heads, dh = c->head_dim, dhr = c->dhr, dc = c->dc;
+    const int dq = dh + dhr, nt = c->nthreads;
+    float* a = (float*)malloc((size_t)T * d * 4);
+    float* cq = (float*)malloc((size_t)T * dc * 4);
+    float* q = (float*)malloc((size_t)T * H * dh * 4);
+    float* k = (float*)malloc((size_t)T * Hkv * dh * 4);
+    float* v = (float*)malloc((size_t)T * Hkv * dh * 4);
+    float* qr = (float*)malloc((size_t)T * H * dhr * 4);
+    float* kr = (float*)malloc((size_t)T * Hkv * dhr * 4);
+    float* att = (float*)malloc((size_t)T * H * dh * 4);
+    float* tmp = (float*)malloc((size_t)T * d * 4);
+    float qv[512];
+    memcpy(a, h, (size_t)T * d * 4);
+    orc_layer_norm(a, L->ln1, T, d, 1e-5f);                                    /* :70 */
+    orc_linear(L->w_dq, L->qt, a, cq, T, dc, d, nt);                            /* :72 w_dqkv */
+    orc_layer_norm(cq, L->q_norm, T, dc, 1e-5f);                                /* :73 */
+    orc_linear(L->w_uq, L->qt, cq, q, T, H * dh, dc, nt);                       /* :75 */
+    orc_linear(L->w_uk, L->qt, cq, k, T, Hkv * dh, dc, nt);                     /* :76 */
+    orc_linear(L->w_k2v, L->qt, k, v, T, Hkv * dh, Hkv * dh, nt);               /* :77 */
+    orc_linear(L->w_qr, L->qt, a, qr, T, H * dhr, d, nt);                       /* :78 */
+    orc_linear(L->w_kr, L->qt, a, kr, T, Hkv * dhr, d, nt);                     /* :79 */
+    for (int t = 0; t < T; t++) {
+        const int pos = start_pos + t;
+        if (L->rope_q_cos)
+            for (int hh = 0; hh < H; hh++) rope_hf_row(qr + ((size_t)t * H + hh) * dhr, L->rope_q_cos, L->rope_q_sin, dhr, pos);
+        if (L->rope_k_cos)
+            for (int hh = 0; hh < Hkv; hh++) rope_hf_row(kr + ((size_t)t * Hkv + hh) * dhr, L->rope_k_cos, L->rope_k_sin, dhr, pos);
+        /* build_qkv (build_qkv_fp32.cu:8-24): K row per kv head [k | kr], V row per kv head */
+        float* krow = m->kc[l] + (size_t)pos * Hkv * dq;
+        for (int hh = 0; hh < Hkv; hh++) {
+            memcpy(krow + hh * dq, k + ((size_t)t * Hkv + hh) * dh, (size_t)dh * 4);
+            memcpy(krow + hh * dq + dh, kr + ((size_t)t * Hkv + hh) * dhr, (size_t)dhr * 4);
+        }
+        memcpy(m->vc[l] + (size_t)pos * Hkv * dh, v + (size_t)t * Hkv * dh, (size_t)Hkv * dh * 4);
+    }
+    const int rep = H / Hkv;
+    for (int t = 0; t < T; t++) {
+        for (int hh = 0; hh < H; hh++) {
+            const int kv = hh / rep;
+            memcpy(qv, q + ((size_t)t * H + hh) * dh, (size_t)dh * 4);
+            memcpy(qv + dh, qr + ((size_t)t * H + hh) * dhr, (size_t)dhr * 4);
+            orc_attn_rows(qv, dq, m->kc[l] + (size_t)kv * dq, Hkv * dq, m->vc[l] + (size_t)kv * dh, Hkv * dh,
+                          att + ((size_t)t * H + hh) * dh, dh, start_pos + t, 1, dq, dh);   /* flash_fp32 */
+        }
+    }
+    orc_linear(L->c_proj, L->qt, att, tmp, T, d, H * dh, nt);                   /* :87 (out of place) */
+    orc_add(h, h, tmp, T * d);
+    free(a); free(cq); free(q); free(k); free(v); free(qr); free(kr); free(att); free(tmp);
+}
+
+int orc_jamba_forward(orc_jamba* m, const int* ids, int T, int start_pos, float* logits, int last_only) {
+    const orc_jamba_cfg* c = &m->c;
+    const int d = c->dim, nt = c->nthreads, hd = c->hidden;
+    if (start_pos < 0 || start_pos + T > c->max_seq) return -3;
+    if (start_pos == 0)
+        for (int l = 0; l < c->n_layers; l++)
+            if (m->lcs[l]) {
+                memset(m->lcs[l], 0, (size_t)c->n_heads * c->head_dim * 4);
+                memset(m->wcs[l], 0, (size_t)c->n_heads * c->head_dim * 4);
+            }
+    float* h = (float*)malloc((size_t)T * d * 4);
+    float* a = (float*)malloc((size_t)T * d * 4);
+    float* g = (float*)malloc((size_t)T * hd * 4);
+    float* u = (float*)malloc((size_t)T * hd * 4);
+    orc_embedding(c->wte, c->qt_wte, ids, h, T, d);
+    for (int l = 0; l < c->n_layers; l++) {
+        const orc_jamba_layer_w* L = &c->layers[l];
+        if (L->type == ORC_JAMBA_SSM) jamba_ssm(m, l, h, T);
+        else jamba_rmla(m, l, h, T, start_pos);
+        memcpy(a, h, (size_t)T * d * 4);                                        /* MLP */
+        orc_layer_norm(a, L->ln2, T, d, 1e-5f);
+        orc_linear(L->w1, L->qt, a, g, T, hd, d, nt);
+        orc_linear(L->w3, L->qt, a, u, T, hd, d, nt);
+        orc_silu_mul(g, g, u, T * hd);
+        orc_linear(L->w2, L->qt, g, a, T, d, hd, nt);
+        orc_add(h, h, a, T * d);
+    }
+    if (c->ln_f) orc_layer_norm(h, c->ln_f, T, d, 1e-5f);                       /* name is not "llama" */
+    const void* lm = c->lm_head ? c->lm_head : c->wte;
+    int qlm = c->lm_head ? c->qt_lm : c->qt_wte;
+    if (last_only) orc_linear(lm, qlm, h + (size_t)(T - 1) * d, logits, 1, c->vocab, d, nt);
+    else orc_linear(lm, qlm, h, logits, T, c->vocab, d, nt);
+    free(h); free(a); free(g); free(u);
+    return 0;
+}
+
+static int jamba_gen(orc_jamba* m, const int* prompt, int n_prompt, int steps, int* out_ids, int recompute) {
+    int V = m->c.vocab;
+    int* gen = (int*)malloc(sizeof(int) * (n_prompt + steps));
+    memcpy(gen, prompt, sizeof(int) * n_prompt);
+    float* logits = (float*)malloc((size_t)V * 4);
+    int len = n_prompt, rc = 0;
+    for (int step = 0; step < steps; step++) {
+        if (recompute || step == 0) rc = orc_jamba_forward(m, gen, len, 0, logits, 1);
+        else rc = orc_jamba_forward(m, gen + len - 1, 1, len - 1, logits, 1);
+        if (rc) break;
+        int nx = orc_argmax(logits, V);
+        gen[len++] = nx;
+        out_ids[step] = nx;
+    }
+    free(gen);
+    free(logits);
+    return rc;
+}
+
+int orc_jamba_generate(orc_jamba* m, const int* p, int n, int steps, int* out) { return jamba_gen(m, p, n, steps, out, 0); }
+int orc_jamba_generate_recompute(orc_jamba* m, const int* p, int n, int steps, int* out) {
+    return jamba_gen(m, p, n, steps, out, 1);
+}

@@ -204,6 +204,55 @@ int      orc_mla_generate(orc_mla* m, const int* prompt, int n_prompt, int steps
  * [max_seq][H*nope], v [max_seq][H*v] (which: 0, 1, 2) */
 const float* orc_mla_cache(orc_mla* m, int layer, int which);
 
+/* ---- RINA Jamba hybrid (SSM + RINA-MLA layers, GQAInference) -------- */
+enum { ORC_JAMBA_SSM = 0, ORC_JAMBA_RMLA = 1 };
+typedef struct {
+    int type;                           /* ORC_JAMBA_SSM or ORC_JAMBA_RMLA */
+    int qt;                             /* quant type of every linear of the layer */
+    const float* ln1; const float* ln2; /* LayerNorm weights [d] */
+    const void* w_dq;                   /* SSM: path.w_dq [dc, d]; RMLA: path.w_dqkv [dc, d] */
+    const float* q_norm;                /* [dc] */
+    const void* w_mem[3];               /* SSM: [H*dh, dc] */
+    const void* w_decay[3];             /* SSM: [H, dc] */
+    const void* w_out;                  /* SSM: [d, d + H*dh] */
+    const void* w_uq;                   /* RMLA: [H*dh, dc] */
+    const void* w_uk;                   /* RMLA: [Hkv*dh, dc] */
+    const void* w_k2v;                  /* RMLA: [Hkv*dh, Hkv*dh] */
+    const void* w_qr;                   /* RMLA: [H*dhr, d] */
+    const void* w_kr;                   /* RMLA: [Hkv*dhr, d] */
+    const void* c_proj;                 /* RMLA: [d, H*dh] */
+    const float* rope_q_cos; const float* rope_q_sin;   /* RMLA: [max_pos][dhr/2] */
+    const float* rope_k_cos; const float* rope_k_sin;
+    const void* w1; const void* w2; const void* w3;     /* SwiGLU [hidden, d], [d, hidden] */
+} orc_jamba_layer_w;
+
+typedef struct {
+    int dim, n_layers, n_heads, n_kv_heads, head_dim, dhr, dc, ssm_steps, hidden, vocab, max_seq;
+    int nthreads;
+    const void* wte; int qt_wte;
+    const float* ln_f;                  /* LayerNorm */
+    const void* lm_head; int qt_lm;     /* NULL -> tied to wte */
+    const orc_jamba_layer_w* layers;
+} orc_jamba_cfg;
+
+typedef struct orc_jamba orc_jamba;
+orc_jamba* orc_jamba_create(const orc_jamba_cfg* cfg);
+void       orc_jamba_destroy(orc_jamba* m);
+/* GQAInference::forward (infer_gqa.cpp:75-105) over RinaSSMImpl
+ * (arch/ssm/rina_ssm_layer.cu:90-126, kernels/ssm_kernels_fp32.cu:6-47)
+ * and RinaMLAImpl (arch/mla/rina_mla_layer.cu:65-98) layers.  Those layers
+ * keep no state, so the reference's semantics are a full recompute over
+ * all tokens each step (tests/test_infer.cu:58-80).  This restatement
+ * carries the scan state (log-cumsum, weighted cumsum) and the RINA-MLA
+ * K/V rows across calls, in the same per-position fp32 operation order, so
+ * a call at start_pos continuing the previous calls equals the full
+ * recompute bit for bit; start_pos == 0 resets the state. */
+int        orc_jamba_forward(orc_jamba* m, const int* ids, int T, int start_pos, float* logits, int last_only);
+/* greedy decode: full prefill, then steps-1 incremental steps */
+int        orc_jamba_generate(orc_jamba* m, const int* prompt, int n_prompt, int steps, int* out_ids);
+/* greedy decode with the reference's full recompute at every step */
+int        orc_jamba_generate_recompute(orc_jamba* m, const int* prompt, int n_prompt, int steps, int* out_ids);
+
 int orc_num_threads(void);
 
 #ifdef __cplusplus

@@ -132,11 +132,7 @@ bool v_init(void* self, const ModelConfig& c, const TensorMap& w, int l) { retur
 int v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
     return ((GQAImpl*)self)->forward(h, b, B, T, s);
 }
-int v_ws(void* self, int d, int H, int dh) {
-    GQAImpl* g = (GQAImpl*)self;
-    (void)d; (void)H; (void)dh;
-    return g->hd;
-}
+int v_ws(void*, int, int, int) { return 0; }   // no per-token scratch beyond ForwardBuffers
 void v_destroy(void* self) { delete (GQAImpl*)self; }
 const LayerVTable kGQAVTable = {v_init, v_forward, v_ws, v_destroy};
 
@@ -149,4 +145,3 @@ Layer create_gqa_layer() {
     return l;
 }
 
-int gqa_layer_hidden(const Layer& l) { return ((const GQAImpl*)l.impl)->hd; }

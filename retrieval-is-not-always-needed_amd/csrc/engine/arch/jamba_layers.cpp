@@ -1,0 +1,257 @@
+// RINA Jamba hybrid layers on the gfx950 C-ABI, with the reference's tensor
+// names:
+//   InertiaWave SSM (arch/ssm/rina_ssm_layer.cu:90-126): x = LN(h, ln1);
+//     cq = LN(W_dq x, q_norm); mem_k = W_mem[k] cq, dec_k = sigmoid(W_decay[k]
+//     cq) (k < ssm_steps); 3-step aggregation and the log-space scan;
+//     h += W_out [x | sf]; MLP.
+//   RINA-MLA (arch/mla/rina_mla_layer.cu:65-98): x = LN(h, ln1);
+//     cq = LN(W_dqkv x, q_norm); q = W_uq cq, k = W_uk cq, v = W_k2v k;
+//     qr = HF-RoPE(W_qr x), kr = HF-RoPE(W_kr x); causal attention with
+//     query [q | qr], key [k | kr], scale 1/sqrt(dh + dhr); h += c_proj o; MLP.
+//   MLP: h += W2 (SiLU(W1 LN(h, ln2)) * W3 LN(h, ln2)).
+// The reference layers keep no state (every step recomputes the whole
+// sequence, tests/test_infer.cu:58-80).  Here the SSM layer keeps its scan
+// state and the RINA-MLA layer its fp32 K/V rows in device memory, advanced
+// one position per token with the reference's per-position operations, so a
+// decode step equals the full recompute.  A host-position call at
+// start_pos 0 restarts the scan; calls must continue the sequence in order.
+#include <algorithm>
+#include <cstdio>
+#include <string>
+#include "core/buffer.h"
+#include "core/config.h"
+#include "core/layer.h"
+#include "core/tensor.h"
+#include "rina_hip.h"
+
+namespace {
+
+std::string tn(int l, const char* c, const char* p) {
+    char b[160];
+    snprintf(b, sizeof b, "transformer.h.%d.%s.%s", l, c, p);
+    return b;
+}
+
+struct Loader {
+    const TensorMap& w;
+    int l;
+    bool ok = true;
+    QuantType qt = QuantType::FP32;
+    bool first = true;
+    const void* lin(const char* c, const char* p) {
+        const WeightTensor* t = w.get(tn(l, c, p));
+        if (!t) { ok = false; return nullptr; }
+        if (first) { qt = t->quant_type; first = false; }
+        else if (t->quant_type != qt) ok = false;       // one quant type per layer
+        return t->data;
+    }
+    const float* f32(const char* c, const char* p, bool required = true) {
+        const WeightTensor* t = w.get(tn(l, c, p));
+        if (!t && required) ok = false;
+        return t ? (const float*)t->data : nullptr;
+    }
+};
+
+template <typename T>
+bool dev_alloc(T** p, size_t n) {
+    if (hipMalloc((void**)p, n * sizeof(T)) != hipSuccess) { *p = nullptr; return false; }
+    return hipMemset(*p, 0, n * sizeof(T)) == hipSuccess;
+}
+
+struct MLPPart {
+    const void *w1 = nullptr, *w2 = nullptr, *w3 = nullptr;
+    const float *ln2 = nullptr;
+    int hd = 0;
+    int run(float* ht, ForwardBuffers& b, int d, int qt, hipStream_t s) const {
+        int rc;
+        rina_linear_seg up{w1, w3, b.g, hd};
+        if ((rc = rina_hip_linear_fused(&up, 1, qt, ht, 1, d, RINA_EPI_SWIGLU, RINA_PRO_LAYERNORM, ln2, 1e-5f, s)))
+            return rc;
+        rina_linear_seg down{w2, nullptr, ht, d};
+        return rina_hip_linear_fused(&down, 1, qt, b.g, 1, hd, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s);
+    }
+};
+
+struct SSMImpl {
+    int d = 0, H = 0, dh = 0, dc = 0, steps = 0;
+    int qt = 0;
+    const float *ln1 = nullptr, *q_norm = nullptr;
+    const void *w_dq = nullptr, *w_mem[3] = {}, *w_decay[3] = {}, *w_out = nullptr;
+    MLPPart mlp;
+    float *lcs = nullptr, *wcs = nullptr;      // scan state [H*dh]
+    float* scratch = nullptr;                  // x2 [d + H*dh] | cq [dc] | mem [3*H*dh] | dec [3*H]
+
+    ~SSMImpl() {
+        if (lcs) (void)hipFree(lcs);
+        if (wcs) (void)hipFree(wcs);
+        if (scratch) (void)hipFree(scratch);
+    }
+
+    bool init(const ModelConfig& cfg, const TensorMap& w, int l) {
+        d = cfg.dim; H = cfg.n_heads; dh = cfg.head_dim;
+        dc = cfg.d_c > 0 ? cfg.d_c : 160;
+        steps = cfg.ssm_steps > 0 ? cfg.ssm_steps : 3;
+        if (steps > 3) return false;
+        Loader L{w, l};
+        w_dq = L.lin("path", "w_dq.weight");
+        for (int k = 0; k < steps; k++) {
+            char b1[48], b2[48];
+            snprintf(b1, sizeof b1, "w_mem.%d.weight", k);
+            snprintf(b2, sizeof b2, "w_decay.%d.weight", k);
+            w_mem[k] = L.lin("path", b1);
+            w_decay[k] = L.lin("path", b2);
+        }
+        w_out = L.lin("path", "w_out.weight");
+        mlp.w1 = L.lin("mlp", "w1.weight"); mlp.w2 = L.lin("mlp", "w2.weight"); mlp.w3 = L.lin("mlp", "w3.weight");
+        q_norm = L.f32("path", "q_norm.weight");
+        ln1 = L.f32("ln1", "weight");
+        mlp.ln2 = L.f32("ln2", "weight");
+        if (!L.ok) return false;
+        qt = (int)L.qt;
+        const WeightTensor* t1 = w.get(tn(l, "mlp", "w1.weight"));
+        mlp.hd = t1->shape[0];
+        return dev_alloc(&lcs, (size_t)H * dh) && dev_alloc(&wcs, (size_t)H * dh) &&
+               dev_alloc(&scratch, (size_t)d + H * dh + dc + 3 * H * dh + 3 * H);
+    }
+
+    int forward(float* h, ForwardBuffers& b, int T, hipStream_t s) {
+        const int start_pos = b.kv_cache.start_pos;
+        float* x2 = scratch;
+        float* cq = x2 + d + H * dh;
+        float* mem = cq + dc;
+        float* dec = mem + 3 * H * dh;
+        int rc;
+#define CK(x) do { if ((rc = (x)) != RINA_OK) return rc; } while (0)
+        for (int t = 0; t < T; t++) {
+            float* ht = h + (size_t)t * d;
+            CK(rina_hip_layer_norm(ht, x2, ln1, 1, d, 1e-5f, s));                              // :93-95
+            rina_linear_seg sq{w_dq, nullptr, cq, dc};
+            CK(rina_hip_linear_fused(&sq, 1, qt, x2, 1, d, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
+            rina_linear_seg sm[3], sd[3];
+            for (int k = 0; k < steps; k++) {
+                sm[k] = {w_mem[k], nullptr, mem + (size_t)k * H * dh, H * dh};
+                sd[k] = {w_decay[k], nullptr, dec + (size_t)k * H, H};
+            }
+            // q_norm fused as the prologue of the memory and decay projections (:97-101)
+            CK(rina_hip_linear_fused(sm, steps, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
+            CK(rina_hip_linear_fused(sd, steps, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
+            const int reset = (!b.d_pos && start_pos == 0 && t == 0) ? 1 : 0;
+            CK(rina_hip_ssm_step(mem, dec, steps, H, dh, lcs, wcs, x2 + d, reset, s));           // :102-109
+            rina_linear_seg so{w_out, nullptr, ht, d};
+            CK(rina_hip_linear_fused(&so, 1, qt, x2, 1, d + H * dh, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
+            CK(mlp.run(ht, b, d, qt, s));
+        }
+#undef CK
+        return RINA_OK;
+    }
+};
+
+struct RMLAImpl {
+    int d = 0, H = 0, Hkv = 0, dh = 0, dhr = 0, dc = 0, max_seq = 0;
+    int qt = 0;
+    const float *ln1 = nullptr, *q_norm = nullptr;
+    const float *rqc = nullptr, *rqs = nullptr, *rkc = nullptr, *rks = nullptr;
+    const void *w_dqkv = nullptr, *w_uq = nullptr, *w_uk = nullptr, *w_k2v = nullptr, *w_qr = nullptr,
+               *w_kr = nullptr, *c_proj = nullptr;
+    MLPPart mlp;
+    float *ck = nullptr, *cv = nullptr;        // fp32 K [max_seq][Hkv][dh+dhr], V [max_seq][Hkv][dh]
+    float* scratch = nullptr;                  // cq | qr | kr | q | k | v | att
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+
+    ~RMLAImpl() {
+        if (ck) (void)hipFree(ck);
+        if (cv) (void)hipFree(cv);
+        if (scratch) (void)hipFree(scratch);
+        if (ws) (void)hipFree(ws);
+    }
+
+    bool init(const ModelConfig& cfg, const TensorMap& w, int l) {
+        d = cfg.dim; H = cfg.n_heads; Hkv = cfg.n_kv_heads; dh = cfg.head_dim;
+        dhr = cfg.d_h_r > 0 ? cfg.d_h_r : 32;
+        dc = cfg.d_c > 0 ? cfg.d_c : 160;
+        max_seq = cfg.max_seq_len > 0 ? cfg.max_seq_len : 512;
+        if (Hkv <= 0 || H % Hkv) return false;
+        Loader L{w, l};
+        w_dqkv = L.lin("path", "w_dqkv.weight");
+        w_qr = L.lin("path", "w_qr.weight");
+        w_kr = L.lin("path", "w_kr.weight");
+        w_uq = L.lin("path", "w_uq.weight");
+        w_uk = L.lin("path", "w_uk.weight");
+        w_k2v = L.lin("path", "w_k2v.weight");
+        c_proj = L.lin("path", "c_proj.weight");
+        mlp.w1 = L.lin("mlp", "w1.weight"); mlp.w2 = L.lin("mlp", "w2.weight"); mlp.w3 = L.lin("mlp", "w3.weight");
+        q_norm = L.f32("path", "q_norm.weight");
+        ln1 = L.f32("ln1", "weight");
+        mlp.ln2 = L.f32("ln2", "weight");
+        rqc = L.f32("path", "rope_q.cos", false); rqs = L.f32("path", "rope_q.sin", false);
+        rkc = L.f32("path", "rope.cos", false); rks = L.f32("path", "rope.sin", false);
+        if (!L.ok) return false;
+        qt = (int)L.qt;
+        mlp.hd = w.get(tn(l, "mlp", "w1.weight"))->shape[0];
+        ws_bytes = rina_hip_dq_attention_workspace(H, dh + dhr, max_seq);
+        const size_t sc = (size_t)dc + H * dhr + Hkv * dhr + H * dh + 2 * Hkv * dh + H * dh;
+        return dev_alloc(&ck, (size_t)max_seq * Hkv * (dh + dhr)) && dev_alloc(&cv, (size_t)max_seq * Hkv * dh) &&
+               dev_alloc(&scratch, sc) && dev_alloc((uint8_t**)&ws, ws_bytes);
+    }
+
+    int forward(float* h, ForwardBuffers& b, int T, hipStream_t s) {
+        const int start_pos = b.kv_cache.start_pos;
+        float* cq = scratch;
+        float* qr = cq + dc;
+        float* kr = qr + H * dhr;
+        float* q = kr + Hkv * dhr;
+        float* k = q + H * dh;
+        float* v = k + Hkv * dh;
+        float* att = v + Hkv * dh;
+        int rc;
+#define CK(x) do { if ((rc = (x)) != RINA_OK) return rc; } while (0)
+        for (int t = 0; t < T; t++) {
+            float* ht = h + (size_t)t * d;
+            // W_dqkv, W_qr, W_kr share x = LN(h, ln1): one launch with the norm as prologue
+            rina_linear_seg s1[3] = {{w_dqkv, nullptr, cq, dc}, {w_qr, nullptr, qr, H * dhr}, {w_kr, nullptr, kr, Hkv * dhr}};
+            CK(rina_hip_linear_fused(s1, 3, qt, ht, 1, d, RINA_EPI_STORE, RINA_PRO_LAYERNORM, ln1, 1e-5f, s));
+            rina_linear_seg s2[2] = {{w_uq, nullptr, q, H * dh}, {w_uk, nullptr, k, Hkv * dh}};
+            CK(rina_hip_linear_fused(s2, 2, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
+            rina_linear_seg s3{w_k2v, nullptr, v, Hkv * dh};
+            CK(rina_hip_linear_fused(&s3, 1, qt, k, 1, Hkv * dh, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
+            CK(rina_hip_dq_decode_attention(q, qr, k, kr, v, rqc, rqs, rkc, rks, ck, cv, H, Hkv, dh, dhr, dh,
+                                            start_pos + t, b.d_pos, max_seq, att, ws, ws_bytes, s));
+            rina_linear_seg so{c_proj, nullptr, ht, d};
+            CK(rina_hip_linear_fused(&so, 1, qt, att, 1, H * dh, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
+            CK(mlp.run(ht, b, d, qt, s));
+        }
+#undef CK
+        return RINA_OK;
+    }
+};
+
+template <typename Impl>
+bool v_init(void* self, const ModelConfig& c, const TensorMap& w, int l) { return ((Impl*)self)->init(c, w, l); }
+template <typename Impl>
+int v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
+    (void)B;
+    return ((Impl*)self)->forward(h, b, T, s);
+}
+int v_ws(void*, int, int, int) { return 0; }
+template <typename Impl>
+void v_destroy(void* self) { delete (Impl*)self; }
+
+const LayerVTable kSSMVTable = {v_init<SSMImpl>, v_forward<SSMImpl>, v_ws, v_destroy<SSMImpl>};
+const LayerVTable kRMLAVTable = {v_init<RMLAImpl>, v_forward<RMLAImpl>, v_ws, v_destroy<RMLAImpl>};
+
+}  // namespace
+
+Layer create_ssm_layer() {
+    Layer l;
+    l.impl = new SSMImpl();
+    l.vtab = &kSSMVTable;
+    return l;
+}
+
+Layer create_rina_mla_layer() {
+    Layer l;
+    l.impl = new RMLAImpl();
+    l.vtab = &kRMLAVTable;
+    return l;
+}

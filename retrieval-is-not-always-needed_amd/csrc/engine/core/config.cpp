@@ -66,6 +66,7 @@ void set_field(ModelConfig& c, const std::string& k, const std::string& v) {
     else if (k == "n_kv_heads") I(c.n_kv_heads);
     else if (k == "head_dim") I(c.head_dim);
     else if (k == "d_c") I(c.d_c);
+    else if (k == "ssm_steps") I(c.ssm_steps);
     else if (k == "d_h_r") I(c.d_h_r);
     else if (k == "vocab_size") I(c.vocab_size);
     else if (k == "max_seq_len" || k == "block_size") I(c.max_seq_len);

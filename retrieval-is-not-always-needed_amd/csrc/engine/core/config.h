@@ -19,6 +19,7 @@ struct ModelConfig {
     std::string name;
     int dim = 0, n_layers = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0;
     int d_c = 0, d_h_r = 0;
+    int ssm_steps = 0;             // RINA SSM layers (config.h:38)
     int vocab_size = 0, max_seq_len = 0;
     int hidden_dim = 0;            // SwiGLU intermediate (0: from w1's shape)
     bool weight_tying = true;

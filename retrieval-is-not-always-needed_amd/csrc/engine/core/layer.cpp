@@ -24,11 +24,15 @@ int Layer::workspace_per_token(int d, int H, int dh) { return vtab->workspace_pe
 
 Layer create_gqa_layer();
 Layer create_mla_layer();
+Layer create_ssm_layer();
+Layer create_rina_mla_layer();
 
 Layer* create_layer_by_type(const std::string& type) {
     Layer* l = new Layer();
     if (type == "standard_gqa" || type == "standard_attention" || type == "gqa") *l = create_gqa_layer();
     else if (type == "deepseek_mla_dense" || type == "deepseek_mla_moe") *l = create_mla_layer();
+    else if (type == "inertia_wave_ssm" || type == "ssm") *l = create_ssm_layer();
+    else if (type == "sparse_gather_fa" || type == "mla") *l = create_rina_mla_layer();
     else { delete l; return nullptr; }
     return l;
 }

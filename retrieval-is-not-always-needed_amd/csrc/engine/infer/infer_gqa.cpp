@@ -9,14 +9,13 @@
 #include <algorithm>
 #include <cstdio>
 #include <memory>
+#include <string>
 #include <vector>
 #include "core/buffer.h"
 #include "core/layer.h"
 #include "infer/greedy.h"
 #include "infer/infer_base.h"
 #include "rina_hip.h"
-
-int gqa_layer_hidden(const Layer& l);
 
 namespace {
 
@@ -39,8 +38,13 @@ struct GQAInference : DeviceGreedyInference {
             return fail("gqa: incomplete config");
         layers = build_layers(cfg, w);
         if ((int)layers.size() != cfg.n_layers || layers.empty()) return fail("gqa: layer init failed");
-        hd = gqa_layer_hidden(*layers[0]);
-        for (auto& l : layers) hd = std::max(hd, gqa_layer_hidden(*l));
+        // MLP width: the widest w1 of any layer (GQA, SSM or RINA-MLA)
+        hd = cfg.hidden_dim;
+        for (int l = 0; l < cfg.n_layers; l++) {
+            const WeightTensor* t = w.get("transformer.h." + std::to_string(l) + ".mlp.w1.weight");
+            if (t && t->n_dim >= 2) hd = std::max(hd, (int)t->shape[0]);
+        }
+        if (hd <= 0) return fail("gqa: cannot size the MLP buffer (no mlp.w1 and no hidden_dim)");
         max_seq = cfg.max_seq_len > 0 ? cfg.max_seq_len : 512;
         vocab = cfg.vocab_size;
         kvd = cfg.n_kv_heads * cfg.head_dim;

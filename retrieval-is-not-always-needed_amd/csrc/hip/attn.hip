@@ -385,6 +385,115 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(SplitArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention with key width dq = da + db != value width dv = 64
+// (RinaMLAImpl, arch/mla/rina_mla_layer.cu:78-86): query [qa | RoPE_hf(qb)],
+// key [ka | RoPE_hf(kb)] per KV head, scale 1/sqrt(dq).  The append kernel
+// rotates (HF pairs 2i, 2i+1) and writes the current K/V rows into fp32
+// caches [max_seq][Hkv][dq] / [max_seq][Hkv][dv]; the split kernel gives
+// each workgroup 32 positions of one query head (8 per wave, loads issued
+// together, lanes over dims) and writes the same (m, l, O) partials as the
+// GQA split kernel, so the same combine kernel finishes it.
+// ---------------------------------------------------------------------------
+struct DqArgs {
+    const float *qa, *qb, *ka, *kb, *v;
+    const float *qc, *qs, *kc, *ks;     // HF RoPE tables [max_seq][db/2] (NULL: none)
+    float* ck;                          // [max_seq][Hkv][dq]
+    float* cv;                          // [max_seq][Hkv][dv]
+    float* wq;                          // [H][dq] rotated queries
+    int H, Hkv, da, db, dv, start_pos, max_seq;
+    const int* d_pos;
+    float scale;
+};
+
+constexpr int kDqChunk = 32;
+
+// grid H + Hkv: workgroup h < H builds query h; the rest append KV head h - H
+__global__ __launch_bounds__(64) void dq_append_kernel(DqArgs a) {
+    const int pos = read_pos(a.start_pos, a.d_pos);
+    if (pos < 0 || pos >= a.max_seq) return;
+    const int dq = a.da + a.db, hb = a.db / 2, t = threadIdx.x;
+    const bool isq = blockIdx.x < (unsigned)a.H;
+    const int h = isq ? blockIdx.x : blockIdx.x - a.H;
+    const float* xa = isq ? a.qa + (int64_t)h * a.da : a.ka + (int64_t)h * a.da;
+    const float* xb = isq ? a.qb + (int64_t)h * a.db : a.kb + (int64_t)h * a.db;
+    const float* tc = isq ? a.qc : a.kc;
+    const float* ts = isq ? a.qs : a.ks;
+    float* dst = isq ? a.wq + (int64_t)h * dq : a.ck + ((int64_t)pos * a.Hkv + h) * dq;
+    for (int i = t; i < a.da; i += 64) gst(dst + i, gld(xa + i));
+    for (int i = t; i < hb; i += 64) {
+        float x0 = gld(xb + 2 * i), x1 = gld(xb + 2 * i + 1);
+        if (tc) {
+            const float c = gld(tc + (int64_t)pos * hb + i), s = gld(ts + (int64_t)pos * hb + i);
+            const float o0 = fmaf(x0, c, -(x1 * s)), o1 = fmaf(x0, s, x1 * c);
+            x0 = o0; x1 = o1;
+        }
+        gst(dst + a.da + 2 * i, x0);
+        gst(dst + a.da + 2 * i + 1, x1);
+    }
+    if (!isq)
+        for (int i = t; i < a.dv; i += 64) gst(a.cv + ((int64_t)pos * a.Hkv + h) * a.dv + i, gld(a.v + (int64_t)h * a.dv + i));
+}
+
+// grid (nchunk, H); dq <= 128, dv == 64
+__global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
+    __shared__ float s_o[4][64];
+    __shared__ float s_m[4], s_l[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos0 = read_pos(a.start_pos, a.d_pos);
+    if (pos0 < 0 || pos0 >= a.max_seq) return;
+    const int L = pos0 + 1, c = blockIdx.x, h = blockIdx.y;
+    const int j0 = c * kDqChunk;
+    if (j0 >= L) return;
+    const int ncv = min(kDqChunk, L - j0);
+    const int dq = a.da + a.db, kvh = h / (a.H / a.Hkv);
+    const float q0 = gld(a.wq + (int64_t)h * dq + lane);
+    const float q1 = lane + 64 < dq ? gld(a.wq + (int64_t)h * dq + lane + 64) : 0.f;
+    constexpr int PW = kDqChunk / 4;
+    float k0[PW], k1[PW], vv[PW];
+#pragma unroll
+    for (int i = 0; i < PW; i++) {
+        const int pp = wave + 4 * i;
+        const int64_t jp = j0 + (pp < ncv ? pp : 0);
+        const float* kr = a.ck + (jp * a.Hkv + kvh) * dq;
+        k0[i] = gld(kr + lane);
+        k1[i] = lane + 64 < dq ? gld(kr + lane + 64) : 0.f;
+        vv[i] = gld(a.cv + (jp * a.Hkv + kvh) * a.dv + lane);
+    }
+    float m = -INFINITY, l = 0.f, o = 0.f;
+#pragma unroll
+    for (int i = 0; i < PW; i++) {
+        const float sc = wave_sum(fmaf(q0, k0[i], q1 * k1[i])) * a.scale;
+        if (wave + 4 * i < ncv) {
+            const float mn = fmaxf(m, sc);
+            const float al = expf(m - mn), pe = expf(sc - mn);
+            l = fmaf(l, al, pe);
+            o = fmaf(o, al, pe * vv[i]);
+            m = mn;
+        }
+    }
+    s_o[wave][lane] = o;
+    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+    __syncthreads();
+    if (wave == 0) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w]);
+        float ot = 0.f, lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float aw = s_m[w] == -INFINITY ? 0.f : expf(s_m[w] - M);
+            ot = fmaf(s_o[w][lane], aw, ot);
+            lt = fmaf(s_l[w], aw, lt);
+        }
+        gst(p.ws_o + ((int64_t)c * a.H + h) * 64 + lane, ot);
+        if (lane == 0) {
+            gst(p.ws_m + (int64_t)c * a.H + h, M);
+            gst(p.ws_l + (int64_t)c * a.H + h, lt);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Generic causal kernel: any T, dh <= 256, pre-RoPE caches.  One wave per
 // (query head, query row); keys in order with the online normalized update
 // of flash_fp32.cu:55-81, parallel over dims.
@@ -577,4 +686,49 @@ extern "C" int rina_hip_gqa_decode_attention(const float* q, const float* k, con
     sa.mode = mode; sa.H = H; sa.Hkv = Hkv; sa.start_pos = start_pos; sa.max_seq = max_seq; sa.d_pos = d_pos;
     sa.scale = 1.0f / sqrtf((float)dh);
     return launch_split_mode<true>(sa, H / Hkv, ws_bytes, workspace, as_stream(stream));
+}
+
+extern "C" size_t rina_hip_dq_attention_workspace(int H, int dq, int max_pos) {
+    if (H < 1 || dq < 1 || max_pos < 1) return 0;
+    const size_t nch = ((size_t)max_pos + kDqChunk - 1) / kDqChunk;
+    return ((size_t)H * dq + nch * H * (2 + 64)) * sizeof(float);
+}
+
+extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, const float* ka, const float* kb,
+                                            const float* v, const float* rope_q_cos, const float* rope_q_sin,
+                                            const float* rope_k_cos, const float* rope_k_sin, float* cache_k,
+                                            float* cache_v, int H, int Hkv, int da, int db, int dv, int start_pos,
+                                            const int* d_pos, int max_seq, float* out, void* workspace,
+                                            size_t ws_bytes, void* stream) {
+    if (!qa || !ka || !v || !cache_k || !cache_v || !out || H < 1 || Hkv < 1 || da < 1 || db < 0 || max_seq < 1)
+        return RINA_ERR_ARG;
+    if (db > 0 && (!qb || !kb)) return RINA_ERR_ARG;
+    if ((!rope_q_cos) != (!rope_q_sin) || (!rope_k_cos) != (!rope_k_sin)) return RINA_ERR_ARG;
+    if (H % Hkv || dv != 64 || da + db > 128 || da + db < 64 || db % 2) return RINA_ERR_SHAPE;
+    if (!d_pos && (start_pos < 0 || start_pos >= max_seq)) return RINA_ERR_RANGE;
+    const int max_pos = d_pos ? max_seq : start_pos + 1;
+    const int nch = (max_pos + kDqChunk - 1) / kDqChunk;
+    if (nch > kMaxChunks) return RINA_ERR_SHAPE;                 // combine merges <= 64 chunks
+    const size_t need = rina_hip_dq_attention_workspace(H, da + db, max_pos);
+    if (!workspace || ws_bytes < need) return RINA_ERR_WORKSPACE;
+    DqArgs a{};
+    a.qa = qa; a.qb = qb; a.ka = ka; a.kb = kb; a.v = v;
+    a.qc = rope_q_cos; a.qs = rope_q_sin; a.kc = rope_k_cos; a.ks = rope_k_sin;
+    a.ck = cache_k; a.cv = cache_v; a.wq = (float*)workspace;
+    a.H = H; a.Hkv = Hkv; a.da = da; a.db = db; a.dv = dv;
+    a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos;
+    a.scale = 1.0f / sqrtf((float)(da + db));
+    SplitArgs p{};
+    p.ws_m = a.wq + (size_t)H * (da + db);
+    p.ws_l = p.ws_m + (size_t)nch * H;
+    p.ws_o = p.ws_l + (size_t)nch * H;
+    p.out = out; p.H = H; p.start_pos = start_pos; p.max_seq = max_seq; p.d_pos = d_pos; p.chunk = kDqChunk;
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(dq_append_kernel, dim3(H + Hkv), dim3(64), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(dq_split_kernel, dim3(nch, H), dim3(256), 0, st, a, p);
+    RINA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(H), dim3(256), 0, st, p);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
 }

@@ -324,3 +324,110 @@ class SynthDeepSeek:
             self._eng.rina_model_destroy(self.model)
             self.model = None
         self.arena.keep.clear()
+
+
+JAMBA = dict(name="rina-gen6-jamba", dim=640, n_layers=16, n_heads=10, n_kv_heads=5, head_dim=64, d_h_r=32, d_c=160,
+             ssm_steps=3, hidden_dim=1536, vocab_size=128256)
+
+
+def jamba_types(n_layers, every=4):
+    """12 SSM + 4 attention layers for 16: attention at every 4th layer."""
+    return ["sparse_gather_fa" if l % every == every - 1 else "inertia_wave_ssm" for l in range(n_layers)]
+
+
+class SynthJamba:
+    """RINA Gen6 Jamba hybrid at random init (config 5): InertiaWave SSM and
+    RINA-MLA layers with Q4_0 linears packed on the device, LayerNorm, fp32
+    tied embedding / LM head, HF RoPE tables."""
+
+    def __init__(self, cfg=JAMBA, seed=1, max_seq=2048, keep_host=False, std=0.02):
+        torch = _torch()
+        c = self.cfg = dict(cfg)
+        self.max_seq = max_seq
+        self.types = jamba_types(c["n_layers"])
+        self.host, self.dev = {}, {}
+        d, H, Hkv, dh, dhr, dc, hd, V = (c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["d_h_r"], c["d_c"],
+                                         c["hidden_dim"], c["vocab_size"])
+        header = {"name": c["name"], "dim": d, "n_layers": c["n_layers"], "n_heads": H, "n_kv_heads": Hkv,
+                  "head_dim": dh, "d_h_r": dhr, "d_c": dc, "ssm_steps": c["ssm_steps"], "vocab_size": V,
+                  "max_seq_len": max_seq, "hidden_dim": hd, "layers": [{"type": t} for t in self.types]}
+        eng = load_engine()
+        self._eng = eng
+        self.arena = DeviceArena()
+        self.model = eng.rina_model_create(json.dumps(header).encode())
+        if not self.model:
+            raise RuntimeError(eng.rina_engine_last_error().decode())
+        idx = [0]
+
+        def add(name, shape, qt, t, host=None):
+            shp = (C.c_int64 * len(shape))(*shape)
+            check(eng.rina_model_add_tensor(self.model, name.encode(), qt, len(shape), shp, t.data_ptr()),
+                  "add_tensor " + name)
+            self.arena.put(t)
+            self.dev[name] = t
+            if keep_host:
+                self.host[name] = host if host is not None else t.cpu().numpy()
+
+        def lin(name, rows, cols, s=std):
+            idx[0] += 1
+            add(name, (rows, cols), QT_Q4_0, pack_on_device(normal(seed * 1000003 + idx[0], rows * cols, s), QT_Q4_0))
+
+        def f32(name, a):
+            a = np.ascontiguousarray(a, np.float32)
+            add(name, a.shape, QT_FP32, torch.from_numpy(a).cuda(), a)
+
+        ang = np.outer(np.arange(max_seq, dtype=np.float32),
+                       (1.0 / (10000.0 ** (np.arange(0, dhr, 2, dtype=np.float32) / dhr))).astype(np.float32))
+        cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+        ones = np.ones(d, np.float32)
+        for l, t in enumerate(self.types):
+            p = "transformer.h.%d." % l
+            f32(p + "ln1.weight", ones)
+            f32(p + "ln2.weight", ones)
+            f32(p + "path.q_norm.weight", np.ones(dc, np.float32))
+            if t == "inertia_wave_ssm":
+                lin(p + "path.w_dq.weight", dc, d)
+                for k in range(c["ssm_steps"]):
+                    lin(p + "path.w_mem.%d.weight" % k, H * dh, dc)
+                    lin(p + "path.w_decay.%d.weight" % k, H, dc)
+                lin(p + "path.w_out.weight", d, d + H * dh)
+            else:
+                lin(p + "path.w_dqkv.weight", dc, d)
+                lin(p + "path.w_uq.weight", H * dh, dc)
+                lin(p + "path.w_uk.weight", Hkv * dh, dc)
+                lin(p + "path.w_k2v.weight", Hkv * dh, Hkv * dh)
+                lin(p + "path.w_qr.weight", H * dhr, d)
+                lin(p + "path.w_kr.weight", Hkv * dhr, d)
+                lin(p + "path.c_proj.weight", d, H * dh)
+                for nm, a in (("rope_q.cos", cos), ("rope_q.sin", sin), ("rope.cos", cos), ("rope.sin", sin)):
+                    f32(p + "path." + nm, a)
+            lin(p + "mlp.w1.weight", hd, d)
+            lin(p + "mlp.w2.weight", d, hd)
+            lin(p + "mlp.w3.weight", hd, d)
+        f32("transformer.wte.weight", normal(seed * 1000003, V * d, std).reshape(V, d))
+        f32("transformer.ln_f.weight", ones)
+
+    def bytes_per_token(self, pos):
+        c = self.cfg
+        d, H, Hkv, dh, dhr, dc, hd, V = (c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["d_h_r"], c["d_c"],
+                                         c["hidden_dim"], c["vocab_size"])
+        q4 = lambda n: n // 32 * 18
+        mlp = 3 * q4(hd * d)
+        ssm = q4(dc * d) + c["ssm_steps"] * (q4(H * dh * dc) + q4(H * dc)) + q4(d * (d + H * dh))
+        att = (q4(dc * d) + q4(H * dh * dc) + q4(Hkv * dh * dc) + q4(Hkv * dh * Hkv * dh) + q4(H * dhr * d) +
+               q4(Hkv * dhr * d) + q4(d * H * dh) + (pos + 1) * Hkv * (dh + dhr + dh) * 4)
+        n_att = sum(1 for t in self.types if t != "inertia_wave_ssm")
+        n_ssm = len(self.types) - n_att
+        return n_ssm * (ssm + mlp) + n_att * (att + mlp) + V * d * 4
+
+    def infer(self, max_seq=None):
+        h = self._eng.rina_infer_create(self.model, b"gqa", None, max_seq or self.max_seq)
+        if not h:
+            raise RuntimeError(self._eng.rina_engine_last_error().decode())
+        return h
+
+    def close(self):
+        if self.model:
+            self._eng.rina_model_destroy(self.model)
+            self.model = None
+        self.arena.keep.clear()

@@ -1,0 +1,153 @@
+"""RINA Jamba hybrid on the GPU: the RINA-MLA decode attention against a
+float64 restatement, and the engine (SSM + RINA-MLA layers through the
+"gqa" Inference) against the CPU oracle: logits and greedy tokens, tiny
+and at the config-5 shape."""
+import ctypes as C
+import importlib
+
+import numpy as np
+import pytest
+
+import _jamba_tiny as jt
+import _numpy_ref as nr
+from _util import assert_close, dev, empty, host, ok, rng, stream
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("P,use_dpos", [(0, False), (9, False), (70, True), (300, False)])
+@pytest.mark.parametrize("H,Hkv,da,db", [(10, 5, 64, 32), (4, 2, 64, 16)])
+def test_dq_decode_attention(rina, P, use_dpos, H, Hkv, da, db):
+    hip = rina.load_hip()
+    dq, dv = da + db, 64
+    max_seq = P + 5
+    r = rng(P + H + db)
+    ck = r.standard_normal((max_seq, Hkv, dq)).astype(np.float32)
+    cv = r.standard_normal((max_seq, Hkv, dv)).astype(np.float32)
+    qa = r.standard_normal((H, da)).astype(np.float32)
+    qb = r.standard_normal((H, db)).astype(np.float32)
+    ka = r.standard_normal((Hkv, da)).astype(np.float32)
+    kb = r.standard_normal((Hkv, db)).astype(np.float32)
+    v = r.standard_normal((Hkv, dv)).astype(np.float32)
+    ang = np.outer(np.arange(max_seq), 1.0 / 10000 ** (np.arange(0, db, 2) / db)).astype(np.float32)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+    def rope(x):   # HF pairs at position P, reference fma form in fp32
+        c, s = cos[P], sin[P]
+        y = x.copy()
+        x0, x1 = x[..., 0::2], x[..., 1::2]
+        y[..., 0::2] = (x0.astype(np.float64) * c - (x1 * s).astype(np.float32)).astype(np.float32)
+        y[..., 1::2] = (x0.astype(np.float64) * s + (x1 * c).astype(np.float32)).astype(np.float32)
+        return y
+
+    qf = np.concatenate([qa, rope(qb)], axis=1).astype(np.float64)
+    kn = np.concatenate([ka, rope(kb)], axis=1)
+    K = ck.astype(np.float64).copy()
+    V = cv.astype(np.float64).copy()
+    K[P], V[P] = kn, v
+    rep = H // Hkv
+    ref = np.concatenate([nr.softmax_attn(qf[h], K[: P + 1, h // rep], V[: P + 1, h // rep], 1 / np.sqrt(dq))
+                          for h in range(H)])
+    wsb = hip.rina_hip_dq_attention_workspace(H, dq, max_seq)
+    ws = empty(wsb, "uint8")
+    ckd, cvd = dev(ck), dev(cv)
+    od = empty(H * dv)
+    cd, sd = dev(cos), dev(sin)
+    pos = dev(np.array([P], np.int32)) if use_dpos else None
+    ok(hip.rina_hip_dq_decode_attention(dev(qa).data_ptr(), dev(qb).data_ptr(), dev(ka).data_ptr(),
+                                        dev(kb).data_ptr(), dev(v).data_ptr(), cd.data_ptr(), sd.data_ptr(),
+                                        cd.data_ptr(), sd.data_ptr(), ckd.data_ptr(), cvd.data_ptr(), H, Hkv, da, db,
+                                        dv, 0 if use_dpos else P, pos.data_ptr() if use_dpos else None, max_seq,
+                                        od.data_ptr(), ws.data_ptr(), wsb, stream()), "dq attention")
+    assert_close(host(od), ref, what="dq attention P %d" % P)
+    gk = host(ckd).reshape(max_seq, Hkv, dq)
+    assert np.max(np.abs(gk[P] - kn)) <= 2e-6 * np.max(np.abs(kn))          # appended K row (rotated)
+    assert np.array_equal(host(cvd).reshape(max_seq, Hkv, dv)[P], v)
+    keep = np.ones(max_seq, bool)
+    keep[P] = False
+    assert np.array_equal(gk[keep], ck[keep])
+
+
+def header(max_seq, cfg=jt.CFG, types=jt.TYPES):
+    c = cfg
+    return {"name": c["name"], "dim": c["dim"], "n_layers": c["n_layers"], "n_heads": c["n_heads"],
+            "n_kv_heads": c["n_kv_heads"], "head_dim": c["head_dim"], "d_h_r": c["d_h_r"], "d_c": c["d_c"],
+            "ssm_steps": c["ssm_steps"], "vocab_size": c["vocab_size"], "max_seq_len": max_seq,
+            "hidden_dim": c["hidden_dim"], "layers": [{"type": t} for t in types]}
+
+
+@pytest.fixture(scope="module")
+def tiny_jamba(rina, orc):
+    synth = importlib.import_module("rina_amd.synth")
+    max_seq = 48
+    tensors, mats, shapes = jt.build(orc, seed=21, max_pos=max_seq)
+    qts = {n: (6 if a.dtype == np.float32 else jt.Q4_0) for n, a in tensors.items()}
+    up = {n: (qts[n], shapes[n], tensors[n]) for n in tensors}
+    hm = synth.HostModel(header(max_seq), up)
+    yield hm, tensors, max_seq
+    hm.close()
+
+
+def test_jamba_engine_forward_logits(rina, orc, tiny_jamba):
+    import torch
+    hm, tensors, max_seq = tiny_jamba
+    eng = rina.load_engine()
+    inf = hm.infer("gqa", max_seq=max_seq)
+    V = jt.CFG["vocab_size"]
+    ids = np.array([5, 17, 3, 90, 42, 7], np.int32)
+    lg = empty(len(ids) * V)
+    rina.check(eng.rina_infer_forward(inf, torch.from_numpy(ids).cuda().data_ptr(), lg.data_ptr(), 1, len(ids), 0,
+                                      stream()), "forward")
+    m, hold = orc.jamba_from_tensors(jt.CFG, tensors, jt.TYPES, jt.Q4_0, max_seq)
+    L = orc.load()
+    ref = np.zeros((len(ids), V), np.float32)
+    assert L.orc_jamba_forward(m, ids.ctypes.data, len(ids), 0, ref.ctypes.data, 0) == 0
+    assert_close(host(lg).reshape(len(ids), V), ref, what="jamba prefill logits")
+    for t, nxt in enumerate([11, 64, 2]):
+        x = np.array([nxt], np.int32)
+        rina.check(eng.rina_infer_forward(inf, torch.from_numpy(x).cuda().data_ptr(), lg.data_ptr(), 1, 1, 6 + t,
+                                          stream()), "decode")
+        r1 = np.zeros(V, np.float32)
+        L.orc_jamba_forward(m, x.ctypes.data, 1, 6 + t, r1.ctypes.data, 0)
+        assert_close(host(lg)[:V], r1, what="jamba decode logits %d" % t)
+    L.orc_jamba_destroy(m)
+    eng.rina_infer_destroy(inf)
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_jamba_engine_greedy_identical(rina, orc, tiny_jamba, use_graph):
+    hm, tensors, max_seq = tiny_jamba
+    eng = rina.load_engine()
+    inf = hm.infer("gqa", max_seq=max_seq)
+    prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+    steps = 24
+    out = (C.c_int * steps)()
+    rina.check(eng.rina_infer_generate(inf, (C.c_int * len(prompt))(*prompt), len(prompt), steps, out,
+                                       1 if use_graph else 0, stream(), None), "generate")
+    eng.rina_infer_destroy(inf)
+    m, hold = orc.jamba_from_tensors(jt.CFG, tensors, jt.TYPES, jt.Q4_0, max_seq)
+    ref = orc.jamba_generate(m, prompt, steps, recompute=True)     # the reference's semantics
+    orc.load().orc_jamba_destroy(m)
+    assert list(out) == ref
+
+
+def test_jamba_config5_shape_greedy(rina, orc):
+    """config-5 widths (640d, 10/5 heads, d_c 160, 12 SSM + 4 RINA-MLA,
+    vocab 128256, Q4_0): greedy tokens identical to the oracle."""
+    synth = importlib.import_module("rina_amd.synth")
+    sm = synth.SynthJamba(seed=3, max_seq=64, keep_host=True)
+    try:
+        eng = rina.load_engine()
+        inf = sm.infer()
+        prompt = [101, 2047, 9, 55555, 3, 777, 12, 40000]
+        steps = 8
+        out = (C.c_int * steps)()
+        rina.check(eng.rina_infer_generate(inf, (C.c_int * len(prompt))(*prompt), len(prompt), steps, out, 1,
+                                           stream(), None), "generate")
+        eng.rina_infer_destroy(inf)
+        m, hold = orc.jamba_from_tensors(sm.cfg, sm.host, sm.types, jt.Q4_0, 64)
+        ref = orc.jamba_generate(m, prompt, steps)
+        orc.load().orc_jamba_destroy(m)
+        assert list(out) == ref
+    finally:
+        sm.close()
