@@ -76,6 +76,7 @@ def main():
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--no-config4", action="store_true", help="skip the DeepSeek MLA + MoE (config 4) decode line")
     ap.add_argument("--config4-steps", type=int, default=32)
+    ap.add_argument("--no-config5", action="store_true", help="skip the RINA Jamba (config 5) decode line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X in this build "
@@ -191,6 +192,35 @@ def main():
         del ds
         torch.cuda.empty_cache()
 
+    # ---- config 5: RINA Gen6 Jamba hybrid, 64-token prompt then 128 greedy steps
+    cfg5 = None
+    if not args.no_config5:
+        p5, s5 = 64, 128
+        jm = synth.SynthJamba(seed=1, max_seq=p5 + s5 + 8)
+        inf5 = jm.infer()
+        pr5 = np.random.default_rng(5).integers(0, jm.cfg["vocab_size"], p5).astype(np.int32)
+        first5 = (C.c_int * 1)()
+        rina.check(eng.rina_infer_generate(inf5, pr5.ctypes.data_as(C.POINTER(C.c_int)), p5, 1, first5, 1, st, None),
+                   "config 5 prefill")
+        out5 = (C.c_int * s5)()
+        torch.cuda.synchronize()
+        tq = time.perf_counter()
+        rina.check(eng.rina_infer_decode(inf5, s5, out5, 1, st, None), "config 5 decode")
+        torch.cuda.synchronize()
+        w5 = time.perf_counter() - tq
+        eng.rina_infer_destroy(inf5)
+        b5 = jm.bytes_per_token(p5 + s5 // 2)
+        cfg5 = {"workload": "RINA Gen6 Jamba hybrid at random init: 640d, 16 layers (12 InertiaWave SSM + 4 RINA-MLA), "
+                            "10/5 heads, d_c 160, LayerNorm + SwiGLU 1536, vocab 128256, Q4_0 linears, fp32 tied LM "
+                            "head, %d-token prompt, %d greedy steps" % (p5, s5),
+                "tokens_per_s": round(s5 / w5, 2), "ms_per_step": round(w5 * 1e3 / s5, 4), "steps": s5,
+                "bytes_per_token": b5, "hbm_gbps": round(b5 * s5 / w5 / 1e9, 1),
+                "hbm_frac": round(b5 * s5 / w5 / HBM_PEAK, 4), "tokens_head": list(first5) + list(out5)[:7]}
+        log("config 5: %.3f ms/step, %.1f tok/s" % (w5 * 1e3 / s5, s5 / w5))
+        jm.close()
+        del jm
+        torch.cuda.empty_cache()
+
     # ---- CPU baseline: the oracle (scalar C restatement) decoding the same model
     cpu = None
     if want_cpu:
@@ -243,6 +273,7 @@ def main():
         "decode_hbm_gbps": round(per_token * tok_s / 1e9, 1),
         "decode_hbm_frac": round(per_token * tok_s / HBM_PEAK, 4),
         "config4_deepseek_mla_moe": cfg4,
+        "config5_rina_jamba": cfg5,
         "cpu_baseline": cpu,
         "tokens_head": tokens[:8],
     }
