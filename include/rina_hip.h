@@ -108,6 +108,12 @@ int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int quant_type,
 int rina_hip_pack_weights(int quant_type, const float* src, int64_t n,
                           void* dst, void* stream);
 
+/* Pack n fp32 values (any n; ceil(n/32) blocks) into RINA_QT_Q4_0 with the
+ * HF loader's rules (src/loader_hf.cpp:196-230): q = clamp(roundf(x/scale),
+ * -7, 7), fp16 scale by truncation (exponent <= 0 -> 0, >= 31 -> 0x7FFF
+ * class); a short last block leaves the missing elements' bytes zero. */
+int rina_hip_pack_weights_hf(const float* src, int64_t n, void* dst, void* stream);
+
 /* Dequantize n elements of a packed weight stream (flat element order) to
  * fp32.  Q2_K replaces dequant_block_q2_K_gpu (ops/linear.cu:322-338);
  * Q4_0/Q4_0F follow the matvec dequant rule (ops/linear.cu:77-81). */

@@ -36,6 +36,7 @@ _HIP_SIGS = {
     "rina_hip_linear_fused": (I32, [C.POINTER(LinearSeg), I32, I32, VP, I32, I32, I32, I32, VP, F32, VP]),
     "rina_hip_pack_weights": (I32, [I32, VP, I64, VP, VP]),
     "rina_hip_dequant_weights": (I32, [I32, VP, I64, VP, VP]),
+    "rina_hip_pack_weights_hf": (I32, [VP, I64, VP, VP]),
     "rina_hip_kv_quantize": (I32, [I32, VP, VP, I64, VP]),
     "rina_hip_kv_dequant": (I32, [I32, VP, VP, I64, VP]),
     "rina_hip_kv_region_bytes": (SZ, [I32, I32, I32, I32]),

@@ -64,6 +64,42 @@ __global__ void pack_q4_kernel(int fp32_scale, const float* __restrict__ src, ui
     }
 }
 
+// fp32 -> fp16 bits by truncation (src/loader_hf.cpp:208-216): top 10
+// mantissa bits, biased exponent <= 0 -> signed zero, >= 31 -> 0x7FFF class.
+__device__ __forceinline__ uint32_t f32_to_f16_trunc(float f) {
+    const uint32_t p = __float_as_uint(f);
+    const uint32_t sign = (p >> 31) & 1u;
+    int exp = (int)((p >> 23) & 0xFFu) - 127 + 15;
+    uint32_t mant = (p >> 13) & 0x3FFu;
+    if (exp <= 0) { exp = 0; mant = 0; }
+    else if (exp >= 31) { exp = 31; mant = 0x3FFu; }
+    return (sign << 15) | ((uint32_t)exp << 10) | mant;
+}
+
+// HF-loader Q4_0 quantizer (src/loader_hf.cpp:196-230): scale = max(amax/7,
+// 1e-10) over the block's present elements, q = clamp(roundf(x/scale), -7, 7)
+// + 7, truncating fp16 scale; bytes of a short last block's missing
+// elements stay zero.  One thread per block.
+__global__ void pack_q4_hf_kernel(const float* __restrict__ src, uint8_t* __restrict__ dst, int64_t n, int64_t nb) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const int64_t start = b * 32;
+    const int cnt = (int)min((int64_t)32, n - start);
+    float amax = 0.f;
+    for (int i = 0; i < cnt; i++) amax = fmaxf(amax, fabsf(src[start + i]));
+    float scale = amax / 7.0f;
+    if (scale < 1e-10f) scale = 1e-10f;
+    uint32_t nib[4] = {0, 0, 0, 0};
+    for (int i = 0; i < cnt; i++) {
+        int q = (int)roundf(src[start + i] / scale);
+        q = min(max(q, -7), 7) + 7;
+        nib[i >> 3] |= (uint32_t)(q & 0xF) << ((i & 7) * 4);
+    }
+    uint16_t* o = (uint16_t*)(dst + b * 18);
+    o[0] = (uint16_t)f32_to_f16_trunc(scale);
+    for (int d = 0; d < 4; d++) { o[1 + 2 * d] = (uint16_t)nib[d]; o[2 + 2 * d] = (uint16_t)(nib[d] >> 16); }
+}
+
 __global__ void dequant_weights_kernel(int qt, const uint8_t* __restrict__ w, float* __restrict__ out, int64_t n) {
     int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= n) return;
@@ -187,6 +223,17 @@ extern "C" int rina_hip_pack_weights(int qt, const float* src, int64_t n, void* 
     if (nb == 0) return RINA_OK;
     hipLaunchKernelGGL(pack_q4_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, as_stream(stream),
                        qt == RINA_QT_Q4_0F ? 1 : 0, src, (uint8_t*)dst, nb);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_pack_weights_hf(const float* src, int64_t n, void* dst, void* stream) {
+    if (!src || !dst || n < 0) return RINA_ERR_ARG;
+    if ((uintptr_t)dst % 2) return RINA_ERR_ARG;
+    const int64_t nb = (n + 31) / 32;
+    if (nb == 0) return RINA_OK;
+    hipLaunchKernelGGL(pack_q4_hf_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, as_stream(stream), src,
+                       (uint8_t*)dst, n, nb);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }

@@ -51,6 +51,23 @@ def test_pack_weights_bitexact(rina, orc, qt):
     assert np.array_equal(host(gpu_pack(rina, qt, x)), orc.pack(qt, x))
 
 
+@pytest.mark.parametrize("n", [32 * 4001, 32 * 57 + 13, 5])
+def test_pack_weights_hf_bitexact(rina, orc, n):
+    """HF-loader quantizer: roundf, truncating fp16 (flush and saturate
+    classes), ragged last block, the 0.49999997f rounding edge."""
+    r = rng(n)
+    x = (r.standard_normal(n) * 0.05).astype(np.float32)
+    if n > 32 * 8:
+        x[:32] = 0.0                                             # scale clamp 1e-10 -> exponent <= 0
+        x[32:64] = r.uniform(-1e-4, 1e-4, 32)                    # tiny scale: flushed fp16
+        x[64:96] = r.uniform(-1e6, 1e6, 32)                      # scale > 65504: 0x7FFF class
+        x[96:128] = np.float32(7.0) * np.arange(32, dtype=np.float32) / 31
+        x[100] = np.float32(0.49999997) * (x[96:128].max() / 7)  # near-.5 tie
+    out = empty((n + 31) // 32 * 18, "uint8")
+    ok(rina.load_hip().rina_hip_pack_weights_hf(dev(x).data_ptr(), n, out.data_ptr(), stream()), "pack hf")
+    assert np.array_equal(host(out), orc.pack(5, x, hf=True))
+
+
 @pytest.mark.parametrize("qt", [5, 7, 10, 6])
 def test_dequant_weights_bitexact(rina, orc, qt):
     n = 256 * 300
