@@ -238,6 +238,26 @@ int rina_hip_moe_ffn(const float* x, const void* gate_exps, const void* up_exps,
                      int d, int ffn, const float* shared_out, float* h, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* The whole MoE MLP block of one token (forward_moe,
+ * deepseek_mla_layer.cu:291-350) for Q2_K experts and shared experts with an
+ * fp32 router, in three launches and without the reference's host round
+ * trip: a2 = RMSNorm(h, ln2); router logits = gate_inp a2; top-k of their
+ * softmax (as rina_hip_moe_topk); G = SiLU(W_g a2) * (W_u a2) for the shared
+ * FFN (shared_ffn rows) and the k selected experts (ffn rows each);
+ * h += down_sh G_sh + sum_j probs[j] down[e_j] G_j, j ascending.  Shapes:
+ * d, ffn <= 2048, d, ffn, shared_ffn multiples of 32, n_experts <= 64,
+ * shared_ffn + k * ffn <= 16384; other shapes and formats return
+ * RINA_ERR_SHAPE / RINA_ERR_QTYPE before anything is launched.  h, ln2,
+ * gate_inp and workspace 16-byte aligned; workspace:
+ * rina_hip_moe_block_workspace bytes (holds a2, the logits, the selected
+ * ids / probs and G after the call). */
+size_t rina_hip_moe_block_workspace(int d, int n_experts, int k, int ffn, int shared_ffn);
+int rina_hip_moe_block(float* h, const float* ln2, float eps, const void* gate_inp, int qt_gate_inp,
+                       const void* gate_sh, const void* up_sh, const void* down_sh, int shared_ffn,
+                       const void* gate_exps, const void* up_exps, const void* down_exps, int quant_type,
+                       int64_t stride_gate_up, int64_t stride_down, int n_experts, int k, int d, int ffn,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* ====================================================================== */
 /* RINA Jamba hybrid (SSM and RINA-MLA layers)                             */
 /* ====================================================================== */

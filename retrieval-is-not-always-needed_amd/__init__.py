@@ -54,6 +54,9 @@ _HIP_SIGS = {
     "rina_hip_moe_topk": (I32, [VP, I32, I32, VP, VP, VP]),
     "rina_hip_moe_workspace": (SZ, [I32, I32]),
     "rina_hip_moe_ffn": (I32, [VP, VP, VP, VP, I32, I64, I64, I32, VP, VP, I32, I32, I32, VP, VP, VP, SZ, VP]),
+    "rina_hip_moe_block_workspace": (SZ, [I32, I32, I32, I32, I32]),
+    "rina_hip_moe_block": (I32, [VP, VP, F32, VP, I32, VP, VP, VP, I32, VP, VP, VP, I32, I64, I64, I32, I32, I32,
+                                 I32, VP, SZ, VP]),
     "rina_hip_ssm_step": (I32, [VP, VP, I32, I32, I32, VP, VP, VP, I32, VP]),
     "rina_hip_dq_attention_workspace": (SZ, [I32, I32, I32]),
     "rina_hip_dq_decode_attention": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, I32, I32, I32, VP,

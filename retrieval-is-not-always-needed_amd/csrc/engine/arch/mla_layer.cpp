@@ -37,6 +37,15 @@ struct MLAImpl {
     WeightRef w_q, w_kv_a, w_kv_b, w_o, w1, w2, w3;
     WeightRef gate_inp, gate_exps, up_exps, down_exps, gate_sh, up_sh, down_sh;
     const float *ln1 = nullptr, *ln2 = nullptr, *k_norm = nullptr, *rope_c = nullptr, *rope_s = nullptr;
+    // fused MoE block (rina_hip_moe_block) and its workspace; shapes it does
+    // not take use the per-operator composition below
+    bool moe_block = false;
+    void* moe_ws = nullptr;
+    size_t moe_ws_bytes = 0;
+
+    ~MLAImpl() {
+        if (moe_ws) (void)hipFree(moe_ws);
+    }
 
     bool init(const ModelConfig& cfg, const TensorMap& w, int l) {
         layer = l;
@@ -81,6 +90,11 @@ struct MLAImpl {
             stride_gu = (int64_t)quantized_size((int64_t)F * d, gate_exps.qt);
             stride_dn = (int64_t)quantized_size((int64_t)d * F, down_exps.qt);
             ok = ok && gate_exps.qt == up_exps.qt && gate_exps.qt == down_exps.qt && gate_sh.qt == up_sh.qt;
+            if (ok && gate_exps.qt == QuantType::GGML_Q2_K && gate_sh.qt == QuantType::GGML_Q2_K &&
+                down_sh.qt == QuantType::GGML_Q2_K && gate_inp.qt == QuantType::FP32) {
+                moe_ws_bytes = rina_hip_moe_block_workspace(d, E, K, F, S);
+                moe_block = moe_ws_bytes > 0 && hipMalloc(&moe_ws, moe_ws_bytes) == hipSuccess;
+            }
         } else {
             ok = ok & ref(tn(l, "mlp", "w1.weight"), w1) & ref(tn(l, "mlp", "w2.weight"), w2) &
                  ref(tn(l, "mlp", "w3.weight"), w3);
@@ -129,6 +143,16 @@ struct MLAImpl {
             return RINA_OK;
         }
         // forward_moe (:291-350), one token at a time
+        if (moe_block) {
+            for (int t = 0; t < n; t++) {
+                rc = rina_hip_moe_block(h + (size_t)t * d, ln2, 1e-5f, gate_inp.data, (int)gate_inp.qt, gate_sh.data,
+                                        up_sh.data, down_sh.data, S, gate_exps.data, up_exps.data, down_exps.data,
+                                        (int)gate_exps.qt, stride_gu, stride_dn, E, K, d, F, moe_ws, moe_ws_bytes, s);
+                if (rc == RINA_ERR_SHAPE || rc == RINA_ERR_QTYPE) { moe_block = false; break; }   // nothing launched
+                if (rc != RINA_OK) return rc;
+            }
+            if (moe_block) return RINA_OK;
+        }
         float* base = b.mla;
         float* a2 = base;
         float* acc = a2 + d;

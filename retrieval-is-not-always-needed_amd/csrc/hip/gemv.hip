@@ -15,7 +15,9 @@
 //   * Row sums reduce through DPP (no LDS); for K > 64 blocks, 2 or 4 waves
 //     split a row and combine through a small LDS array.
 // Epilogues fuse the reference's follow-up launches (residual add, SiLU*up).
+#include <type_traits>
 #include "rina_common.hpp"
+#include "q2k_col.hpp"
 
 namespace {
 
@@ -26,7 +28,6 @@ constexpr int kWG = 256;
 constexpr int kMaxChunks = 4;              // 16-byte chunks per thread per tile
 constexpr int kTileBytes = kWG * kMaxChunks * 16;   // 16 KiB per tile (all matrices)
 
-enum { FMT_Q4_0 = 0, FMT_Q4_0F = 1, FMT_Q2_K = 2 };
 
 struct GemvSeg {
     const uint8_t* w;
@@ -124,62 +125,6 @@ __device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t sh
     return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
 }
 
-// Activation columns owned by one lane, as block floating point: the column's
-// values x_i = X_i * 2^(e-22) with integers |X_i| < 2^22 (e: exponent of the
-// column's max |x|), and X_i split into three signed 8-bit digit planes
-// X = d0 + 256 d1 + 65536 d2.  A weight block then needs only integer dot
-// products (v_dot4c_i32_i8, 4 MACs per instruction, exact) and one fp32
-// scale per block: the error is that of rounding x to 22 significant bits of
-// its column maximum, below the fp32 accumulation error of the reference loop.
-// Plane dword t of a Q4 column holds the digits of values 8(t/2)+2b+(t%2),
-// b = 0..3: the order of the nibble bytes after the low/high split.
-template <int FMT, int CPL>
-struct XCols {
-    static constexpr int UNIT = (FMT == FMT_Q2_K) ? 16 : 32;
-    static constexpr int ND = UNIT / 4;   // dwords per digit plane
-    int32_t dg[CPL][3][ND];
-    float tt[CPL][3];   // 7 * (sum of plane digits): the -7 nibble offset
-    float xe[CPL];      // 2^(e-22)
-    float xs[CPL];      // fp32 sum of the column (Q2_K min term)
-};
-
-template <int FMT, int CPL>
-__device__ __forceinline__ void digitize(XCols<FMT, CPL>& xc, int j, const float (&x)[XCols<FMT, CPL>::UNIT]) {
-    constexpr int UNIT = XCols<FMT, CPL>::UNIT;
-    float mx = 0.f, sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < UNIT; i++) { mx = fmaxf(mx, fabsf(x[i])); sum += x[i]; }
-    int e = 0;
-    if (mx > 0.f) (void)frexpf(mx, &e);            // mx < 2^e
-    const float up = ldexpf(1.0f, 22 - e);
-    xc.xe[j] = ldexpf(1.0f, e - 22);
-    xc.xs[j] = sum;
-    int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-    for (int t = 0; t < XCols<FMT, CPL>::ND; t++) {
-        uint32_t p0 = 0, p1 = 0, p2 = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int k = (FMT == FMT_Q2_K) ? 4 * t + b : 8 * (t >> 1) + 2 * b + (t & 1);
-            int X = (int)rintf(x[k] * up);
-            int d0 = ((X + 128) & 255) - 128;
-            int X1 = (X - d0) >> 8;
-            int d1 = ((X1 + 128) & 255) - 128;
-            int d2 = (X1 - d1) >> 8;
-            s0 += d0; s1 += d1; s2 += d2;
-            p0 |= (uint32_t)(d0 & 255) << (8 * b);
-            p1 |= (uint32_t)(d1 & 255) << (8 * b);
-            p2 |= (uint32_t)(d2 & 255) << (8 * b);
-        }
-        xc.dg[j][0][t] = (int32_t)p0;
-        xc.dg[j][1][t] = (int32_t)p1;
-        xc.dg[j][2][t] = (int32_t)p2;
-    }
-    xc.tt[j][0] = 7.0f * (float)s0;
-    xc.tt[j][1] = 7.0f * (float)s1;
-    xc.tt[j][2] = 7.0f * (float)s2;
-}
-
 // exact integer sum_i (q_i - 7) X_i of one Q4 block (nib: its 16 nibble bytes), as float
 template <int FMT, int CPL>
 __device__ __forceinline__ float q4_dot(const uint32_t (&nib)[4], const XCols<FMT, CPL>& xc, int j) {
@@ -212,7 +157,6 @@ __device__ __forceinline__ float q2_dot(const uint32_t (&q)[4], uint32_t sh, con
     return fmaf(65536.0f, (float)a2, fmaf(256.0f, (float)a1, (float)a0));
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
 template <int NMAT>
 __device__ __forceinline__ void epilogue(const GemvArgs& a, int s, int n, const float (&v)[2]) {
@@ -444,12 +388,6 @@ __global__ __launch_bounds__(kWG) void gemv_quant_kernel(GemvArgs a) {
 // chains.  No LDS and no barrier unless a row spans several waves (WPR > 1,
 // one LDS exchange per row group).
 // ---------------------------------------------------------------------------
-typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
-
-// 16-byte streaming load from a 4-byte aligned global address
-__device__ __forceinline__ u32x4_a4 gld_nt_a4(const uint8_t* p) {
-    return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_a4*)p);
-}
 
 template <int FMT>
 __device__ __forceinline__ void load_q4_block(const uint8_t* p, float& sc, uint32_t (&nib)[4]) {
@@ -479,6 +417,25 @@ struct DirectBlk {
     int seg[RB], row[RB];
     bool ok[RB];
 };
+
+// Q2_K in the direct kernel: a lane's column is 32 consecutive values of a
+// row, which in the 256-value block layout (ops/linear.cu:322-338) is shift
+// group g of one 128-value page: the page's 32 qs bytes (2 bits per value at
+// bit 2g of byte i for value i of each 16-value half), the two half scale
+// bytes (sc | m << 4) and the block's fp16 d, dmin.  32-value columns never
+// straddle a block because row starts are multiples of 32 values.
+template <int RB>
+struct DirectBlkQ2 {
+    uint32_t qs[RB][2][8];
+    uint32_t sm[RB][2];     // scale bytes of halves 0 and 1 (low 16 bits)
+    uint32_t dd[RB][2];     // d | dmin << 16
+    int sh[RB];             // 2g
+    int seg[RB], row[RB];
+    bool ok[RB];
+};
+
+template <int FMT, int RB>
+using DirectBlkT = typename std::conditional<FMT == FMT_Q2_K, DirectBlkQ2<RB>, DirectBlk<RB>>::type;
 
 __device__ __forceinline__ uint64_t uni64(const void* p) {
     const uint64_t v = (uint64_t)p;
@@ -540,6 +497,34 @@ __device__ __forceinline__ void direct_issue(const GemvArgs& a, const DirectSegs
     }
 }
 
+// Q2_K: column u of row n is flat elements [nK + 32u, nK + 32u + 32).
+template <int FMT, int NMAT, int RB>
+__device__ __forceinline__ void direct_issue(const GemvArgs& a, const DirectSegs& S, int grp, int u, bool active,
+                                             DirectBlkQ2<RB>& b) {
+#pragma unroll
+    for (int i = 0; i < RB; i++) {
+        const int vr = grp * RB + i;
+        const int sg = S.seg_of(vr);
+        b.seg[i] = sg;
+        b.row[i] = (grp < a.total_tiles && vr < a.R) ? vr - S.t0(sg) : -1;
+        const bool ok = active && b.row[i] >= 0;
+        const int64_t e = ok ? (int64_t)b.row[i] * a.K + 32 * u : 0;
+        const int64_t off = (e >> 8) * 84;
+        const int page = (int)(e >> 7) & 1, g = (int)(e >> 5) & 3;
+        b.sh[i] = 2 * g;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            const uint8_t* bp = S.wt(sg, m) + off;
+            const u32x4_a4 q0 = gld_nt_a4(bp + 16 + 32 * page), q1 = gld_nt_a4(bp + 32 + 32 * page);
+            b.qs[i][m][0] = q0.x; b.qs[i][m][1] = q0.y; b.qs[i][m][2] = q0.z; b.qs[i][m][3] = q0.w;
+            b.qs[i][m][4] = q1.x; b.qs[i][m][5] = q1.y; b.qs[i][m][6] = q1.z; b.qs[i][m][7] = q1.w;
+            b.sm[i][m] = gld_nt((const uint16_t*)(bp + 8 * page + 2 * g));
+            b.dd[i][m] = gld_nt((const uint32_t*)(bp + 80));
+        }
+        b.ok[i] = ok;
+    }
+}
+
 template <int NMAT>
 __device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const DirectSegs& S, int sg, int n,
                                                 const float (&v)[2]) {
@@ -549,168 +534,10 @@ __device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const DirectS
     else gst(y, v[0]);
 }
 
-// Workgroup-cooperative activation prep for the direct kernel: the K values
-// are split over the 256 threads (TPC threads per 32-value column, 8..32
-// values each) instead of every wave digitizing the whole row; the optional
-// norm prologue reduces over the workgroup.  Digit planes, offsets and
-// exponents go to LDS as [plane][dword][column] so each consumer lane then
-// reads its column conflict-free.
-struct PrepLds {
-    int32_t dg[3][8][256];
-    float tt[3][256];
-    float xe[256];
-    float red[8];
-};
-
-__device__ __forceinline__ float block_sum4(float v, float* red, int slot) {
-    v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) red[slot * 4 + (threadIdx.x >> 6)] = v;
-    __syncthreads();
-    return (red[slot * 4 + 0] + red[slot * 4 + 1]) + (red[slot * 4 + 2] + red[slot * 4 + 3]);
-}
-
-// sum / max over groups of TPC consecutive lanes (TPC 1, 2 or 4)
-template <int TPC>
-__device__ __forceinline__ float grp_max(float v) {
-    if (TPC >= 2) v = fmaxf(v, dpp_f<0xB1>(v));
-    if (TPC >= 4) v = fmaxf(v, dpp_f<0x4E>(v));
-    return v;
-}
-template <int TPC>
-__device__ __forceinline__ int grp_sum_i(int v) {
-    if (TPC >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
-    if (TPC >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
-    return v;
-}
-
-template <int TPC, int PRO>
-struct PrepRaw {
-    static constexpr int VPC = 32 / TPC;           // values per thread
-    float x[VPC];
-    float w[PRO != RINA_PRO_NONE ? VPC : 1];
-};
-
-// issued before the weight loads: vmcnt retires loads in issue order
-template <int TPC, int PRO>
-__device__ __forceinline__ void wg_prep_load(const GemvArgs& a, PrepRaw<TPC, PRO>& r) {
-    constexpr int VPC = 32 / TPC;
-    const int tid = threadIdx.x;
-    const int u = tid / TPC, j = tid % TPC;
-    const bool on = u < a.K / 32;
-    float (&x)[VPC] = r.x;
-    auto& w = r.w;
-    {
-        const int uu = on ? u : 0;
-        const f32x4* xp = (const f32x4*)(a.x + (int64_t)uu * 32 + j * VPC);
-#pragma unroll
-        for (int i = 0; i < VPC / 4; i++) {
-            f32x4 v = gld(xp + i);
-            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-        }
-        if constexpr (PRO != RINA_PRO_NONE) {
-            const f32x4* wp = (const f32x4*)(a.nw + (int64_t)uu * 32 + j * VPC);
-#pragma unroll
-            for (int i = 0; i < VPC / 4; i++) {
-                f32x4 v = gld(wp + i);
-                w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-            }
-        }
-    }
-}
-
-template <int TPC, int PRO>
-__device__ __forceinline__ void wg_prep_x(const GemvArgs& a, PrepRaw<TPC, PRO>& r, PrepLds& L) {
-    constexpr int VPC = 32 / TPC;
-    const int tid = threadIdx.x;
-    const int u = tid / TPC, j = tid % TPC;
-    const bool on = u < a.K / 32;
-    float (&x)[VPC] = r.x;
-    auto& w = r.w;
-    if (!on) {
-#pragma unroll
-        for (int i = 0; i < VPC; i++) x[i] = 0.f;
-    }
-    if constexpr (PRO != RINA_PRO_NONE) {
-        const float d = (float)a.K;
-        float mean = 0.f;
-        if (PRO == RINA_PRO_LAYERNORM) {
-            float sm = 0.f;
-#pragma unroll
-            for (int i = 0; i < VPC; i++) sm += x[i];
-            mean = block_sum4(sm, L.red, 0) / d;
-        }
-        float ss = 0.f;
-        if (on) {
-#pragma unroll
-            for (int i = 0; i < VPC; i++) {
-                const float t = x[i] - mean;
-                ss = fmaf(t, t, ss);
-            }
-        }
-        const float inv = 1.0f / sqrtf(block_sum4(ss, L.red, 1) / d + a.eps);
-#pragma unroll
-        for (int i = 0; i < VPC; i++) x[i] = on ? (x[i] - mean) * inv * w[i] : 0.f;
-    }
-    float mx = 0.f;
-#pragma unroll
-    for (int i = 0; i < VPC; i++) mx = fmaxf(mx, fabsf(x[i]));
-    mx = grp_max<TPC>(mx);
-    int e = 0;
-    if (mx > 0.f) (void)frexpf(mx, &e);            // mx < 2^e
-    const float up = ldexpf(1.0f, 22 - e);
-    int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-    for (int tl = 0; tl < VPC / 4; tl++) {         // local dword pair index tl/2, parity tl%2
-        uint32_t p0 = 0, p1 = 0, p2 = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int k = 8 * (tl >> 1) + 2 * b + (tl & 1);
-            const int X = (int)rintf(x[k] * up);
-            const int d0 = ((X + 128) & 255) - 128;
-            const int X1 = (X - d0) >> 8;
-            const int d1 = ((X1 + 128) & 255) - 128;
-            const int d2 = (X1 - d1) >> 8;
-            s0 += d0; s1 += d1; s2 += d2;
-            p0 |= (uint32_t)(d0 & 255) << (8 * b);
-            p1 |= (uint32_t)(d1 & 255) << (8 * b);
-            p2 |= (uint32_t)(d2 & 255) << (8 * b);
-        }
-        if (on) {
-            const int t = j * (VPC / 4) + tl;
-            L.dg[0][t][u] = (int32_t)p0;
-            L.dg[1][t][u] = (int32_t)p1;
-            L.dg[2][t][u] = (int32_t)p2;
-        }
-    }
-    s0 = grp_sum_i<TPC>(s0);
-    s1 = grp_sum_i<TPC>(s1);
-    s2 = grp_sum_i<TPC>(s2);
-    if (on && j == 0) {
-        L.tt[0][u] = 7.0f * (float)s0;
-        L.tt[1][u] = 7.0f * (float)s1;
-        L.tt[2][u] = 7.0f * (float)s2;
-        L.xe[u] = ldexpf(1.0f, e - 22);
-    }
-    __syncthreads();
-}
-
-template <int FMT>
-__device__ __forceinline__ void read_cols(const PrepLds& L, int u, bool active, XCols<FMT, 1>& xc) {
-    const int uu = active ? u : 0;
-#pragma unroll
-    for (int p = 0; p < 3; p++) {
-#pragma unroll
-        for (int t = 0; t < 8; t++) xc.dg[0][p][t] = L.dg[p][t][uu];
-        xc.tt[0][p] = L.tt[p][uu];
-    }
-    xc.xe[0] = L.xe[uu];
-    xc.xs[0] = 0.f;
-}
-
 // Row sums of one row group and their epilogue.
 template <int FMT, int WPR, int NMAT, int RB>
-__device__ __forceinline__ void direct_consume(const GemvArgs& a, const DirectSegs& S, const XCols<FMT, 1>& xc,
-                                               const DirectBlk<RB>& cur, int it, int rs, int cp,
+__device__ __forceinline__ void direct_consume(const GemvArgs& a, const DirectSegs& S, const DCols<FMT>& xc,
+                                               const DirectBlkT<FMT, RB>& cur, int it, int rs, int cp,
                                                float (*red)[RB * NMAT][WPR]) {
     constexpr int RPI = 4 / WPR;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -718,8 +545,12 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const DirectSe
 #pragma unroll
     for (int i = 0; i < RB; i++)
 #pragma unroll
-        for (int m = 0; m < NMAT; m++)
-            part[i][m] = wave_sum((cur.ok[i] ? cur.sc[i][m] : 0.f) * xc.xe[0] * q4_dot(cur.nib[i][m], xc, 0));
+        for (int m = 0; m < NMAT; m++) {
+            if constexpr (FMT == FMT_Q2_K)
+                part[i][m] = wave_sum(cur.ok[i] ? q2_col(cur.qs[i][m], cur.sm[i][m], cur.dd[i][m], cur.sh[i], xc) : 0.f);
+            else
+                part[i][m] = wave_sum((cur.ok[i] ? cur.sc[i][m] : 0.f) * xc.xe[0] * q4_dot(cur.nib[i][m], xc, 0));
+        }
     if (WPR == 1) {
         if (lane == 0) {
 #pragma unroll
@@ -777,12 +608,13 @@ __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
     __shared__ PrepLds prep;
     constexpr int TPC = WPR == 1 ? 4 : WPR == 2 ? 2 : 1;
     PrepRaw<TPC, PRO> raw;
-    wg_prep_load<TPC, PRO>(a, raw);
+    const PrepSrc src{a.x, a.nw, a.K, a.eps};
+    wg_prep_load<TPC, PRO>(src, raw);
     int it = blockIdx.x;
-    DirectBlk<RB> A, B;
+    DirectBlkT<FMT, RB> A, B;
     direct_issue<FMT, NMAT, RB>(a, S, it * RPI + rs, u, active, A);
-    wg_prep_x<TPC, PRO>(a, raw, prep);
-    XCols<FMT, 1> xc;
+    wg_prep_x<FMT, TPC, PRO>(src, raw, prep);
+    DCols<FMT> xc;
     read_cols<FMT>(prep, u, active, xc);
 
     for (;;) {
@@ -1036,7 +868,8 @@ int launch_direct(GemvArgs& a, hipStream_t st) {
     constexpr int RPI = 4 / WPR;
     int cus = rina_num_cus();
     int wgs = (a.total_tiles + RPI - 1) / RPI;
-    int per_cu = RB >= 8 ? 2 : RB == 4 ? 3 : 4;   // workgroups resident per CU at this register count
+    // workgroups resident per CU at this register count
+    int per_cu = FMT == FMT_Q2_K ? (RB >= 4 ? (NMAT == 2 ? 2 : 3) : 4) : (RB >= 8 ? 2 : RB == 4 ? 3 : 4);
     int grid = wgs < cus * per_cu ? wgs : cus * per_cu;
     hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB>), dim3(grid), dim3(kWG), 0, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
@@ -1048,7 +881,7 @@ int direct_rb(GemvArgs& a, int rb, hipStream_t st) {
         case 1: return launch_direct<FMT, WPR, NMAT, PRO, 1>(a, st);
         case 2: return launch_direct<FMT, WPR, NMAT, PRO, 2>(a, st);
         case 4: return launch_direct<FMT, WPR, NMAT, PRO, 4>(a, st);
-        default: return launch_direct<FMT, WPR, NMAT, PRO, 8>(a, st);
+        default: return launch_direct<FMT, WPR, NMAT, PRO, (FMT == FMT_Q2_K ? 4 : 8)>(a, st);
     }
 }
 
@@ -1065,6 +898,10 @@ int dispatch_direct(GemvArgs& a, int wpr, int rb, int pro, hipStream_t st) {
     if (wpr == 2) return direct_pro<FMT, 2, NMAT>(a, rb, pro, st);
     return direct_pro<FMT, 4, NMAT>(a, rb, pro, st);
 }
+
+// M = 1 shapes the direct-load kernel takes: 32-value columns, at most one
+// per lane of four waves.
+bool direct_ok(int fmt, int K) { return fmt >= 0 && K % 32 == 0 && K <= 8192; }
 
 // waves per row / units per lane for a row of `nunits` work units
 void split_row(int nunits, int& wpr, int& cpl) {
@@ -1091,7 +928,8 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
     a.eps = eps;
     int64_t rowbytes = fmt == FMT_Q4_0 ? (int64_t)(K / 32) * 18 : fmt == FMT_Q4_0F ? (int64_t)(K / 32) * 20 : 0;
     a.rowbytes = (int)rowbytes;
-    if (fmt != FMT_Q2_K && cpl == 1) {
+    if (direct_ok(fmt, K)) {
+        split_row(K / 32, wpr, cpl);
         // direct-load kernel: virtual rows over all segments, RB rows per wave
         int rows = 0;
         for (int s = 0; s < nseg; s++) {
@@ -1107,8 +945,11 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
         int64_t waves = (int64_t)rina_num_cus() * 8;
         int64_t want = ((int64_t)rows * wpr + waves - 1) / waves;
         int rb = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : 8;
+        if (fmt == FMT_Q2_K && rb > 4) rb = 4;   // 10 registers per Q2_K column block
         a.R = rows;
         a.total_tiles = (rows + rb - 1) / rb;
+        if (fmt == FMT_Q2_K)
+            return nmat == 2 ? dispatch_direct<FMT_Q2_K, 2>(a, wpr, rb, pro, st) : dispatch_direct<FMT_Q2_K, 1>(a, wpr, rb, pro, st);
         if (fmt == FMT_Q4_0)
             return nmat == 2 ? dispatch_direct<FMT_Q4_0, 2>(a, wpr, rb, pro, st) : dispatch_direct<FMT_Q4_0, 1>(a, wpr, rb, pro, st);
         return nmat == 2 ? dispatch_direct<FMT_Q4_0F, 2>(a, wpr, rb, pro, st) : dispatch_direct<FMT_Q4_0F, 1>(a, wpr, rb, pro, st);
@@ -1214,10 +1055,10 @@ extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int 
     int unit = qt == RINA_QT_GGML_Q2_K ? 16 : 32;
     int wpr = 1, cpl = 1;
     if (qt != RINA_QT_FP32 && K % unit == 0) split_row(K / unit, wpr, cpl);
-    // direct Q4 kernel: any waves-per-row; Q2_K tile kernel: one wave per row
-    const bool q4 = qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F;
+    // direct kernel: any waves-per-row; Q2_K tile kernel: one wave per row
+    const bool direct = qt != RINA_QT_FP32 && direct_ok(fmt_of(qt), K);
     bool fused_pro = M == 1 && ((qt == RINA_QT_FP32 && K <= 16384) ||
-                                (qt != RINA_QT_FP32 && (wpr == 1 || q4) && cpl == 1 && (uintptr_t)input % 16 == 0 &&
+                                (qt != RINA_QT_FP32 && (direct || (wpr == 1 && cpl == 1)) && (uintptr_t)input % 16 == 0 &&
                                  (uintptr_t)nw % 16 == 0));
     if (pro != RINA_PRO_NONE && !fused_pro) {
         // normalize into library scratch first (prompt rows, unusual shapes)

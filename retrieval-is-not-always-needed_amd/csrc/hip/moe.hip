@@ -1,0 +1,433 @@
+// MoE MLP block of one decode token (forward_moe of
+// arch/mla/deepseek_mla_layer.cu:291-350) for Q2_K experts, in three
+// launches instead of the reference's norm, shared gate/up, shared down,
+// router, host top-k and per-expert matvec chain:
+//   1. router:  a2 = RMSNorm(h, ln2); logits = W_gate_inp a2 (fp32 router,
+//               one wave per expert, every workgroup normalizes h itself).
+//   2. gate/up: every workgroup takes the top-k of softmax(logits) from the
+//               E logits; the rows of the shared FFN and of the k selected
+//               experts give G = SiLU(W_g a2) * (W_u a2).  Integer dot
+//               products on the 2-bit fields against block floating point
+//               digits of a2 (prepared once per workgroup).
+//   3. down:    h_i += W_sd[i] . G_sh + sum_j p_j (W_d[e_j][i] . G_j), one
+//               wave per row over all its columns (fp32 products weighted
+//               by the probabilities, then one reduction: the same terms as
+//               the reference's shared matvec + saxpy chain, summed in
+//               another order).  G is digitized into LDS per workgroup.
+#include "q2k_col.hpp"
+
+namespace {
+
+struct MoeBlkArgs {
+    const float* ln2;
+    float eps;
+    const float* wr;                      // router [E, d] fp32
+    const uint8_t *sg, *su, *sd;          // shared gate/up [S, d], down [d, S]
+    const uint8_t *wg, *wu, *wd;          // stacked routed experts
+    int64_t stride_gu, stride_dn;
+    int E, k, d, F, S;
+    float* G;                             // ws [S + k F]
+    float* a2;                            // ws [d]
+    float* logits;                        // ws [E]
+    int* ids;                             // ws [k]
+    float* probs;                         // ws [k]
+    float* h;                             // residual stream [d]
+};
+
+constexpr int kMoeMaxD = 2048;    // one 32-value column per lane of a wave
+
+// ---------------------------------------------------------------------------
+// 1. router
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_router_kernel(MoeBlkArgs a) {
+    __shared__ __align__(16) float s_x[kMoeMaxD];
+    __shared__ float red[8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave's router row first (it does not depend on the norm)
+    const int e = blockIdx.x * 4 + wave;
+    const float* wrow = a.wr + (int64_t)(e < a.E ? e : 0) * a.d;
+    f32x4 w[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const int i = 4 * lane + 256 * t;
+        w[t] = i < a.d ? gld((const f32x4*)(wrow + i)) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    f32x4 hv[2], wv[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = 4 * tid + 1024 * r;
+        const bool on = i < a.d;
+        hv[r] = on ? gld((const f32x4*)(a.h + i)) : f32x4{0.f, 0.f, 0.f, 0.f};
+        wv[r] = on ? gld((const f32x4*)(a.ln2 + i)) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        ss = fmaf(hv[r].x, hv[r].x, ss);
+        ss = fmaf(hv[r].y, hv[r].y, ss);
+        ss = fmaf(hv[r].z, hv[r].z, ss);
+        ss = fmaf(hv[r].w, hv[r].w, ss);
+    }
+    const float inv = 1.0f / sqrtf(block_sum4(ss, red, 0) / (float)a.d + a.eps);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = 4 * tid + 1024 * r;
+        if (i < a.d) {
+            const f32x4 v = {hv[r].x * inv * wv[r].x, hv[r].y * inv * wv[r].y, hv[r].z * inv * wv[r].z,
+                             hv[r].w * inv * wv[r].w};
+            *(f32x4*)(s_x + i) = v;
+            if (blockIdx.x == 0) gst((f32x4*)(a.a2 + i), v);
+        }
+    }
+    __syncthreads();
+    if (e >= a.E) return;
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const int i = 4 * lane + 256 * t;
+        if (i < a.d) {
+            const f32x4 x = *(const f32x4*)(s_x + i);
+            acc = fmaf(w[t].x, x.x, acc);
+            acc = fmaf(w[t].y, x.y, acc);
+            acc = fmaf(w[t].z, x.z, acc);
+            acc = fmaf(w[t].w, x.w, acc);
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) gst(a.logits + e, acc);
+}
+
+// ---------------------------------------------------------------------------
+// 2. gate/up
+// ---------------------------------------------------------------------------
+
+// Top-k of softmax(logits) by one wave (E <= 64, lane = expert), the
+// reference's selection (deepseek_mla_layer.cu:310-326): it keeps the k
+// largest probabilities with strict ">" (of equal values the earlier expert
+// stays), in ascending order with equal values later-expert first.  Here k
+// rounds each take the largest remaining probability, the lowest expert
+// among equal ones, and fill the slots from the top.  The normalizer is
+// summed in expert order as the reference's loop does (the exponentials of
+// experts >= E are exact zeros).  s_tmp: 64 floats of the wave's own LDS.
+__device__ __forceinline__ void topk_wave(const MoeBlkArgs& a, int* s_ids, float* s_pr, float* s_tmp,
+                                          bool publish) {
+    const int lane = threadIdx.x & 63;
+    const float x = lane < a.E ? gld(a.logits + lane) : -INFINITY;
+    const float mx = wave_max(x);
+    const float ex = lane < a.E ? expf(x - mx) : 0.f;
+    s_tmp[lane] = ex;
+    if (lane < a.k) s_ids[lane] = -1;
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        const f32x4 v = *(const f32x4*)(s_tmp + 4 * q);
+        sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+    }
+    const float p = ex * (1.0f / sum);
+    float pv = lane < a.E ? p : -INFINITY;
+    for (int t = 0; t < a.k; t++) {
+        const float m = wave_max(pv);
+        if (m == -INFINITY) break;                 // fewer than k finite probabilities
+        const uint64_t hit = __ballot(pv == m);
+        const int win = __builtin_ctzll(hit);      // lowest expert among equal values
+        if (lane == win) {
+            const int slot = a.k - 1 - t;
+            s_ids[slot] = lane;
+            s_pr[slot] = p;
+            if (publish) {
+                gst(a.ids + slot, lane);
+                gst(a.probs + slot, p);
+            }
+            pv = -INFINITY;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+constexpr int kGuRB = 4;   // row pairs per wave per group
+
+struct GuBlk {
+    Q2Col c[kGuRB][2];
+    int vr[kGuRB];          // virtual row (output index), -1 past the end
+    bool ok[kGuRB];         // row has an expert (lane also active)
+    bool rowok[kGuRB];
+};
+
+__device__ __forceinline__ void gu_issue(const MoeBlkArgs& a, const int* s_ids, int grp, int R, bool active,
+                                         GuBlk& b) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kGuRB; i++) {
+        const int vr = grp * kGuRB + i;
+        const bool valid = vr < R;
+        const uint8_t *wg = a.sg, *wu = a.su;
+        int row = vr;
+        bool rowok = valid;
+        if (vr >= a.S) {
+            const int j = min((vr - a.S) / a.F, a.k - 1);
+            row = vr - a.S - j * a.F;
+            const int e = s_ids[j];
+            rowok = valid && e >= 0 && e < a.E;
+            const int64_t eo = rowok ? (int64_t)e : 0;
+            wg = a.wg + eo * a.stride_gu;
+            wu = a.wu + eo * a.stride_gu;
+        }
+        const bool ok = rowok && active;
+        const uint32_t e0 = ok ? (uint32_t)row * (uint32_t)a.d + 32u * lane : 0u;
+        q2_col_issue32(wg, e0, b.c[i][0]);
+        q2_col_issue32(wu, e0, b.c[i][1]);
+        b.vr[i] = valid ? vr : -1;
+        b.ok[i] = ok;
+        b.rowok[i] = rowok;
+    }
+}
+
+__device__ __forceinline__ void gu_consume(const MoeBlkArgs& a, const DCols<FMT_Q2_K>& xc, const GuBlk& b) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kGuRB; i++) {
+        const float g = wave_sum(b.ok[i] ? q2_col(b.c[i][0], xc) : 0.f);
+        const float u = wave_sum(b.ok[i] ? q2_col(b.c[i][1], xc) : 0.f);
+        if (lane == 0 && b.vr[i] >= 0) gst(a.G + b.vr[i], b.rowok[i] ? silu_mul(g, u) : 0.f);
+    }
+}
+
+// Every wave selects the experts itself (no barrier before its first weight
+// loads); the loads are in flight while the workgroup digitizes a2.
+__global__ __launch_bounds__(256) void moe_gate_up_q2_kernel(MoeBlkArgs a) {
+    __shared__ PrepLds prep;
+    __shared__ int s_ids_w[4][16];
+    __shared__ float s_pr_w[4][16];
+    __shared__ __align__(16) float s_tmp_w[4][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const PrepSrc src{a.a2, nullptr, a.d, 0.f};
+    PrepRaw<4, RINA_PRO_NONE> raw;
+    wg_prep_load<4, RINA_PRO_NONE>(src, raw);
+    const int* s_ids = s_ids_w[wave];
+    topk_wave(a, s_ids_w[wave], s_pr_w[wave], s_tmp_w[wave], blockIdx.x == 0 && wave == 0);
+    const bool active = lane < a.d / 32;
+    const int R = a.S + a.k * a.F;
+    const int ngrp = (R + kGuRB - 1) / kGuRB;
+    const int step = gridDim.x * 4;
+    int grp = blockIdx.x * 4 + wave;
+    GuBlk A, B;
+    gu_issue(a, s_ids, grp < ngrp ? grp : 0, R, active && grp < ngrp, A);
+    wg_prep_x<FMT_Q2_K, 4, RINA_PRO_NONE>(src, raw, prep);
+    DCols<FMT_Q2_K> xc;
+    read_cols<FMT_Q2_K>(prep, lane, active, xc);
+    if (grp >= ngrp) return;
+    for (;;) {
+        if (grp + step < ngrp) {
+            gu_issue(a, s_ids, grp + step, R, active, B);
+            gu_consume(a, xc, A);
+        } else {
+            gu_consume(a, xc, A);
+            break;
+        }
+        grp += step;
+        if (grp + step < ngrp) {
+            gu_issue(a, s_ids, grp + step, R, active, A);
+            gu_consume(a, xc, B);
+        } else {
+            gu_consume(a, xc, B);
+            break;
+        }
+        grp += step;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 3. down
+// ---------------------------------------------------------------------------
+
+// G as block floating point digit columns in LDS: per 32-value column one
+// 28-dword record (3 planes x 8 dwords of digits in natural order, the fp32
+// sums of the two halves, 2^(e-22), padding).  A 28-dword lane stride keeps
+// the 16 lanes of a 16-byte LDS read on distinct banks.
+constexpr int kRec = 28;
+
+// Four threads per column (8 values each) digitize G cooperatively; every
+// round's loads go out first.
+__device__ __forceinline__ void stage_g_digits(const float* G, int ncol, uint32_t* rec) {
+    constexpr int ROUNDS = 4;                      // 512 threads x 4 rounds / 4 = 512 columns
+    const int tid = threadIdx.x, j = tid & 3;
+    const int rounds = (ncol + 127) / 128;         // uniform: the group shuffles see full waves
+    f32x4 v[ROUNDS][2];
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const int c = (tid >> 2) + 128 * r;
+        const bool on = c < ncol && r < rounds;
+        const f32x4* src = (const f32x4*)(G + 32 * (on ? c : 0) + 8 * j);
+        v[r][0] = on ? gld(src) : f32x4{0.f, 0.f, 0.f, 0.f};
+        v[r][1] = on ? gld(src + 1) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        if (r >= rounds) break;
+        const int c = (tid >> 2) + 128 * r;
+        const float x[8] = {v[r][0].x, v[r][0].y, v[r][0].z, v[r][0].w, v[r][1].x, v[r][1].y, v[r][1].z, v[r][1].w};
+        float mx = 0.f, hs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) { mx = fmaxf(mx, fabsf(x[i])); hs += x[i]; }
+        mx = grp_max<4>(mx);
+        hs += dpp_f<0xB1>(hs);                     // sum of the 16-value half (threads j, j^1)
+        int e = 0;
+        if (mx > 0.f) (void)frexpf(mx, &e);
+        const float up = ldexpf(1.0f, 22 - e);
+        uint32_t p[3][2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            digits4(x[4 * t], x[4 * t + 1], x[4 * t + 2], x[4 * t + 3], up, p[0][t], p[1][t], p[2][t]);
+        if (c < ncol) {
+            uint32_t* rc = rec + c * kRec;
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                rc[8 * k + 2 * j] = p[k][0];
+                rc[8 * k + 2 * j + 1] = p[k][1];
+            }
+            if ((j & 1) == 0) rc[24 + (j >> 1)] = __float_as_uint(hs);
+            if (j == 0) rc[26] = __float_as_uint(ldexpf(1.0f, e - 22));
+        }
+    }
+}
+
+__device__ __forceinline__ void read_rec(const uint32_t* rc, DCols<FMT_Q2_K>& xc) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4* r4 = (const u4*)rc;
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+        const u4 v = r4[q];
+        const int k = q >> 1, t = 4 * (q & 1);
+        xc.dg[0][k][t] = (int32_t)v.x; xc.dg[0][k][t + 1] = (int32_t)v.y;
+        xc.dg[0][k][t + 2] = (int32_t)v.z; xc.dg[0][k][t + 3] = (int32_t)v.w;
+    }
+    const u4 v = r4[6];
+    xc.tt[0][0] = __uint_as_float(v.x);
+    xc.tt[0][1] = __uint_as_float(v.y);
+    xc.tt[0][2] = 0.f;
+    xc.xe[0] = __uint_as_float(v.z);
+    xc.xs[0] = 0.f;
+}
+
+// Every wave owns one output row.  The row's columns over all its sources
+// (the shared chunk columns, then each selected expert's columns, the same
+// order as G's 32-value columns) are dealt to the lanes in rounds of 64, so
+// no lane idles on a short expert row; each column's product is weighted by
+// its source's probability (1 for the shared FFN) and one wave reduction
+// gives the row.  The loads go out before the workgroup digitizes G.
+constexpr int kDnRounds = 8;   // columns per lane: (shared + k * ffn) / 32 <= 512
+
+__global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
+    extern __shared__ __align__(16) uint32_t s_rec[];   // [n / 32][kRec]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = a.S + a.k * a.F;                 // multiple of 32
+    const int ncol = n / 32, fcols = a.F / 32, scols = a.S / 32;
+    const int rounds = (ncol + 63) / 64;
+    const int i = blockIdx.x * 8 + wave;           // grid covers d rows exactly once
+    const bool row_on = i < a.d;
+    const int ir = row_on ? i : 0;
+    const float inv_f = 1.0f / (float)fcols;
+
+    Q2Col c[kDnRounds];
+    float wt[kDnRounds];
+    int col[kDnRounds];
+#pragma unroll
+    for (int r = 0; r < kDnRounds; r++) {
+        const int cc = 64 * r + lane;
+        const uint8_t* w = a.sd;
+        uint32_t e0 = 0;
+        float f = 0.f;
+        if (r < rounds && row_on && cc < ncol) {
+            if (cc < scols) {
+                e0 = (uint32_t)ir * (uint32_t)a.S + 32u * cc;
+                f = 1.0f;
+            } else {
+                const int t = cc - scols;
+                int j = (int)((float)t * inv_f);       // t < 512: exact after one correction each way
+                j -= j * fcols > t;
+                j += (j + 1) * fcols <= t;
+                const int e = gld(a.ids + j);
+                if (e >= 0 && e < a.E) {
+                    w = a.wd + (int64_t)e * a.stride_dn;
+                    e0 = (uint32_t)ir * (uint32_t)a.F + 32u * (uint32_t)(t - j * fcols);
+                    f = gld(a.probs + j);
+                }
+            }
+        }
+        wt[r] = f;
+        col[r] = cc < ncol ? cc : 0;
+        q2_col_issue32(w, e0, c[r]);
+    }
+    stage_g_digits(a.G, ncol, s_rec);
+    __syncthreads();
+    if (!row_on) return;
+
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < kDnRounds; r++) {
+        if (r >= rounds) break;
+        if (wt[r] != 0.f) {
+            DCols<FMT_Q2_K> xc;
+            read_rec(s_rec + col[r] * kRec, xc);
+            acc = fmaf(wt[r], q2_col(c[r], xc), acc);
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) gst(a.h + i, gld(a.h + i) + acc);
+}
+
+}  // namespace
+
+extern "C" size_t rina_hip_moe_block_workspace(int d, int n_experts, int k, int ffn, int shared_ffn) {
+    if (d < 1 || n_experts < 1 || k < 1 || ffn < 1 || shared_ffn < 1) return 0;
+    return ((size_t)shared_ffn + (size_t)k * ffn + d + n_experts + 2 * (size_t)k + 4) * sizeof(float);
+}
+
+extern "C" int rina_hip_moe_block(float* h, const float* ln2, float eps, const void* gate_inp, int qt_gate_inp,
+                                  const void* gate_sh, const void* up_sh, const void* down_sh, int shared_ffn,
+                                  const void* gate_exps, const void* up_exps, const void* down_exps, int qt,
+                                  int64_t stride_gate_up, int64_t stride_down, int n_experts, int k, int d, int ffn,
+                                  void* workspace, size_t ws_bytes, void* stream) {
+    if (!h || !ln2 || !gate_inp || !gate_sh || !up_sh || !down_sh || !gate_exps || !up_exps || !down_exps ||
+        n_experts < 1 || k < 1 || k > n_experts || d < 1 || ffn < 1 || shared_ffn < 1)
+        return RINA_ERR_ARG;
+    if (qt != RINA_QT_GGML_Q2_K || qt_gate_inp != RINA_QT_FP32) return RINA_ERR_QTYPE;
+    const int S = shared_ffn, F = ffn;
+    if (d % 32 || d > kMoeMaxD || F % 32 || F > kMoeMaxD || S % 32 || n_experts > 64 || k > 16) return RINA_ERR_SHAPE;
+    const int n = S + k * F;
+    const size_t lds = (size_t)(n / 32) * kRec * sizeof(uint32_t);
+    if (lds > 64 * 1024 || n > 16384) return RINA_ERR_SHAPE;
+    if (((uintptr_t)h | (uintptr_t)ln2 | (uintptr_t)gate_inp | (uintptr_t)workspace) % 16 ||
+        ((uintptr_t)gate_sh | (uintptr_t)up_sh | (uintptr_t)down_sh | (uintptr_t)gate_exps | (uintptr_t)up_exps |
+         (uintptr_t)down_exps) % 4 || stride_gate_up % 4 || stride_down % 4)
+        return RINA_ERR_SHAPE;
+    if (!workspace || ws_bytes < rina_hip_moe_block_workspace(d, n_experts, k, F, S)) return RINA_ERR_WORKSPACE;
+    MoeBlkArgs a{};
+    a.ln2 = ln2; a.eps = eps;
+    a.wr = (const float*)gate_inp;
+    a.sg = (const uint8_t*)gate_sh; a.su = (const uint8_t*)up_sh; a.sd = (const uint8_t*)down_sh;
+    a.wg = (const uint8_t*)gate_exps; a.wu = (const uint8_t*)up_exps; a.wd = (const uint8_t*)down_exps;
+    a.stride_gu = stride_gate_up; a.stride_dn = stride_down;
+    a.E = n_experts; a.k = k; a.d = d; a.F = F; a.S = S;
+    a.G = (float*)workspace;
+    a.a2 = a.G + n;                    // n % 32 == 0: stays 16-byte aligned
+    a.logits = a.a2 + d;
+    a.ids = (int*)(a.logits + n_experts);
+    a.probs = (float*)(a.ids + k);
+    a.h = h;
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(moe_router_kernel, dim3((n_experts + 3) / 4), dim3(256), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    const int cus = rina_num_cus();
+    const int ngrp = (n + kGuRB - 1) / kGuRB;
+    int g1 = (ngrp + 3) / 4;
+    if (g1 > cus * 2) g1 = cus * 2;
+    hipLaunchKernelGGL(moe_gate_up_q2_kernel, dim3(g1), dim3(256), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(moe_down_q2_kernel, dim3((d + 7) / 8), dim3(512), lds, st, a);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}

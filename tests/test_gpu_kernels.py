@@ -100,7 +100,9 @@ def test_linear_q4(rina, orc, qt, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 2048), (1, 576, 2048), (1, 2048, 1408), (1, 1408, 2048),
-                                   (1, 96, 10944), (1, 4096, 512), (3, 64, 1408), (1, 77, 1408)])
+                                   (1, 96, 10944), (1, 4096, 512), (3, 64, 1408), (1, 77, 1408),
+                                   (1, 300, 2816), (1, 200, 4096), (1, 96, 8192), (1, 50, 160), (1, 33, 96),
+                                   (1, 40, 48), (1, 102400 // 8, 2048)])
 def test_linear_q2k(rina, orc, M, N, K):
     w = q2k_blocks(N + K, N * K)
     x = rng(K).standard_normal((M, K)).astype(np.float32)
@@ -453,8 +455,6 @@ def test_linear_norm_prologue(rina, orc, qt, pro, M, K):
     r = rng(qt * 10 + pro + K)
     N = 256
     if qt == 10:
-        if K % 256:
-            pytest.skip("Q2_K rows of 640 are not 16-value aligned")
         w = q2k_blocks(K, N * K)
     else:
         wf = (r.standard_normal(N * K) * 0.02).astype(np.float32)

@@ -151,6 +151,79 @@ def test_moe_ffn_vs_float64(rina, orc, d, F, E, k, qt):
     assert_close(host(hd), ref, what="moe d %d F %d" % (d, F))
 
 
+@pytest.mark.parametrize("d,F,S,E,k", [(2048, 1408, 2816, 64, 6), (256, 64, 128, 8, 3), (512, 96, 192, 16, 4),
+                                       (1024, 2048, 64, 32, 2)])
+def test_moe_block_vs_float64(rina, orc, d, F, S, E, k):
+    """Fused MoE block (norm, router, top-k, shared + routed experts, residual)
+    against a float64 restatement of forward_moe; selected ids and probs
+    against the oracle's top-k of the float64 logits."""
+    hip = rina.load_hip()
+    r = rng(d + F + S + k)
+    parts = {nm: [packed_only(orc, Q2K, *shp, r) for _ in range(E)] for nm, shp in
+             (("g", (F, d)), ("u", (F, d)), ("dn", (d, F)))}
+    gate, up, down = (np.concatenate(parts[nm]) for nm in ("g", "u", "dn"))
+    sgu, sdn = gate.nbytes // E, down.nbytes // E
+    sg, sg64 = weight(orc, Q2K, S, d, r)
+    su, su64 = weight(orc, Q2K, S, d, r)
+    sd, sd64 = weight(orc, Q2K, d, S, r)
+    wr = (r.standard_normal((E, d)) * 0.05).astype(np.float32)
+    ln2 = r.uniform(0.8, 1.2, d).astype(np.float32)
+    h0 = (r.standard_normal(d) * 2).astype(np.float32)
+    h64 = h0.astype(np.float64)
+    a2 = h64 / np.sqrt((h64 ** 2).mean() + 1e-5) * ln2
+    lg = wr.astype(np.float64) @ a2
+    p = np.exp(lg - lg.max())
+    p /= p.sum()
+    order = np.argsort(-p, kind="stable")
+    assert p[order[k - 1]] - p[order[k]] > 1e-4, "router near tie: choose another seed"
+    ids_o, pr_o = orc.moe_topk(lg.astype(np.float32), k)
+
+    def silu(v):
+        return v / (1 + np.exp(-v))
+
+    acc = sd64 @ (silu(sg64 @ a2) * (su64 @ a2))
+    for j in range(k):
+        e = ids_o[j]
+        g = as_f64(Q2K, parts["g"][e], F, d) @ a2
+        u = as_f64(Q2K, parts["u"][e], F, d) @ a2
+        acc = acc + p[e] * (as_f64(Q2K, parts["dn"][e], d, F) @ (silu(g) * u))
+    ref = h64 + acc
+    hd = dev(h0)
+    wsb = hip.rina_hip_moe_block_workspace(d, E, k, F, S)
+    ws = empty(wsb // 4 + 4)
+    keep = [dev(t) for t in (ln2, wr, sg, su, sd, gate, up, down)]
+    ok(hip.rina_hip_moe_block(hd.data_ptr(), keep[0].data_ptr(), np.float32(1e-5), keep[1].data_ptr(), FP32,
+                              keep[2].data_ptr(), keep[3].data_ptr(), keep[4].data_ptr(), S, keep[5].data_ptr(),
+                              keep[6].data_ptr(), keep[7].data_ptr(), Q2K, sgu, sdn, E, k, d, F, ws.data_ptr(), wsb,
+                              stream()), "moe block")
+    assert_close(host(hd), ref, what="moe block d %d F %d S %d" % (d, F, S))
+    wh = host(ws)
+    n = S + k * F
+    got_ids = wh[n + d + E: n + d + E + k].view(np.int32)
+    assert got_ids.tolist() == ids_o.tolist()
+    assert np.allclose(wh[n + d + E + k: n + d + E + 2 * k], pr_o, rtol=1e-5, atol=0)
+    # a second call on the updated stream reuses the workspace
+    ok(hip.rina_hip_moe_block(hd.data_ptr(), keep[0].data_ptr(), np.float32(1e-5), keep[1].data_ptr(), FP32,
+                              keep[2].data_ptr(), keep[3].data_ptr(), keep[4].data_ptr(), S, keep[5].data_ptr(),
+                              keep[6].data_ptr(), keep[7].data_ptr(), Q2K, sgu, sdn, E, k, d, F, ws.data_ptr(), wsb,
+                              stream()), "moe block 2")
+    assert np.all(np.isfinite(host(hd)))
+
+
+def test_moe_block_rejects_unsupported(rina):
+    hip = rina.load_hip()
+    buf = empty(1 << 16)
+    ptr = buf.data_ptr()
+    args = lambda d, F, S, E, k, qt, qr: (ptr, ptr, np.float32(1e-5), ptr, qr, ptr, ptr, ptr, S, ptr, ptr, ptr, qt,
+                                          256, 256, E, k, d, F, ptr, 1 << 18, stream())
+    assert hip.rina_hip_moe_block(*args(256, 48, 64, 8, 3, Q2K, FP32)) == -3    # F % 32
+    assert hip.rina_hip_moe_block(*args(256, 64, 64, 8, 3, Q4F, FP32)) == -2
+    assert hip.rina_hip_moe_block(*args(256, 64, 64, 8, 3, Q2K, Q2K)) == -2    # router not fp32
+    assert hip.rina_hip_moe_block(*args(4096, 64, 64, 8, 3, Q2K, FP32)) == -3
+    assert hip.rina_hip_moe_block(*args(256, 64, 64, 128, 3, Q2K, FP32)) == -3  # E > 64
+    assert hip.rina_hip_moe_block(*args(256, 64, 64 * 300, 8, 7, Q2K, FP32)) == -3   # shared + k ffn > 16384
+
+
 # ---- engine ---------------------------------------------------------------
 
 def header(max_seq):
