@@ -64,6 +64,98 @@ def roofline(bytes_per_launch, seconds, traffic=None):
             "frac": round(a / HBM_PEAK, 4), "traffic": traffic}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_lm_head_fp32.json")
+COPY_BYTES = 512 << 20          # calibration copy: 512 MiB read + 512 MiB written (> the 256 MB MALL)
+
+
+def traffic_probe(iters):
+    """Run under rocprofv3 --pmc: the LM head matvec (128256 x 2048 fp32) and
+    a plain device copy of COPY_BYTES, `iters` launches each."""
+    import torch
+    rina = pkg()
+    hip = rina.load_hip()
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    st = stream.cuda_stream
+    d, V = 2048, 128256
+    w = torch.randn(V * d, device="cuda") * 0.02
+    x = torch.randn(d, device="cuda")
+    y = torch.empty(V, device="cuda")
+    src = torch.randn(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        rina.check(hip.rina_hip_linear(w.data_ptr(), rina.QT_FP32, x.data_ptr(), y.data_ptr(), 1, V, d, st), "lm head")
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("probe done", flush=True)
+
+
+def _pmc_avg(db, counter):
+    """Per-dispatch average of `counter` (KiB) for the LM head kernel and the copy kernel."""
+    import sqlite3
+    c = sqlite3.connect(db)
+    cols = [r[1] for r in c.execute("pragma table_info(counters_collection)")]
+    ix = {n: i for i, n in enumerate(cols)}
+    vals = {"lm": [], "copy": []}
+    for r in c.execute("select * from counters_collection").fetchall():
+        if r[ix["counter_name"]] != counter:
+            continue
+        name = r[ix["kernel_name"]]
+        key = "lm" if "gemv_f32_kernel" in name else "copy" if "copyBuffer" in name else None
+        if key:
+            vals[key].append(float(r[ix["value"]]))
+    return {k: (sum(v) / len(v) if v else None) for k, v in vals.items()}, {k: len(v) for k, v in vals.items()}
+
+
+def measure_traffic(iters=10):
+    """Two rocprofv3 --pmc passes over traffic_probe (FETCH_SIZE, then
+    WRITE_SIZE), each counter scaled by its reading on the plain copy of known
+    size; writes TRAFFIC_FILE.  The profiler runs as a child process."""
+    import subprocess
+    import tempfile
+    out = {}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="rina_pmc_", dir="/tmp")
+        cmd = ["rocprofv3", "--pmc", counter, "-d", d, "-o", "run", "--", sys.executable,
+               os.path.abspath(__file__), "--traffic-probe", str(iters)]
+        log("running: " + " ".join(cmd))
+        subprocess.run(cmd, cwd="/tmp", env=env, check=True, timeout=180)
+        db = [os.path.join(r, f) for r, _, fs in os.walk(d) for f in fs if f.endswith("_results.db")][0]
+        avg, n = _pmc_avg(db, counter)
+        log("%s KiB/dispatch: %s (dispatches %s)" % (counter, avg, n))
+        factor = COPY_BYTES / (avg["copy"] * 1024.0)       # bytes per counted KiB
+        out[counter] = {"lm_kib": avg["lm"], "copy_kib": avg["copy"], "factor": factor,
+                        "lm_bytes": avg["lm"] * 1024.0 * factor}
+    lm_alg = 128256 * 2048 * 4 + 2048 * 4 + 128256 * 4
+    res = {"kernel": "gemv_f32_kernel (tied LM head 128256x2048 fp32)", "algorithmic_bytes": lm_alg,
+           "fetch_bytes": round(out["FETCH_SIZE"]["lm_bytes"]), "write_bytes": round(out["WRITE_SIZE"]["lm_bytes"]),
+           "hbm_bytes": round(out["FETCH_SIZE"]["lm_bytes"] + out["WRITE_SIZE"]["lm_bytes"]),
+           "calibration": "plain device copy of %d bytes (reads and writes %d bytes)" % (COPY_BYTES, COPY_BYTES),
+           "counters": out, "command": "python bench.py --measure-traffic"}
+    res["traffic_over_algorithmic"] = round(res["hbm_bytes"] / lm_alg, 4)
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res), flush=True)
+
+
+def committed_traffic():
+    """HBM bytes per launch of the LM head from the committed PMC measurement."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t["hbm_bytes"], {
+            "fetch_bytes": t["fetch_bytes"], "write_bytes": t["write_bytes"],
+            "over_algorithmic": t["traffic_over_algorithmic"],
+            "source": "profiles/traffic_lm_head_fp32.json (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by "
+                      "the same counter on a plain copy of known size)"}
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,7 +169,16 @@ def main():
     ap.add_argument("--no-config4", action="store_true", help="skip the DeepSeek MLA + MoE (config 4) decode line")
     ap.add_argument("--config4-steps", type=int, default=32)
     ap.add_argument("--no-config5", action="store_true", help="skip the RINA Jamba (config 5) decode line")
+    ap.add_argument("--traffic-probe", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--measure-traffic", action="store_true",
+                    help="run the two rocprofv3 --pmc passes for the LM head's HBM traffic and write them to profiles/")
     args = ap.parse_args()
+    if args.traffic_probe:
+        traffic_probe(args.traffic_probe)
+        return
+    if args.measure_traffic:
+        measure_traffic()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X in this build "
               "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
@@ -127,7 +228,8 @@ def main():
     lm_bytes = V * d * 4 + d * 4 + V * 4
     t_lm = time_kernel(torch, lambda i=0: hip.rina_hip_linear(wte.data_ptr(), rina.QT_FP32, x.data_ptr(), y.data_ptr(),
                                                               1, V, d, st), args.kernel_iters)
-    lm_roof = roofline(lm_bytes, t_lm)
+    traffic, traffic_detail = committed_traffic()
+    lm_roof = roofline(lm_bytes, t_lm, traffic)
     log("lm_head fp32 GEMV: %.1f us, %.0f GB/s" % (t_lm * 1e6, lm_bytes / t_lm / 1e9))
 
     # ---- Q4_0F SwiGLU matvec over the model's own layers (ring > MALL)
@@ -265,7 +367,7 @@ def main():
                                "greedy" % (cfg["n_layers"], args.prompt),
                    "prompt": args.prompt, "kv": "fp32", "weights": "Q4_0F"},
         "roofline": dict(lm_roof, kernel="gemv_f32_kernel (tied LM head 128256x2048 fp32)",
-                         bytes_per_launch=lm_bytes, avg_us=round(t_lm * 1e6, 2)),
+                         bytes_per_launch=lm_bytes, avg_us=round(t_lm * 1e6, 2), traffic_detail=traffic_detail),
         "roofline_other": {
             "q4_0f_swiglu_w1w3": dict(sw_roof, bytes_per_launch=sw_bytes, avg_us=round(t_sw * 1e6, 2)),
             "config1_q4_0_gemv_8192x2048": dict(q4_roof, bytes_per_launch=q4_bytes, avg_us=round(t_q4 * 1e6, 3)),
