@@ -685,7 +685,63 @@ __device__ __forceinline__ float f32_row_dot(const float* w, const float* xl, in
     return (s0 + s1) + (s2 + s3);
 }
 
-template <int NMAT, bool VEC>
+// Rows of K <= 2048 values: a wave takes RPW rows at a time and issues all
+// their 16-byte loads (NV per lane per row, lane + 64 t) before any
+// arithmetic, so a lane keeps RPW * NV loads in flight.
+template <int NMAT, int NV>
+__device__ __forceinline__ void f32_rows_short(const F32Args& a, const float* xs_lds, int gw, int nw) {
+    constexpr int RPW = NMAT == 2 ? 2 : 4;
+    const int lane = threadIdx.x & 63;
+    const int K = a.K, n4 = K >> 2;
+    const f32x4* x4 = (const f32x4*)xs_lds;
+    for (int r0 = gw * RPW; r0 < a.total_rows; r0 += nw * RPW) {
+        f32x4 w[RPW][NMAT][NV];
+        int seg[RPW], row[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const int vr = min(r0 + r, a.total_rows - 1);
+            int s = 0;
+            if (a.nseg > 1 && vr >= a.seg[1].tile0) s = 1;
+            if (a.nseg > 2 && vr >= a.seg[2].tile0) s = 2;
+            seg[r] = s;
+            row[r] = vr - a.seg[s].tile0;
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                const f32x4* wr = (const f32x4*)(m == 0 ? a.seg[s].w : a.seg[s].w2) + (int64_t)row[r] * n4;
+#pragma unroll
+                for (int t = 0; t < NV; t++) {
+                    const int k = lane + 64 * t;
+                    w[r][m][t] = gld_nt(wr + (k < n4 ? k : 0));
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            float v[2];
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                for (int t = 0; t < NV; t++) {
+                    const int k = lane + 64 * t;
+                    const f32x4 b = k < n4 ? x4[k] : f32x4{0.f, 0.f, 0.f, 0.f};
+                    float& acc = (t & 1) ? s1 : s0;
+                    acc = fmaf(b.x, w[r][m][t].x, acc); acc = fmaf(b.y, w[r][m][t].y, acc);
+                    acc = fmaf(b.z, w[r][m][t].z, acc); acc = fmaf(b.w, w[r][m][t].w, acc);
+                }
+                v[m] = wave_sum(s0 + s1);
+            }
+            if (lane == 0 && r0 + r < a.total_rows) {
+                float* y = a.seg[seg[r]].y + row[r];
+                if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
+                else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
+                else gst(y, v[0]);
+            }
+        }
+    }
+}
+
+template <int NMAT, bool VEC, int NV>
 __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     extern __shared__ __align__(16) float xs_lds[];
     __shared__ float red[8];
@@ -717,6 +773,10 @@ __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     }
     __syncthreads();
     const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
+    if constexpr (NV > 0) {
+        f32_rows_short<NMAT, NV>(a, xs_lds, gw, nw);
+        return;
+    }
     for (int vr = gw; vr < a.total_rows; vr += nw) {
         int s = 0;
         if (a.nseg > 1 && vr >= a.seg[1].tile0) s = 1;
@@ -1014,13 +1074,32 @@ int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int e
     size_t lds = (size_t)K * 4;
     if (lds > 64 * 1024) return RINA_ERR_SHAPE;
     bool two = (epi == RINA_EPI_SWIGLU);
-    if (two) {
-        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<2, true>), dim3(grid), dim3(kWG), lds, st, a);
-        else hipLaunchKernelGGL((gemv_f32_kernel<2, false>), dim3(grid), dim3(kWG), lds, st, a);
-    } else {
-        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<1, true>), dim3(grid), dim3(kWG), lds, st, a);
-        else hipLaunchKernelGGL((gemv_f32_kernel<1, false>), dim3(grid), dim3(kWG), lds, st, a);
+    // short rows (K <= 2048, 16-byte aligned): several rows per wave with all
+    // loads in flight; NV = 16-byte loads per lane per row
+    const int nv = vec && K <= 2048 ? (K / 4 + 63) / 64 : 0;
+    if (nv > 0) {
+        const int rpw = two ? 2 : 4;
+        int g2 = (rows + 4 * rpw - 1) / (4 * rpw);
+        if (g2 < grid) grid = g2;
     }
+#define F32_LAUNCH(NM, V, NVV) hipLaunchKernelGGL((gemv_f32_kernel<NM, V, NVV>), dim3(grid), dim3(kWG), lds, st, a)
+    if (nv > 0) {
+        switch ((nv <= 2 ? 2 : nv <= 4 ? 4 : 8) * (two ? -1 : 1)) {
+            case 2: F32_LAUNCH(1, true, 2); break;
+            case 4: F32_LAUNCH(1, true, 4); break;
+            case 8: F32_LAUNCH(1, true, 8); break;
+            case -2: F32_LAUNCH(2, true, 2); break;
+            case -4: F32_LAUNCH(2, true, 4); break;
+            default: F32_LAUNCH(2, true, 8); break;
+        }
+    } else if (two) {
+        if (vec) F32_LAUNCH(2, true, 0);
+        else F32_LAUNCH(2, false, 0);
+    } else {
+        if (vec) F32_LAUNCH(1, true, 0);
+        else F32_LAUNCH(1, false, 0);
+    }
+#undef F32_LAUNCH
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 
