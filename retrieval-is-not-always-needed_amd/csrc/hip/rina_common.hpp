@@ -98,14 +98,21 @@ __device__ __forceinline__ float sum16(float v) {
     return v;
 }
 
-// Sum over the whole wave, result uniform.
+// DPP with a row mask: rows outside ROWS read 0 (the identity of the adds below).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false));
+}
+
+// Sum over the whole wave, result uniform.  After the row sums R0..R3,
+// row_bcast:15 adds R0 into row 1 and R2 into row 3, row_bcast:31 adds row
+// 1's (R1 + R0) into row 3, and lane 63 holds (R3 + R2) + (R1 + R0): the
+// pairing (R0 + R1) + (R2 + R3), bit for bit, with one readlane.
 __device__ __forceinline__ float wave_sum(float v) {
     v = sum16(v);
-    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return (r0 + r1) + (r2 + r3);
+    v += dpp_rows<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
+    v += dpp_rows<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
