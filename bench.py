@@ -44,18 +44,28 @@ def pkg():
     return mod
 
 
-def time_kernel(torch, fn, iters):
-    """Average device time (s) of fn() launches on torch's current stream."""
+def time_kernel(torch, fn, iters, replays=3):
+    """Average device time (s) per fn(i) launch on torch's current stream:
+    `iters` launches are captured once as a HIP graph and the graph is
+    replayed between two HIP events on that stream, so the host's launch
+    rate does not enter the figure."""
     st = torch.cuda.current_stream()
     fn()
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        for i in range(iters):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for i in range(iters):
-        fn(i)
+    for _ in range(replays):
+        g.replay()
     e1.record(st)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / iters
+    del g
+    return e0.elapsed_time(e1) / 1e3 / (iters * replays)
 
 
 def roofline(bytes_per_launch, seconds, traffic=None):
