@@ -64,8 +64,9 @@ int rina_hip_linear(const void* weight, int quant_type, const float* input,
                     float* output, int M, int N, int K, void* stream);
 
 /* Fused matvec launch (no single reference counterpart: it fuses calls the
- * reference makes back to back).  Up to 3 weight segments share one input
- * vector and one launch:
+ * reference makes back to back).  Up to 6 weight segments share one input
+ * vector and one launch (M == 1 Q4_0 / Q4_0F / Q2_K rows of K <= 8192,
+ * K % 32 == 0; other shapes run 3 segments per launch):
  *   RINA_EPI_STORE   out_s = W_s . x          (q/k/v: gqa_layer.cu:139-141)
  *   RINA_EPI_ADD     out_s = out_s + W_s . x  (w_o/w2 + launch_add:
  *                                              gqa_layer.cu:272-273,282-283)
@@ -96,6 +97,17 @@ int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int quant_type,
                           const float* input, int M, int K, int epilogue,
                           int prologue, const float* norm_w, float eps,
                           void* stream);
+
+/* rina_hip_linear_fused that also stores the normalized input row
+ * (prologue != RINA_PRO_NONE, M == 1) into norm_out [K]: the reference's
+ * norm launch and the first matvec that reads it in one launch, with the
+ * normalized row left for later consumers (the SSM layer's W_dq and W_out,
+ * arch/ssm/rina_ssm_layer.cu:93-112).  norm_out must not alias input or
+ * an output. */
+int rina_hip_linear_fused_ex(const rina_linear_seg* segs, int nseg, int quant_type,
+                             const float* input, int M, int K, int epilogue,
+                             int prologue, const float* norm_w, float eps,
+                             float* norm_out, void* stream);
 
 /* ====================================================================== */
 /* Weight formats                                                          */

@@ -34,6 +34,7 @@ class LinearSeg(C.Structure):
 _HIP_SIGS = {
     "rina_hip_linear": (I32, [VP, I32, VP, VP, I32, I32, I32, VP]),
     "rina_hip_linear_fused": (I32, [C.POINTER(LinearSeg), I32, I32, VP, I32, I32, I32, I32, VP, F32, VP]),
+    "rina_hip_linear_fused_ex": (I32, [C.POINTER(LinearSeg), I32, I32, VP, I32, I32, I32, I32, VP, F32, VP, VP]),
     "rina_hip_pack_weights": (I32, [I32, VP, I64, VP, VP]),
     "rina_hip_dequant_weights": (I32, [I32, VP, I64, VP, VP]),
     "rina_hip_pack_weights_hf": (I32, [VP, I64, VP, VP]),

@@ -124,17 +124,17 @@ struct SSMImpl {
 #define CK(x) do { if ((rc = (x)) != RINA_OK) return rc; } while (0)
         for (int t = 0; t < T; t++) {
             float* ht = h + (size_t)t * d;
-            CK(rina_hip_layer_norm(ht, x2, ln1, 1, d, 1e-5f, s));                              // :93-95
+            // x = LN(h, ln1) as W_dq's prologue; the launch also stores x for W_out (:93-96)
             rina_linear_seg sq{w_dq, nullptr, cq, dc};
-            CK(rina_hip_linear_fused(&sq, 1, qt, x2, 1, d, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
-            rina_linear_seg sm[3], sd[3];
+            CK(rina_hip_linear_fused_ex(&sq, 1, qt, ht, 1, d, RINA_EPI_STORE, RINA_PRO_LAYERNORM, ln1, 1e-5f, x2, s));
+            // the memory and decay projections share LN(cq, q_norm): one launch (:97-101)
+            rina_linear_seg sp[6];
             for (int k = 0; k < steps; k++) {
-                sm[k] = {w_mem[k], nullptr, mem + (size_t)k * H * dh, H * dh};
-                sd[k] = {w_decay[k], nullptr, dec + (size_t)k * H, H};
+                sp[k] = {w_mem[k], nullptr, mem + (size_t)k * H * dh, H * dh};
+                sp[steps + k] = {w_decay[k], nullptr, dec + (size_t)k * H, H};
             }
-            // q_norm fused as the prologue of the memory and decay projections (:97-101)
-            CK(rina_hip_linear_fused(sm, steps, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
-            CK(rina_hip_linear_fused(sd, steps, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
+            CK(rina_hip_linear_fused(sp, 2 * steps, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f,
+                                     s));
             const int reset = (!b.d_pos && start_pos == 0 && t == 0) ? 1 : 0;
             CK(rina_hip_ssm_step(mem, dec, steps, H, dh, lcs, wcs, x2 + d, reset, s));           // :102-109
             rina_linear_seg so{w_out, nullptr, ht, d};

@@ -37,9 +37,13 @@ struct GemvSeg {
     int tile0;
 };
 
+constexpr int kMaxDirectSegs = 6;   // row segments of one direct-kernel launch (tile kernel: 3)
+
 struct GemvArgs {
     GemvSeg seg[3];
+    GemvSeg seg_hi[3];   // segments 3..5 (direct kernel only, read with constant indices)
     int nseg;
+    float* xn;           // direct kernel with a norm prologue: workgroup 0 stores the normalized row (or NULL)
     const float* x;
     int K;
     int R;            // rows per tile
@@ -448,35 +452,50 @@ __device__ __forceinline__ uint64_t uni64(const void* p) {
 // of segment sg is picked with integer arithmetic on these values: indexing
 // the argument struct (or any array) with a run-time segment number makes
 // the compiler copy it to scratch memory.
+template <int NS>
 struct DirectSegs {
-    uint64_t w0, w1, w2, v0, v1, v2, y0, y1, y2;
-    int t1, t2, nseg;
+    uint64_t w[NS], v[NS], y[NS];
+    int t[NS];
+    int nseg;
     __device__ __forceinline__ explicit DirectSegs(const GemvArgs& a) {
-        w0 = uni64(a.seg[0].w); w1 = uni64(a.seg[1].w); w2 = uni64(a.seg[2].w);
-        v0 = uni64(a.seg[0].w2); v1 = uni64(a.seg[1].w2); v2 = uni64(a.seg[2].w2);
-        y0 = uni64(a.seg[0].y); y1 = uni64(a.seg[1].y); y2 = uni64(a.seg[2].y);
-        t1 = __builtin_amdgcn_readfirstlane(a.seg[1].tile0);
-        t2 = __builtin_amdgcn_readfirstlane(a.seg[2].tile0);
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const GemvSeg& g = i < 3 ? a.seg[i] : a.seg_hi[i - 3];
+            w[i] = uni64(g.w);
+            v[i] = uni64(g.w2);
+            y[i] = uni64(g.y);
+            t[i] = __builtin_amdgcn_readfirstlane(g.tile0);
+        }
         nseg = __builtin_amdgcn_readfirstlane(a.nseg);
     }
+    // segments are in row order: the segment of virtual row vr
     __device__ __forceinline__ int seg_of(int vr) const {
-        return (nseg > 2 && vr >= t2) ? 2 : (nseg > 1 && vr >= t1) ? 1 : 0;
+        int s = 0;
+#pragma unroll
+        for (int i = 1; i < NS; i++) s += (i < nseg && vr >= t[i]) ? 1 : 0;
+        return s;
     }
-    __device__ __forceinline__ static uint64_t sel(int sg, uint64_t f0, uint64_t f1, uint64_t f2) {
-        const uint64_t m1 = (uint64_t)0 - (uint64_t)(sg == 1), m2 = (uint64_t)0 - (uint64_t)(sg == 2);
-        const uint64_t m0 = ~(m1 | m2);
-        return (f0 & m0) | (f1 & m1) | (f2 & m2);
+    __device__ __forceinline__ static uint64_t sel(int sg, const uint64_t (&f)[NS]) {
+        uint64_t r = 0;
+#pragma unroll
+        for (int i = 0; i < NS; i++) r |= f[i] & ((uint64_t)0 - (uint64_t)(sg == i));
+        return r;
     }
-    __device__ __forceinline__ int t0(int sg) const { return (int)sel(sg, 0, (uint64_t)t1, (uint64_t)t2); }
+    __device__ __forceinline__ int t0(int sg) const {
+        int r = 0;
+#pragma unroll
+        for (int i = 0; i < NS; i++) r |= t[i] & -(int)(sg == i);
+        return r;
+    }
     __device__ __forceinline__ const uint8_t* wt(int sg, int m) const {
-        return (const uint8_t*)(m == 0 ? sel(sg, w0, w1, w2) : sel(sg, v0, v1, v2));
+        return (const uint8_t*)(m == 0 ? sel(sg, w) : sel(sg, v));
     }
-    __device__ __forceinline__ float* out(int sg) const { return (float*)sel(sg, y0, y1, y2); }
+    __device__ __forceinline__ float* out(int sg) const { return (float*)sel(sg, y); }
 };
 
 // Issue the loads of row group grp (virtual rows grp*RB ..) for block column u.
-template <int FMT, int NMAT, int RB>
-__device__ __forceinline__ void direct_issue(const GemvArgs& a, const DirectSegs& S, int grp, int u, bool active,
+template <int FMT, int NMAT, int RB, typename Segs>
+__device__ __forceinline__ void direct_issue(const GemvArgs& a, const Segs& S, int grp, int u, bool active,
                                              DirectBlk<RB>& b) {
     constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
 #pragma unroll
@@ -498,8 +517,8 @@ __device__ __forceinline__ void direct_issue(const GemvArgs& a, const DirectSegs
 }
 
 // Q2_K: column u of row n is flat elements [nK + 32u, nK + 32u + 32).
-template <int FMT, int NMAT, int RB>
-__device__ __forceinline__ void direct_issue(const GemvArgs& a, const DirectSegs& S, int grp, int u, bool active,
+template <int FMT, int NMAT, int RB, typename Segs>
+__device__ __forceinline__ void direct_issue(const GemvArgs& a, const Segs& S, int grp, int u, bool active,
                                              DirectBlkQ2<RB>& b) {
 #pragma unroll
     for (int i = 0; i < RB; i++) {
@@ -525,8 +544,8 @@ __device__ __forceinline__ void direct_issue(const GemvArgs& a, const DirectSegs
     }
 }
 
-template <int NMAT>
-__device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const DirectSegs& S, int sg, int n,
+template <int NMAT, typename Segs>
+__device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const Segs& S, int sg, int n,
                                                 const float (&v)[2]) {
     float* y = S.out(sg) + n;
     if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
@@ -535,8 +554,8 @@ __device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const DirectS
 }
 
 // Row sums of one row group and their epilogue.
-template <int FMT, int WPR, int NMAT, int RB>
-__device__ __forceinline__ void direct_consume(const GemvArgs& a, const DirectSegs& S, const DCols<FMT>& xc,
+template <int FMT, int WPR, int NMAT, int RB, typename Segs>
+__device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S, const DCols<FMT>& xc,
                                                const DirectBlkT<FMT, RB>& cur, int it, int rs, int cp,
                                                float (*red)[RB * NMAT][WPR]) {
     constexpr int RPI = 4 / WPR;
@@ -590,7 +609,7 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const DirectSe
 // Workgroup iterations alternate between two register sets (A, B): the next
 // group's loads are issued before the current group is reduced, and each
 // path has its own straight-line code so the load counters stay exact.
-template <int FMT, int WPR, int NMAT, int PRO, int RB>
+template <int FMT, int WPR, int NMAT, int PRO, int RB, int NS>
 __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
     constexpr int RPI = 4 / WPR;                 // row groups per workgroup iteration
     __shared__ float red[RPI][RB * NMAT][WPR];
@@ -601,14 +620,14 @@ __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
     const bool active = u < a.K / 32;
     const int G = gridDim.x;
     const int ngrp = a.total_tiles;
-    const DirectSegs S(a);
+    const DirectSegs<NS> S(a);
 
     // activation loads, then the first row group's weight loads, then the
     // activation prep (overlapping the weight loads)
     __shared__ PrepLds prep;
     constexpr int TPC = WPR == 1 ? 4 : WPR == 2 ? 2 : 1;
     PrepRaw<TPC, PRO> raw;
-    const PrepSrc src{a.x, a.nw, a.K, a.eps};
+    const PrepSrc src{a.x, a.nw, a.K, a.eps, a.xn};
     wg_prep_load<TPC, PRO>(src, raw);
     int it = blockIdx.x;
     DirectBlkT<FMT, RB> A, B;
@@ -923,7 +942,7 @@ int dispatch_wpr(GemvArgs& a, int wpr, int cpl, int pro, hipStream_t st) {
     }
 }
 
-template <int FMT, int WPR, int NMAT, int PRO, int RB>
+template <int FMT, int WPR, int NMAT, int PRO, int RB, int NS>
 int launch_direct(GemvArgs& a, hipStream_t st) {
     constexpr int RPI = 4 / WPR;
     int cus = rina_num_cus();
@@ -931,17 +950,24 @@ int launch_direct(GemvArgs& a, hipStream_t st) {
     // workgroups resident per CU at this register count
     int per_cu = FMT == FMT_Q2_K ? (RB >= 4 ? (NMAT == 2 ? 2 : 3) : 4) : (RB >= 8 ? 2 : RB == 4 ? 3 : 4);
     int grid = wgs < cus * per_cu ? wgs : cus * per_cu;
-    hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB>), dim3(grid), dim3(kWG), 0, st, a);
+    hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB, NS>), dim3(grid), dim3(kWG), 0, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 
 template <int FMT, int WPR, int NMAT, int PRO>
 int direct_rb(GemvArgs& a, int rb, hipStream_t st) {
+    if (a.nseg > 3) {   // more than 3 segments: the 6-segment table, 1 or 2 rows per wave
+        if constexpr (NMAT == 1) {
+            return rb <= 1 ? launch_direct<FMT, WPR, 1, PRO, 1, kMaxDirectSegs>(a, st)
+                           : launch_direct<FMT, WPR, 1, PRO, 2, kMaxDirectSegs>(a, st);
+        }
+        return RINA_ERR_ARG;
+    }
     switch (rb) {
-        case 1: return launch_direct<FMT, WPR, NMAT, PRO, 1>(a, st);
-        case 2: return launch_direct<FMT, WPR, NMAT, PRO, 2>(a, st);
-        case 4: return launch_direct<FMT, WPR, NMAT, PRO, 4>(a, st);
-        default: return launch_direct<FMT, WPR, NMAT, PRO, (FMT == FMT_Q2_K ? 4 : 8)>(a, st);
+        case 1: return launch_direct<FMT, WPR, NMAT, PRO, 1, 3>(a, st);
+        case 2: return launch_direct<FMT, WPR, NMAT, PRO, 2, 3>(a, st);
+        case 4: return launch_direct<FMT, WPR, NMAT, PRO, 4, 3>(a, st);
+        default: return launch_direct<FMT, WPR, NMAT, PRO, (FMT == FMT_Q2_K ? 4 : 8), 3>(a, st);
     }
 }
 
@@ -971,7 +997,7 @@ void split_row(int nunits, int& wpr, int& cpl) {
 }
 
 int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, int K, int epi, int pro,
-               const float* nw, float eps, hipStream_t st) {
+               const float* nw, float eps, float* xn, hipStream_t st) {
     int fmt = fmt_of(qt);
     int nmat = (epi == RINA_EPI_SWIGLU) ? 2 : 1;
     int unit = fmt == FMT_Q2_K ? 16 : 32;
@@ -993,13 +1019,15 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
         // direct-load kernel: virtual rows over all segments, RB rows per wave
         int rows = 0;
         for (int s = 0; s < nseg; s++) {
-            a.seg[s].w = (const uint8_t*)segs[s].weight;
-            a.seg[s].w2 = (const uint8_t*)segs[s].weight2;
-            a.seg[s].y = segs[s].out;
-            a.seg[s].N = segs[s].N;
-            a.seg[s].tile0 = rows;
+            GemvSeg& g = s < 3 ? a.seg[s] : a.seg_hi[s - 3];
+            g.w = (const uint8_t*)segs[s].weight;
+            g.w2 = (const uint8_t*)segs[s].weight2;
+            g.y = segs[s].out;
+            g.N = segs[s].N;
+            g.tile0 = rows;
             rows += segs[s].N;
         }
+        a.xn = pro != RINA_PRO_NONE ? xn : nullptr;
         // rows per wave: about two workgroups per CU (each preps the
         // activation once), up to 8 rows per wave
         int64_t waves = (int64_t)rina_num_cus() * 8;
@@ -1117,12 +1145,14 @@ bool qt_supported(int qt) {
 
 }  // namespace
 
-extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int qt, const float* input,
-                                     int M, int K, int epi, int pro, const float* nw, float eps, void* stream) {
-    if (!segs || nseg < 1 || nseg > 3 || !input || M < 1 || K < 1) return RINA_ERR_ARG;
+extern "C" int rina_hip_linear_fused_ex(const rina_linear_seg* segs, int nseg, int qt, const float* input, int M,
+                                        int K, int epi, int pro, const float* nw, float eps, float* norm_out,
+                                        void* stream) {
+    if (!segs || nseg < 1 || nseg > kMaxDirectSegs || !input || M < 1 || K < 1) return RINA_ERR_ARG;
     if (!qt_supported(qt)) return RINA_ERR_QTYPE;
     if (epi < RINA_EPI_STORE || epi > RINA_EPI_SWIGLU) return RINA_ERR_ARG;
     if (pro < RINA_PRO_NONE || pro > RINA_PRO_LAYERNORM || (pro != RINA_PRO_NONE && !nw)) return RINA_ERR_ARG;
+    if (norm_out && (pro == RINA_PRO_NONE || M != 1)) return RINA_ERR_ARG;
     if (epi == RINA_EPI_SWIGLU && nseg != 1) return RINA_ERR_ARG;
     if ((qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && (K % 32)) return RINA_ERR_SHAPE;
     for (int s = 0; s < nseg; s++) {
@@ -1134,20 +1164,32 @@ extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int 
     int unit = qt == RINA_QT_GGML_Q2_K ? 16 : 32;
     int wpr = 1, cpl = 1;
     if (qt != RINA_QT_FP32 && K % unit == 0) split_row(K / unit, wpr, cpl);
-    // direct kernel: any waves-per-row; Q2_K tile kernel: one wave per row
-    const bool direct = qt != RINA_QT_FP32 && direct_ok(fmt_of(qt), K);
+    // direct kernel: any waves-per-row, up to kMaxDirectSegs segments; other
+    // kernels: 3 segments per launch
+    const bool direct = M == 1 && qt != RINA_QT_FP32 && direct_ok(fmt_of(qt), K) && (uintptr_t)input % 16 == 0;
     bool fused_pro = M == 1 && ((qt == RINA_QT_FP32 && K <= 16384) ||
                                 (qt != RINA_QT_FP32 && (direct || (wpr == 1 && cpl == 1)) && (uintptr_t)input % 16 == 0 &&
                                  (uintptr_t)nw % 16 == 0));
-    if (pro != RINA_PRO_NONE && !fused_pro) {
-        // normalize into library scratch first (prompt rows, unusual shapes)
-        float* tmp = (float*)rina_scratch((size_t)M * K * 4);
+    if (direct && norm_out && (uintptr_t)norm_out % 16) fused_pro = false;
+    if (pro != RINA_PRO_NONE && (!fused_pro || (norm_out && !direct))) {
+        // normalize first (into norm_out when given, else library scratch):
+        // prompt rows, unusual shapes
+        float* tmp = norm_out ? norm_out : (float*)rina_scratch((size_t)M * K * 4);
         if (!tmp) return RINA_ERR_HIP;
         int rc = pro == RINA_PRO_RMSNORM ? rina_hip_rms_norm(input, tmp, nw, M, K, eps, stream)
                                          : rina_hip_layer_norm(input, tmp, nw, M, K, eps, stream);
         if (rc) return rc;
         input = tmp;
         pro = RINA_PRO_NONE;
+        norm_out = nullptr;
+    }
+    if (nseg > 3 && !direct) {   // the other kernels take 3 segments per launch
+        for (int s0 = 0; s0 < nseg; s0 += 3) {
+            int rc = rina_hip_linear_fused_ex(segs + s0, nseg - s0 < 3 ? nseg - s0 : 3, qt, input, M, K, epi, pro, nw,
+                                              eps, nullptr, stream);
+            if (rc) return rc;
+        }
+        return RINA_OK;
     }
     if (M > 1) {
         for (int s = 0; s < nseg; s++) {
@@ -1164,7 +1206,12 @@ extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int 
         }
         return RINA_OK;
     }
-    return gemv_quant(segs, nseg, qt, input, K, epi, pro, nw, eps, st);
+    return gemv_quant(segs, nseg, qt, input, K, epi, pro, nw, eps, norm_out, st);
+}
+
+extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int qt, const float* input, int M, int K,
+                                     int epi, int pro, const float* nw, float eps, void* stream) {
+    return rina_hip_linear_fused_ex(segs, nseg, qt, input, M, K, epi, pro, nw, eps, nullptr, stream);
 }
 
 extern "C" int rina_hip_linear(const void* weight, int qt, const float* input, float* output, int M, int N, int K,

@@ -193,6 +193,7 @@ struct PrepSrc {
     const float* nw;
     int K;
     float eps;
+    float* xn = nullptr;   // with a norm prologue: workgroup 0 stores the normalized row here
 };
 
 // Workgroup-cooperative activation prep for the direct kernel: the K values
@@ -305,6 +306,11 @@ __device__ __forceinline__ void wg_prep_x(const PrepSrc& a, PrepRaw<TPC, PRO>& r
         const float inv = 1.0f / sqrtf(block_sum4(ss, L.red, 1) / d + a.eps);
 #pragma unroll
         for (int i = 0; i < VPC; i++) x[i] = on ? (x[i] - mean) * inv * w[i] : 0.f;
+        if (a.xn && blockIdx.x == 0 && on) {
+            f32x4* xo = (f32x4*)(a.xn + (int64_t)u * 32 + j * VPC);
+#pragma unroll
+            for (int i = 0; i < VPC / 4; i++) gst(xo + i, f32x4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]});
+        }
     }
     float mx = 0.f;
 #pragma unroll

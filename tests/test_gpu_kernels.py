@@ -172,6 +172,50 @@ def test_linear_fused_epilogues(rina, orc, qt):
     assert_close(host(gd), ref, what="swiglu")
 
 
+@pytest.mark.parametrize("qt,K", [(5, 640), (7, 2048), (10, 2048), (10, 1408), (6, 640), (5, 10240)])
+@pytest.mark.parametrize("pro", [0, 1, 2])
+def test_linear_fused_six_segments_and_norm_out(rina, orc, qt, K, pro):
+    """Up to 6 segments on one input (one launch on the direct path, 3 per
+    launch elsewhere) and the normalized row stored by the prologue."""
+    hip = rina.load_hip()
+    L = orc.load()
+    r = rng(qt * 1000 + K + pro)
+    Ns = (200, 37, 64, 150, 10, 96)
+
+    def mk(n):
+        if qt == 10:
+            return q2k_blocks(int(r.integers(1 << 30)), n * K)
+        wf = (r.standard_normal(n * K) * 0.02).astype(np.float32)
+        return wf if qt == 6 else orc.pack(qt, wf)
+
+    ws = [mk(n) for n in Ns]
+    x = (r.standard_normal(K) * 2 + 0.3).astype(np.float32)
+    nw = r.uniform(0.5, 1.5, K).astype(np.float32)
+    wd = [dev(w) for w in ws]
+    outs = [empty(n) for n in Ns]
+    xn = empty(K)
+    segs = (rina.LinearSeg * 6)(*[rina.LinearSeg(wd[i].data_ptr(), None, outs[i].data_ptr(), Ns[i]) for i in range(6)])
+    ok(hip.rina_hip_linear_fused_ex(segs, 6, qt, dev(x).data_ptr(), 1, K, rina.EPI_STORE, pro,
+                                    dev(nw).data_ptr() if pro else None, np.float32(1e-5),
+                                    xn.data_ptr() if pro else None, stream()), "six segments")
+    xr = x.copy()
+    if pro:
+        (L.orc_rms_norm if pro == 1 else L.orc_layer_norm)(xr.ctypes.data, nw.ctypes.data, 1, K, np.float32(1e-5))
+        assert_close(host(xn), xr, what="normalized row")
+    for i in range(6):
+        assert_close(host(outs[i]), orc.linear(ws[i], qt, xr, Ns[i], K)[0], what="segment %d" % i)
+
+
+def test_linear_fused_ex_rejects(rina):
+    hip = rina.load_hip()
+    buf = empty(1 << 16)
+    seg = (rina.LinearSeg * 7)(*[rina.LinearSeg(buf.data_ptr(), None, buf.data_ptr(), 4) for _ in range(7)])
+    p = buf.data_ptr()
+    assert hip.rina_hip_linear_fused_ex(seg, 7, 5, p, 1, 64, 0, 0, None, 0.0, None, stream()) == -1   # > 6 segments
+    assert hip.rina_hip_linear_fused_ex(seg, 1, 5, p, 1, 64, 0, 0, None, 0.0, p, stream()) == -1      # norm_out w/o prologue
+    assert hip.rina_hip_linear_fused_ex(seg, 1, 5, p, 2, 64, 0, 1, p, 0.0, p, stream()) == -1         # norm_out with M > 1
+
+
 @pytest.mark.parametrize("fmt", [1, 2, 3, 4])
 def test_kv_quantize_bitexact(rina, orc, fmt):
     hip = rina.load_hip()
