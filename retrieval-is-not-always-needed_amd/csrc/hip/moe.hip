@@ -248,26 +248,38 @@ __global__ __launch_bounds__(256) void moe_gate_up_q2_kernel(MoeBlkArgs a) {
 // the 16 lanes of a 16-byte LDS read on distinct banks.
 constexpr int kRec = 28;
 
-// Four threads per column (8 values each) digitize G cooperatively; every
-// round's loads go out first.
-__device__ __forceinline__ void stage_g_digits(const float* G, int ncol, uint32_t* rec) {
-    constexpr int ROUNDS = 4;                      // 512 threads x 4 rounds / 4 = 512 columns
+// Four threads per column (8 values each) digitize G cooperatively.  The
+// loads are issued by stage_g_load (before the weight loads, so waiting for
+// them does not wait for the weights: loads retire in issue order) and
+// consumed by stage_g_digits.
+constexpr int kStageRounds = 4;                    // 512 threads x 4 rounds / 4 = 512 columns
+
+struct GStage {
+    f32x4 v[kStageRounds][2];
+};
+
+__device__ __forceinline__ void stage_g_load(const float* G, int ncol, GStage& g) {
     const int tid = threadIdx.x, j = tid & 3;
-    const int rounds = (ncol + 127) / 128;         // uniform: the group shuffles see full waves
-    f32x4 v[ROUNDS][2];
+    const int rounds = (ncol + 127) / 128;
 #pragma unroll
-    for (int r = 0; r < ROUNDS; r++) {
+    for (int r = 0; r < kStageRounds; r++) {
         const int c = (tid >> 2) + 128 * r;
         const bool on = c < ncol && r < rounds;
         const f32x4* src = (const f32x4*)(G + 32 * (on ? c : 0) + 8 * j);
-        v[r][0] = on ? gld(src) : f32x4{0.f, 0.f, 0.f, 0.f};
-        v[r][1] = on ? gld(src + 1) : f32x4{0.f, 0.f, 0.f, 0.f};
+        g.v[r][0] = on ? gld(src) : f32x4{0.f, 0.f, 0.f, 0.f};
+        g.v[r][1] = on ? gld(src + 1) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+}
+
+__device__ __forceinline__ void stage_g_digits(const GStage& g, int ncol, uint32_t* rec) {
+    const int tid = threadIdx.x, j = tid & 3;
+    const int rounds = (ncol + 127) / 128;         // uniform: the group shuffles see full waves
 #pragma unroll
-    for (int r = 0; r < ROUNDS; r++) {
+    for (int r = 0; r < kStageRounds; r++) {
         if (r >= rounds) break;
         const int c = (tid >> 2) + 128 * r;
-        const float x[8] = {v[r][0].x, v[r][0].y, v[r][0].z, v[r][0].w, v[r][1].x, v[r][1].y, v[r][1].z, v[r][1].w};
+        const float x[8] = {g.v[r][0].x, g.v[r][0].y, g.v[r][0].z, g.v[r][0].w,
+                            g.v[r][1].x, g.v[r][1].y, g.v[r][1].z, g.v[r][1].w};
         float mx = 0.f, hs = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) { mx = fmaxf(mx, fabsf(x[i])); hs += x[i]; }
@@ -331,6 +343,17 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     const int ir = row_on ? i : 0;
     const float inv_f = 1.0f / (float)fcols;
 
+    // G and the selected experts / probabilities load together (one round
+    // trip); the weight addresses need the expert ids
+    GStage gs;
+    stage_g_load(a.G, ncol, gs);
+    int sid[16];
+    float spr[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        sid[j] = j < a.k ? __builtin_amdgcn_readfirstlane(gld(a.ids + j)) : -1;
+        spr[j] = j < a.k ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gld(a.probs + j)))) : 0.f;
+    }
     Q2Col c[kDnRounds];
     float wt[kDnRounds];
     int col[kDnRounds];
@@ -349,11 +372,17 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
                 int j = (int)((float)t * inv_f);       // t < 512: exact after one correction each way
                 j -= j * fcols > t;
                 j += (j + 1) * fcols <= t;
-                const int e = gld(a.ids + j);
+                int e = -1;
+                float pj = 0.f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    e = j == q ? sid[q] : e;
+                    pj = j == q ? spr[q] : pj;
+                }
                 if (e >= 0 && e < a.E) {
                     w = a.wd + (int64_t)e * a.stride_dn;
                     e0 = (uint32_t)ir * (uint32_t)a.F + 32u * (uint32_t)(t - j * fcols);
-                    f = gld(a.probs + j);
+                    f = pj;
                 }
             }
         }
@@ -361,7 +390,7 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
         col[r] = cc < ncol ? cc : 0;
         q2_col_issue32(w, e0, c[r]);
     }
-    stage_g_digits(a.G, ncol, s_rec);
+    stage_g_digits(gs, ncol, s_rec);
     __syncthreads();
     if (!row_on) return;
 

@@ -129,17 +129,16 @@ __device__ __forceinline__ float q2_col(const uint32_t (&qs)[8], uint32_t sm, ui
 // bytes and the block's d / dmin.
 struct Q2Col {
     uint32_t qs[8];
-    uint32_t sm, dd;
-    int sh;
+    uint32_t sm;    // half scale bytes (bits 0-15) | 2g << 16
+    uint32_t dd;
 };
 
 __device__ __forceinline__ void q2_col_load(const uint8_t* bp, int page, int g, Q2Col& c) {
     const u32x4_a4 q0 = gld_nt_a4(bp + 16 + 32 * page), q1 = gld_nt_a4(bp + 32 + 32 * page);
     c.qs[0] = q0.x; c.qs[1] = q0.y; c.qs[2] = q0.z; c.qs[3] = q0.w;
     c.qs[4] = q1.x; c.qs[5] = q1.y; c.qs[6] = q1.z; c.qs[7] = q1.w;
-    c.sm = gld_nt((const uint16_t*)(bp + 8 * page + 2 * g));
+    c.sm = (uint32_t)gld_nt((const uint16_t*)(bp + 8 * page + 2 * g)) | ((uint32_t)(2 * g) << 16);
     c.dd = gld_nt((const uint32_t*)(bp + 80));
-    c.sh = 2 * g;
 }
 
 __device__ __forceinline__ void q2_col_issue(const uint8_t* w, int64_t e0, Q2Col& c) {
@@ -155,7 +154,7 @@ __device__ __forceinline__ void q2_col_issue32(const uint8_t* w, uint32_t e0, Q2
 }
 
 __device__ __forceinline__ float q2_col(const Q2Col& c, const DCols<FMT_Q2_K>& xc) {
-    return q2_col(c.qs, c.sm, c.dd, c.sh, xc);
+    return q2_col(c.qs, c.sm & 0xFFFFu, c.dd, (int)(c.sm >> 16), xc);
 }
 
 // Digits of one 32-value column in the Q2_K (natural) order with the fp32
