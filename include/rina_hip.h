@@ -229,6 +229,23 @@ int rina_hip_mla_decode_attention(const float* q, const float* kva, const float*
                                   int nope, int rope, int v_dim, int dc, int start_pos,
                                   const int* d_pos, int max_seq, float* out,
                                   void* workspace, size_t workspace_bytes, void* stream);
+/* The same with pos_hint: the largest position *d_pos can hold when the
+ * launch runs (-1: max_seq - 1; ignored without d_pos).  It only selects the
+ * kernels: below 256 positions, with dc == 512, rope <= 64, nope <= 128,
+ * v <= 128 and Q2_K / Q4_0 / Q4_0F weights, one launch per call (every
+ * workgroup of a head forms q_lat, the record and the softmax and computes
+ * a quarter of W_vb), else the three-launch chunked path.  Either computes
+ * every position correctly.  No counterpart in the reference: a graph that
+ * is replayed at growing positions passes the bound of its replays. */
+/* The position count below which rina_hip_mla_decode_attention_ex takes
+ * the one-launch path (256). */
+int rina_hip_mla_fused_positions(void);
+int rina_hip_mla_decode_attention_ex(const float* q, const float* kva, const float* k_norm,
+                                     float eps, const float* rope_cos, const float* rope_sin,
+                                     const void* w_kv_b, int qt_kv_b, float* cache, int H,
+                                     int nope, int rope, int v_dim, int dc, int start_pos,
+                                     const int* d_pos, int max_seq, int pos_hint, float* out,
+                                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Router top-k of deepseek_mla_layer.cu:310-326 on the device: softmax of
  * the E logits, insertion top-k kept ascending (strict ">", the earlier

@@ -129,10 +129,10 @@ struct MLAImpl {
         }
         float* cache = b.mla_cache.layer(layer);
         for (int t = 0; t < n; t++)
-            CK(rina_hip_mla_decode_attention(q + (size_t)t * qd, kva + (size_t)t * kvw, k_norm, 1e-5f, rope_c, rope_s,
-                                             w_kv_b.data, (int)w_kv_b.qt, cache, H, nope, rope, vd, dc,
-                                             start_pos + t, b.d_pos, b.mla_cache.max_seq, att + (size_t)t * H * vd,
-                                             b.attn_ws, b.attn_ws_bytes, s));
+            CK(rina_hip_mla_decode_attention_ex(q + (size_t)t * qd, kva + (size_t)t * kvw, k_norm, 1e-5f, rope_c,
+                                                rope_s, w_kv_b.data, (int)w_kv_b.qt, cache, H, nope, rope, vd, dc,
+                                                start_pos + t, b.d_pos, b.mla_cache.max_seq, b.pos_hint,
+                                                att + (size_t)t * H * vd, b.attn_ws, b.attn_ws_bytes, s));
         rina_linear_seg o{w_o.data, nullptr, h, d};
         CK(rina_hip_linear_fused(&o, 1, (int)w_o.qt, att, n, H * vd, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
         if (!is_moe) {

@@ -57,6 +57,7 @@ struct ForwardBuffers {
     void* attn_ws = nullptr;     // split-sequence attention partials
     size_t attn_ws_bytes = 0;
     const int* d_pos = nullptr;  // device position (graph decode) or nullptr
+    int pos_hint = -1;           // with d_pos: the largest position it holds (-1: unknown)
     // optional parity tap: the fp32 K (as cached: pre- or post-RoPE) and V
     // rows each layer appends, [n_layers][2][max_seq][kv_dim]; host-position
     // forward() calls only

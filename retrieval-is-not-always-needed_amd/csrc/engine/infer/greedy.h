@@ -2,7 +2,9 @@
 // (the loop of rina-engine/src/main.cpp:666-690, moved onto the GPU): the
 // argmax kernel writes the next id into the device id buffer and advances a
 // device position, so one decode step is position-independent and is
-// captured once as a HIP graph and replayed.
+// captured once as a HIP graph and replayed.  An orchestrator whose kernels
+// differ below and above some position (graph_split()) gets one graph per
+// side, each captured with the bound of the positions it replays at.
 #pragma once
 #include <hip/hip_runtime_api.h>
 #include <string>
@@ -15,12 +17,14 @@ struct DeviceGreedyInference : Inference {
     int max_seq = 0;
     int vocab = 0;
     int gen_len = 0;           // ids valid in d_ids after the last generate / decode_more
-    hipGraphExec_t graph = nullptr;
-    hipStream_t graph_stream = nullptr;
+    hipGraphExec_t graph[2] = {nullptr, nullptr};   // positions below / from graph_split()
+    hipStream_t graph_stream[2] = {nullptr, nullptr};
+    int pos_hint = -1;         // largest position of the next device-position run (-1: unknown)
     std::string tag = "infer";
 
     ~DeviceGreedyInference() override {
-        if (graph) (void)hipGraphExecDestroy(graph);
+        for (auto& g : graph)
+            if (g) (void)hipGraphExecDestroy(g);
         if (d_ids) (void)hipFree(d_ids);
         if (d_pos) (void)hipFree(d_pos);
     }
@@ -34,10 +38,31 @@ struct DeviceGreedyInference : Inference {
     virtual int ensure_cap(int n) = 0;
     // last-row logits buffer of the device loop
     virtual float* lm_buffer() = 0;
+    // first position of the second decode graph (0: one graph for all)
+    virtual int graph_split() const { return 0; }
 
     bool alloc_ids() {
         return hipMalloc(&d_ids, sizeof(int) * (max_seq + 1)) == hipSuccess &&
                hipMalloc(&d_pos, sizeof(int)) == hipSuccess;
+    }
+
+    // (re)capture decode graph c, valid for device positions <= hint
+    int capture(int c, int hint, hipStream_t s) {
+        if (graph[c] && graph_stream[c] == s) return RINA_OK;
+        if (graph[c]) { (void)hipGraphExecDestroy(graph[c]); graph[c] = nullptr; }
+        hipGraph_t g = nullptr;
+        pos_hint = hint;
+        if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return RINA_ERR_HIP;
+        int crc = decode_step(s);
+        hipError_t ce = hipStreamEndCapture(s, &g);
+        pos_hint = -1;
+        if (crc) { if (g) (void)hipGraphDestroy(g); return crc; }
+        if (ce != hipSuccess) return RINA_ERR_HIP;
+        hipError_t ie = hipGraphInstantiate(&graph[c], g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ie != hipSuccess) { graph[c] = nullptr; return RINA_ERR_HIP; }
+        graph_stream[c] = s;
+        return RINA_OK;
     }
 
     int decode_step(hipStream_t s) {
@@ -69,28 +94,30 @@ struct DeviceGreedyInference : Inference {
     int decode_more(int steps, int* out, bool use_graph, hipStream_t s, float* decode_ms) override {
         if (gen_len < 1) { err_ = tag + ": decode_more before generate"; return RINA_ERR_ARG; }
         if (steps < 1 || gen_len + steps - 1 > max_seq) { err_ = tag + ": decode exceeds max_seq"; return RINA_ERR_RANGE; }
-        int rc;
-        if (use_graph && (!graph || graph_stream != s)) {
-            if (graph) { (void)hipGraphExecDestroy(graph); graph = nullptr; }
-            hipGraph_t g = nullptr;
-            if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return RINA_ERR_HIP;
-            int crc = decode_step(s);
-            hipError_t ce = hipStreamEndCapture(s, &g);
-            if (crc) { if (g) (void)hipGraphDestroy(g); return crc; }
-            if (ce != hipSuccess) return RINA_ERR_HIP;
-            hipError_t ie = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(g);
-            if (ie != hipSuccess) { graph = nullptr; return RINA_ERR_HIP; }
-            graph_stream = s;
+        const int split = graph_split();
+        const int pos_first = gen_len - 1;   // position of the first step's id
+        int rc = RINA_OK;
+        if (use_graph) {
+            // capture the graphs this call replays before the timed loop
+            for (int c = 0; c < 2; c++) {
+                const bool needed = c == 0 ? (split <= 0 || pos_first < split)
+                                           : (split > 0 && pos_first + steps - 1 >= split);
+                if (needed && (rc = capture(c, c == 0 && split > 0 ? split - 1 : -1, s))) return rc;
+            }
         }
         hipEvent_t e0 = nullptr, e1 = nullptr;
         (void)hipEventCreate(&e0);
         (void)hipEventCreate(&e1);
         (void)hipEventRecord(e0, s);
-        rc = RINA_OK;
         for (int i = 0; i < steps && rc == RINA_OK; i++) {
-            if (use_graph) rc = hipGraphLaunch(graph, s) == hipSuccess ? RINA_OK : RINA_ERR_HIP;
-            else rc = decode_step(s);
+            const int pos = pos_first + i;
+            if (use_graph) {
+                const int c = split > 0 && pos >= split ? 1 : 0;
+                rc = hipGraphLaunch(graph[c], s) == hipSuccess ? RINA_OK : RINA_ERR_HIP;
+            } else {
+                pos_hint = pos;
+                rc = decode_step(s);
+            }
         }
         (void)hipEventRecord(e1, s);
         if (rc == RINA_OK && hipMemcpyAsync(out, d_ids + gen_len, sizeof(int) * steps, hipMemcpyDeviceToHost, s) != hipSuccess)

@@ -83,12 +83,16 @@ struct MLAInference : DeviceGreedyInference {
 
     float* lm_buffer() override { return bufs.fwd.lm; }
 
+    // below this position the latent attention runs as one launch
+    int graph_split() const override { return std::min(max_seq, rina_hip_mla_fused_positions()); }
+
     int run(const int* ids, const int* pos_dev, int T, int start_pos, float* logits, bool last_only,
             hipStream_t s) override {
         int rc;
         ForwardBuffers& f = bufs.fwd;
         f.mla_cache.start_pos = start_pos;
         f.d_pos = pos_dev;
+        f.pos_hint = pos_dev ? pos_hint : -1;
         if ((rc = rina_hip_embedding(wte->data, (int)wte->quant_type, ids, pos_dev, f.h, T, cfg.dim, s))) return rc;
         for (auto& l : layers)
             if ((rc = l->forward(f.h, f, 1, T, s))) return rc;

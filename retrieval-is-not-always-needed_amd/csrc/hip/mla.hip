@@ -10,14 +10,16 @@
 // expanded K/V) and folds W_kb into the query and W_vb after the softmax:
 //   q_lat_h = W_kb_h^T q_nope_h,  s_j = (q_lat_h . c_j + q_rope_h . kpe_j) scale,
 //   o_h = W_vb_h (sum_j p_j c_j).
-// Three launches: prep (q_lat, rotated q_rope, latent append at pos0),
-// split (chunk partials over positions, one workgroup per chunk and head),
-// out (chunk merge and W_vb per head).
+// Short contexts: one launch (mla_fused_kernel).  Longer ones: three
+// launches, prep (q_lat, rotated q_rope, latent append at pos0), split
+// (chunk partials over positions, one workgroup per chunk and head), out
+// (chunk merge and W_vb per head).
 //
 // MoE: device top-k (no host round trip), a gathered SiLU*up matvec over the
 // selected experts, and the down projection that accumulates the experts in
 // the reference's ascending order onto the shared-expert output and adds the
 // residual.
+#include <algorithm>
 #include "rina_common.hpp"
 
 namespace {
@@ -321,6 +323,324 @@ __global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// The whole attention in one launch (short contexts)
+// ---------------------------------------------------------------------------
+// grid (H, kFusedY), 1024 threads.  Every workgroup of head h forms q_lat_h
+// (W_kb_h^T q_nope_h), the new latent record (kept in LDS; workgroup (0, 0)
+// also stores it in the cache), the softmax over the cache in blocks of 64
+// positions (4 per wave; the first block's loads go out at kernel entry with
+// the weight loads) and o_lat; then it computes its quarter of the W_vb rows.
+// The workgroups of a head repeat the attention instead of exchanging
+// partials: an exchange inside one launch needs device-scope fences, which
+// cost more than the repeated work, and the three-launch path pays a
+// dependent launch per stage.  Any position count is computed correctly;
+// past one block every further block costs a load round trip, so the host
+// uses this kernel below kFusedMaxPos positions.
+
+constexpr int kFusedDc = 512;                 // latent width this kernel is built for
+constexpr int kFusedNcu = kFusedDc / 16;      // 16-value units per latent row
+constexpr int kFusedRs = 1024 / kFusedNcu;    // row slices of the W_kb contraction
+constexpr int kFusedRec = 9;                  // record floats per lane: dc + rope <= 576
+constexpr int kFusedPw = 4;                   // positions per wave per block
+constexpr int kFusedBlock = 16 * kFusedPw;
+constexpr int kFusedY = 4;                    // workgroups per head
+constexpr int kFusedMaxPos = 256;
+
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// The raw bytes of the 16 values [e0, e0 + 16) of a quantized weight stream
+// (e0 % 16 == 0), loaded at once and decoded where they are used.
+struct RawUnit {
+    uint32_t q[4];   // Q2_K: qs bytes; Q4_0F: nibble bytes in q[0..1]; Q4_0: nibble half-words
+    uint32_t m;      // Q2_K: d | dmin << 16; Q4_0F: fp32 scale bits; Q4_0: fp16 scale bits
+    uint32_t s;      // Q2_K: 4-bit scale | 4-bit min byte, | 2g << 8 (the field shift)
+};
+
+template <int QT>
+__device__ __forceinline__ void raw_issue(RawUnit& u, const uint8_t* w, int64_t e0) {
+    if (QT == RINA_QT_GGML_Q2_K) {
+        const uint8_t* bp = w + (e0 >> 8) * 84;
+        const int inb = (int)(e0 & 255);
+        const int page = inb >> 7, g = (inb >> 5) & 3, h2 = (inb >> 4) & 1;
+        const u32x4_a4 v = gld((const u32x4_a4*)(bp + 16 + 32 * page + 16 * h2));
+        u.q[0] = v.x; u.q[1] = v.y; u.q[2] = v.z; u.q[3] = v.w;
+        u.m = gld((const uint32_t*)(bp + 80));
+        u.s = (uint32_t)gld(bp + 8 * page + 2 * g + h2) | ((uint32_t)(2 * g) << 8);
+    } else if (QT == RINA_QT_Q4_0F) {
+        const uint8_t* bp = w + (e0 >> 5) * 20;
+        const uint32_t* np = (const uint32_t*)(bp + 4 + 8 * ((e0 >> 4) & 1));
+        u.q[0] = gld(np); u.q[1] = gld(np + 1);
+        u.m = gld((const uint32_t*)bp);
+    } else {   // Q4_0: 18-byte blocks, 2-byte aligned
+        const uint8_t* bp = w + (e0 >> 5) * 18;
+        const uint16_t* np = (const uint16_t*)(bp + 2 + 8 * ((e0 >> 4) & 1));
+#pragma unroll
+        for (int d = 0; d < 4; d++) u.q[d] = gld(np + d);
+        u.m = gld((const uint16_t*)bp);
+    }
+}
+
+// the 8 nibble bytes of a Q4 unit as two dwords (value 2j: low nibble of
+// byte j, value 2j + 1: its high nibble)
+template <int QT>
+__device__ __forceinline__ void raw_nibbles(const RawUnit& u, uint32_t& d0, uint32_t& d1, float& sc) {
+    if (QT == RINA_QT_Q4_0F) {
+        d0 = u.q[0]; d1 = u.q[1];
+        sc = __uint_as_float(u.m);
+    } else {
+        d0 = u.q[0] | (u.q[1] << 16); d1 = u.q[2] | (u.q[3] << 16);
+        sc = f16_to_f32(u.m);
+    }
+}
+
+__device__ __forceinline__ float ubyte(uint32_t t, int b) { return (float)((t >> (8 * b)) & 0xFF); }
+
+// acc[j] += c * w_j - (the unit's offset term, gathered in bias): the
+// dequantized unit w_j = dl v_j - ml (Q2_K) or sc (n_j - 7) (Q4) scaled by c.
+template <int QT>
+__device__ __forceinline__ void raw_fold(const RawUnit& u, float c, float (&acc)[16], float& bias) {
+    if (QT == RINA_QT_GGML_Q2_K) {
+        const float a = c * (f16_to_f32(u.m & 0xFFFF) * (float)(u.s & 0xF));
+        bias = fmaf(c, f16_to_f32(u.m >> 16) * (float)((u.s >> 4) & 0xF), bias);
+        const int sh = (int)(u.s >> 8);
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t t = and_opaque(u.q[d] >> sh, 0x03030303u);
+#pragma unroll
+            for (int b = 0; b < 4; b++) acc[4 * d + b] = fmaf(a, ubyte(t, b), acc[4 * d + b]);
+        }
+    } else {
+        uint32_t dw[2];
+        float sc;
+        raw_nibbles<QT>(u, dw[0], dw[1], sc);
+        const float a = c * sc;
+        bias = fmaf(7.0f, a, bias);
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const uint32_t lo = and_opaque(dw[d], 0x0F0F0F0Fu), hi = and_opaque(dw[d] >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                acc[8 * d + 2 * b] = fmaf(a, ubyte(lo, b), acc[8 * d + 2 * b]);
+                acc[8 * d + 2 * b + 1] = fmaf(a, ubyte(hi, b), acc[8 * d + 2 * b + 1]);
+            }
+        }
+    }
+}
+
+// sum_j w_j x_j over the unit, x: 16 floats in LDS (16-byte aligned)
+template <int QT>
+__device__ __forceinline__ float raw_dot(const RawUnit& u, const float* x) {
+    float xv[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const f32x4 t = ((const f32x4*)x)[q];
+        xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+    }
+    float d = 0.f, xs = 0.f;
+    if (QT == RINA_QT_GGML_Q2_K) {
+        const int sh = (int)(u.s >> 8);
+#pragma unroll
+        for (int dw = 0; dw < 4; dw++) {
+            const uint32_t t = and_opaque(u.q[dw] >> sh, 0x03030303u);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                d = fmaf(ubyte(t, b), xv[4 * dw + b], d);
+                xs += xv[4 * dw + b];
+            }
+        }
+        const float dl = f16_to_f32(u.m & 0xFFFF) * (float)(u.s & 0xF);
+        const float ml = f16_to_f32(u.m >> 16) * (float)((u.s >> 4) & 0xF);
+        return fmaf(dl, d, -(ml * xs));
+    } else {
+        uint32_t dw[2];
+        float sc;
+        raw_nibbles<QT>(u, dw[0], dw[1], sc);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t lo = and_opaque(dw[k], 0x0F0F0F0Fu), hi = and_opaque(dw[k] >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                d = fmaf(ubyte(lo, b), xv[8 * k + 2 * b], d);
+                d = fmaf(ubyte(hi, b), xv[8 * k + 2 * b + 1], d);
+                xs += xv[8 * k + 2 * b] + xv[8 * k + 2 * b + 1];
+            }
+        }
+        return sc * fmaf(-7.0f, xs, d);
+    }
+}
+
+// the cache records of this wave's positions blk + wave + 16 i (positions
+// >= pos0 read nothing: pos0's record comes from LDS, later ones are masked)
+__device__ __forceinline__ void fused_load_block(float (&kv)[kFusedPw][kFusedRec], const float* cache, int blk,
+                                                 int wave, int pos0, int R, int lane) {
+#pragma unroll
+    for (int i = 0; i < kFusedPw; i++) {
+        const int p = blk + wave + 16 * i;
+        const float* rec = cache + (int64_t)p * R;
+#pragma unroll
+        for (int j = 0; j < kFusedRec; j++)
+            kv[i][j] = (p < pos0 && lane + 64 * j < R) ? gld(rec + lane + 64 * j) : 0.f;
+    }
+}
+
+template <int QT>
+__global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
+    __shared__ __align__(16) float s_part[kFusedRs * kFusedDc];   // W_kb partials, then wave partials
+    __shared__ __align__(16) float s_q[64 * kFusedRec];           // q_lat | rotated q_rope
+    __shared__ __align__(16) float s_rec[64 * kFusedRec];         // the new record
+    __shared__ __align__(16) float s_lat[kFusedDc];
+    __shared__ float s_qn[128];
+    __shared__ float s_m[16], s_l[16], s_aw[16], s_red[5];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos0 = read_pos(a.start_pos, a.d_pos);
+    if (pos0 < 0 || pos0 >= a.max_seq) return;
+    const int h = blockIdx.x, y = blockIdx.y;
+    const int R = kFusedDc + a.rope, hr = a.rope / 2, L = pos0 + 1;
+    const int cu = tid & (kFusedNcu - 1), rs = tid / kFusedNcu;
+    // weight loads: W_kb_h rows rs + 32 r (column unit cu), one W_vb_h row
+    RawUnit wk[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int i = rs + kFusedRs * r;
+        if (i < a.nope) raw_issue<QT>(wk[r], a.wkvb, ((int64_t)h * a.nope + i) * kFusedDc + 16 * cu);
+    }
+    const int vq = (a.v + kFusedY - 1) / kFusedY;
+    const int vrow = y * vq + rs;
+    const bool vok = rs < vq && vrow < a.v;
+    RawUnit wv;
+    if (vok) raw_issue<QT>(wv, a.wkvb, ((int64_t)a.H * a.nope + (int64_t)h * a.v + vrow) * kFusedDc + 16 * cu);
+    float kv[kFusedPw][kFusedRec];
+    fused_load_block(kv, a.cache, 0, wave, pos0, R, lane);
+    // q_nope, rotated q_rope, the record's RoPE half and norm partials (the
+    // sum order of mla_prep_kernel: threads 0..255, k = tid, tid + 256)
+    if (tid < a.nope) s_qn[tid] = gld(a.q + (int64_t)h * a.nope + tid);
+    if (tid < hr) {
+        const float* qr = a.q + (int64_t)a.H * a.nope + (int64_t)h * a.rope;
+        float x0 = gld(qr + tid), x1 = gld(qr + tid + hr);
+        float k0 = gld(a.kva + kFusedDc + tid), k1 = gld(a.kva + kFusedDc + tid + hr);
+        if (a.rc) {
+            const float c = gld(a.rc + (int64_t)pos0 * hr + tid), s = gld(a.rs + (int64_t)pos0 * hr + tid);
+            rope_pair(x0, x1, c, s, x0, x1);
+            rope_pair(k0, k1, c, s, k0, k1);
+        }
+        s_q[kFusedDc + tid] = x0;
+        s_q[kFusedDc + tid + hr] = x1;
+        s_rec[kFusedDc + tid] = k0;
+        s_rec[kFusedDc + tid + hr] = k1;
+        if (h == 0 && y == 0) {
+            float* rec = a.cache + (int64_t)pos0 * R;
+            gst(rec + kFusedDc + tid, k0);
+            gst(rec + kFusedDc + tid + hr, k1);
+        }
+    }
+    float cx = 0.f, cn = 0.f;
+    if (tid < kFusedDc) { cx = gld(a.kva + tid); cn = gld(a.k_norm + tid); }
+    if (tid < 256) {
+        const float x1 = gld(a.kva + tid + 256);
+        const float ss = wave_sum(fmaf(x1, x1, fmaf(cx, cx, 0.f)));
+        if (lane == 0) s_red[wave] = ss;
+    }
+    __syncthreads();
+    // q_lat partials of this thread's rows, then the normalized record
+    {
+        float acc[16], bias = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[j] = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int i = rs + kFusedRs * r;
+            if (i < a.nope) raw_fold<QT>(wk[r], s_qn[i], acc, bias);
+        }
+        f32x4* dst = (f32x4*)(s_part + rs * kFusedDc + 16 * cu);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            dst[q] = f32x4{acc[4 * q] - bias, acc[4 * q + 1] - bias, acc[4 * q + 2] - bias, acc[4 * q + 3] - bias};
+    }
+    if (tid < kFusedDc) {
+        const float inv = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)kFusedDc + a.eps);
+        const float v = cx * inv * cn;
+        s_rec[tid] = v;
+        if (h == 0 && y == 0) gst(a.cache + (int64_t)pos0 * R + tid, v);
+    }
+    __syncthreads();
+    if (tid < kFusedDc) {
+        float t = 0.f;
+#pragma unroll 8
+        for (int r = 0; r < kFusedRs; r++) t += s_part[r * kFusedDc + tid];
+        s_q[tid] = t;
+    }
+    __syncthreads();
+    // softmax over the cache, per wave: scores of a block first, then one
+    // rescale of the running sums per block
+    float qv[kFusedRec];
+#pragma unroll
+    for (int j = 0; j < kFusedRec; j++) qv[j] = lane + 64 * j < R ? s_q[lane + 64 * j] : 0.f;
+    float m = -INFINITY, l = 0.f, o[kFusedDc / 64];
+#pragma unroll
+    for (int j = 0; j < kFusedDc / 64; j++) o[j] = 0.f;
+    for (int blk = 0; blk < L; blk += kFusedBlock) {
+        if (blk) fused_load_block(kv, a.cache, blk, wave, pos0, R, lane);
+        float s[kFusedPw];
+        float mb = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kFusedPw; i++) {
+            const int p = blk + wave + 16 * i;
+            s[i] = -INFINITY;
+            if (p < L) {
+                if (p == pos0) {
+#pragma unroll
+                    for (int j = 0; j < kFusedRec; j++) kv[i][j] = lane + 64 * j < R ? s_rec[lane + 64 * j] : 0.f;
+                }
+                float dot = 0.f;
+#pragma unroll
+                for (int j = 0; j < kFusedRec; j++) dot = fmaf(qv[j], kv[i][j], dot);
+                s[i] = wave_sum(dot) * a.scale;
+                mb = fmaxf(mb, s[i]);
+            }
+        }
+        if (mb == -INFINITY) continue;
+        const float mn = fmaxf(m, mb), al = expf(m - mn);
+        l *= al;
+#pragma unroll
+        for (int j = 0; j < kFusedDc / 64; j++) o[j] *= al;
+        m = mn;
+#pragma unroll
+        for (int i = 0; i < kFusedPw; i++) {
+            if (s[i] == -INFINITY) continue;
+            const float pe = expf(s[i] - mn);
+            l += pe;
+#pragma unroll
+            for (int j = 0; j < kFusedDc / 64; j++) o[j] = fmaf(pe, kv[i][j], o[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kFusedDc / 64; j++) s_part[wave * kFusedDc + lane + 64 * j] = o[j];
+    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+    __syncthreads();
+    if (wave == 0) {
+        const float mw = lane < 16 ? s_m[lane] : -INFINITY;
+        const float M = wave_max(mw);
+        const float aw = mw == -INFINITY ? 0.f : expf(mw - M);
+        const float den = wave_sum(lane < 16 ? aw * s_l[lane] : 0.f);
+        if (lane < 16) s_aw[lane] = aw;
+        if (lane == 0) s_red[4] = den;
+    }
+    __syncthreads();
+    if (tid < kFusedDc) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; w++) t = fmaf(s_aw[w], s_part[w * kFusedDc + tid], t);
+        s_lat[tid] = t * (1.0f / s_red[4]);
+    }
+    __syncthreads();
+    // W_vb row vrow: the 32 units of the row are lanes 0..31 or 32..63
+    float pv = vok ? raw_dot<QT>(wv, s_lat + 16 * cu) : 0.f;
+    pv = sum16(pv);
+    pv += dpp_rows<0x142, 0xA>(pv);   // row_bcast:15: lane 31 = lanes 0..31, lane 63 = lanes 32..63
+    if (vok && (lane & 31) == 31) gst(a.out + (int64_t)h * a.v + vrow, pv);
+}
+
+// ---------------------------------------------------------------------------
 // MoE
 // ---------------------------------------------------------------------------
 
@@ -456,6 +776,12 @@ bool unit_qt(int qt) {
 
 int mla_nchunk(int max_pos) { return (max_pos + kMlaChunk - 1) / kMlaChunk; }
 
+// shapes mla_fused_kernel is built for (the DeepSeek-V2 latent width)
+bool mla_fused_ok(int qt, int nope, int rope, int v, int dc) {
+    return (qt == RINA_QT_GGML_Q2_K || qt == RINA_QT_Q4_0F || qt == RINA_QT_Q4_0) && dc == kFusedDc &&
+           rope <= 64 && nope <= 128 && v <= 128;
+}
+
 }  // namespace
 
 extern "C" size_t rina_hip_mla_attention_workspace(int H, int dc, int rope, int max_pos) {
@@ -468,11 +794,11 @@ extern "C" size_t rina_hip_mla_cache_bytes(int dc, int rope, int max_seq) {
     return (size_t)max_seq * (dc + rope) * sizeof(float);
 }
 
-extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, const float* k_norm, float eps,
-                                             const float* rope_cos, const float* rope_sin, const void* w_kv_b,
-                                             int qt_kv_b, float* cache, int H, int nope, int rope, int v_dim, int dc,
-                                             int start_pos, const int* d_pos, int max_seq, float* out,
-                                             void* workspace, size_t ws_bytes, void* stream) {
+extern "C" int rina_hip_mla_decode_attention_ex(const float* q, const float* kva, const float* k_norm, float eps,
+                                                const float* rope_cos, const float* rope_sin, const void* w_kv_b,
+                                                int qt_kv_b, float* cache, int H, int nope, int rope, int v_dim,
+                                                int dc, int start_pos, const int* d_pos, int max_seq, int pos_hint,
+                                                float* out, void* workspace, size_t ws_bytes, void* stream) {
     if (!q || !kva || !k_norm || !w_kv_b || !cache || !out || H < 1 || nope < 1 || v_dim < 1 || max_seq < 1)
         return RINA_ERR_ARG;
     if (!unit_qt(qt_kv_b)) return RINA_ERR_QTYPE;
@@ -497,6 +823,17 @@ extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, c
     a.ws_l = a.ws_m + (size_t)nch * H;
     a.ws_o = a.ws_l + (size_t)nch * H;
     hipStream_t st = as_stream(stream);
+    // positions the launch will see: known without d_pos, else the caller's
+    // bound (any position is computed correctly by either path)
+    const int lmax = d_pos ? (pos_hint >= 0 ? std::min(pos_hint + 1, max_seq) : max_seq) : start_pos + 1;
+    if (lmax <= kFusedMaxPos && mla_fused_ok(qt_kv_b, nope, rope, v_dim, dc)) {
+        const dim3 grid(H, kFusedY);
+        if (qt_kv_b == RINA_QT_GGML_Q2_K) hipLaunchKernelGGL(mla_fused_kernel<RINA_QT_GGML_Q2_K>, grid, dim3(1024), 0, st, a);
+        else if (qt_kv_b == RINA_QT_Q4_0F) hipLaunchKernelGGL(mla_fused_kernel<RINA_QT_Q4_0F>, grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL(mla_fused_kernel<RINA_QT_Q4_0>, grid, dim3(1024), 0, st, a);
+        RINA_LAUNCH_CHECK();
+        return RINA_OK;
+    }
     hipLaunchKernelGGL(mla_prep_kernel, dim3(H + 1, 4), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(mla_split_kernel, dim3(nch, H), dim3(256), 0, st, a);
@@ -504,6 +841,18 @@ extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, c
     hipLaunchKernelGGL(mla_out_kernel, dim3(H, (v_dim + 15) / 16), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
+}
+
+extern "C" int rina_hip_mla_fused_positions(void) { return kFusedMaxPos; }
+
+extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, const float* k_norm, float eps,
+                                             const float* rope_cos, const float* rope_sin, const void* w_kv_b,
+                                             int qt_kv_b, float* cache, int H, int nope, int rope, int v_dim, int dc,
+                                             int start_pos, const int* d_pos, int max_seq, float* out,
+                                             void* workspace, size_t ws_bytes, void* stream) {
+    return rina_hip_mla_decode_attention_ex(q, kva, k_norm, eps, rope_cos, rope_sin, w_kv_b, qt_kv_b, cache, H, nope,
+                                            rope, v_dim, dc, start_pos, d_pos, max_seq, -1, out, workspace, ws_bytes,
+                                            stream);
 }
 
 extern "C" int rina_hip_moe_topk(const float* logits, int n_experts, int k, int* ids, float* probs, void* stream) {

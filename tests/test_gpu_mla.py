@@ -14,7 +14,7 @@ from _util import assert_close, dev, empty, host, ok, rng, stream
 
 pytestmark = pytest.mark.gpu
 
-Q2K, Q4F, FP32 = 10, 7, 6
+Q2K, Q4F, FP32, Q40 = 10, 7, 6, 5
 
 
 def rope_tables(rope, n, theta=10000.0):
@@ -35,14 +35,20 @@ def weight(orc, qt, rows, cols, r):
 
 
 @pytest.mark.parametrize("shape", ["tiny", "dsv2lite"])
-@pytest.mark.parametrize("qt", [Q2K, Q4F])
-@pytest.mark.parametrize("P,use_dpos", [(0, False), (5, False), (40, True), (100, False)])
-def test_mla_decode_attention(rina, orc, shape, qt, P, use_dpos):
+@pytest.mark.parametrize("qt", [Q2K, Q4F, Q40])
+# (position, device position, pos_hint, minimum max_seq).  At the
+# DeepSeek-V2-Lite shape: one-launch path below 256 positions (one and
+# several 64-position blocks, a device position past its hint), three-launch
+# path at 300 positions and for a device position with no usable bound.
+@pytest.mark.parametrize("P,use_dpos,hint,min_seq", [(0, False, -1, 0), (5, False, -1, 0), (40, True, -1, 0),
+                                                     (40, True, -1, 400), (40, True, 63, 400), (100, False, -1, 0),
+                                                     (200, True, 10, 0), (300, False, -1, 0)])
+def test_mla_decode_attention(rina, orc, shape, qt, P, use_dpos, hint, min_seq):
     hip = rina.load_hip()
     L = orc.load()
     H, nope, rope, vd, dc = (4, 32, 16, 32, 64) if shape == "tiny" else (16, 128, 64, 128, 512)
     R = dc + rope
-    max_seq = P + 7
+    max_seq = max(P + 7, min_seq)
     r = rng(P * 3 + H + qt)
     wkvb, W = weight(orc, qt, H * (nope + vd), dc, r)
     q = r.standard_normal(H * (nope + rope)).astype(np.float32)
@@ -74,11 +80,11 @@ def test_mla_decode_attention(rina, orc, shape, qt, P, use_dpos):
     cd = dev(cache)
     od = empty(H * vd)
     pos = dev(np.array([P], np.int32)) if use_dpos else None
-    ok(hip.rina_hip_mla_decode_attention(dev(q).data_ptr(), dev(kva).data_ptr(), dev(knorm).data_ptr(),
-                                         np.float32(1e-5), dev(cos).data_ptr(), dev(sin).data_ptr(),
-                                         dev(wkvb).data_ptr(), qt, cd.data_ptr(), H, nope, rope, vd, dc,
-                                         0 if use_dpos else P, pos.data_ptr() if use_dpos else None, max_seq,
-                                         od.data_ptr(), ws.data_ptr(), ws_bytes, stream()), "mla attention")
+    ok(hip.rina_hip_mla_decode_attention_ex(dev(q).data_ptr(), dev(kva).data_ptr(), dev(knorm).data_ptr(),
+                                            np.float32(1e-5), dev(cos).data_ptr(), dev(sin).data_ptr(),
+                                            dev(wkvb).data_ptr(), qt, cd.data_ptr(), H, nope, rope, vd, dc,
+                                            0 if use_dpos else P, pos.data_ptr() if use_dpos else None, max_seq,
+                                            hint, od.data_ptr(), ws.data_ptr(), ws_bytes, stream()), "mla attention")
     assert_close(host(od), ref, what="mla %s qt %d P %d" % (shape, qt, P))
     gc = host(cd).reshape(max_seq, R)
     assert np.array_equal(gc[P, dc:].view(np.uint32), kpe.view(np.uint32))     # RoPE: same fma form
