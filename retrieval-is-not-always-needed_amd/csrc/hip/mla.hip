@@ -340,20 +340,24 @@ __global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
 constexpr int kFusedDc = 512;                 // latent width this kernel is built for
 constexpr int kFusedNcu = kFusedDc / 16;      // 16-value units per latent row
 constexpr int kFusedRs = 1024 / kFusedNcu;    // row slices of the W_kb contraction
-constexpr int kFusedRec = 9;                  // record floats per lane: dc + rope <= 576
+constexpr int kFusedRope = 64;
+constexpr int kFusedR = kFusedDc + kFusedRope;   // record floats: 576, 9 per lane
+constexpr int kFusedRec = kFusedR / 64;
 constexpr int kFusedPw = 4;                   // positions per wave per block
 constexpr int kFusedBlock = 16 * kFusedPw;
 constexpr int kFusedY = 4;                    // workgroups per head
 constexpr int kFusedMaxPos = 256;
 
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 // The raw bytes of the 16 values [e0, e0 + 16) of a quantized weight stream
 // (e0 % 16 == 0), loaded at once and decoded where they are used.
 struct RawUnit {
     uint32_t q[4];   // Q2_K: qs bytes; Q4_0F: nibble bytes in q[0..1]; Q4_0: nibble half-words
     uint32_t m;      // Q2_K: d | dmin << 16; Q4_0F: fp32 scale bits; Q4_0: fp16 scale bits
-    uint32_t s;      // Q2_K: 4-bit scale | 4-bit min byte, | 2g << 8 (the field shift)
+    uint32_t s;      // Q2_K: the 4-bit scale | 4-bit min byte
+    int sh;          // Q2_K: the 2-bit field's shift 2g (from the address: no wait on the loads)
 };
 
 template <int QT>
@@ -365,7 +369,8 @@ __device__ __forceinline__ void raw_issue(RawUnit& u, const uint8_t* w, int64_t 
         const u32x4_a4 v = gld((const u32x4_a4*)(bp + 16 + 32 * page + 16 * h2));
         u.q[0] = v.x; u.q[1] = v.y; u.q[2] = v.z; u.q[3] = v.w;
         u.m = gld((const uint32_t*)(bp + 80));
-        u.s = (uint32_t)gld(bp + 8 * page + 2 * g + h2) | ((uint32_t)(2 * g) << 8);
+        u.s = gld(bp + 8 * page + 2 * g + h2);
+        u.sh = 2 * g;
     } else if (QT == RINA_QT_Q4_0F) {
         const uint8_t* bp = w + (e0 >> 5) * 20;
         const uint32_t* np = (const uint32_t*)(bp + 4 + 8 * ((e0 >> 4) & 1));
@@ -401,8 +406,8 @@ template <int QT>
 __device__ __forceinline__ void raw_fold(const RawUnit& u, float c, float (&acc)[16], float& bias) {
     if (QT == RINA_QT_GGML_Q2_K) {
         const float a = c * (f16_to_f32(u.m & 0xFFFF) * (float)(u.s & 0xF));
-        bias = fmaf(c, f16_to_f32(u.m >> 16) * (float)((u.s >> 4) & 0xF), bias);
-        const int sh = (int)(u.s >> 8);
+        bias = fmaf(c, f16_to_f32(u.m >> 16) * (float)(u.s >> 4), bias);
+        const int sh = u.sh;
 #pragma unroll
         for (int d = 0; d < 4; d++) {
             const uint32_t t = and_opaque(u.q[d] >> sh, 0x03030303u);
@@ -438,7 +443,7 @@ __device__ __forceinline__ float raw_dot(const RawUnit& u, const float* x) {
     }
     float d = 0.f, xs = 0.f;
     if (QT == RINA_QT_GGML_Q2_K) {
-        const int sh = (int)(u.s >> 8);
+        const int sh = u.sh;
 #pragma unroll
         for (int dw = 0; dw < 4; dw++) {
             const uint32_t t = and_opaque(u.q[dw] >> sh, 0x03030303u);
@@ -449,7 +454,7 @@ __device__ __forceinline__ float raw_dot(const RawUnit& u, const float* x) {
             }
         }
         const float dl = f16_to_f32(u.m & 0xFFFF) * (float)(u.s & 0xF);
-        const float ml = f16_to_f32(u.m >> 16) * (float)((u.s >> 4) & 0xF);
+        const float ml = f16_to_f32(u.m >> 16) * (float)(u.s >> 4);
         return fmaf(dl, d, -(ml * xs));
     } else {
         uint32_t dw[2];
@@ -469,59 +474,74 @@ __device__ __forceinline__ float raw_dot(const RawUnit& u, const float* x) {
     }
 }
 
-// the cache records of this wave's positions blk + wave + 16 i (positions
-// >= pos0 read nothing: pos0's record comes from LDS, later ones are masked)
+// The cache records of this wave's positions blk + wave + 16 i; lane l
+// holds record floats l + 64 j (dword loads: each record line is touched
+// once per wave).  Every load is issued (positions >= pos0 read record 0 and
+// are never used): branches around loads make the compiler wait for every
+// earlier load at the join.
 __device__ __forceinline__ void fused_load_block(float (&kv)[kFusedPw][kFusedRec], const float* cache, int blk,
-                                                 int wave, int pos0, int R, int lane) {
+                                                 int wave, int pos0, int lane) {
 #pragma unroll
     for (int i = 0; i < kFusedPw; i++) {
         const int p = blk + wave + 16 * i;
-        const float* rec = cache + (int64_t)p * R;
+        const float* rec = cache + (int64_t)(p < pos0 ? p : 0) * kFusedR + lane;
 #pragma unroll
-        for (int j = 0; j < kFusedRec; j++)
-            kv[i][j] = (p < pos0 && lane + 64 * j < R) ? gld(rec + lane + 64 * j) : 0.f;
+        for (int j = 0; j < kFusedRec; j++) kv[i][j] = gld(rec + 64 * j);
     }
 }
 
 template <int QT>
 __global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
     __shared__ __align__(16) float s_part[kFusedRs * kFusedDc];   // W_kb partials, then wave partials
-    __shared__ __align__(16) float s_q[64 * kFusedRec];           // q_lat | rotated q_rope
-    __shared__ __align__(16) float s_rec[64 * kFusedRec];         // the new record
+    __shared__ __align__(16) float s_q[kFusedR];                  // q_lat | rotated q_rope
+    __shared__ __align__(16) float s_rec[kFusedR];                // the new record
     __shared__ __align__(16) float s_lat[kFusedDc];
     __shared__ float s_qn[128];
-    __shared__ float s_m[16], s_l[16], s_aw[16], s_red[5];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ float s_m[16], s_l[16], s_red[4];
+    // the wave index as a uniform value: position tests become scalar branches
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;
     const int h = blockIdx.x, y = blockIdx.y;
-    const int R = kFusedDc + a.rope, hr = a.rope / 2, L = pos0 + 1;
+    const int R = kFusedR, hr = kFusedRope / 2, L = pos0 + 1;
     const int cu = tid & (kFusedNcu - 1), rs = tid / kFusedNcu;
-    // weight loads: W_kb_h rows rs + 32 r (column unit cu), one W_vb_h row
+    // the small loads first (q_nope, q_rope, k_pe, RoPE tables, c_kv,
+    // k_norm): waiting for them then leaves the weight and cache loads,
+    // issued after, in flight
+    const int ti = tid < hr ? tid : 0;
+    const float* qr = a.q + (int64_t)a.H * a.nope + (int64_t)h * kFusedRope;
+    const float qn = gld(a.q + (int64_t)h * a.nope + (tid < a.nope ? tid : 0));
+    float x0 = gld(qr + ti), x1 = gld(qr + ti + hr);
+    float k0 = gld(a.kva + kFusedDc + ti), k1 = gld(a.kva + kFusedDc + ti + hr);
+    float rc = 1.f, rsn = 0.f;
+    if (a.rc) { rc = gld(a.rc + (int64_t)pos0 * hr + ti); rsn = gld(a.rs + (int64_t)pos0 * hr + ti); }
+    const float cx = gld(a.kva + (tid & (kFusedDc - 1))), cn = gld(a.k_norm + (tid & (kFusedDc - 1)));
+    const float cx2 = gld(a.kva + (tid & 255) + 256);
+    __builtin_amdgcn_sched_barrier(0);   // keep the issue order: small loads, weights, cache
+    // weight loads: W_kb_h rows rs + 32 r (column unit cu; rows past nope
+    // re-read row 0 with coefficient 0), one W_vb_h row
     RawUnit wk[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int i = rs + kFusedRs * r;
-        if (i < a.nope) raw_issue<QT>(wk[r], a.wkvb, ((int64_t)h * a.nope + i) * kFusedDc + 16 * cu);
+        raw_issue<QT>(wk[r], a.wkvb, ((int64_t)h * a.nope + (i < a.nope ? i : 0)) * kFusedDc + 16 * cu);
     }
     const int vq = (a.v + kFusedY - 1) / kFusedY;
     const int vrow = y * vq + rs;
     const bool vok = rs < vq && vrow < a.v;
     RawUnit wv;
-    if (vok) raw_issue<QT>(wv, a.wkvb, ((int64_t)a.H * a.nope + (int64_t)h * a.v + vrow) * kFusedDc + 16 * cu);
+    raw_issue<QT>(wv, a.wkvb, ((int64_t)a.H * a.nope + (int64_t)h * a.v + (vok ? vrow : 0)) * kFusedDc + 16 * cu);
+    __builtin_amdgcn_sched_barrier(0);
     float kv[kFusedPw][kFusedRec];
-    fused_load_block(kv, a.cache, 0, wave, pos0, R, lane);
+    fused_load_block(kv, a.cache, 0, wave, pos0, lane);
+    __builtin_amdgcn_sched_barrier(0);
     // q_nope, rotated q_rope, the record's RoPE half and norm partials (the
     // sum order of mla_prep_kernel: threads 0..255, k = tid, tid + 256)
-    if (tid < a.nope) s_qn[tid] = gld(a.q + (int64_t)h * a.nope + tid);
+    if (tid < a.nope) s_qn[tid] = qn;
     if (tid < hr) {
-        const float* qr = a.q + (int64_t)a.H * a.nope + (int64_t)h * a.rope;
-        float x0 = gld(qr + tid), x1 = gld(qr + tid + hr);
-        float k0 = gld(a.kva + kFusedDc + tid), k1 = gld(a.kva + kFusedDc + tid + hr);
         if (a.rc) {
-            const float c = gld(a.rc + (int64_t)pos0 * hr + tid), s = gld(a.rs + (int64_t)pos0 * hr + tid);
-            rope_pair(x0, x1, c, s, x0, x1);
-            rope_pair(k0, k1, c, s, k0, k1);
+            rope_pair(x0, x1, rc, rsn, x0, x1);
+            rope_pair(k0, k1, rc, rsn, k0, k1);
         }
         s_q[kFusedDc + tid] = x0;
         s_q[kFusedDc + tid + hr] = x1;
@@ -533,11 +553,8 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
             gst(rec + kFusedDc + tid + hr, k1);
         }
     }
-    float cx = 0.f, cn = 0.f;
-    if (tid < kFusedDc) { cx = gld(a.kva + tid); cn = gld(a.k_norm + tid); }
     if (tid < 256) {
-        const float x1 = gld(a.kva + tid + 256);
-        const float ss = wave_sum(fmaf(x1, x1, fmaf(cx, cx, 0.f)));
+        const float ss = wave_sum(fmaf(cx2, cx2, fmaf(cx, cx, 0.f)));
         if (lane == 0) s_red[wave] = ss;
     }
     __syncthreads();
@@ -549,7 +566,7 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int i = rs + kFusedRs * r;
-            if (i < a.nope) raw_fold<QT>(wk[r], s_qn[i], acc, bias);
+            raw_fold<QT>(wk[r], i < a.nope ? s_qn[i] : 0.f, acc, bias);
         }
         f32x4* dst = (f32x4*)(s_part + rs * kFusedDc + 16 * cu);
 #pragma unroll
@@ -571,35 +588,38 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
     }
     __syncthreads();
     // softmax over the cache, per wave: scores of a block first, then one
-    // rescale of the running sums per block
+    // rescale of the running sums per block.  Scores are kept in base-2
+    // units (log2 e folded into the scale) for the hardware exp2.
+    const int wu = wave;
     float qv[kFusedRec];
 #pragma unroll
-    for (int j = 0; j < kFusedRec; j++) qv[j] = lane + 64 * j < R ? s_q[lane + 64 * j] : 0.f;
+    for (int j = 0; j < kFusedRec; j++) qv[j] = s_q[lane + 64 * j];
+    const float sc2 = a.scale * 1.44269504088896341f;
     float m = -INFINITY, l = 0.f, o[kFusedDc / 64];
 #pragma unroll
     for (int j = 0; j < kFusedDc / 64; j++) o[j] = 0.f;
     for (int blk = 0; blk < L; blk += kFusedBlock) {
-        if (blk) fused_load_block(kv, a.cache, blk, wave, pos0, R, lane);
+        if (blk) fused_load_block(kv, a.cache, blk, wu, pos0, lane);
         float s[kFusedPw];
         float mb = -INFINITY;
 #pragma unroll
         for (int i = 0; i < kFusedPw; i++) {
-            const int p = blk + wave + 16 * i;
+            const int p = blk + wu + 16 * i;
             s[i] = -INFINITY;
             if (p < L) {
                 if (p == pos0) {
 #pragma unroll
-                    for (int j = 0; j < kFusedRec; j++) kv[i][j] = lane + 64 * j < R ? s_rec[lane + 64 * j] : 0.f;
+                    for (int j = 0; j < kFusedRec; j++) kv[i][j] = s_rec[lane + 64 * j];
                 }
                 float dot = 0.f;
 #pragma unroll
                 for (int j = 0; j < kFusedRec; j++) dot = fmaf(qv[j], kv[i][j], dot);
-                s[i] = wave_sum(dot) * a.scale;
+                s[i] = wave_sum(dot) * sc2;
                 mb = fmaxf(mb, s[i]);
             }
         }
         if (mb == -INFINITY) continue;
-        const float mn = fmaxf(m, mb), al = expf(m - mn);
+        const float mn = fmaxf(m, mb), al = __builtin_amdgcn_exp2f(m - mn);
         l *= al;
 #pragma unroll
         for (int j = 0; j < kFusedDc / 64; j++) o[j] *= al;
@@ -607,34 +627,34 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
 #pragma unroll
         for (int i = 0; i < kFusedPw; i++) {
             if (s[i] == -INFINITY) continue;
-            const float pe = expf(s[i] - mn);
+            const float pe = __builtin_amdgcn_exp2f(s[i] - mn);
             l += pe;
 #pragma unroll
             for (int j = 0; j < kFusedDc / 64; j++) o[j] = fmaf(pe, kv[i][j], o[j]);
         }
     }
 #pragma unroll
-    for (int j = 0; j < kFusedDc / 64; j++) s_part[wave * kFusedDc + lane + 64 * j] = o[j];
-    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+    for (int j = 0; j < kFusedDc / 64; j++) s_part[wu * kFusedDc + lane + 64 * j] = o[j];
+    if (lane == 0) { s_m[wu] = m; s_l[wu] = l; }
     __syncthreads();
-    if (wave == 0) {
-        const float mw = lane < 16 ? s_m[lane] : -INFINITY;
-        const float M = wave_max(mw);
-        const float aw = mw == -INFINITY ? 0.f : expf(mw - M);
-        const float den = wave_sum(lane < 16 ? aw * s_l[lane] : 0.f);
-        if (lane < 16) s_aw[lane] = aw;
-        if (lane == 0) s_red[4] = den;
-    }
-    __syncthreads();
+    // merge of the 16 waves (every merging thread forms the wave weights)
     if (tid < kFusedDc) {
-        float t = 0.f;
+        float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 16; w++) t = fmaf(s_aw[w], s_part[w * kFusedDc + tid], t);
-        s_lat[tid] = t * (1.0f / s_red[4]);
+        for (int w = 0; w < 16; w++) M = fmaxf(M, s_m[w]);
+        float t = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; w++) {
+            const float mw = s_m[w];
+            const float aw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+            den = fmaf(aw, s_l[w], den);
+            t = fmaf(aw, s_part[w * kFusedDc + tid], t);
+        }
+        s_lat[tid] = t * (1.0f / den);
     }
     __syncthreads();
     // W_vb row vrow: the 32 units of the row are lanes 0..31 or 32..63
-    float pv = vok ? raw_dot<QT>(wv, s_lat + 16 * cu) : 0.f;
+    float pv = raw_dot<QT>(wv, s_lat + 16 * cu);
     pv = sum16(pv);
     pv += dpp_rows<0x142, 0xA>(pv);   // row_bcast:15: lane 31 = lanes 0..31, lane 63 = lanes 32..63
     if (vok && (lane & 31) == 31) gst(a.out + (int64_t)h * a.v + vrow, pv);
@@ -779,7 +799,7 @@ int mla_nchunk(int max_pos) { return (max_pos + kMlaChunk - 1) / kMlaChunk; }
 // shapes mla_fused_kernel is built for (the DeepSeek-V2 latent width)
 bool mla_fused_ok(int qt, int nope, int rope, int v, int dc) {
     return (qt == RINA_QT_GGML_Q2_K || qt == RINA_QT_Q4_0F || qt == RINA_QT_Q4_0) && dc == kFusedDc &&
-           rope <= 64 && nope <= 128 && v <= 128;
+           rope == kFusedRope && nope <= 128 && v <= 128;
 }
 
 }  // namespace
