@@ -14,9 +14,10 @@
 // query heads of that KV head are reduced with DPP inside the 8-lane group.
 // Every 8-lane slot keeps its own online softmax over the positions it takes
 // (no barrier in the loop; the next positions' K/V loads are in flight while
-// the current ones are consumed); slots merge through cross-lane shuffles and
-// one LDS exchange, and the chunk writes (max, sum, O) partials.  The combine
-// kernel merges the chunks of each head.  Optionally the split kernel also
+// the current ones are consumed); the slots merge through one LDS exchange,
+// and the chunk writes (max, sum, O) partials with the maxima in base-2 units
+// (scores carry log2 e, weights are exp2 values).  The combine kernel merges
+// the chunks of each head.  Optionally the split kernel also
 // applies RoPE to q and the current k and appends K/V at the current position
 // (the workgroup holding that position), replacing the separate append launch.
 #include "rina_common.hpp"
@@ -135,8 +136,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     constexpr int PPW = 64 / LPP;        // positions per wave step (slots)
     constexpr int GS = 4 * PPW;          // positions per workgroup step
     constexpr int QH = HG * REP;         // query heads in the group
-    __shared__ float s_o[4][QH][DH];
-    __shared__ float s_m[4][QH], s_l[4][QH];
+    constexpr int NS = 4 * PPW;          // softmax slots of the workgroup
+    __shared__ __align__(16) float s_o[NS][QH][DH];
+    __shared__ __align__(16) float s_m[QH][NS];
+    __shared__ __align__(16) float s_aw[QH][NS];
+    __shared__ float s_l[QH][NS], s_M[QH];
     __shared__ float s_k[FUSED ? HG * DH : 1], s_v[FUSED ? HG * DH : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -201,7 +205,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     float kA[8], vA[8], kB[8], vB[8];
     issue(0, kA, vA);
 
+    // scores in base-2 units: log2 e and the scale folded into q, so the
+    // softmax weights are hardware exp2 values
     float qv[REP][8];
+    const float qsc = a.scale * 1.44269504088896341f;
 #pragma unroll
     for (int r = 0; r < REP; r++) {
         if (FUSED && a.qc) rope8(dim0, qraw[r], qpair[r], tc, ts, qv[r]);
@@ -209,6 +216,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; i++) qv[r][i] = qraw[r][i];
         }
+#pragma unroll
+        for (int i = 0; i < 8; i++) qv[r][i] *= qsc;
     }
     float kcur[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (has_cur) {
@@ -242,11 +251,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
             float p = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) p = fmaf(qv[r][i], kx[i], p);
-            const float sc = sum8(p) * a.scale;
+            const float sc = sum8(p);
             if (valid) {
                 const float mn = fmaxf(m_run[r], sc);
-                const float al = expf(m_run[r] - mn);   // 0 while nothing is accumulated
-                const float pe = expf(sc - mn);
+                const float al = __builtin_amdgcn_exp2f(m_run[r] - mn);   // 0 while nothing is accumulated
+                const float pe = __builtin_amdgcn_exp2f(sc - mn);
                 l_run[r] = fmaf(l_run[r], al, pe);
 #pragma unroll
                 for (int i = 0; i < 8; i++) ov[r][i] = fmaf(ov[r][i], al, pe * vx[i]);
@@ -273,57 +282,61 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
         st++;
     }
 
-    // merge the wave's slots (lanes lig, lig+LPP, ...) by shuffles
-#pragma unroll
-    for (int off = LPP; off < 64; off <<= 1) {
+    // merge of the NS slots through LDS: every slot's (m, l, O) is written,
+    // the slot weights 2^(m - M) are formed once per (head, slot), then each
+    // output dim sums the weighted slots
+    if ((lig & 7) == 0) {
 #pragma unroll
         for (int r = 0; r < REP; r++) {
-            const float mo = __shfl_xor(m_run[r], off), lo = __shfl_xor(l_run[r], off);
-            const float mn = fmaxf(m_run[r], mo);
-            const float a1 = m_run[r] == -INFINITY ? 0.f : expf(m_run[r] - mn);
-            const float a2 = mo == -INFINITY ? 0.f : expf(mo - mn);
-            l_run[r] = l_run[r] * a1 + lo * a2;
-#pragma unroll
-            for (int i = 0; i < 8; i++) ov[r][i] = ov[r][i] * a1 + __shfl_xor(ov[r][i], off) * a2;
-            m_run[r] = mn;
+            s_m[kvl * REP + r][wslot] = m_run[r];
+            s_l[kvl * REP + r][wslot] = l_run[r];
         }
     }
-    if (lane < LPP) {
 #pragma unroll
-        for (int r = 0; r < REP; r++) {
+    for (int r = 0; r < REP; r++) {
+        f32x4* dst = (f32x4*)&s_o[wslot][kvl * REP + r][dim0];
+        dst[0] = f32x4{ov[r][0], ov[r][1], ov[r][2], ov[r][3]};
+        dst[1] = f32x4{ov[r][4], ov[r][5], ov[r][6], ov[r][7]};
+    }
+    if (FUSED && has_cur && wave == 0 && lane < LPP) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) s_o[wave][kvl * REP + r][dim0 + i] = ov[r][i];
-            if ((lig & 7) == 0) {
-                s_m[wave][kvl * REP + r] = m_run[r];
-                s_l[wave][kvl * REP + r] = l_run[r];
-            }
+        for (int i = 0; i < 8; i++) {
+            s_k[kvl * DH + dim0 + i] = kcur[i];
+            s_v[kvl * DH + dim0 + i] = vcur[i];
         }
-        if (FUSED && has_cur && wave == 0) {
+    }
+    __syncthreads();
+    if (tid < QH * NS) {
+        const int qh = tid / NS, sl = tid % NS;
+        float M = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                s_k[kvl * DH + dim0 + i] = kcur[i];
-                s_v[kvl * DH + dim0 + i] = vcur[i];
-            }
+        for (int k = 0; k < NS; k += 4) {
+            const f32x4 mv = *(const f32x4*)&s_m[qh][k];
+            M = fmaxf(fmaxf(M, fmaxf(mv.x, mv.y)), fmaxf(mv.z, mv.w));
         }
+        const float mo = s_m[qh][sl];
+        s_aw[qh][sl] = mo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - M);
+        if (sl == 0) s_M[qh] = M;
     }
     __syncthreads();
     for (int e = tid; e < QH * DH; e += 256) {
         const int qh = e / DH, d = e % DH;
-        float M = -INFINITY;
+        float o = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w][qh]);
-        float o = 0.f, l = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const float mw = s_m[w][qh];
-            const float aw = mw == -INFINITY ? 0.f : expf(mw - M);
-            o = fmaf(s_o[w][qh][d], aw, o);
-            l = fmaf(s_l[w][qh], aw, l);
+        for (int k = 0; k < NS; k += 4) {
+            const f32x4 w4 = *(const f32x4*)&s_aw[qh][k];
+            o = fmaf(s_o[k][qh][d], w4.x, o);
+            o = fmaf(s_o[k + 1][qh][d], w4.y, o);
+            o = fmaf(s_o[k + 2][qh][d], w4.z, o);
+            o = fmaf(s_o[k + 3][qh][d], w4.w, o);
         }
         const int h = hg0 * REP + qh;
         gst(a.ws_o + ((int64_t)c * a.H + h) * DH + d, o);
         if (d == 0) {
-            gst(a.ws_m + (int64_t)c * a.H + h, M);
+            float l = 0.f;
+#pragma unroll
+            for (int k = 0; k < NS; k++) l = fmaf(s_l[qh][k], s_aw[qh][k], l);
+            gst(a.ws_m + (int64_t)c * a.H + h, s_M[qh]);
             gst(a.ws_l + (int64_t)c * a.H + h, l);
         }
     }
@@ -374,7 +387,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(SplitArgs a) {
     }
     const float ml = lane < nch ? mr : -INFINITY;
     const float M = wave_max(ml);
-    const float wl = lane < nch ? expf(ml - M) : 0.f;
+    const float wl = lane < nch ? __builtin_amdgcn_exp2f(ml - M) : 0.f;   // partial maxima in base-2 units
     const float lt = wave_sum(wl * lr);
     float o = 0.f;
 #pragma unroll
@@ -459,13 +472,15 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
         k1[i] = lane + 64 < dq ? gld(kr + lane + 64) : 0.f;
         vv[i] = gld(a.cv + (jp * a.Hkv + kvh) * a.dv + lane);
     }
+    // scores in base-2 units (the partials the combine kernel merges)
+    const float sc2 = a.scale * 1.44269504088896341f;
     float m = -INFINITY, l = 0.f, o = 0.f;
 #pragma unroll
     for (int i = 0; i < PW; i++) {
-        const float sc = wave_sum(fmaf(q0, k0[i], q1 * k1[i])) * a.scale;
+        const float sc = wave_sum(fmaf(q0, k0[i], q1 * k1[i])) * sc2;
         if (wave + 4 * i < ncv) {
             const float mn = fmaxf(m, sc);
-            const float al = expf(m - mn), pe = expf(sc - mn);
+            const float al = __builtin_amdgcn_exp2f(m - mn), pe = __builtin_amdgcn_exp2f(sc - mn);
             l = fmaf(l, al, pe);
             o = fmaf(o, al, pe * vv[i]);
             m = mn;
@@ -481,7 +496,7 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
         float ot = 0.f, lt = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const float aw = s_m[w] == -INFINITY ? 0.f : expf(s_m[w] - M);
+            const float aw = s_m[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w] - M);
             ot = fmaf(s_o[w][lane], aw, ot);
             lt = fmaf(s_l[w], aw, lt);
         }
