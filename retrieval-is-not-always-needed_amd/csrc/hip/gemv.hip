@@ -1032,6 +1032,17 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
         // activation once), up to 8 rows per wave
         int64_t waves = (int64_t)rina_num_cus() * 8;
         int64_t want = ((int64_t)rows * wpr + waves - 1) / waves;
+        if (fmt != FMT_Q2_K) {
+            // measured on the Q4 decode shapes: two matrices per row want
+            // more waves (SwiGLU 8192 x 2048: 2 rows per wave, 8.1 -> 7.5 us);
+            // a long row makes every workgroup's activation prep costly, so
+            // fewer, fuller workgroups (K 8192: 8 rows, 6.6 -> 5.9 us); single
+            // matrices of 2048+ rows take at least 2 rows per wave (W_o
+            // 2048 x 2048: 3.4 -> 3.25 us; a 1536-row SwiGLU loses with 2)
+            if (nmat == 2) want = (want + 1) / 2;
+            if (wpr >= 4) want *= 2;
+            if (nmat == 1 && rows >= 2048 && want < 2) want = 2;
+        }
         int rb = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : 8;
         if (fmt == FMT_Q2_K && rb > 4) rb = 4;   // 10 registers per Q2_K column block
         a.R = rows;
