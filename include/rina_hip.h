@@ -274,7 +274,8 @@ int rina_hip_moe_ffn(const float* x, const void* gate_exps, const void* up_exps,
  * softmax (as rina_hip_moe_topk); G = SiLU(W_g a2) * (W_u a2) for the shared
  * FFN (shared_ffn rows) and the k selected experts (ffn rows each);
  * h += down_sh G_sh + sum_j probs[j] down[e_j] G_j, j ascending.  Shapes:
- * d, ffn <= 2048, d, ffn, shared_ffn multiples of 32, n_experts <= 64,
+ * d, ffn <= 2048, d a multiple of 128, ffn, shared_ffn multiples of 32,
+ * n_experts <= 64,
  * shared_ffn + k * ffn <= 16384; other shapes and formats return
  * RINA_ERR_SHAPE / RINA_ERR_QTYPE before anything is launched.  h, ln2,
  * gate_inp and workspace 16-byte aligned; workspace:

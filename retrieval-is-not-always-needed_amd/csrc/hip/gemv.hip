@@ -430,7 +430,7 @@ struct DirectBlk {
 // straddle a block because row starts are multiples of 32 values.
 template <int RB>
 struct DirectBlkQ2 {
-    uint32_t qs[RB][2][8];
+    uint32_t qs[RB][2][2];  // quad form: this lane's quarter of the half page's qs bytes
     uint32_t sm[RB][2];     // scale bytes of halves 0 and 1 (low 16 bits)
     uint32_t dd[RB][2];     // d | dmin << 16
     int sh[RB];             // 2g
@@ -533,12 +533,11 @@ __device__ __forceinline__ void direct_issue(const GemvArgs& a, const Segs& S, i
         b.sh[i] = 2 * g;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            const uint8_t* bp = S.wt(sg, m) + off;
-            const u32x4_a4 q0 = gld_nt_a4(bp + 16 + 32 * page), q1 = gld_nt_a4(bp + 32 + 32 * page);
-            b.qs[i][m][0] = q0.x; b.qs[i][m][1] = q0.y; b.qs[i][m][2] = q0.z; b.qs[i][m][3] = q0.w;
-            b.qs[i][m][4] = q1.x; b.qs[i][m][5] = q1.y; b.qs[i][m][6] = q1.z; b.qs[i][m][7] = q1.w;
-            b.sm[i][m] = gld_nt((const uint16_t*)(bp + 8 * page + 2 * g));
-            b.dd[i][m] = gld_nt((const uint32_t*)(bp + 80));
+            Q2ColQ c;
+            q2_colq_load(S.wt(sg, m) + off, page, g, c);
+            b.qs[i][m][0] = c.q[0]; b.qs[i][m][1] = c.q[1];
+            b.sm[i][m] = c.sm & 0xFFFFu;
+            b.dd[i][m] = c.dd;
         }
         b.ok[i] = ok;
     }
@@ -565,8 +564,13 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S,
     for (int i = 0; i < RB; i++)
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            if constexpr (FMT == FMT_Q2_K)
-                part[i][m] = wave_sum(cur.ok[i] ? q2_col(cur.qs[i][m], cur.sm[i][m], cur.dd[i][m], cur.sh[i], xc) : 0.f);
+            if constexpr (FMT == FMT_Q2_K) {
+                // the quad exchange runs on every lane, outside the row test
+                const Q2ColQ cq{{cur.qs[i][m][0], cur.qs[i][m][1]}, 0u, 0u};
+                Q2Col c;
+                q2_colq_expand(cq, c);
+                part[i][m] = wave_sum(cur.ok[i] ? q2_col(c.qs, cur.sm[i][m], cur.dd[i][m], cur.sh[i], xc) : 0.f);
+            }
             else
                 part[i][m] = wave_sum((cur.ok[i] ? cur.sc[i][m] : 0.f) * xc.xe[0] * q4_dot(cur.nib[i][m], xc, 0));
         }
@@ -987,7 +991,9 @@ int dispatch_direct(GemvArgs& a, int wpr, int rb, int pro, hipStream_t st) {
 
 // M = 1 shapes the direct-load kernel takes: 32-value columns, at most one
 // per lane of four waves.
-bool direct_ok(int fmt, int K) { return fmt >= 0 && K % 32 == 0 && K <= 8192; }
+// Q2_K: K % 128 == 0 keeps the four lanes of a quad on one half page (the
+// quad form of the column loads)
+bool direct_ok(int fmt, int K) { return fmt >= 0 && K % (fmt == FMT_Q2_K ? 128 : 32) == 0 && K <= 8192; }
 
 // waves per row / units per lane for a row of `nunits` work units
 void split_row(int nunits, int& wpr, int& cpl) {
@@ -1044,7 +1050,7 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
             if (nmat == 1 && rows >= 2048 && want < 2) want = 2;
         }
         int rb = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : 8;
-        if (fmt == FMT_Q2_K && rb > 4) rb = 4;   // 10 registers per Q2_K column block
+        if (fmt == FMT_Q2_K && rb > 4) rb = 4;   // 8 rows measured slower (LM head 32 -> 35 us)
         a.R = rows;
         a.total_tiles = (rows + rb - 1) / rb;
         if (fmt == FMT_Q2_K)

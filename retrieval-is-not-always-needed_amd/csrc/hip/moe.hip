@@ -148,7 +148,7 @@ __device__ __forceinline__ void topk_wave(const MoeBlkArgs& a, int* s_ids, float
 constexpr int kGuRB = 4;   // row pairs per wave per group
 
 struct GuBlk {
-    Q2Col c[kGuRB][2];
+    Q2ColQ c[kGuRB][2];     // quad form: d % 128 == 0 keeps every quad on one half page
     int vr[kGuRB];          // virtual row (output index), -1 past the end
     bool ok[kGuRB];         // row has an expert (lane also active)
     bool rowok[kGuRB];
@@ -175,8 +175,8 @@ __device__ __forceinline__ void gu_issue(const MoeBlkArgs& a, const int* s_ids, 
         }
         const bool ok = rowok && active;
         const uint32_t e0 = ok ? (uint32_t)row * (uint32_t)a.d + 32u * lane : 0u;
-        q2_col_issue32(wg, e0, b.c[i][0]);
-        q2_col_issue32(wu, e0, b.c[i][1]);
+        q2_colq_issue32(wg, e0, b.c[i][0]);
+        q2_colq_issue32(wu, e0, b.c[i][1]);
         b.vr[i] = valid ? vr : -1;
         b.ok[i] = ok;
         b.rowok[i] = rowok;
@@ -187,8 +187,11 @@ __device__ __forceinline__ void gu_consume(const MoeBlkArgs& a, const DCols<FMT_
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < kGuRB; i++) {
-        const float g = wave_sum(b.ok[i] ? q2_col(b.c[i][0], xc) : 0.f);
-        const float u = wave_sum(b.ok[i] ? q2_col(b.c[i][1], xc) : 0.f);
+        Q2Col cg, cu;   // the quad exchange runs on every lane, outside the row test
+        q2_colq_expand(b.c[i][0], cg);
+        q2_colq_expand(b.c[i][1], cu);
+        const float g = wave_sum(b.ok[i] ? q2_col(cg, xc) : 0.f);
+        const float u = wave_sum(b.ok[i] ? q2_col(cu, xc) : 0.f);
         if (lane == 0 && b.vr[i] >= 0) gst(a.G + b.vr[i], b.rowok[i] ? silu_mul(g, u) : 0.f);
     }
 }
@@ -425,7 +428,7 @@ extern "C" int rina_hip_moe_block(float* h, const float* ln2, float eps, const v
         return RINA_ERR_ARG;
     if (qt != RINA_QT_GGML_Q2_K || qt_gate_inp != RINA_QT_FP32) return RINA_ERR_QTYPE;
     const int S = shared_ffn, F = ffn;
-    if (d % 32 || d > kMoeMaxD || F % 32 || F > kMoeMaxD || S % 32 || n_experts > 64 || k > 16) return RINA_ERR_SHAPE;
+    if (d % 128 || d > kMoeMaxD || F % 32 || F > kMoeMaxD || S % 32 || n_experts > 64 || k > 16) return RINA_ERR_SHAPE;
     const int n = S + k * F;
     const size_t lds = (size_t)(n / 32) * kRec * sizeof(uint32_t);
     if (lds > 64 * 1024 || n > 16384) return RINA_ERR_SHAPE;

@@ -157,6 +157,53 @@ __device__ __forceinline__ float q2_col(const Q2Col& c, const DCols<FMT_Q2_K>& x
     return q2_col(c.qs, c.sm & 0xFFFFu, c.dd, (int)(c.sm >> 16), xc);
 }
 
+// Quad form of the column loads.  When lane u holds column u of a row
+// (e0 = row K + 32u, K % 128 == 0), the four lanes of a quad hold the
+// columns g = 0..3 of one half page, and their 2-bit fields live in the same
+// 32 qs bytes.  Each lane loads one quarter (8 bytes) and the quarters are
+// exchanged with DPP quad broadcasts where the column is used, so the qs
+// bytes pass through the load path once instead of four times.  All four
+// lanes of a quad must be active at the exchange.
+struct Q2ColQ {
+    uint32_t q[2];  // qs bytes 8t .. 8t + 7 of the half page, t = lane & 3
+    uint32_t sm;    // as Q2Col::sm
+    uint32_t dd;
+};
+
+__device__ __forceinline__ void q2_colq_load(const uint8_t* bp, int page, int g, Q2ColQ& c) {
+    typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+    const u32x2_a4 q = __builtin_nontemporal_load(
+        (const __attribute__((address_space(1))) u32x2_a4*)(bp + 16 + 32 * page + 8 * (threadIdx.x & 3)));
+    c.q[0] = q.x; c.q[1] = q.y;
+    c.sm = (uint32_t)gld_nt((const uint16_t*)(bp + 8 * page + 2 * g)) | ((uint32_t)(2 * g) << 16);
+    c.dd = gld_nt((const uint32_t*)(bp + 80));
+}
+
+__device__ __forceinline__ void q2_colq_issue32(const uint8_t* w, uint32_t e0, Q2ColQ& c) {
+    q2_colq_load(w + (e0 >> 8) * 84u, (int)(e0 >> 7) & 1, (int)(e0 >> 5) & 3, c);
+}
+
+__device__ __forceinline__ void q2_colq_issue(const uint8_t* w, int64_t e0, Q2ColQ& c) {
+    q2_colq_load(w + (e0 >> 8) * 84, (int)(e0 >> 7) & 1, (int)(e0 >> 5) & 3, c);
+}
+
+// value of lane K of the quad in every lane of the quad: ds_swizzle in
+// quad-permute mode (bit 15 set, lane selects in bits 0-7), which runs on the
+// LDS crossbar instead of the vector ALU these kernels are bound by
+template <int K>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x8000 | (K * 0x55));
+}
+
+__device__ __forceinline__ void q2_colq_expand(const Q2ColQ& c, Q2Col& o) {
+    o.qs[0] = quad_bcast<0>(c.q[0]); o.qs[1] = quad_bcast<0>(c.q[1]);
+    o.qs[2] = quad_bcast<1>(c.q[0]); o.qs[3] = quad_bcast<1>(c.q[1]);
+    o.qs[4] = quad_bcast<2>(c.q[0]); o.qs[5] = quad_bcast<2>(c.q[1]);
+    o.qs[6] = quad_bcast<3>(c.q[0]); o.qs[7] = quad_bcast<3>(c.q[1]);
+    o.sm = c.sm;
+    o.dd = c.dd;
+}
+
 // Digits of one 32-value column in the Q2_K (natural) order with the fp32
 // sums of its two halves, as the matvec kernels' workgroup prep makes them.
 __device__ __forceinline__ void digitize_q2col(DCols<FMT_Q2_K>& xc, const float (&x)[32]) {

@@ -223,6 +223,7 @@ def test_moe_block_rejects_unsupported(rina):
     args = lambda d, F, S, E, k, qt, qr: (ptr, ptr, np.float32(1e-5), ptr, qr, ptr, ptr, ptr, S, ptr, ptr, ptr, qt,
                                           256, 256, E, k, d, F, ptr, 1 << 18, stream())
     assert hip.rina_hip_moe_block(*args(256, 48, 64, 8, 3, Q2K, FP32)) == -3    # F % 32
+    assert hip.rina_hip_moe_block(*args(160, 64, 64, 8, 3, Q2K, FP32)) == -3    # d % 128
     assert hip.rina_hip_moe_block(*args(256, 64, 64, 8, 3, Q4F, FP32)) == -2
     assert hip.rina_hip_moe_block(*args(256, 64, 64, 8, 3, Q2K, Q2K)) == -2    # router not fp32
     assert hip.rina_hip_moe_block(*args(4096, 64, 64, 8, 3, Q2K, FP32)) == -3
