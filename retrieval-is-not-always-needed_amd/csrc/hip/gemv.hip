@@ -430,7 +430,12 @@ struct DirectBlk {
 // straddle a block because row starts are multiples of 32 values.
 template <int RB>
 struct DirectBlkQ2 {
-    uint32_t qs[RB][2][2];  // quad form: this lane's quarter of the half page's qs bytes
+    // 4+ rows per wave: quad form (this lane's quarter of the half page's qs
+    // bytes, exchanged at use); 1-2 rows: the whole 32 bytes per lane, since
+    // with so few loads in flight the exchange's latency costs more than the
+    // repeated bytes (W_o 2048 x 2048: 3.7 vs 4.4 us)
+    static constexpr bool QUAD = RB >= 4;
+    uint32_t qs[RB][2][QUAD ? 2 : 8];
     uint32_t sm[RB][2];     // scale bytes of halves 0 and 1 (low 16 bits)
     uint32_t dd[RB][2];     // d | dmin << 16
     int sh[RB];             // 2g
@@ -533,11 +538,20 @@ __device__ __forceinline__ void direct_issue(const GemvArgs& a, const Segs& S, i
         b.sh[i] = 2 * g;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            Q2ColQ c;
-            q2_colq_load(S.wt(sg, m) + off, page, g, c);
-            b.qs[i][m][0] = c.q[0]; b.qs[i][m][1] = c.q[1];
-            b.sm[i][m] = c.sm & 0xFFFFu;
-            b.dd[i][m] = c.dd;
+            if constexpr (DirectBlkQ2<RB>::QUAD) {
+                Q2ColQ c;
+                q2_colq_load(S.wt(sg, m) + off, page, g, c);
+                b.qs[i][m][0] = c.q[0]; b.qs[i][m][1] = c.q[1];
+                b.sm[i][m] = c.sm & 0xFFFFu;
+                b.dd[i][m] = c.dd;
+            } else {
+                Q2Col c;
+                q2_col_load(S.wt(sg, m) + off, page, g, c);
+#pragma unroll
+                for (int z = 0; z < 8; z++) b.qs[i][m][z] = c.qs[z];
+                b.sm[i][m] = c.sm & 0xFFFFu;
+                b.dd[i][m] = c.dd;
+            }
         }
         b.ok[i] = ok;
     }
@@ -565,10 +579,15 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S,
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             if constexpr (FMT == FMT_Q2_K) {
-                // the quad exchange runs on every lane, outside the row test
-                const Q2ColQ cq{{cur.qs[i][m][0], cur.qs[i][m][1]}, 0u, 0u};
                 Q2Col c;
-                q2_colq_expand(cq, c);
+                if constexpr (DirectBlkQ2<RB>::QUAD) {
+                    // the quad exchange runs on every lane, outside the row test
+                    const Q2ColQ cq{{cur.qs[i][m][0], cur.qs[i][m][1]}, 0u, 0u};
+                    q2_colq_expand(cq, c);
+                } else {
+#pragma unroll
+                    for (int z = 0; z < 8; z++) c.qs[z] = cur.qs[i][m][z];
+                }
                 part[i][m] = wave_sum(cur.ok[i] ? q2_col(c.qs, cur.sm[i][m], cur.dd[i][m], cur.sh[i], xc) : 0.f);
             }
             else
@@ -992,7 +1011,7 @@ int dispatch_direct(GemvArgs& a, int wpr, int rb, int pro, hipStream_t st) {
 // M = 1 shapes the direct-load kernel takes: 32-value columns, at most one
 // per lane of four waves.
 // Q2_K: K % 128 == 0 keeps the four lanes of a quad on one half page (the
-// quad form of the column loads)
+// quad form of the column loads, 4+ rows per wave)
 bool direct_ok(int fmt, int K) { return fmt >= 0 && K % (fmt == FMT_Q2_K ? 128 : 32) == 0 && K <= 8192; }
 
 // waves per row / units per lane for a row of `nunits` work units
