@@ -783,7 +783,66 @@ __device__ __forceinline__ void f32_rows_short(const F32Args& a, const float* xs
     }
 }
 
-template <int NMAT, bool VEC, int NV>
+// Rows of K = 128 NV values (K/4 a multiple of 32, not of 64: K = 640 is the
+// Jamba LM head): each half wave takes a row, so a lane's NV 16-byte loads
+// per row are all in use.  A wave takes 2 * RP rows at a time, all loads
+// issued first; the half-wave sums come from lanes 31 and 63 after the
+// row_bcast step of the wave reduction.
+template <int NMAT, int NV, int RP>
+__device__ __forceinline__ void f32_rows_half(const F32Args& a, const float* xs_lds, int gw, int nw) {
+    constexpr int RPW = 2 * RP;
+    const int lane = threadIdx.x & 63, hl = lane & 31, half = lane >> 5;
+    const int n4 = a.K >> 2;
+    const f32x4* x4 = (const f32x4*)xs_lds;
+    f32x4 xv[NV];
+#pragma unroll
+    for (int t = 0; t < NV; t++) xv[t] = x4[hl + 32 * t];
+    for (int r0 = gw * RPW; r0 < a.total_rows; r0 += nw * RPW) {
+        f32x4 w[RP][NMAT][NV];
+        int seg[RP], row[RP];
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            const int vr = min(r0 + 2 * p + half, a.total_rows - 1);
+            int s = 0;
+            if (a.nseg > 1 && vr >= a.seg[1].tile0) s = 1;
+            if (a.nseg > 2 && vr >= a.seg[2].tile0) s = 2;
+            seg[p] = s;
+            row[p] = vr - a.seg[s].tile0;
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                const f32x4* wr = (const f32x4*)(m == 0 ? a.seg[s].w : a.seg[s].w2) + (int64_t)row[p] * n4;
+#pragma unroll
+                for (int t = 0; t < NV; t++) w[p][m][t] = gld_nt(wr + hl + 32 * t);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            float v[2];
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                for (int t = 0; t < NV; t++) {
+                    float& acc = (t & 1) ? s1 : s0;
+                    acc = fmaf(xv[t].x, w[p][m][t].x, acc); acc = fmaf(xv[t].y, w[p][m][t].y, acc);
+                    acc = fmaf(xv[t].z, w[p][m][t].z, acc); acc = fmaf(xv[t].w, w[p][m][t].w, acc);
+                }
+                float h = sum16(s0 + s1);
+                h += dpp_rows<0x142, 0xA>(h);   // row_bcast:15: lane 31 = lanes 0..31, lane 63 = 32..63
+                v[m] = h;
+            }
+            if (hl == 31 && r0 + 2 * p + half < a.total_rows) {
+                float* y = a.seg[seg[p]].y + row[p];
+                if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
+                else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
+                else gst(y, v[0]);
+            }
+        }
+    }
+}
+
+// NV > 0: rows of K <= 2048 (f32_rows_short); HALF: the half-wave rows
+template <int NMAT, bool VEC, int NV, bool HALF = false>
 __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     extern __shared__ __align__(16) float xs_lds[];
     __shared__ float red[8];
@@ -815,7 +874,10 @@ __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     }
     __syncthreads();
     const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
-    if constexpr (NV > 0) {
+    if constexpr (HALF) {
+        f32_rows_half<NMAT, NV, NMAT == 2 ? 2 : 4>(a, xs_lds, gw, nw);
+        return;
+    } else if constexpr (NV > 0) {
         f32_rows_short<NMAT, NV>(a, xs_lds, gw, nw);
         return;
     }
@@ -1141,13 +1203,31 @@ int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int e
     // short rows (K <= 2048, 16-byte aligned): several rows per wave with all
     // loads in flight; NV = 16-byte loads per lane per row
     const int nv = vec && K <= 2048 ? (K / 4 + 63) / 64 : 0;
-    if (nv > 0) {
+    // K / 4 an odd multiple of 32 (K = 128, 384, 640, 896): half-wave rows
+    const int nvh = vec && (K / 4) % 64 == 32 && K <= 896 ? K / 128 : 0;
+    if (nvh > 0) {
+        const int rpw = two ? 4 : 8;
+        int g2 = (rows + 4 * rpw - 1) / (4 * rpw);
+        if (g2 < grid) grid = g2;
+    } else if (nv > 0) {
         const int rpw = two ? 2 : 4;
         int g2 = (rows + 4 * rpw - 1) / (4 * rpw);
         if (g2 < grid) grid = g2;
     }
 #define F32_LAUNCH(NM, V, NVV) hipLaunchKernelGGL((gemv_f32_kernel<NM, V, NVV>), dim3(grid), dim3(kWG), lds, st, a)
-    if (nv > 0) {
+#define F32_HALF(NM, NVV) hipLaunchKernelGGL((gemv_f32_kernel<NM, true, NVV, true>), dim3(grid), dim3(kWG), lds, st, a)
+    if (nvh > 0) {
+        switch (nvh * (two ? -1 : 1)) {
+            case 1: F32_HALF(1, 1); break;
+            case 3: F32_HALF(1, 3); break;
+            case 5: F32_HALF(1, 5); break;
+            case 7: F32_HALF(1, 7); break;
+            case -1: F32_HALF(2, 1); break;
+            case -3: F32_HALF(2, 3); break;
+            case -5: F32_HALF(2, 5); break;
+            default: F32_HALF(2, 7); break;
+        }
+    } else if (nv > 0) {
         switch ((nv <= 2 ? 2 : nv <= 4 ? 4 : 8) * (two ? -1 : 1)) {
             case 2: F32_LAUNCH(1, true, 2); break;
             case 4: F32_LAUNCH(1, true, 4); break;
@@ -1164,6 +1244,7 @@ int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int e
         else F32_LAUNCH(1, false, 0);
     }
 #undef F32_LAUNCH
+#undef F32_HALF
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 

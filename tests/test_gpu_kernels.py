@@ -117,6 +117,39 @@ def test_linear_fp32(rina, orc, M, N, K):
     assert_close(run_linear(rina, w, 6, x, N, K), orc.linear(w, 6, x, N, K), what="fp32 %s" % ((M, N, K),))
 
 
+@pytest.mark.parametrize("K", [128, 384, 640, 896])
+def test_linear_fp32_half_rows(rina, orc, K):
+    # K/4 an odd multiple of 32: one row per half wave; three segments of
+    # row counts that are not multiples of the rows per wave, add and SwiGLU
+    hip = rina.load_hip()
+    r = rng(K + 5)
+    Ns = (1001, 37, 130)
+    ws = [(r.standard_normal(n * K) * 0.05).astype(np.float32) for n in Ns]
+    x = r.standard_normal(K).astype(np.float32)
+    xd = dev(x)
+    wd = [dev(w) for w in ws]
+    outs = [empty(n) for n in Ns]
+    segs = (rina.LinearSeg * 3)(*[rina.LinearSeg(wd[i].data_ptr(), None, outs[i].data_ptr(), Ns[i]) for i in range(3)])
+    ok(hip.rina_hip_linear_fused(segs, 3, 6, xd.data_ptr(), 1, K, rina.EPI_STORE, 0, None, 0.0, stream()), "store")
+    for i in range(3):
+        assert_close(host(outs[i]), orc.linear(ws[i], 6, x, Ns[i], K)[0], what="K %d seg %d" % (K, i))
+    base = r.standard_normal(Ns[0]).astype(np.float32)
+    yd = dev(base)
+    seg = rina.LinearSeg(wd[0].data_ptr(), None, yd.data_ptr(), Ns[0])
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, 6, xd.data_ptr(), 1, K, rina.EPI_ADD, 0, None, 0.0, stream()), "add")
+    assert_close(host(yd), base + orc.linear(ws[0], 6, x, Ns[0], K)[0], what="K %d add" % K)
+    w3 = (r.standard_normal(Ns[0] * K) * 0.05).astype(np.float32)
+    gd = empty(Ns[0])
+    seg = rina.LinearSeg(wd[0].data_ptr(), dev(w3).data_ptr(), gd.data_ptr(), Ns[0])
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, 6, xd.data_ptr(), 1, K, rina.EPI_SWIGLU, 0, None, 0.0, stream()),
+       "swiglu")
+    g = orc.linear(ws[0], 6, x, Ns[0], K)[0]
+    u = orc.linear(w3, 6, x, Ns[0], K)[0]
+    ref = np.zeros(Ns[0], np.float32)
+    orc.load().orc_silu_mul(ref.ctypes.data, g.ctypes.data, u.ctypes.data, Ns[0])
+    assert_close(host(gd), ref, what="K %d swiglu" % K)
+
+
 @pytest.mark.parametrize("qt", [7, 6])
 def test_linear_in_place(rina, orc, qt):
     # input == output: defined as out of place (the reference's in-place w_o call races)
