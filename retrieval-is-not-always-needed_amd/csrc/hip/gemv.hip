@@ -647,7 +647,6 @@ __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
 
     // activation loads, then the first row group's weight loads, then the
     // activation prep (overlapping the weight loads)
-    __shared__ PrepLds prep;
     constexpr int TPC = WPR == 1 ? 4 : WPR == 2 ? 2 : 1;
     PrepRaw<TPC, PRO> raw;
     const PrepSrc src{a.x, a.nw, a.K, a.eps, a.xn};
@@ -655,9 +654,16 @@ __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
     int it = blockIdx.x;
     DirectBlkT<FMT, RB> A, B;
     direct_issue<FMT, NMAT, RB>(a, S, it * RPI + rs, u, active, A);
-    wg_prep_x<FMT, TPC, PRO>(src, raw, prep);
     DCols<FMT> xc;
-    read_cols<FMT>(prep, u, active, xc);
+    if constexpr (WPR == 4) {
+        // u == threadIdx.x: every thread prepares its own column
+        __shared__ float red[8];
+        own_prep_x<FMT, PRO>(src, raw, red, xc);
+    } else {
+        __shared__ PrepLds prep;
+        wg_prep_x<FMT, TPC, PRO>(src, raw, prep);
+        read_cols<FMT>(prep, u, active, xc);
+    }
 
     for (;;) {
         if ((it + G) * RPI < ngrp) {

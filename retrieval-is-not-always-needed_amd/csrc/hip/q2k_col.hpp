@@ -408,6 +408,49 @@ __device__ __forceinline__ void wg_prep_x(const PrepSrc& a, PrepRaw<TPC, PRO>& r
     __syncthreads();
 }
 
+// Prep for four waves per row (K > 4096): thread t prepares column t, which
+// is the column lane t % 64 of wave t / 64 consumes, so the digits go
+// straight to the thread's registers (the same digits as the LDS path, bit
+// for bit) with no LDS exchange, and without a norm prologue no barrier.
+template <int FMT, int PRO>
+__device__ __forceinline__ void own_prep_x(const PrepSrc& a, PrepRaw<1, PRO>& r, float* red, DCols<FMT>& xc) {
+    const int u = threadIdx.x;
+    const bool on = u < a.K / 32;
+    float (&x)[32] = r.x;
+    if (!on) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) x[i] = 0.f;
+    }
+    if constexpr (PRO != RINA_PRO_NONE) {
+        const float d = (float)a.K;
+        float mean = 0.f;
+        if (PRO == RINA_PRO_LAYERNORM) {
+            float sm = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; i++) sm += x[i];
+            mean = block_sum4(sm, red, 0) / d;
+        }
+        float ss = 0.f;
+        if (on) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                const float t = x[i] - mean;
+                ss = fmaf(t, t, ss);
+            }
+        }
+        const float inv = 1.0f / sqrtf(block_sum4(ss, red, 1) / d + a.eps);
+#pragma unroll
+        for (int i = 0; i < 32; i++) x[i] = on ? (x[i] - mean) * inv * r.w[i] : 0.f;
+        if (a.xn && blockIdx.x == 0 && on) {
+            f32x4* xo = (f32x4*)(a.xn + (int64_t)u * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) gst(xo + i, f32x4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]});
+        }
+    }
+    if constexpr (FMT == FMT_Q2_K) digitize_q2col(xc, x);
+    else digitize<FMT, 1>(xc, 0, x);
+}
+
 template <int FMT>
 __device__ __forceinline__ void read_cols(const PrepLds& L, int u, bool active, DCols<FMT>& xc) {
     const int uu = active ? u : 0;
