@@ -179,6 +179,8 @@ def main():
     ap.add_argument("--no-config4", action="store_true", help="skip the DeepSeek MLA + MoE (config 4) decode line")
     ap.add_argument("--config4-steps", type=int, default=32)
     ap.add_argument("--no-config5", action="store_true", help="skip the RINA Jamba (config 5) decode line")
+    ap.add_argument("--no-config3", action="store_true", help="skip the context-4096 quantized-KV (config 3) line")
+    ap.add_argument("--config3-steps", type=int, default=8)
     ap.add_argument("--traffic-probe", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 --pmc passes for the LM head's HBM traffic and write them to profiles/")
@@ -278,7 +280,7 @@ def main():
     if not args.no_config4:
         t4 = time.time()
         p4, s4 = 32, args.config4_steps
-        ds = synth.SynthDeepSeek(seed=1, max_seq=p4 + s4 + 8)
+        ds = synth.SynthDeepSeek(seed=1, max_seq=max(2048, p4 + s4 + 8))   # context 2048
         log("config 4 model built in %.1fs" % (time.time() - t4))
         inf4 = ds.infer()
         pr4 = np.random.default_rng(4).integers(0, ds.cfg["vocab_size"], p4).astype(np.int32)
@@ -295,7 +297,7 @@ def main():
         b4 = ds.bytes_per_token(p4 + 1 + s4 // 2)
         cfg4 = {"workload": "DeepSeek-V2-Lite-shaped MLA + MoE decode: 27 layers (1 dense + 26 MoE, 64 experts top-6 "
                             "of 1408, 2 shared), d 2048, 16 heads, kv_lora_rank 512, rope 64, vocab 102400, random "
-                            "Q2_K weights, latent fp32 cache, %d-token prompt, greedy" % p4,
+                            "Q2_K weights, latent fp32 cache of 2048 positions, %d-token prompt, greedy" % p4,
                 "tokens_per_s": round(s4 / w4, 2), "ms_per_step": round(w4 * 1e3 / s4, 4), "steps": s4,
                 "bytes_per_token": b4, "hbm_gbps": round(b4 * s4 / w4 / 1e9, 1),
                 "hbm_frac": round(b4 * s4 / w4 / HBM_PEAK, 4), "tokens_head": list(first4) + list(out4)[:6]}
@@ -308,7 +310,7 @@ def main():
     cfg5 = None
     if not args.no_config5:
         p5, s5 = 64, 128
-        jm = synth.SynthJamba(seed=1, max_seq=p5 + s5 + 8)
+        jm = synth.SynthJamba(seed=1, max_seq=max(2048, p5 + s5 + 8))   # context 2048
         inf5 = jm.infer()
         pr5 = np.random.default_rng(5).integers(0, jm.cfg["vocab_size"], p5).astype(np.int32)
         # two generated tokens: the second step captures the decode graph
@@ -326,7 +328,7 @@ def main():
         b5 = jm.bytes_per_token(p5 + 1 + s5 // 2)
         cfg5 = {"workload": "RINA Gen6 Jamba hybrid at random init: 640d, 16 layers (12 InertiaWave SSM + 4 RINA-MLA), "
                             "10/5 heads, d_c 160, LayerNorm + SwiGLU 1536, vocab 128256, Q4_0 linears, fp32 tied LM "
-                            "head, %d-token prompt, %d greedy steps" % (p5, s5),
+                            "head, context 2048, %d-token prompt, %d greedy steps" % (p5, s5),
                 "tokens_per_s": round(s5 / w5, 2), "ms_per_step": round(w5 * 1e3 / s5, 4), "steps": s5,
                 "bytes_per_token": b5, "hbm_gbps": round(b5 * s5 / w5 / 1e9, 1),
                 "hbm_frac": round(b5 * s5 / w5 / HBM_PEAK, 4), "tokens_head": list(first5) + list(out5)[:7]}
@@ -334,6 +336,43 @@ def main():
         jm.close()
         del jm
         torch.cuda.empty_cache()
+
+    # ---- config 3: the same model at context 4096, KV cache q8 / q4 / q2k_q1v.
+    # A 4090-token seeded prompt is prefilled (untimed; the second generated
+    # token captures the decode graph), then greedy steps at positions
+    # 4092.. are timed.
+    cfg3 = None
+    if not args.no_config3:
+        n3, s3, ms3 = 4090, args.config3_steps, 4104
+        t3 = time.time()
+        sm3 = synth.SynthLlama(cfg, qt=rina.QT_Q4_0F, seed=1, max_seq=ms3)
+        log("config 3 model built in %.1fs" % (time.time() - t3))
+        pr3 = np.random.default_rng(3).integers(0, cfg["vocab_size"], n3).astype(np.int32)
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        rec = {"q8": (34, 34), "q4": (18, 18), "q2k_q1v": (10, 6)}     # K / V bytes per 32 values
+        modes = {}
+        for mode in ("q8", "q4", "q2k_q1v"):
+            inf3 = sm3.infer(mode, ms3)
+            f3 = (C.c_int * 2)()
+            rina.check(eng.rina_infer_generate(inf3, pr3.ctypes.data_as(C.POINTER(C.c_int)), n3, 2, f3, 1, st, None),
+                       "config 3 prefill")
+            o3 = (C.c_int * s3)()
+            torch.cuda.synchronize()
+            tq = time.perf_counter()
+            rina.check(eng.rina_infer_decode(inf3, s3, o3, 1, st, None), "config 3 decode")
+            torch.cuda.synchronize()
+            w3 = time.perf_counter() - tq
+            eng.rina_infer_destroy(inf3)
+            kv_tok = cfg["n_layers"] * (n3 + 2 + s3 // 2) * (kvd // 32) * sum(rec[mode])
+            modes[mode] = {"tokens_per_s": round(s3 / w3, 2), "ms_per_step": round(w3 * 1e3 / s3, 4),
+                           "kv_bytes_per_token": kv_tok, "tokens_head": list(f3) + list(o3)[:4]}
+            log("config 3 %s: %.3f ms/step, %.1f tok/s" % (mode, w3 * 1e3 / s3, s3 / w3))
+        sm3.close()
+        del sm3
+        torch.cuda.empty_cache()
+        cfg3 = {"workload": "Llama-3.2-1B-shaped decode at context 4096 (4090-token seeded prompt, steps at positions "
+                            "%d..%d), Q4_0F linears, fp32 tied LM head, KV cache q8 / q4 / q2k_q1v" % (n3 + 2, n3 + 1 + s3),
+                "steps": s3, "modes": modes}
 
     # ---- CPU baseline: the oracle (scalar C restatement) decoding the same model
     cpu = None
@@ -386,6 +425,7 @@ def main():
         },
         "decode_hbm_gbps": round(per_token * tok_s / 1e9, 1),
         "decode_hbm_frac": round(per_token * tok_s / HBM_PEAK, 4),
+        "config3_ctx4096_quant_kv": cfg3,
         "config4_deepseek_mla_moe": cfg4,
         "config5_rina_jamba": cfg5,
         "cpu_baseline": cpu,
