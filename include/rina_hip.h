@@ -303,6 +303,20 @@ int rina_hip_moe_block(float* h, const float* ln2, float eps, const void* gate_i
 int rina_hip_ssm_step(const float* mem, const float* dec_raw, int steps, int H, int dh,
                       float* lcs, float* wcs, float* sf_out, int reset, void* stream);
 
+/* The SSM layer's step after cq = LN(W_dq x) in one launch: LN(cq, q_norm)
+ * (LayerNorm, weight only, eps), mem_k = W_mem[k] . cq [H*dh] and
+ * dec_k = W_decay[k] . cq [H] for k < steps, then rina_hip_ssm_step on them
+ * (arch/ssm/rina_ssm_layer.cu:97-109: the q_norm launch, the 2*steps
+ * projections and the scan, fused; no counterpart as one reference call).
+ * w_mem / w_decay: arrays of `steps` packed weights [H*dh, dc] / [H, dc].
+ * RINA_QT_Q4_0 / RINA_QT_Q4_0F only (else RINA_ERR_QTYPE), dc % 32 == 0 and
+ * dc <= 512 (else RINA_ERR_SHAPE); both before anything is launched, so a
+ * caller can fall back to rina_hip_linear_fused + rina_hip_ssm_step. */
+int rina_hip_ssm_proj_step(const float* cq, const float* q_norm, float eps,
+                           const void* const* w_mem, const void* const* w_decay,
+                           int quant_type, int steps, int H, int dh, int dc,
+                           float* lcs, float* wcs, float* sf_out, int reset, void* stream);
+
 /* Decode attention of RinaMLAImpl (arch/mla/rina_mla_layer.cu:78-86) at
  * pos0 = start_pos + (d_pos ? *d_pos : 0): query [qa | RoPE_hf(qb)] per head
  * (qa [H*da], qb [H*db]), key [ka | RoPE_hf(kb)] and value v per KV head

@@ -80,6 +80,7 @@ struct SSMImpl {
     MLPPart mlp;
     float *lcs = nullptr, *wcs = nullptr;      // scan state [H*dh]
     float* scratch = nullptr;                  // x2 [d + H*dh] | cq [dc] | mem [3*H*dh] | dec [3*H]
+    bool fused = true;                         // rina_hip_ssm_proj_step takes this layer's shape
 
     ~SSMImpl() {
         if (lcs) (void)hipFree(lcs);
@@ -127,16 +128,26 @@ struct SSMImpl {
             // x = LN(h, ln1) as W_dq's prologue; the launch also stores x for W_out (:93-96)
             rina_linear_seg sq{w_dq, nullptr, cq, dc};
             CK(rina_hip_linear_fused_ex(&sq, 1, qt, ht, 1, d, RINA_EPI_STORE, RINA_PRO_LAYERNORM, ln1, 1e-5f, x2, s));
-            // the memory and decay projections share LN(cq, q_norm): one launch (:97-101)
-            rina_linear_seg sp[6];
-            for (int k = 0; k < steps; k++) {
-                sp[k] = {w_mem[k], nullptr, mem + (size_t)k * H * dh, H * dh};
-                sp[steps + k] = {w_decay[k], nullptr, dec + (size_t)k * H, H};
-            }
-            CK(rina_hip_linear_fused(sp, 2 * steps, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f,
-                                     s));
             const int reset = (!b.d_pos && start_pos == 0 && t == 0) ? 1 : 0;
-            CK(rina_hip_ssm_step(mem, dec, steps, H, dh, lcs, wcs, x2 + d, reset, s));           // :102-109
+            // LN(cq, q_norm), the memory and decay projections and the scan
+            // step (:97-109) in one launch where the kernel takes the shape
+            rc = fused ? rina_hip_ssm_proj_step(cq, q_norm, 1e-5f, w_mem, w_decay, qt, steps, H, dh, dc, lcs, wcs,
+                                                x2 + d, reset, s)
+                       : RINA_ERR_SHAPE;
+            if (rc == RINA_ERR_QTYPE || rc == RINA_ERR_SHAPE) {
+                fused = false;
+                // the projections share LN(cq, q_norm): one launch, then the step
+                rina_linear_seg sp[6];
+                for (int k = 0; k < steps; k++) {
+                    sp[k] = {w_mem[k], nullptr, mem + (size_t)k * H * dh, H * dh};
+                    sp[steps + k] = {w_decay[k], nullptr, dec + (size_t)k * H, H};
+                }
+                CK(rina_hip_linear_fused(sp, 2 * steps, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm,
+                                         1e-5f, s));
+                CK(rina_hip_ssm_step(mem, dec, steps, H, dh, lcs, wcs, x2 + d, reset, s));
+            } else if (rc != RINA_OK) {
+                return rc;
+            }
             rina_linear_seg so{w_out, nullptr, ht, d};
             CK(rina_hip_linear_fused(&so, 1, qt, x2, 1, d + H * dh, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
             CK(mlp.run(ht, b, d, qt, s));

@@ -97,6 +97,50 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f 
 template <int FMT>
 using DCols = XCols<FMT == FMT_Q2_K ? FMT_Q4_0 : FMT, 1>;
 
+__device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t sh) {
+    return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
+}
+
+// exact integer sum_i (q_i - 7) X_i of one Q4 block (nib: its 16 nibble bytes), as float
+template <int FMT, int CPL>
+__device__ __forceinline__ float q4_dot(const uint32_t (&nib)[4], const XCols<FMT, CPL>& xc, int j) {
+    int a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const int lo = (int)and_opaque(nib[d], 0x0F0F0F0Fu), hi = (int)and_opaque(nib[d] >> 4, 0x0F0F0F0Fu);
+        a0 = __builtin_amdgcn_sdot4(lo, xc.dg[j][0][2 * d], a0, false);
+        a1 = __builtin_amdgcn_sdot4(lo, xc.dg[j][1][2 * d], a1, false);
+        a2 = __builtin_amdgcn_sdot4(lo, xc.dg[j][2][2 * d], a2, false);
+        a0 = __builtin_amdgcn_sdot4(hi, xc.dg[j][0][2 * d + 1], a0, false);
+        a1 = __builtin_amdgcn_sdot4(hi, xc.dg[j][1][2 * d + 1], a1, false);
+        a2 = __builtin_amdgcn_sdot4(hi, xc.dg[j][2][2 * d + 1], a2, false);
+    }
+    const float f0 = (float)a0 - xc.tt[j][0], f1 = (float)a1 - xc.tt[j][1], f2 = (float)a2 - xc.tt[j][2];
+    return fmaf(65536.0f, f2, fmaf(256.0f, f1, f0));
+}
+
+// One Q4 block (18-byte Q4_0 with fp16 scale, 20-byte Q4_0F with fp32 scale)
+// at p: its scale and 16 nibble bytes, 4-byte aligned loads.
+template <int FMT>
+__device__ __forceinline__ void load_q4_block(const uint8_t* p, float& sc, uint32_t (&nib)[4]) {
+    if constexpr (FMT == FMT_Q4_0F) {
+        const u32x4_a4 v = gld_nt_a4(p);
+        const uint32_t t = gld_nt((const uint32_t*)(p + 16));
+        sc = __uint_as_float(v.x);
+        nib[0] = v.y; nib[1] = v.z; nib[2] = v.w; nib[3] = t;
+    } else {
+        // 18-byte block: 20-byte window from the dword at or below its start
+        const uintptr_t al = (uintptr_t)p & ~(uintptr_t)3;
+        const uint32_t sh = (uint32_t)((uintptr_t)p & 3) * 8;        // 0 or 16
+        const u32x4_a4 v = gld_nt_a4((const uint8_t*)al);
+        const uint32_t t = gld_nt((const uint32_t*)(al + 16));
+        const uint32_t d[5] = {v.x, v.y, v.z, v.w, t};
+        sc = f16_to_f32(sh ? (d[0] >> 16) : (d[0] & 0xFFFF));
+#pragma unroll
+        for (int k = 0; k < 4; k++) nib[k] = (uint32_t)((((uint64_t)d[k + 1] << 32) | d[k]) >> (16 + sh));
+    }
+}
+
 // One 32-value Q2_K column: exact integer dots of the two 16-value halves
 // (shift sh selects the lane's 2-bit field of each qs byte), weighted by the
 // halves' 4-bit scales, then d * 2^(e-22) * sum - dmin * (m0 x0 + m1 x1)
