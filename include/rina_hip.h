@@ -310,7 +310,7 @@ int rina_hip_ssm_step(const float* mem, const float* dec_raw, int steps, int H, 
  * projections and the scan, fused; no counterpart as one reference call).
  * w_mem / w_decay: arrays of `steps` packed weights [H*dh, dc] / [H, dc].
  * RINA_QT_Q4_0 / RINA_QT_Q4_0F only (else RINA_ERR_QTYPE), dc % 32 == 0 and
- * dc <= 512 (else RINA_ERR_SHAPE); both before anything is launched, so a
+ * dc <= 256 (else RINA_ERR_SHAPE); both before anything is launched, so a
  * caller can fall back to rina_hip_linear_fused + rina_hip_ssm_step. */
 int rina_hip_ssm_proj_step(const float* cq, const float* q_norm, float eps,
                            const void* const* w_mem, const void* const* w_decay,

@@ -14,17 +14,18 @@ namespace {
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // One scan advance for element j from the step's projections (decay rows
-// pre-sigmoid), shared by both kernels.
-__device__ __forceinline__ void ssm_advance(const float (&dr)[3], const float (&m)[3], int steps, int j, float* lcs,
-                                            float* wcs, float* sf, int reset) {
+// pre-sigmoid) and the state l0 = lcs[j], w0 = wcs[j] (read by the caller,
+// early), shared by both kernels.
+__device__ __forceinline__ void ssm_advance(const float (&dr)[3], const float (&m)[3], int steps, float l0, float w0,
+                                            int j, float* lcs, float* wcs, float* sf, int reset) {
     float dd[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) dd[k] = k < steps ? sigmoid_f(dr[k]) : 1.0f;
     float da = dd[0] * dd[1] * dd[2];                          // ssm_agg: da
     const float ma = fmaf(m[0] * dd[1], dd[2], m[1] * dd[2]) + m[2];
     if (da <= 1e-38f) da = 1e-38f;                             // ssm_scan
-    float l = reset ? 0.f : gld(lcs + j);
-    float w = reset ? 0.f : gld(wcs + j);
+    float l = reset ? 0.f : l0;
+    float w = reset ? 0.f : w0;
     l += logf(da);
     const float ca = expf(l);
     w += ma / fmaxf(ca, 1e-30f);
@@ -45,7 +46,7 @@ __global__ __launch_bounds__(256) void ssm_step_kernel(const float* mem, const f
         dr[k] = k < steps ? gld(dec + k * H + h) : 0.0f;
         m[k] = k < steps ? gld(mem + (int64_t)k * H * dh + j) : 0.0f;
     }
-    ssm_advance(dr, m, steps, j, lcs, wcs, sf, reset);
+    ssm_advance(dr, m, steps, gld(lcs + j), gld(wcs + j), j, lcs, wcs, sf, reset);
 }
 
 // ---------------------------------------------------------------------------
@@ -53,13 +54,19 @@ __global__ __launch_bounds__(256) void ssm_step_kernel(const float* mem, const f
 // cq = LN(W_dq x) is LN(cq, q_norm), the memory projections W_mem[k] (H*dh
 // rows) and decay projections W_decay[k] (H rows), then the aggregation and
 // scan (arch/ssm/rina_ssm_layer.cu:97-109).  One wave owns EPW elements of
-// head h: the decay rows of h and the memory rows of its elements (steps each),
-// NCP lanes per row (lane c: 32-value column c of the row, one Q4 block),
-// RPP = 64 / NCP rows per pass, 2 passes.  Every lane normalizes its own
-// column of cq itself (the LayerNorm sums run over the row's NCP lanes with
-// DPP), digitizes it and dots its blocks; the row sums are DPP sums over
-// the NCP lanes, and lanes e < EPW gather their element's rows with
-// ds_bpermute and advance the scan.  No LDS array and no barrier.
+// head h: the decay rows of h and the memory rows of its elements (steps
+// each), at most 16 rows in 2 passes of 8.
+//   prep:  lane 8c + t takes the 4 values of plane dword t of 32-value
+//          column c (values 8(t/2) + 2b + t%2, the Q4 nibble order) of
+//          LN(cq, q_norm): the LayerNorm sums are wave sums, the column
+//          maximum and digit sums run over the column's 8 lanes with DPP,
+//          so each lane digitizes 4 values instead of 32;
+//   dot:   lane 8g + c dots column c of row 8p + g (one Q4 block per pass)
+//          with the column's digits gathered by ds_bpermute; the row sums
+//          are DPP sums over 8 lanes;
+//   scan:  lanes e < EPW gather their element's rows with ds_bpermute and
+//          advance the scan.
+// No LDS array and no barrier.  dc <= 256 (8 columns).
 // ---------------------------------------------------------------------------
 struct SsmProjArgs {
     const float* cq;
@@ -72,49 +79,51 @@ struct SsmProjArgs {
 };
 
 constexpr int kProjPasses = 2;
+constexpr int kProjRows = 8;      // rows per pass (8 lanes per row)
 
-template <int NCP>
-__device__ __forceinline__ float grp_sum(float v) {
-    if constexpr (NCP == 8) return sum8(v);
-    else return sum16(v);
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+    return v;
 }
 
-template <int FMT, int NCP>
+__device__ __forceinline__ int32_t bperm(int lane, int32_t v) { return __builtin_amdgcn_ds_bpermute(lane * 4, v); }
+
+__device__ __forceinline__ float bperm_f(int lane, float v) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(lane * 4, __float_as_int(v)));
+}
+
+template <int FMT>
 __global__ __launch_bounds__(64) void ssm_proj_step_kernel(SsmProjArgs a) {
     constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
-    constexpr int RPP = 64 / NCP;
     const int lane = threadIdx.x;
-    const int g = lane / NCP, c = lane % NCP;
     const int h = blockIdx.x, e0 = blockIdx.y * a.epw;
     const int nc = a.dc / 32, steps = a.steps, epw = a.epw;
     const int nrows = steps * (epw + 1);
-    const bool on = c < nc;
     const int rowbytes = nc * BB;
 
-    // cq and q_norm column first (clamped: lanes past the row read column 0)
-    float x[32], w[32];
-    {
-        const f32x4* xp = (const f32x4*)(a.cq + 32 * (on ? c : 0));
-        const f32x4* wp = (const f32x4*)(a.qn + 32 * (on ? c : 0));
+    // prep operands first: lane 8pc + t, values 8(t/2) + 2b + t%2 of
+    // column pc (clamped: lanes past the row read column 0)
+    const int pc = lane >> 3, t = lane & 7;
+    const bool pon = pc < nc;
+    const int vb = 32 * (pon ? pc : 0) + 8 * (t >> 1) + (t & 1);
+    float xv[4], wv[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const f32x4 v = gld(xp + i);
-            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-        }
+    for (int b = 0; b < 4; b++) xv[b] = gld(a.cq + vb + 2 * b);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const f32x4 v = gld(wp + i);
-            w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-        }
-    }
+    for (int b = 0; b < 4; b++) wv[b] = gld(a.qn + vb + 2 * b);
+
     // then this lane's weight blocks, unconditional (rows past the wave's
     // set read block 0 of W_mem[0] and get scale 0)
+    const int g = lane >> 3, c = lane & 7;
+    const bool on = c < nc;
     float sc[kProjPasses];
     uint32_t nib[kProjPasses][4];
     bool ok[kProjPasses];
 #pragma unroll
     for (int p = 0; p < kProjPasses; p++) {
-        const int r = p * RPP + g;
+        const int r = p * kProjRows + g;
         ok[p] = on && r < nrows;
         const uint8_t* base = a.wm0;
         int row = 0;
@@ -131,30 +140,60 @@ __global__ __launch_bounds__(64) void ssm_proj_step_kernel(SsmProjArgs a) {
         const int64_t off = ok[p] ? (int64_t)row * rowbytes + c * BB : 0;
         load_q4_block<FMT>(base + off, sc[p], nib[p]);
     }
+    // the scan state of lane e < epw's element (other lanes: element 0)
+    const int je = h * a.dh + e0 + (lane < epw ? lane : 0);
+    const float l0 = gld(a.lcs + je), w0 = gld(a.wcs + je);
     __builtin_amdgcn_sched_barrier(0);
 
-    // LN(cq, q_norm) of this lane's column: sums over the row's NCP lanes
+    // LN(cq, q_norm): mean and variance over the dc values (wave sums)
     const float d = (float)a.dc;
-    float sm = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) sm += on ? x[i] : 0.f;
-    const float mean = grp_sum<NCP>(sm) / d;
+    const float mean = wave_sum(pon ? (xv[0] + xv[1]) + (xv[2] + xv[3]) : 0.f) / d;
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const float t = x[i] - mean;
-        ss = fmaf(t, t, ss);
+    for (int b = 0; b < 4; b++) {
+        const float u = xv[b] - mean;
+        ss = fmaf(u, u, ss);
     }
-    const float inv = 1.0f / sqrtf(grp_sum<NCP>(on ? ss : 0.f) / d + a.eps);
+    const float inv = 1.0f / sqrtf(wave_sum(pon ? ss : 0.f) / d + a.eps);
+    float xn[4];
+    float mx = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; i++) x[i] = on ? (x[i] - mean) * inv * w[i] : 0.f;
+    for (int b = 0; b < 4; b++) {
+        xn[b] = pon ? (xv[b] - mean) * inv * wv[b] : 0.f;
+        mx = fmaxf(mx, fabsf(xn[b]));
+    }
+    // block floating point of the column (its 8 lanes): x = X 2^(e-22)
+    mx = max8(mx);
+    int ex = 0;
+    if (mx > 0.f) (void)frexpf(mx, &ex);          // mx < 2^ex
+    const float up = ldexpf(1.0f, 22 - ex);
+    const float xe_p = ldexpf(1.0f, ex - 22);
+    uint32_t q0, q1, q2;
+    digits4(xn[0], xn[1], xn[2], xn[3], up, q0, q1, q2);
+    // 7 * (sum of each plane's digits): small integers, exact in fp32
+    const float tt0 = 7.0f * sum8((float)dsum4(q0, 0));
+    const float tt1 = 7.0f * sum8((float)dsum4(q1, 0));
+    const float tt2 = 7.0f * sum8((float)dsum4(q2, 0));
+
+    // dot layout: gather column c's digits from lanes 8c .. 8c + 7
     XCols<FMT, 1> xc;
-    digitize<FMT, 1>(xc, 0, x);
+    const int src = 8 * c;
+#pragma unroll
+    for (int tt = 0; tt < 8; tt++) {
+        xc.dg[0][0][tt] = bperm(src + tt, (int32_t)q0);
+        xc.dg[0][1][tt] = bperm(src + tt, (int32_t)q1);
+        xc.dg[0][2][tt] = bperm(src + tt, (int32_t)q2);
+    }
+    xc.tt[0][0] = bperm_f(src, tt0);
+    xc.tt[0][1] = bperm_f(src, tt1);
+    xc.tt[0][2] = bperm_f(src, tt2);
+    xc.xe[0] = bperm_f(src, xe_p);
+    xc.xs[0] = 0.f;
 
     float v[kProjPasses];
 #pragma unroll
     for (int p = 0; p < kProjPasses; p++)
-        v[p] = grp_sum<NCP>((ok[p] ? sc[p] : 0.f) * xc.xe[0] * q4_dot(nib[p], xc, 0));
+        v[p] = sum8((ok[p] ? sc[p] : 0.f) * xc.xe[0] * q4_dot(nib[p], xc, 0));
 
     // lane e < epw: decay rows 0..steps-1 (pass 0, groups 0..2) and memory
     // rows steps + k*epw + e of its element
@@ -162,14 +201,14 @@ __global__ __launch_bounds__(64) void ssm_proj_step_kernel(SsmProjArgs a) {
     float dr[3], mm[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
-        dr[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[0]), (k < RPP ? k : 0) * NCP));
+        dr[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[0]), k * 8));
         const int r = steps + k * epw + e;
-        const int src = (r % RPP) * NCP * 4;
-        const float m0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(v[0])));
-        const float m1 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(v[1])));
-        mm[k] = k < steps ? (r / RPP ? m1 : m0) : 0.f;
+        const int sl = (r % kProjRows) * 8;
+        const float m0 = bperm_f(sl, v[0]);
+        const float m1 = bperm_f(sl, v[1]);
+        mm[k] = k < steps ? (r / kProjRows ? m1 : m0) : 0.f;
     }
-    if (lane < epw) ssm_advance(dr, mm, steps, h * a.dh + e0 + lane, a.lcs, a.wcs, a.sf, a.reset);
+    if (lane < epw) ssm_advance(dr, mm, steps, l0, w0, je, a.lcs, a.wcs, a.sf, a.reset);
 }
 
 }  // namespace
@@ -186,9 +225,9 @@ extern "C" int rina_hip_ssm_step(const float* mem, const float* dec_raw, int ste
 
 // Elements per wave of the fused kernel: the most (up to 4) whose decay and
 // memory rows fit the wave's two passes, dividing dh.
-static int ssm_proj_epw(int steps, int dh, int rpp) {
+static int ssm_proj_epw(int steps, int dh) {
     for (int epw = 4; epw >= 1; epw /= 2)
-        if (dh % epw == 0 && steps * (epw + 1) <= kProjPasses * rpp) return epw;
+        if (dh % epw == 0 && steps * (epw + 1) <= kProjPasses * kProjRows) return epw;
     return 0;
 }
 
@@ -201,10 +240,8 @@ extern "C" int rina_hip_ssm_proj_step(const float* cq, const float* q_norm, floa
     for (int k = 0; k < steps; k++)
         if (!w_mem[k] || !w_decay[k]) return RINA_ERR_ARG;
     if (quant_type != RINA_QT_Q4_0 && quant_type != RINA_QT_Q4_0F) return RINA_ERR_QTYPE;
-    const int nc = dc / 32;
-    if (dc % 32 || nc > 16) return RINA_ERR_SHAPE;
-    const int ncp = nc <= 8 ? 8 : 16;
-    const int epw = ssm_proj_epw(steps, dh, 64 / ncp);
+    if (dc % 32 || dc > 256) return RINA_ERR_SHAPE;
+    const int epw = ssm_proj_epw(steps, dh);
     if (epw < 1) return RINA_ERR_SHAPE;
     SsmProjArgs a{};
     a.cq = cq;
@@ -228,13 +265,8 @@ extern "C" int rina_hip_ssm_proj_step(const float* cq, const float* q_norm, floa
     a.reset = reset;
     const dim3 grid(H, dh / epw);
     hipStream_t st = as_stream(stream);
-    if (quant_type == RINA_QT_Q4_0) {
-        if (ncp == 8) hipLaunchKernelGGL((ssm_proj_step_kernel<FMT_Q4_0, 8>), grid, dim3(64), 0, st, a);
-        else hipLaunchKernelGGL((ssm_proj_step_kernel<FMT_Q4_0, 16>), grid, dim3(64), 0, st, a);
-    } else {
-        if (ncp == 8) hipLaunchKernelGGL((ssm_proj_step_kernel<FMT_Q4_0F, 8>), grid, dim3(64), 0, st, a);
-        else hipLaunchKernelGGL((ssm_proj_step_kernel<FMT_Q4_0F, 16>), grid, dim3(64), 0, st, a);
-    }
+    if (quant_type == RINA_QT_Q4_0) hipLaunchKernelGGL((ssm_proj_step_kernel<FMT_Q4_0>), grid, dim3(64), 0, st, a);
+    else hipLaunchKernelGGL((ssm_proj_step_kernel<FMT_Q4_0F>), grid, dim3(64), 0, st, a);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }

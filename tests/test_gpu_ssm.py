@@ -60,7 +60,7 @@ SHAPES = [  # H, dh, dc, steps
     (4, 64, 64, 3),
     (3, 6, 160, 2),      # dh not a multiple of 4: 2 elements per wave
     (2, 5, 96, 1),       # odd dh: 1 element per wave
-    (2, 32, 512, 3),     # 16 lanes per row
+    (2, 32, 256, 3),     # 8 columns
     (1, 8, 32, 3),
 ]
 
@@ -116,7 +116,7 @@ def test_ssm_proj_step_rejects(rina):
     assert hip.rina_hip_ssm_proj_step(*args(10, 2, 8, 256, 3)) == -2        # Q2_K
     assert hip.rina_hip_ssm_proj_step(*args(6, 2, 8, 64, 3)) == -2         # fp32
     assert hip.rina_hip_ssm_proj_step(*args(5, 2, 8, 48, 3)) == -3         # dc % 32
-    assert hip.rina_hip_ssm_proj_step(*args(5, 2, 8, 544, 3)) == -3        # dc > 512
+    assert hip.rina_hip_ssm_proj_step(*args(5, 2, 8, 288, 3)) == -3        # dc > 256
     assert hip.rina_hip_ssm_proj_step(*args(5, 2, 8, 64, 4)) == -1         # steps > 3
     assert hip.rina_hip_ssm_proj_step(*args(5, 2, 8, 64, 2, (VP * 3)(p, None, p))) == -1
     torch = __import__("torch")
