@@ -400,19 +400,22 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(SplitArgs a) {
 // ---------------------------------------------------------------------------
 // Decode attention with key width dq = da + db != value width dv = 64
 // (RinaMLAImpl, arch/mla/rina_mla_layer.cu:78-86): query [qa | RoPE_hf(qb)],
-// key [ka | RoPE_hf(kb)] per KV head, scale 1/sqrt(dq).  The append kernel
-// rotates (HF pairs 2i, 2i+1) and writes the current K/V rows into fp32
-// caches [max_seq][Hkv][dq] / [max_seq][Hkv][dv]; the split kernel gives
-// each workgroup 32 positions of one query head (8 per wave, loads issued
-// together, lanes over dims) and writes the same (m, l, O) partials as the
-// GQA split kernel, so the same combine kernel finishes it.
+// key [ka | RoPE_hf(kb)] per KV head, scale 1/sqrt(dq), fp32 caches
+// [max_seq][Hkv][dq] / [max_seq][Hkv][dv].  The split kernel gives each
+// workgroup 32 positions of one query head (8 per wave, loads issued
+// together, lanes over dims); every workgroup rotates its query row itself
+// (HF pairs 2i, 2i+1), the one holding the current position also forms the
+// current K/V rows in registers and uses them for that position, and the
+// first query head of each KV head there appends them to the caches (no
+// workgroup of the launch reads that cache row).  It writes the same
+// (m, l, O) partials as the GQA split kernel, so the same combine kernel
+// finishes it.
 // ---------------------------------------------------------------------------
 struct DqArgs {
     const float *qa, *qb, *ka, *kb, *v;
     const float *qc, *qs, *kc, *ks;     // HF RoPE tables [max_seq][db/2] (NULL: none)
     float* ck;                          // [max_seq][Hkv][dq]
     float* cv;                          // [max_seq][Hkv][dv]
-    float* wq;                          // [H][dq] rotated queries
     int H, Hkv, da, db, dv, start_pos, max_seq;
     const int* d_pos;
     float scale;
@@ -421,33 +424,25 @@ struct DqArgs {
 constexpr int kDqChunk = 32;
 
 // grid H + Hkv: workgroup h < H builds query h; the rest append KV head h - H
-__global__ __launch_bounds__(64) void dq_append_kernel(DqArgs a) {
-    const int pos = read_pos(a.start_pos, a.d_pos);
-    if (pos < 0 || pos >= a.max_seq) return;
-    const int dq = a.da + a.db, hb = a.db / 2, t = threadIdx.x;
-    const bool isq = blockIdx.x < (unsigned)a.H;
-    const int h = isq ? blockIdx.x : blockIdx.x - a.H;
-    const float* xa = isq ? a.qa + (int64_t)h * a.da : a.ka + (int64_t)h * a.da;
-    const float* xb = isq ? a.qb + (int64_t)h * a.db : a.kb + (int64_t)h * a.db;
-    const float* tc = isq ? a.qc : a.kc;
-    const float* ts = isq ? a.qs : a.ks;
-    float* dst = isq ? a.wq + (int64_t)h * dq : a.ck + ((int64_t)pos * a.Hkv + h) * dq;
-    for (int i = t; i < a.da; i += 64) gst(dst + i, gld(xa + i));
-    for (int i = t; i < hb; i += 64) {
-        float x0 = gld(xb + 2 * i), x1 = gld(xb + 2 * i + 1);
-        if (tc) {
-            const float c = gld(tc + (int64_t)pos * hb + i), s = gld(ts + (int64_t)pos * hb + i);
-            const float o0 = fmaf(x0, c, -(x1 * s)), o1 = fmaf(x0, s, x1 * c);
-            x0 = o0; x1 = o1;
-        }
-        gst(dst + a.da + 2 * i, x0);
-        gst(dst + a.da + 2 * i + 1, x1);
-    }
-    if (!isq)
-        for (int i = t; i < a.dv; i += 64) gst(a.cv + ((int64_t)pos * a.Hkv + h) * a.dv + i, gld(a.v + (int64_t)h * a.dv + i));
+// Dim i (< da + db) of the row [xa | RoPE_hf(xb)] at position pos (tables
+// [max_seq][db/2], NULL: no rotation), the rotation in the reference's
+// fused-multiply form.  Every load is issued unconditionally (clamped
+// indices) so the caller's load counters stay exact.
+__device__ __forceinline__ float dq_dim(const float* xa, const float* xb, const float* tc, const float* ts, int da,
+                                        int db, int pos, int i) {
+    const int hb = db / 2;
+    const int j = i - da, pi = j < 0 ? 0 : (j >> 1 < hb ? j >> 1 : hb - 1);
+    const float va = gld(xa + (i < da ? i : da - 1));
+    const float* xbb = db > 0 ? xb : xa;
+    const float x0 = gld(xbb + (db > 0 ? 2 * pi : 0)), x1 = gld(xbb + (db > 0 ? 2 * pi + 1 : 0));
+    const bool rot = tc != nullptr && db > 0;
+    const float c = gld((rot ? tc : xbb) + (rot ? (int64_t)pos * hb + pi : 0));
+    const float sn = gld((rot ? ts : xbb) + (rot ? (int64_t)pos * hb + pi : 0));
+    const float cc = rot ? c : 1.0f, ss = rot ? sn : 0.0f;
+    const float vb = (j & 1) ? fmaf(x0, ss, x1 * cc) : fmaf(x0, cc, -(x1 * ss));
+    return i < da ? va : vb;
 }
 
-// grid (nchunk, H); dq <= 128, dv == 64
 __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     __shared__ float s_o[4][64];
     __shared__ float s_m[4], s_l[4];
@@ -458,9 +453,23 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     const int j0 = c * kDqChunk;
     if (j0 >= L) return;
     const int ncv = min(kDqChunk, L - j0);
-    const int dq = a.da + a.db, kvh = h / (a.H / a.Hkv);
-    const float q0 = gld(a.wq + (int64_t)h * dq + lane);
-    const float q1 = lane + 64 < dq ? gld(a.wq + (int64_t)h * dq + lane + 64) : 0.f;
+    const int dq = a.da + a.db, rep = a.H / a.Hkv, kvh = h / rep;
+    const bool has_cur = pos0 < j0 + kDqChunk;      // this chunk holds the current position
+    // the rotated query row and the current key / value rows (dims lane,
+    // lane + 64; the key row is used in the chunk holding pos0), before the
+    // cache loads
+    const int i1 = lane + 64 < dq ? lane + 64 : dq - 1;
+    const float* qa = a.qa + (int64_t)h * a.da;
+    const float* qb = a.qb + (int64_t)h * a.db;
+    const bool hi = lane + 64 < dq;
+    const float* ka = a.ka + (int64_t)kvh * a.da;
+    const float* kb = a.kb + (int64_t)kvh * a.db;
+    const float q0 = dq_dim(qa, qb, a.qc, a.qs, a.da, a.db, pos0, lane);
+    const float q1v = dq_dim(qa, qb, a.qc, a.qs, a.da, a.db, pos0, i1);
+    const float kc0 = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, pos0, lane);
+    const float kc1v = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, pos0, i1);
+    const float vc = gld(a.v + (int64_t)kvh * a.dv + lane);
+    const float q1 = hi ? q1v : 0.f, kc1 = hi ? kc1v : 0.f;
     constexpr int PW = kDqChunk / 4;
     float k0[PW], k1[PW], vv[PW];
 #pragma unroll
@@ -477,14 +486,24 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     float m = -INFINITY, l = 0.f, o = 0.f;
 #pragma unroll
     for (int i = 0; i < PW; i++) {
-        const float sc = wave_sum(fmaf(q0, k0[i], q1 * k1[i])) * sc2;
+        const bool cur = has_cur && j0 + wave + 4 * i == pos0;   // wave-uniform
+        const float kk0 = cur ? kc0 : k0[i], kk1 = cur ? kc1 : k1[i], vx = cur ? vc : vv[i];
+        const float sc = wave_sum(fmaf(q0, kk0, q1 * kk1)) * sc2;
         if (wave + 4 * i < ncv) {
             const float mn = fmaxf(m, sc);
             const float al = __builtin_amdgcn_exp2f(m - mn), pe = __builtin_amdgcn_exp2f(sc - mn);
             l = fmaf(l, al, pe);
-            o = fmaf(o, al, pe * vv[i]);
+            o = fmaf(o, al, pe * vx);
             m = mn;
         }
+    }
+    // append at pos0 by the KV head's first query head (no workgroup of
+    // this launch reads that row)
+    if (has_cur && h % rep == 0 && wave == 0) {
+        float* kd = a.ck + ((int64_t)pos0 * a.Hkv + kvh) * dq;
+        gst(kd + lane, kc0);
+        if (lane + 64 < dq) gst(kd + lane + 64, kc1);
+        gst(a.cv + ((int64_t)pos0 * a.Hkv + kvh) * a.dv + lane, vc);
     }
     s_o[wave][lane] = o;
     if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
@@ -705,8 +724,9 @@ extern "C" int rina_hip_gqa_decode_attention(const float* q, const float* k, con
 
 extern "C" size_t rina_hip_dq_attention_workspace(int H, int dq, int max_pos) {
     if (H < 1 || dq < 1 || max_pos < 1) return 0;
+    (void)dq;
     const size_t nch = ((size_t)max_pos + kDqChunk - 1) / kDqChunk;
-    return ((size_t)H * dq + nch * H * (2 + 64)) * sizeof(float);
+    return nch * H * (2 + 64) * sizeof(float);
 }
 
 extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, const float* ka, const float* kb,
@@ -729,18 +749,16 @@ extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, co
     DqArgs a{};
     a.qa = qa; a.qb = qb; a.ka = ka; a.kb = kb; a.v = v;
     a.qc = rope_q_cos; a.qs = rope_q_sin; a.kc = rope_k_cos; a.ks = rope_k_sin;
-    a.ck = cache_k; a.cv = cache_v; a.wq = (float*)workspace;
+    a.ck = cache_k; a.cv = cache_v;
     a.H = H; a.Hkv = Hkv; a.da = da; a.db = db; a.dv = dv;
     a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos;
     a.scale = 1.0f / sqrtf((float)(da + db));
     SplitArgs p{};
-    p.ws_m = a.wq + (size_t)H * (da + db);
+    p.ws_m = (float*)workspace;
     p.ws_l = p.ws_m + (size_t)nch * H;
     p.ws_o = p.ws_l + (size_t)nch * H;
     p.out = out; p.H = H; p.start_pos = start_pos; p.max_seq = max_seq; p.d_pos = d_pos; p.chunk = kDqChunk;
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(dq_append_kernel, dim3(H + Hkv), dim3(64), 0, st, a);
-    RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(dq_split_kernel, dim3(nch, H), dim3(256), 0, st, a, p);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(attn_combine_kernel, dim3(H), dim3(256), 0, st, p);

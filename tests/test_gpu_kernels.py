@@ -378,7 +378,8 @@ def test_attention_other_shapes(rina, orc, H, Hkv, dh):
 
 @pytest.mark.parametrize("mode", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("P,H,Hkv,use_dpos", [(0, 32, 8, False), (37, 32, 8, False), (543, 32, 8, True),
-                                              (1500, 32, 8, False), (70, 10, 5, False), (16, 8, 8, True)])
+                                              (1500, 32, 8, False), (70, 10, 5, False), (16, 8, 8, True),
+                                              (300, 32, 4, True), (1500, 32, 4, False)])
 def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
     """RoPE + K/V append + attention in one call == rope_append then attention
     (oracle): the rotated K row and the appended cache bytes bit-exact, the
@@ -434,6 +435,44 @@ def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
         want_v = vc.copy(); want_v[P] = v
         assert np.array_equal(gk, orc.kv_quantize(kf, want_k))
         assert np.array_equal(gv, orc.kv_quantize(vf, want_v))
+
+
+def test_decode_attention_sequence(rina, orc):
+    """40 consecutive decode calls at a device position (the decode loop):
+    every output against the oracle over the cache as it grows, so each call
+    starts from the completion counters the previous call left."""
+    hip = rina.load_hip()
+    L = orc.load()
+    H, Hkv, dh, max_seq, P0, n = 32, 8, 64, 600, 500, 40
+    kvd = Hkv * dh
+    r = rng(4242)
+    kc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    vc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    cos, sin = rope_tables(dh, max_seq)
+    ws_bytes = hip.rina_hip_gqa_attention_workspace(1, H, dh, max_seq)
+    ws = empty(ws_bytes, "uint8")
+    ckd, cvd = dev(kc), dev(vc)
+    cd, sd = dev(cos), dev(sin)
+    od = empty(H * dh)
+    pos = dev(np.array([P0], np.int32))
+    for i in range(n):
+        P = P0 + i
+        q = r.standard_normal(H * dh).astype(np.float32)
+        k = r.standard_normal(kvd).astype(np.float32)
+        v = r.standard_normal(kvd).astype(np.float32)
+        pos.copy_(dev(np.array([P], np.int32)))
+        ok(hip.rina_hip_gqa_decode_attention(dev(q).data_ptr(), dev(k).data_ptr(), dev(v).data_ptr(), cd.data_ptr(),
+                                             sd.data_ptr(), cd.data_ptr(), sd.data_ptr(), ckd.data_ptr(),
+                                             cvd.data_ptr(), 0, H, Hkv, dh, 0, pos.data_ptr(), max_seq,
+                                             od.data_ptr(), None, ws.data_ptr(), ws_bytes, stream()), "decode")
+        qr, kr = q.copy(), k.copy()
+        L.orc_rope_neox(qr.ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, H, dh, P)
+        L.orc_rope_neox(kr.ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, Hkv, dh, P)
+        ref = np.zeros(H * dh, np.float32)
+        L.orc_gqa_attention(qr.ctypes.data, kr.ctypes.data, v.ctypes.data, kc.ctypes.data, vc.ctypes.data, None,
+                            None, 0, 0, None, None, 1, P, H, Hkv, dh, ref.ctypes.data)
+        assert_close(host(od), ref, what="decode call %d (P %d)" % (i, P))
+        kc[P], vc[P] = kr, v
 
 
 @pytest.mark.parametrize("mode", [0, 2])
