@@ -24,6 +24,16 @@ typedef struct rina_infer rina_infer;   /* Inference */
 rina_model* rina_model_create(const char* config_json);
 void rina_model_destroy(rina_model* m);
 
+/* load_model (rina-engine/src/loader.cpp:149-152): a .rinn file, or a
+ * directory holding weights.rinn (512-byte header, JSON config, tensor
+ * index, data; tools/convert_llama_to_rinn.py:97-123 writes it).  Every
+ * tensor is uploaded to device memory the model owns (freed by
+ * rina_model_destroy).  FP32, Q4_0 and Q4_0F tensors, as the reference's
+ * reader; NULL on a missing file, a bad magic, a truncated file or another
+ * quant type (the reference prints and leaves that tensor empty), with the
+ * reason in rina_engine_last_error and nothing left allocated. */
+rina_model* rina_model_load(const char* path);
+
 /* Register one tensor under its reference name (e.g.
  * "transformer.h.0.attn.w_q.weight").  data: device pointer to the packed
  * tensor in `quant_type` (core/quant.h ids); shape [ndim] with the row

@@ -81,6 +81,7 @@ _HIP_SIGS = {
 _ENG_SIGS = {
     "rina_model_create": (VP, [C.c_char_p]),
     "rina_model_destroy": (None, [VP]),
+    "rina_model_load": (VP, [C.c_char_p]),
     "rina_model_add_tensor": (I32, [VP, C.c_char_p, I32, I32, C.POINTER(I64), VP]),
     "rina_infer_create": (VP, [VP, C.c_char_p, C.c_char_p, I32]),
     "rina_infer_destroy": (None, [VP]),

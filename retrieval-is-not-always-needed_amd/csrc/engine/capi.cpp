@@ -3,6 +3,7 @@
 #include <memory>
 #include <string>
 #include "core/config.h"
+#include "core/loader.h"
 #include "core/tensor.h"
 #include "infer/infer_base.h"
 #include "rina_engine.h"
@@ -30,6 +31,18 @@ extern "C" rina_model* rina_model_create(const char* json) {
     auto* m = new rina_model();
     std::string err;
     if (!parse_config(json, m->cfg, &err)) {
+        g_err = err;
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+extern "C" rina_model* rina_model_load(const char* path) {
+    if (!path) { g_err = "rina_model_load: null path"; return nullptr; }
+    auto* m = new rina_model();
+    std::string err;
+    if (!load_rinn(path, m->cfg, m->tensors, &err)) {
         g_err = err;
         delete m;
         return nullptr;

@@ -81,6 +81,42 @@ def pack_on_device(x_host, qt, stream=None):
     return out
 
 
+def write_rinn(path, config, tensors):
+    """Write a .rinn file in the layout of tools/convert_llama_to_rinn.py:97-123
+    (read by loader.cpp:14-141): a 512-byte header ("RINN", version 1, the
+    tensor count, config / index / data offsets), the config as JSON, the
+    tensor index (u16 name length, name, 4 x i32 shape padded with zeros,
+    u8 quant type, u16 block size (32 for Q4 types, 1 for fp32), u64 offset,
+    u64 size), then the tensor bytes from the first 256-byte boundary after
+    the index, back to back.  tensors: (name, shape, quant_type, bytes-like)
+    in file order."""
+    import struct
+    cj = json.dumps(config).encode("utf-8")
+    entries = []
+    for name, shape, qt, data in tensors:
+        nb = name.encode()
+        b = bytes(memoryview(np.ascontiguousarray(data)).cast("B"))
+        shp = list(shape) + [0] * (4 - len(shape))
+        entries.append((nb, shp, int(qt), 32 if qt in (QT_Q4_0, QT_Q4_0F) else 1, b))
+    idx_sz = sum(2 + len(nb) + 16 + 1 + 2 + 8 + 8 for nb, _, _, _, _ in entries)
+    data_off = ((512 + len(cj) + idx_sz + 255) // 256) * 256
+    hdr = bytearray(512)
+    hdr[0:4] = b"RINN"
+    struct.pack_into("<I", hdr, 4, 1)
+    struct.pack_into("<I", hdr, 8, len(entries))
+    struct.pack_into("<QQQQQ", hdr, 16, 512, len(cj), 512 + len(cj), idx_sz, data_off)
+    with open(path, "wb") as f:
+        f.write(hdr)
+        f.write(cj)
+        off = data_off
+        for nb, shp, qt, bs, b in entries:
+            f.write(struct.pack("<H", len(nb)) + nb + struct.pack("<4i", *shp) + struct.pack("<BHQQ", qt, bs, off, len(b)))
+            off += len(b)
+        f.write(b"\x00" * (data_off - f.tell()))
+        for _, _, _, _, b in entries:
+            f.write(b)
+
+
 class SynthLlama:
     """A Llama-shaped GQA model with random weights, built on the device.
 
@@ -96,6 +132,7 @@ class SynthLlama:
         self.arena = DeviceArena()
         self.host = {}
         self.dev = {}
+        self.shapes, self.qts, self.order = {}, {}, []
         eng = load_engine()
         c = self.cfg
         d, H, Hkv, dh, hd, V, L = (c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["hidden_dim"],
@@ -115,6 +152,8 @@ class SynthLlama:
                   "add_tensor " + name)
             self.arena.put(data_dev)
             self.dev[name] = data_dev
+            self.shapes[name], self.qts[name] = tuple(shape), qt_
+            self.order.append(name)
             if keep_host:
                 self.host[name] = host if host is not None else data_dev.cpu().numpy()
 
@@ -145,6 +184,22 @@ class SynthLlama:
                 add(p + nm, (max_seq, dh // 2), QT_FP32, t, h)
         add("transformer.ln_f.weight", (d,), QT_FP32, torch.from_numpy(ones.copy()).cuda(), ones)
         self.cos, self.sin = cos, sin
+
+    def save_rinn(self, path):
+        """The model as a .rinn file (write_rinn; needs keep_host=True), with
+        the converter's config keys (convert_llama_to_rinn.py:46-53) plus
+        hidden_dim and the KV mode."""
+        if not self.host:
+            raise RuntimeError("save_rinn needs a model built with keep_host=True")
+        c = self.cfg
+        L = c["n_layers"]
+        config = {"name": c["name"], "dim": c["dim"], "n_layers": L, "n_heads": c["n_heads"],
+                  "n_kv_heads": c["n_kv_heads"], "head_dim": c["head_dim"], "d_c": 0, "d_h_r": c["head_dim"],
+                  "vocab_size": c["vocab_size"], "block_size": self.max_seq, "ssm_steps": 0, "weight_tying": True,
+                  "quant_mode": "", "ssm_qbits": 0, "hidden_dim": c["hidden_dim"], "kv_quant_mode": self.kv_mode,
+                  "layers": [{"type": "standard_attention"} for _ in range(L)]}
+        tensors = [(n, self.shapes[n], self.qts[n], self.host[n]) for n in self.order]
+        write_rinn(path, config, tensors)
 
     def weight_bytes_per_token(self):
         c = self.cfg
