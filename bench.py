@@ -230,6 +230,22 @@ def main():
     log("decode: %d steps, %.3f ms/step (device %.3f ms/step), %.1f tok/s" %
         (args.steps, wall * 1e3 / args.steps, ms.value / args.steps, tok_s))
     tokens = list(first) + list(out)
+    # prompt phase of the same model (context only; not the metric): the
+    # 512-token prefill with the last row's logits and its argmax, timed on
+    # its second run (the first sizes the activation buffers)
+    pre_ms = []
+    one = (C.c_int * 1)()
+    for _ in range(2):
+        torch.cuda.synchronize()
+        t_p = time.perf_counter()
+        rina.check(eng.rina_infer_generate(inf, prompt.ctypes.data_as(C.POINTER(C.c_int)), args.prompt, 1, one, 0,
+                                           st, None), "prefill")
+        torch.cuda.synchronize()
+        pre_ms.append((time.perf_counter() - t_p) * 1e3)
+    prefill = {"prompt": args.prompt, "ms": round(pre_ms[-1], 3),
+               "tokens_per_s": round(args.prompt / (pre_ms[-1] / 1e3), 1),
+               "note": "Q4 linears on v_mfma_f32_16x16x4f32 (fp32 products, fp32 sums)"}
+    log("prefill: %d tokens in %.2f ms (%.0f tok/s)" % (args.prompt, pre_ms[-1], prefill["tokens_per_s"]))
     eng.rina_infer_destroy(inf)
 
     # ---- dominant kernel: fp32 tied LM head GEMV (128256 x 2048), HIP events on our stream
@@ -425,6 +441,7 @@ def main():
         },
         "decode_hbm_gbps": round(per_token * tok_s / 1e9, 1),
         "decode_hbm_frac": round(per_token * tok_s / HBM_PEAK, 4),
+        "prefill_config2": prefill,
         "config3_ctx4096_quant_kv": cfg3,
         "config4_deepseek_mla_moe": cfg4,
         "config5_rina_jamba": cfg5,

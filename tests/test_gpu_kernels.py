@@ -584,3 +584,31 @@ def test_linear_norm_prologue(rina, orc, qt, pro, M, K):
     xn = x.copy()
     (L.orc_rms_norm if pro == 1 else L.orc_layer_norm)(xn.ctypes.data, nw.ctypes.data, M, K, np.float32(1e-5))
     assert_close(host(y).reshape(M, N), orc.linear(w, qt, xn, N, K), what="prologue %d qt %d" % (pro, qt))
+
+
+@pytest.mark.parametrize("qt", [5, 7])
+@pytest.mark.parametrize("M,N,K", [(16, 64, 32), (100, 200, 512), (64, 2048, 2048), (130, 77, 320), (512, 96, 1024)])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_linear_prefill_mfma(rina, orc, qt, M, N, K, epi):
+    """Prompt-sized M on the matrix-core path: store, residual add and
+    SiLU*up epilogues against the oracle's per-row matvec (fp32 products of
+    the dequantized weights, fp32 sums)."""
+    hip = rina.load_hip()
+    r = rng(M * 7 + N + K + qt * 3 + epi)
+    w = orc.pack(qt, (r.standard_normal(N * K) * 0.02).astype(np.float32))
+    w3 = orc.pack(qt, (r.standard_normal(N * K) * 0.02).astype(np.float32))
+    x = r.standard_normal((M, K)).astype(np.float32)
+    y0 = r.standard_normal((M, N)).astype(np.float32)
+    y = dev(y0)
+    seg = rina.LinearSeg(dev(w).data_ptr(), dev(w3).data_ptr() if epi == 2 else None, y.data_ptr(), N)
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, dev(x).data_ptr(), M, K, epi, 0, None, 0.0, stream()),
+       "prefill")
+    g = orc.linear(w, qt, x, N, K).astype(np.float64)
+    if epi == 0:
+        ref = g
+    elif epi == 1:
+        ref = y0.astype(np.float64) + g
+    else:
+        u = orc.linear(w3, qt, x, N, K).astype(np.float64)
+        ref = g / (1.0 + np.exp(-g)) * u
+    assert_close(host(y).reshape(M, N), ref, what="prefill q%d epi %d %s" % (qt, epi, (M, N, K)))
