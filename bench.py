@@ -244,7 +244,8 @@ def main():
         pre_ms.append((time.perf_counter() - t_p) * 1e3)
     prefill = {"prompt": args.prompt, "ms": round(pre_ms[-1], 3),
                "tokens_per_s": round(args.prompt / (pre_ms[-1] / 1e3), 1),
-               "note": "Q4 linears on v_mfma_f32_16x16x4f32 (fp32 products, fp32 sums)"}
+               "note": "Q4 linears on v_mfma_f32_16x16x4f32 (fp32 products, fp32 sums); prompt attention "
+                       "from position 0 in 64-position blocks (one softmax rescale per block)"}
     log("prefill: %d tokens in %.2f ms (%.0f tok/s)" % (args.prompt, pre_ms[-1], prefill["tokens_per_s"]))
     eng.rina_infer_destroy(inf)
 

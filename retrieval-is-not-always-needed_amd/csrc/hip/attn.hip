@@ -537,6 +537,89 @@ __device__ __forceinline__ float cache_val(int fmt, const uint8_t* c, int64_t id
     return kvq::dequant_one(fmt, c + (idx >> 5) * kvq::block_bytes(fmt), (int)(idx & 31));
 }
 
+// Prompt attention from position 0 (every key and value is a current row,
+// dh == 64): one wave per (query head, 16 query rows).  Keys and values
+// come in blocks of 64 positions: lane j holds key j of the block (64
+// floats) and lane d holds dim d of the block's 64 values, so a query's 64
+// scores are one FMA chain per lane (the query from LDS, broadcast) and its
+// output update is one FMA chain per lane (the weights from LDS, broadcast).
+// Softmax per block in base-2 units (scale and log2 e folded into the
+// query): one maximum and one rescale per query and block.  Causal: query
+// row t sees positions 0..t.
+constexpr int kPromptRows = 16;
+
+__global__ __launch_bounds__(64) void attn_prompt_kernel(AttnArgs a) {
+    constexpr int DH = 64;
+    __shared__ __align__(16) float s_q[kPromptRows][DH];
+    __shared__ __align__(16) float s_o[kPromptRows][DH];
+    __shared__ float s_m[kPromptRows], s_l[kPromptRows];
+    __shared__ __align__(16) float s_p[DH];
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int t0 = blockIdx.y * kPromptRows;
+    const int nq = min(kPromptRows, a.T - t0);
+    const int kvd = a.Hkv * DH, kvh = h / (a.H / a.Hkv);
+    const float qsc = a.scale * 1.44269504088896341f;
+    for (int i = 0; i < nq; i++) {
+        s_q[i][lane] = a.q[((int64_t)(t0 + i) * a.H + h) * DH + lane] * qsc;
+        s_o[i][lane] = 0.f;
+    }
+    if (lane < kPromptRows) {
+        s_m[lane] = -INFINITY;
+        s_l[lane] = 0.f;
+    }
+    const int tmax = t0 + nq - 1;
+    for (int j0 = 0; j0 <= tmax; j0 += 64) {
+        // key j0 + lane (clamped past tmax: masked below) and value dim lane
+        const int jk = min(j0 + lane, tmax);
+        const f32x4* kp = (const f32x4*)(a.kcur + (int64_t)jk * kvd + kvh * DH);
+        float kr[DH];
+#pragma unroll
+        for (int i = 0; i < DH / 4; i++) {
+            const f32x4 v = gld(kp + i);
+            kr[4 * i] = v.x; kr[4 * i + 1] = v.y; kr[4 * i + 2] = v.z; kr[4 * i + 3] = v.w;
+        }
+        float vr[64];
+#pragma unroll
+        for (int j = 0; j < 64; j++) vr[j] = gld(a.vcur + (int64_t)min(j0 + j, tmax) * kvd + kvh * DH + lane);
+        const int i0 = j0 > t0 ? j0 - t0 : 0;                  // rows before j0 see nothing of this block
+#pragma unroll 1
+        for (int i = i0; i < nq; i++) {
+            const int t = t0 + i;
+            float sc = 0.f;
+#pragma unroll
+            for (int d = 0; d < DH; d += 4) {
+                const f32x4 qv = *(const f32x4*)&s_q[i][d];
+                sc = fmaf(qv.x, kr[d], sc);
+                sc = fmaf(qv.y, kr[d + 1], sc);
+                sc = fmaf(qv.z, kr[d + 2], sc);
+                sc = fmaf(qv.w, kr[d + 3], sc);
+            }
+            if (j0 + lane > t) sc = -INFINITY;
+            const float mo = s_m[i];
+            const float mn = fmaxf(mo, wave_max(sc));           // finite: position j0 <= t is in the block
+            const float al = __builtin_amdgcn_exp2f(mo - mn);
+            const float p = __builtin_amdgcn_exp2f(sc - mn);
+            const float ls = wave_sum(p);
+            s_p[lane] = p;
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < 64; j += 4) {
+                const f32x4 pv = *(const f32x4*)&s_p[j];
+                acc = fmaf(pv.x, vr[j], acc);
+                acc = fmaf(pv.y, vr[j + 1], acc);
+                acc = fmaf(pv.z, vr[j + 2], acc);
+                acc = fmaf(pv.w, vr[j + 3], acc);
+            }
+            s_o[i][lane] = fmaf(s_o[i][lane], al, acc);
+            if (lane == 0) {
+                s_m[i] = mn;
+                s_l[i] = fmaf(s_l[i], al, ls);
+            }
+        }
+    }
+    for (int i = 0; i < nq; i++) a.out[((int64_t)(t0 + i) * a.H + h) * DH + lane] = s_o[i][lane] / s_l[i];
+}
+
 __global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs a, int kf, int vf) {
     const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
@@ -691,6 +774,12 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
     a.mode = mode; a.pre_rope = pre_rope; a.T = T; a.H = H; a.Hkv = Hkv; a.dh = dh;
     a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos;
     a.scale = 1.0f / sqrtf((float)dh);
+    // a prompt from position 0 reads only the current rows
+    if (T > 1 && !d_pos && start_pos == 0 && dh == 64 && ((uintptr_t)kcur % 16 == 0)) {
+        hipLaunchKernelGGL(attn_prompt_kernel, dim3(H, (T + kPromptRows - 1) / kPromptRows), dim3(64), 0, st, a);
+        RINA_LAUNCH_CHECK();
+        return RINA_OK;
+    }
     hipLaunchKernelGGL(attn_generic_kernel, dim3(H, T), dim3(64), 0, st, a, kf, vf);
     RINA_LAUNCH_CHECK();
     return RINA_OK;

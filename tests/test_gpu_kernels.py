@@ -370,6 +370,14 @@ def test_attention_multi_row(rina, orc, mode, P, T):
     assert_close(got, ref, what="rows mode %d P %d T %d" % (mode, P, T))
 
 
+@pytest.mark.parametrize("T,H,Hkv", [(100, 32, 8), (300, 32, 8), (129, 10, 5), (64, 8, 8)])
+def test_attention_prompt_from_zero(rina, orc, T, H, Hkv):
+    """Prompt rows from position 0 (the block-softmax prompt kernel): several
+    64-position blocks, ragged row groups, causal against the oracle."""
+    got, ref = attention_case(rina, orc, 0, 0, T, H=H, Hkv=Hkv)
+    assert_close(got, ref, what="prompt T %d H %d/%d" % (T, H, Hkv))
+
+
 @pytest.mark.parametrize("H,Hkv,dh", [(10, 5, 64), (16, 16, 128), (4, 2, 32)])
 def test_attention_other_shapes(rina, orc, H, Hkv, dh):
     got, ref = attention_case(rina, orc, 0, 20, 1, H=H, Hkv=Hkv, dh=dh)
