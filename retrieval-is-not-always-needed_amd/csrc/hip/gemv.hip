@@ -954,13 +954,15 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs a) {
 
 // ---------------------------------------------------------------------------
 // M >= 16 with Q4 weights on the matrix cores (prompt phase):
-// v_mfma_f32_16x16x4f32 over 64 x 64 output tiles, K stepped by one 32-value
-// block.  The x tile and the dequantized weight tile ((q - 7) * scale, the
+// v_mfma_f32_16x16x4f32 over BM x 64 output tiles (BM 64, or 32 when 64-row
+// tiles would leave fewer than two workgroups per CU), K stepped by one
+// 32-value block.  The x tile and the dequantized weight tile ((q - 7) * scale, the
 // reference dequant's per-element value) sit in LDS as fp32, K-major with a
 // row stride of 80 floats (a 64-lane fragment read touches every bank
 // twice), so each product is the reference's fp32 product and the matrix
 // cores accumulate in fp32 (the sums in another order).  Wave w owns the
-// 32 x 32 quarter (w / 2, w % 2) as 2 x 2 MFMA tiles per matrix; the next
+// (BM / 2) x 32 quarter (w / 2, w % 2) as (BM / 32) x 2 MFMA tiles per
+// matrix; the next
 // block's x values and weight bytes are loaded into registers while the
 // current block is multiplied.
 // MFMA operand layout (16x16x4 f32): lane l supplies A[l % 16][l / 16] and
@@ -970,19 +972,20 @@ typedef float f32x4m __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaLd = 80;
 
-template <int FMT, int NMAT>
+template <int FMT, int NMAT, int BM>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
     constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
+    constexpr int MI = BM / 32;                    // MFMA tiles per wave along M
     __shared__ float xs[32][kMfmaLd];
     __shared__ float ws[NMAT][32][kMfmaLd];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * 64;
     const int nb = a.K / 32;
-    // staging: thread t takes row t / 4 of the x tile and of each weight
-    // tile, values 8 (t % 4) .. 8 (t % 4) + 7 of the block
+    // staging: thread t takes row t / 4 of the x tile (rows < BM) and of
+    // each weight tile, values 8 (t % 4) .. 8 (t % 4) + 7 of the block
     const int sr = tid >> 2, sq = tid & 3;
-    const bool xok = m0 + sr < a.M, wok = n0 + sr < a.N;
+    const bool xok = sr < BM && m0 + sr < a.M, wok = n0 + sr < a.N;
     const float* xrow = a.x + (int64_t)(xok ? m0 + sr : 0) * a.K + 8 * sq;
     const int64_t wrow = (int64_t)(wok ? n0 + sr : 0) * nb * BB;
     f32x4 xr0, xr1;
@@ -1007,8 +1010,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
     // value 8 sq + t of the block is nibble t of wnb (byte t / 2, low nibble for even t)
     auto store_blk = [&]() {
         const float xv[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
+        if (sr < BM) {
 #pragma unroll
-        for (int t = 0; t < 8; t++) xs[8 * sq + t][sr] = xok ? xv[t] : 0.f;
+            for (int t = 0; t < 8; t++) xs[8 * sq + t][sr] = xok ? xv[t] : 0.f;
+        }
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             const float sc = FMT == FMT_Q4_0F ? __uint_as_float(wsc[m]) : f16_to_f32((uint16_t)wsc[m]);
@@ -1017,13 +1022,13 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
                 ws[m][8 * sq + t][sr] = wok ? (float)((int)((wnb[m] >> (4 * t)) & 0xF) - 7) * sc : 0.f;
         }
     };
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int wm = (wave >> 1) * 16 * MI, wn = (wave & 1) * 32;
     const int fr = lane & 15, fk = lane >> 4;
-    f32x4m acc[NMAT][2][2];
+    f32x4m acc[NMAT][MI][2];
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < MI; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++) acc[m][i][j] = f32x4m{0.f, 0.f, 0.f, 0.f};
     load_blk(0);
@@ -1035,19 +1040,22 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             const int k = 4 * kk + fk;
-            const float a0 = xs[k][wm + fr], a1 = xs[k][wm + 16 + fr];
+            float av[MI];
+#pragma unroll
+            for (int i = 0; i < MI; i++) av[i] = xs[k][wm + 16 * i + fr];
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
                 const float b0 = ws[m][k][wn + fr], b1 = ws[m][k][wn + 16 + fr];
-                acc[m][0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[m][0][0], 0, 0, 0);
-                acc[m][0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[m][0][1], 0, 0, 0);
-                acc[m][1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[m][1][0], 0, 0, 0);
-                acc[m][1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[m][1][1], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < MI; i++) {
+                    acc[m][i][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], b0, acc[m][i][0], 0, 0, 0);
+                    acc[m][i][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], b1, acc[m][i][1], 0, 0, 0);
+                }
             }
         }
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -1329,15 +1337,21 @@ int gemm_tiled(const rina_linear_seg& seg, int qt, const float* x, int M, int K,
     // matrix cores for prompt-sized M and Q4 weights (K % 32 == 0, x rows
     // 16-byte aligned; weight rows are 4-byte aligned for Q4_0F)
     if (M >= 16 && (qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && K % 32 == 0 && (uintptr_t)x % 16 == 0) {
-        const dim3 g((seg.N + 63) / 64, (M + 63) / 64);
         const bool two = epi == RINA_EPI_SWIGLU;
+        const int64_t t64 = (int64_t)((seg.N + 63) / 64) * ((M + 63) / 64);
+        const bool half = t64 < 2LL * rina_num_cus();        // 32-row tiles: more workgroups in flight
+        const dim3 g((seg.N + 63) / 64, half ? (M + 31) / 32 : (M + 63) / 64);
+#define MFMA_LAUNCH(F, NM) \
+    do { if (half) hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 32>), g, dim3(256), 0, st, a); \
+         else hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 64>), g, dim3(256), 0, st, a); } while (0)
         if (qt == RINA_QT_Q4_0F) {
-            if (two) hipLaunchKernelGGL((gemm_mfma_kernel<FMT_Q4_0F, 2>), g, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((gemm_mfma_kernel<FMT_Q4_0F, 1>), g, dim3(256), 0, st, a);
+            if (two) MFMA_LAUNCH(FMT_Q4_0F, 2);
+            else MFMA_LAUNCH(FMT_Q4_0F, 1);
         } else {
-            if (two) hipLaunchKernelGGL((gemm_mfma_kernel<FMT_Q4_0, 2>), g, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((gemm_mfma_kernel<FMT_Q4_0, 1>), g, dim3(256), 0, st, a);
+            if (two) MFMA_LAUNCH(FMT_Q4_0, 2);
+            else MFMA_LAUNCH(FMT_Q4_0, 1);
         }
+#undef MFMA_LAUNCH
         return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
     }
     dim3 grid((seg.N + 63) / 64, (M + 31) / 32);

@@ -595,7 +595,8 @@ def test_linear_norm_prologue(rina, orc, qt, pro, M, K):
 
 
 @pytest.mark.parametrize("qt", [5, 7])
-@pytest.mark.parametrize("M,N,K", [(16, 64, 32), (100, 200, 512), (64, 2048, 2048), (130, 77, 320), (512, 96, 1024)])
+@pytest.mark.parametrize("M,N,K", [(16, 64, 32), (100, 200, 512), (64, 2048, 2048), (130, 77, 320), (512, 96, 1024),
+                                   (520, 4096, 64)])   # the last one takes 64-row tiles, the others 32-row tiles
 @pytest.mark.parametrize("epi", [0, 1, 2])
 def test_linear_prefill_mfma(rina, orc, qt, M, N, K, epi):
     """Prompt-sized M on the matrix-core path: store, residual add and
