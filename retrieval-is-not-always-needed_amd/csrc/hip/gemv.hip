@@ -972,15 +972,34 @@ typedef float f32x4m __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaLd = 80;
 
+// Up to 3 weight segments sharing x (q / k / v) in one launch: column
+// tiles t0[s] .. of segment s, in order.
+struct MfmaArgs {
+    GemmArgs g;                  // g.w / g.w2 / g.y / g.N: segment 0
+    const uint8_t* w[3];
+    float* y[3];
+    int N[3];
+    int t0[3];
+    int nseg;
+};
+
 template <int FMT, int NMAT, int BM>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(MfmaArgs ma) {
     constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
     constexpr int MI = BM / 32;                    // MFMA tiles per wave along M
     __shared__ float xs[32][kMfmaLd];
     __shared__ float ws[NMAT][32][kMfmaLd];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * 64;
+    // this workgroup's segment (wave-uniform selects, no indexed argument reads)
+    GemmArgs a = ma.g;
+    const int bx = blockIdx.x;
+    const int sg = (ma.nseg > 1 && bx >= ma.t0[1]) + (ma.nseg > 2 && bx >= ma.t0[2]);
+    a.w = sg == 0 ? ma.w[0] : sg == 1 ? ma.w[1] : ma.w[2];
+    a.y = sg == 0 ? ma.y[0] : sg == 1 ? ma.y[1] : ma.y[2];
+    a.N = sg == 0 ? ma.N[0] : sg == 1 ? ma.N[1] : ma.N[2];
+    const int tb = sg == 0 ? ma.t0[0] : sg == 1 ? ma.t0[1] : ma.t0[2];
+    const int m0 = blockIdx.y * BM, n0 = (bx - tb) * 64;
     const int nb = a.K / 32;
     // staging: thread t takes row t / 4 of the x tile (rows < BM) and of
     // each weight tile, values 8 (t % 4) .. 8 (t % 4) + 7 of the block
@@ -1331,29 +1350,49 @@ int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int e
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 
+bool mfma_ok(int qt, const float* x, int M, int K) {
+    return M >= 16 && (qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && K % 32 == 0 && (uintptr_t)x % 16 == 0;
+}
+
+// Matrix-core prompt matmul over up to 3 segments sharing x (one launch).
+int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int M, int K, int epi, hipStream_t st) {
+    MfmaArgs ma{};
+    ma.g = GemmArgs{(const uint8_t*)segs[0].weight, epi == RINA_EPI_SWIGLU ? (const uint8_t*)segs[0].weight2 : nullptr,
+                    x, segs[0].out, M, segs[0].N, K, qt, epi};
+    ma.nseg = nseg;
+    int tiles = 0;
+    for (int s = 0; s < 3; s++) {
+        const int ss = s < nseg ? s : 0;
+        ma.w[s] = (const uint8_t*)segs[ss].weight;
+        ma.y[s] = segs[ss].out;
+        ma.N[s] = segs[ss].N;
+        ma.t0[s] = s < nseg ? tiles : 1 << 30;
+        if (s < nseg) tiles += (segs[s].N + 63) / 64;
+    }
+    const bool two = epi == RINA_EPI_SWIGLU;
+    const int64_t t64 = (int64_t)tiles * ((M + 63) / 64);
+    const bool half = t64 < 2LL * rina_num_cus();        // 32-row tiles: more workgroups in flight
+    const dim3 g(tiles, half ? (M + 31) / 32 : (M + 63) / 64);
+#define MFMA_LAUNCH(F, NM) \
+    do { if (half) hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 32>), g, dim3(256), 0, st, ma); \
+         else hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 64>), g, dim3(256), 0, st, ma); } while (0)
+    if (qt == RINA_QT_Q4_0F) {
+        if (two) MFMA_LAUNCH(FMT_Q4_0F, 2);
+        else MFMA_LAUNCH(FMT_Q4_0F, 1);
+    } else {
+        if (two) MFMA_LAUNCH(FMT_Q4_0, 2);
+        else MFMA_LAUNCH(FMT_Q4_0, 1);
+    }
+#undef MFMA_LAUNCH
+    return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
+}
+
 int gemm_tiled(const rina_linear_seg& seg, int qt, const float* x, int M, int K, int epi, hipStream_t st) {
-    GemmArgs a{(const uint8_t*)seg.weight, epi == RINA_EPI_SWIGLU ? (const uint8_t*)seg.weight2 : nullptr,
-               x, seg.out, M, seg.N, K, qt, epi};
     // matrix cores for prompt-sized M and Q4 weights (K % 32 == 0, x rows
     // 16-byte aligned; weight rows are 4-byte aligned for Q4_0F)
-    if (M >= 16 && (qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && K % 32 == 0 && (uintptr_t)x % 16 == 0) {
-        const bool two = epi == RINA_EPI_SWIGLU;
-        const int64_t t64 = (int64_t)((seg.N + 63) / 64) * ((M + 63) / 64);
-        const bool half = t64 < 2LL * rina_num_cus();        // 32-row tiles: more workgroups in flight
-        const dim3 g((seg.N + 63) / 64, half ? (M + 31) / 32 : (M + 63) / 64);
-#define MFMA_LAUNCH(F, NM) \
-    do { if (half) hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 32>), g, dim3(256), 0, st, a); \
-         else hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 64>), g, dim3(256), 0, st, a); } while (0)
-        if (qt == RINA_QT_Q4_0F) {
-            if (two) MFMA_LAUNCH(FMT_Q4_0F, 2);
-            else MFMA_LAUNCH(FMT_Q4_0F, 1);
-        } else {
-            if (two) MFMA_LAUNCH(FMT_Q4_0, 2);
-            else MFMA_LAUNCH(FMT_Q4_0, 1);
-        }
-#undef MFMA_LAUNCH
-        return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
-    }
+    if (mfma_ok(qt, x, M, K)) return gemm_mfma(&seg, 1, qt, x, M, K, epi, st);
+    GemmArgs a{(const uint8_t*)seg.weight, epi == RINA_EPI_SWIGLU ? (const uint8_t*)seg.weight2 : nullptr,
+               x, seg.out, M, seg.N, K, qt, epi};
     dim3 grid((seg.N + 63) / 64, (M + 31) / 32);
     hipLaunchKernelGGL(gemm_tile_kernel, grid, dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
@@ -1412,6 +1451,7 @@ extern "C" int rina_hip_linear_fused_ex(const rina_linear_seg* segs, int nseg, i
         return RINA_OK;
     }
     if (M > 1) {
+        if (mfma_ok(qt, input, M, K)) return gemm_mfma(segs, nseg, qt, input, M, K, epi, st);   // nseg <= 3 here
         for (int s = 0; s < nseg; s++) {
             int rc = gemm_tiled(segs[s], qt, input, M, K, epi, st);
             if (rc) return rc;

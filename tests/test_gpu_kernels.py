@@ -621,3 +621,24 @@ def test_linear_prefill_mfma(rina, orc, qt, M, N, K, epi):
         u = orc.linear(w3, qt, x, N, K).astype(np.float64)
         ref = g / (1.0 + np.exp(-g)) * u
     assert_close(host(y).reshape(M, N), ref, what="prefill q%d epi %d %s" % (qt, epi, (M, N, K)))
+
+
+@pytest.mark.parametrize("qt", [5, 7])
+@pytest.mark.parametrize("Ns,epi", [((256, 64, 64), 0), ((100, 37), 1), ((2048, 512, 512), 0)])
+def test_linear_prefill_segments(rina, orc, qt, Ns, epi):
+    """Several weight segments on one prompt (q / k / v) in one matrix-core
+    launch: each segment's rows against the oracle."""
+    hip = rina.load_hip()
+    r = rng(sum(Ns) + qt + epi)
+    M, K = 100, 512
+    ws = [orc.pack(qt, (r.standard_normal(n * K) * 0.02).astype(np.float32)) for n in Ns]
+    x = r.standard_normal((M, K)).astype(np.float32)
+    y0 = [r.standard_normal((M, n)).astype(np.float32) for n in Ns]
+    ys = [dev(y) for y in y0]
+    wd = [dev(w) for w in ws]
+    segs = (rina.LinearSeg * len(Ns))(*[rina.LinearSeg(wd[i].data_ptr(), None, ys[i].data_ptr(), Ns[i])
+                                        for i in range(len(Ns))])
+    ok(hip.rina_hip_linear_fused(segs, len(Ns), qt, dev(x).data_ptr(), M, K, epi, 0, None, 0.0, stream()), "segs")
+    for i, n in enumerate(Ns):
+        ref = orc.linear(ws[i], qt, x, n, K).astype(np.float64) + (y0[i] if epi == 1 else 0.0)
+        assert_close(host(ys[i]).reshape(M, n), ref, what="segment %d of %s" % (i, Ns))
