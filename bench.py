@@ -277,6 +277,23 @@ def main():
     sw_roof = roofline(sw_bytes, t_sw)
     log("Q4_0F W1/W3 SwiGLU matvec: %.1f us, %.0f GB/s" % (t_sw * 1e6, sw_bytes / t_sw / 1e9))
 
+    # ---- prompt phase: the same W1/W3 SwiGLU at M = args.prompt rows on the
+    # matrix cores (fp32 MFMA peak), HIP events on our stream
+    Mp = args.prompt
+    xp = torch.randn(Mp * d, device="cuda")
+    gp = torch.empty(Mp * hd, device="cuda")
+    segp = [rina.LinearSeg(w1s[i].data_ptr(), w3s[i].data_ptr(), gp.data_ptr(), hd) for i in range(len(w1s))]
+
+    def swiglu_p(i=0):
+        return hip.rina_hip_linear_fused(C.byref(segp[i % nl]), 1, rina.QT_Q4_0F, xp.data_ptr(), Mp, d,
+                                         rina.EPI_SWIGLU, rina.PRO_NONE, None, 0.0, st)
+    t_swp = time_kernel(torch, swiglu_p, 8, replays=2)
+    swp_flop = 2 * 2 * Mp * hd * d
+    swp_roof = {"bound": "mfma", "achieved": round(swp_flop / t_swp / 1e12, 2), "peak": 157.3, "unit": "TFLOP/s",
+                "frac": round(swp_flop / t_swp / 157.3e12, 4), "traffic": None}
+    log("prompt W1/W3 SwiGLU (M %d): %.1f us, %.1f TFLOP/s" % (Mp, t_swp * 1e6, swp_flop / t_swp / 1e12))
+    del xp, gp
+
     # ---- config 1: Q4_0 GEMV 8192 x 2048 over a ring of 64 weight copies (~604 MB)
     N1, K1 = 8192, 2048
     w0 = synth.normal(1, N1 * K1, 0.02)
@@ -439,6 +456,8 @@ def main():
         "roofline_other": {
             "q4_0f_swiglu_w1w3": dict(sw_roof, bytes_per_launch=sw_bytes, avg_us=round(t_sw * 1e6, 2)),
             "config1_q4_0_gemv_8192x2048": dict(q4_roof, bytes_per_launch=q4_bytes, avg_us=round(t_q4 * 1e6, 3)),
+            "prefill_q4_0f_swiglu_m%d" % Mp: dict(swp_roof, flop_per_launch=swp_flop, avg_us=round(t_swp * 1e6, 2),
+                                                  kernel="gemm_mfma_kernel (v_mfma_f32_16x16x4f32)"),
         },
         "decode_hbm_gbps": round(per_token * tok_s / 1e9, 1),
         "decode_hbm_frac": round(per_token * tok_s / HBM_PEAK, 4),
