@@ -695,7 +695,12 @@ int launch_split(SplitArgs a, int rep, size_t ws_bytes, void* ws, hipStream_t st
     a.ws_m = (float*)ws;
     a.ws_l = a.ws_m + (size_t)nchunk * a.H;
     a.ws_o = a.ws_l + (size_t)nchunk * a.H;
-    dim3 grid(nchunk, a.Hkv / HG);
+    // x padded to a multiple of the 8 XCDs: workgroups are dealt to the XCDs
+    // round-robin in linear order, so every head group of chunk c then runs
+    // on the XCD of c and the cache lines that two groups' spans share are
+    // fetched into one L2 (the padding workgroups start past max_seq and
+    // return at once)
+    dim3 grid((nchunk + 7) / 8 * 8, a.Hkv / HG);
     switch (rep) {
         case 1: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 1, FUSED>), grid, dim3(256), 0, st, a); break;
         case 2: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 2, FUSED>), grid, dim3(256), 0, st, a); break;
