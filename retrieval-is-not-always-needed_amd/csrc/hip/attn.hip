@@ -853,7 +853,9 @@ extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, co
     p.ws_o = p.ws_l + (size_t)nch * H;
     p.out = out; p.H = H; p.start_pos = start_pos; p.max_seq = max_seq; p.d_pos = d_pos; p.chunk = kDqChunk;
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(dq_split_kernel, dim3(nch, H), dim3(256), 0, st, a, p);
+    // chunks padded to the 8 XCDs: the query heads of one chunk share its
+    // cache rows in one L2 (padding workgroups start past max_seq and return)
+    hipLaunchKernelGGL(dq_split_kernel, dim3((nch + 7) / 8 * 8, H), dim3(256), 0, st, a, p);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(attn_combine_kernel, dim3(H), dim3(256), 0, st, p);
     RINA_LAUNCH_CHECK();

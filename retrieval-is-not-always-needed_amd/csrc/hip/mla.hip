@@ -856,7 +856,10 @@ extern "C" int rina_hip_mla_decode_attention_ex(const float* q, const float* kva
     }
     hipLaunchKernelGGL(mla_prep_kernel, dim3(H + 1, 4), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
-    hipLaunchKernelGGL(mla_split_kernel, dim3(nch, H), dim3(256), 0, st, a);
+    // chunks padded to the 8 XCDs: every head of a chunk reads the same
+    // latent records, fetched into one L2 (padding workgroups start past
+    // max_seq and return)
+    hipLaunchKernelGGL(mla_split_kernel, dim3((nch + 7) / 8 * 8, H), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(mla_out_kernel, dim3(H, (v_dim + 15) / 16), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
