@@ -355,9 +355,13 @@ int rina_hip_rope(float* x, const float* cos_t, const float* sin_t, int T, int H
                   void* stream);
 /* out[n,d] = dequant(W[ids[i]]) for fp32 / Q4_0 / Q4_0F / Q2_K rows —
  * launch_embedding (ops/embedding.cu:200-230); ids are read at
- * ids + (d_pos ? *d_pos : 0). */
+ * ids + (d_pos ? *d_pos : 0).  vocab > 0: the table's row count; an id
+ * outside [0, vocab) is clamped into it (the reference reads it unchecked,
+ * which on a GPU faults); vocab <= 0: only negative ids are clamped (to 0)
+ * and the caller guarantees id < rows. */
 int rina_hip_embedding(const void* weight, int quant_type, const int* ids,
-                       const int* d_pos, float* out, int n, int d, void* stream);
+                       const int* d_pos, float* out, int n, int d, int vocab,
+                       void* stream);
 /* o = silu(g) * u — launch_silu_mul (ops/silu_mul.cu:5-12) */
 int rina_hip_silu_mul(float* o, const float* g, const float* u, int64_t n, void* stream);
 /* c = a + b — launch_add (ops/saxpy.cu:10-21) */
@@ -365,11 +369,21 @@ int rina_hip_add(float* c, const float* a, const float* b, int64_t n, void* stre
 /* d += p * s — launch_saxpy (ops/saxpy.cu:5-17) */
 int rina_hip_saxpy(float* d, const float* s, float p, int64_t n, void* stream);
 /* Greedy argmax with the strict ">" from -1e10 rule of sample()
- * (src/main.cpp:139-146): the lowest index wins ties.  Writes the index to
- * out_idx[0]; when d_pos is not NULL also stores it at
- * ids_out[*d_pos + 1] and increments *d_pos (device-side decode loop). */
+ * (src/main.cpp:139-146): the lowest index wins ties (+0 and -0 are equal).
+ * Writes the index to out_idx[0]; when d_pos is not NULL also stores it at
+ * ids_out[*d_pos + 1] and increments *d_pos (device-side decode loop).
+ * The candidates meet in one 8-byte key slot per device that the library
+ * owns: calls that overlap on two streams of one device race on it (use
+ * rina_hip_argmax_ws there). */
 int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out,
                     int* d_pos, void* stream);
+/* rina_hip_argmax with the caller's key slot: key_slot is 8 bytes of
+ * 8-byte-aligned device memory that holds zero before the first call (the
+ * call leaves it zero again).  Calls with different slots never share
+ * state, so decode loops on different streams can run together.  No
+ * counterpart in the reference (its sample() runs on the host). */
+int rina_hip_argmax_ws(const float* x, int n, int* out_idx, int* ids_out,
+                       int* d_pos, void* key_slot, void* stream);
 
 /* Library version / self-description. */
 const char* rina_hip_version(void);

@@ -70,11 +70,12 @@ _HIP_SIGS = {
     "rina_hip_rms_norm": (I32, [VP, VP, VP, I32, I32, F32, VP]),
     "rina_hip_layer_norm": (I32, [VP, VP, VP, I32, I32, F32, VP]),
     "rina_hip_rope": (I32, [VP, VP, VP, I32, I32, I32, I32, VP, I32, VP]),
-    "rina_hip_embedding": (I32, [VP, I32, VP, VP, VP, I32, I32, VP]),
+    "rina_hip_embedding": (I32, [VP, I32, VP, VP, VP, I32, I32, I32, VP]),
     "rina_hip_silu_mul": (I32, [VP, VP, VP, I64, VP]),
     "rina_hip_add": (I32, [VP, VP, VP, I64, VP]),
     "rina_hip_saxpy": (I32, [VP, VP, F32, I64, VP]),
     "rina_hip_argmax": (I32, [VP, I32, VP, VP, VP, VP]),
+    "rina_hip_argmax_ws": (I32, [VP, I32, VP, VP, VP, VP, VP]),
     "rina_hip_version": (C.c_char_p, []),
 }
 

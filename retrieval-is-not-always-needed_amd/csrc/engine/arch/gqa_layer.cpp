@@ -60,6 +60,19 @@ struct GQAImpl {
         f32(tn(l, "attn", "rope.sin"), rk_sin);
         // the fused launches need one quant type per fused group
         ok = ok && w_q.qt == w_k.qt && w_q.qt == w_v.qt && w1.qt == w3.qt;
+        if (!ok) return false;
+        // shapes the config implies (the kernels index by them)
+        const int64_t kvd = (int64_t)Hkv * dh, qd = (int64_t)H * dh;
+        const int64_t ms = cfg.max_seq_len > 0 ? cfg.max_seq_len : 512;
+        auto is = [&](const char* c, const char* p, int64_t n) { return elems_are(w.get(tn(l, c, p)), n); };
+        ok = is("attn", "w_q.weight", qd * d) && is("attn", "w_k.weight", kvd * d) && is("attn", "w_v.weight", kvd * d) &&
+             is("attn", "w_o.weight", (int64_t)d * qd) && is("mlp", "w1.weight", (int64_t)hd * d) &&
+             is("mlp", "w3.weight", (int64_t)hd * d) && is("mlp", "w2.weight", (int64_t)d * hd) &&
+             is("ln1", "weight", d) && is("ln2", "weight", d);
+        for (const char* r : {"rope_q.cos", "rope_q.sin", "rope.cos", "rope.sin"}) {
+            const WeightTensor* t = w.get(tn(l, "attn", r));
+            if (t && !elems_at_least(t, ms * (dh / 2))) ok = false;
+        }
         return ok;
     }
 
@@ -129,12 +142,12 @@ struct GQAImpl {
 };
 
 bool v_init(void* self, const ModelConfig& c, const TensorMap& w, int l) { return ((GQAImpl*)self)->init(c, w, l); }
-int v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
-    return ((GQAImpl*)self)->forward(h, b, B, T, s);
+void v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
+    b.fail(((GQAImpl*)self)->forward(h, b, B, T, s));
 }
 int v_ws(void*, int, int, int) { return 0; }   // no per-token scratch beyond ForwardBuffers
 void v_destroy(void* self) { delete (GQAImpl*)self; }
-const LayerVTable kGQAVTable = {v_init, v_forward, v_ws, v_destroy};
+const LayerVTable kGQAVTable = {v_init, v_forward, layer_no_backward, v_ws, layer_no_saved, v_destroy};
 
 }  // namespace
 

@@ -32,23 +32,27 @@ std::string tn(int l, const char* c, const char* p) {
     return b;
 }
 
+// Tensor lookup with the element count the config implies (the kernels
+// index by the config, so a smaller tensor would be read past its end).
 struct Loader {
     const TensorMap& w;
     int l;
     bool ok = true;
     QuantType qt = QuantType::FP32;
     bool first = true;
-    const void* lin(const char* c, const char* p) {
+    const void* lin(const char* c, const char* p, int64_t rows, int64_t cols) {
         const WeightTensor* t = w.get(tn(l, c, p));
-        if (!t) { ok = false; return nullptr; }
+        if (!elems_are(t, rows * cols)) { ok = false; return t ? t->data : nullptr; }
         if (first) { qt = t->quant_type; first = false; }
         else if (t->quant_type != qt) ok = false;       // one quant type per layer
         return t->data;
     }
-    const float* f32(const char* c, const char* p, bool required = true) {
+    // n > 0: exactly n values; n < 0: at least -n values (RoPE tables)
+    const float* f32(const char* c, const char* p, int64_t n, bool required = true) {
         const WeightTensor* t = w.get(tn(l, c, p));
-        if (!t && required) ok = false;
-        return t ? (const float*)t->data : nullptr;
+        if (!t) { if (required) ok = false; return nullptr; }
+        if (t->quant_type != QuantType::FP32 || !(n > 0 ? elems_are(t, n) : elems_at_least(t, -n))) ok = false;
+        return (const float*)t->data;
     }
 };
 
@@ -93,24 +97,27 @@ struct SSMImpl {
         dc = cfg.d_c > 0 ? cfg.d_c : 160;
         steps = cfg.ssm_steps > 0 ? cfg.ssm_steps : 3;
         if (steps > 3) return false;
+        const WeightTensor* t1 = w.get(tn(l, "mlp", "w1.weight"));
+        if (!t1 || t1->n_dim < 2) return false;
+        mlp.hd = t1->shape[0];
         Loader L{w, l};
-        w_dq = L.lin("path", "w_dq.weight");
+        w_dq = L.lin("path", "w_dq.weight", dc, d);
         for (int k = 0; k < steps; k++) {
             char b1[48], b2[48];
             snprintf(b1, sizeof b1, "w_mem.%d.weight", k);
             snprintf(b2, sizeof b2, "w_decay.%d.weight", k);
-            w_mem[k] = L.lin("path", b1);
-            w_decay[k] = L.lin("path", b2);
+            w_mem[k] = L.lin("path", b1, (int64_t)H * dh, dc);
+            w_decay[k] = L.lin("path", b2, H, dc);
         }
-        w_out = L.lin("path", "w_out.weight");
-        mlp.w1 = L.lin("mlp", "w1.weight"); mlp.w2 = L.lin("mlp", "w2.weight"); mlp.w3 = L.lin("mlp", "w3.weight");
-        q_norm = L.f32("path", "q_norm.weight");
-        ln1 = L.f32("ln1", "weight");
-        mlp.ln2 = L.f32("ln2", "weight");
+        w_out = L.lin("path", "w_out.weight", d, (int64_t)d + H * dh);
+        mlp.w1 = L.lin("mlp", "w1.weight", mlp.hd, d);
+        mlp.w2 = L.lin("mlp", "w2.weight", d, mlp.hd);
+        mlp.w3 = L.lin("mlp", "w3.weight", mlp.hd, d);
+        q_norm = L.f32("path", "q_norm.weight", dc);
+        ln1 = L.f32("ln1", "weight", d);
+        mlp.ln2 = L.f32("ln2", "weight", d);
         if (!L.ok) return false;
         qt = (int)L.qt;
-        const WeightTensor* t1 = w.get(tn(l, "mlp", "w1.weight"));
-        mlp.hd = t1->shape[0];
         return dev_alloc(&lcs, (size_t)H * dh) && dev_alloc(&wcs, (size_t)H * dh) &&
                dev_alloc(&scratch, (size_t)d + H * dh + dc + 3 * H * dh + 3 * H);
     }
@@ -183,23 +190,28 @@ struct RMLAImpl {
         dc = cfg.d_c > 0 ? cfg.d_c : 160;
         max_seq = cfg.max_seq_len > 0 ? cfg.max_seq_len : 512;
         if (Hkv <= 0 || H % Hkv) return false;
+        const WeightTensor* t1 = w.get(tn(l, "mlp", "w1.weight"));
+        if (!t1 || t1->n_dim < 2) return false;
+        mlp.hd = t1->shape[0];
         Loader L{w, l};
-        w_dqkv = L.lin("path", "w_dqkv.weight");
-        w_qr = L.lin("path", "w_qr.weight");
-        w_kr = L.lin("path", "w_kr.weight");
-        w_uq = L.lin("path", "w_uq.weight");
-        w_uk = L.lin("path", "w_uk.weight");
-        w_k2v = L.lin("path", "w_k2v.weight");
-        c_proj = L.lin("path", "c_proj.weight");
-        mlp.w1 = L.lin("mlp", "w1.weight"); mlp.w2 = L.lin("mlp", "w2.weight"); mlp.w3 = L.lin("mlp", "w3.weight");
-        q_norm = L.f32("path", "q_norm.weight");
-        ln1 = L.f32("ln1", "weight");
-        mlp.ln2 = L.f32("ln2", "weight");
-        rqc = L.f32("path", "rope_q.cos", false); rqs = L.f32("path", "rope_q.sin", false);
-        rkc = L.f32("path", "rope.cos", false); rks = L.f32("path", "rope.sin", false);
+        w_dqkv = L.lin("path", "w_dqkv.weight", dc, d);
+        w_qr = L.lin("path", "w_qr.weight", (int64_t)H * dhr, d);
+        w_kr = L.lin("path", "w_kr.weight", (int64_t)Hkv * dhr, d);
+        w_uq = L.lin("path", "w_uq.weight", (int64_t)H * dh, dc);
+        w_uk = L.lin("path", "w_uk.weight", (int64_t)Hkv * dh, dc);
+        w_k2v = L.lin("path", "w_k2v.weight", (int64_t)Hkv * dh, (int64_t)Hkv * dh);
+        c_proj = L.lin("path", "c_proj.weight", d, (int64_t)H * dh);
+        mlp.w1 = L.lin("mlp", "w1.weight", mlp.hd, d);
+        mlp.w2 = L.lin("mlp", "w2.weight", d, mlp.hd);
+        mlp.w3 = L.lin("mlp", "w3.weight", mlp.hd, d);
+        q_norm = L.f32("path", "q_norm.weight", dc);
+        ln1 = L.f32("ln1", "weight", d);
+        mlp.ln2 = L.f32("ln2", "weight", d);
+        const int64_t rope_n = -(int64_t)max_seq * (dhr / 2);
+        rqc = L.f32("path", "rope_q.cos", rope_n, false); rqs = L.f32("path", "rope_q.sin", rope_n, false);
+        rkc = L.f32("path", "rope.cos", rope_n, false); rks = L.f32("path", "rope.sin", rope_n, false);
         if (!L.ok) return false;
         qt = (int)L.qt;
-        mlp.hd = w.get(tn(l, "mlp", "w1.weight"))->shape[0];
         ws_bytes = rina_hip_dq_attention_workspace(H, dh + dhr, max_seq);
         const size_t sc = (size_t)dc + H * dhr + Hkv * dhr + H * dh + 2 * Hkv * dh + H * dh;
         return dev_alloc(&ck, (size_t)max_seq * Hkv * (dh + dhr)) && dev_alloc(&cv, (size_t)max_seq * Hkv * dh) &&
@@ -240,16 +252,18 @@ struct RMLAImpl {
 template <typename Impl>
 bool v_init(void* self, const ModelConfig& c, const TensorMap& w, int l) { return ((Impl*)self)->init(c, w, l); }
 template <typename Impl>
-int v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
+void v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
     (void)B;
-    return ((Impl*)self)->forward(h, b, T, s);
+    b.fail(((Impl*)self)->forward(h, b, T, s));
 }
 int v_ws(void*, int, int, int) { return 0; }
 template <typename Impl>
 void v_destroy(void* self) { delete (Impl*)self; }
 
-const LayerVTable kSSMVTable = {v_init<SSMImpl>, v_forward<SSMImpl>, v_ws, v_destroy<SSMImpl>};
-const LayerVTable kRMLAVTable = {v_init<RMLAImpl>, v_forward<RMLAImpl>, v_ws, v_destroy<RMLAImpl>};
+const LayerVTable kSSMVTable = {v_init<SSMImpl>, v_forward<SSMImpl>, layer_no_backward, v_ws, layer_no_saved,
+                                v_destroy<SSMImpl>};
+const LayerVTable kRMLAVTable = {v_init<RMLAImpl>, v_forward<RMLAImpl>, layer_no_backward, v_ws, layer_no_saved,
+                                 v_destroy<RMLAImpl>};
 
 }  // namespace
 

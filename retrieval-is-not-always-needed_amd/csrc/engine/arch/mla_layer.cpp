@@ -72,6 +72,16 @@ struct MLAImpl {
                   f32(tn(l, "ln2", "weight"), ln2);
         f32(tn(l, "attn", "rope_q.cos"), rope_c);
         f32(tn(l, "attn", "rope_q.sin"), rope_s);
+        auto is = [&](const char* c, const char* p, int64_t n) { return elems_are(w.get(tn(l, c, p)), n); };
+        const int64_t ms = cfg.max_seq_len > 0 ? cfg.max_seq_len : 512;
+        ok = ok && is("attn", "w_q.weight", (int64_t)H * (nope + rope) * d) &&
+             is("attn", "w_kv_a.weight", (int64_t)(dc + rope) * d) && is("attn", "k_norm.weight", dc) &&
+             is("attn", "w_kv_b.weight", (int64_t)H * (nope + vd) * dc) && is("attn", "w_o.weight", (int64_t)d * H * vd) &&
+             is("ln1", "weight", d) && is("ln2", "weight", d);
+        for (const char* r : {"rope_q.cos", "rope_q.sin"}) {
+            const WeightTensor* t = w.get(tn(l, "attn", r));
+            if (t && !elems_at_least(t, ms * (rope / 2))) ok = false;
+        }
         const WeightTensor* gi = w.get(tn(l, "mlp", "gate_inp.weight"));
         is_moe = gi != nullptr;
         if (is_moe) {
@@ -90,6 +100,11 @@ struct MLAImpl {
             stride_gu = (int64_t)quantized_size((int64_t)F * d, gate_exps.qt);
             stride_dn = (int64_t)quantized_size((int64_t)d * F, down_exps.qt);
             ok = ok && gate_exps.qt == up_exps.qt && gate_exps.qt == down_exps.qt && gate_sh.qt == up_sh.qt;
+            // shapes the config implies (the kernels index by them)
+            ok = ok && K >= 1 && K <= E && is("mlp", "gate_inp.weight", (int64_t)E * d) &&
+                 is("mlp", "gate_exps.weight", (int64_t)E * F * d) && is("mlp", "up_exps.weight", (int64_t)E * F * d) &&
+                 is("mlp", "down_exps.weight", (int64_t)E * d * F) && is("mlp", "gate_shexp.weight", (int64_t)S * d) &&
+                 is("mlp", "up_shexp.weight", (int64_t)S * d) && is("mlp", "down_shexp.weight", (int64_t)d * S);
             if (ok && gate_exps.qt == QuantType::GGML_Q2_K && gate_sh.qt == QuantType::GGML_Q2_K &&
                 down_sh.qt == QuantType::GGML_Q2_K && gate_inp.qt == QuantType::FP32) {
                 moe_ws_bytes = rina_hip_moe_block_workspace(d, E, K, F, S);
@@ -100,7 +115,8 @@ struct MLAImpl {
                  ref(tn(l, "mlp", "w3.weight"), w3);
             const WeightTensor* t = w.get(tn(l, "mlp", "w1.weight"));
             hd = t ? (int)t->shape[0] : cfg.hidden_dim;
-            ok = ok && w1.qt == w3.qt;
+            ok = ok && w1.qt == w3.qt && is("mlp", "w1.weight", (int64_t)hd * d) && is("mlp", "w3.weight", (int64_t)hd * d) &&
+                 is("mlp", "w2.weight", (int64_t)d * hd);
         }
         return ok;
     }
@@ -178,12 +194,12 @@ struct MLAImpl {
 };
 
 bool v_init(void* self, const ModelConfig& c, const TensorMap& w, int l) { return ((MLAImpl*)self)->init(c, w, l); }
-int v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
-    return ((MLAImpl*)self)->forward(h, b, B, T, s);
+void v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
+    b.fail(((MLAImpl*)self)->forward(h, b, B, T, s));
 }
 int v_ws(void* self, int, int, int) { return ((MLAImpl*)self)->scratch_per_token(); }
 void v_destroy(void* self) { delete (MLAImpl*)self; }
-const LayerVTable kMLAVTable = {v_init, v_forward, v_ws, v_destroy};
+const LayerVTable kMLAVTable = {v_init, v_forward, layer_no_backward, v_ws, layer_no_saved, v_destroy};
 
 }  // namespace
 

@@ -1,4 +1,5 @@
 // extern "C" surface of the engine (include/rina_engine.h).
+#include <cstdint>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -64,7 +65,12 @@ extern "C" int rina_model_add_tensor(rina_model* m, const char* name, int qt, in
     t.n_dim = ndim;
     t.quant_type = (QuantType)qt;
     t.n_elems = 1;
-    for (int i = 0; i < ndim; i++) { t.shape[i] = (int)shape[i]; t.n_elems *= shape[i]; }
+    for (int i = 0; i < ndim; i++) {
+        if (shape[i] <= 0 || shape[i] > INT32_MAX || __builtin_mul_overflow(t.n_elems, shape[i], &t.n_elems) ||
+            t.n_elems > ((int64_t)1 << 48))
+            return set_err(RINA_ERR_ARG, std::string("add_tensor: non-positive or oversized shape for ") + name);
+        t.shape[i] = (int)shape[i];
+    }
     t.owned = false;
     m->tensors.add(name, std::move(t));
     return RINA_OK;
@@ -97,7 +103,7 @@ extern "C" void rina_infer_destroy(rina_infer* r) {
 
 extern "C" int rina_infer_forward(rina_infer* r, const int* ids, float* logits, int B, int T, int start_pos, void* stream) {
     if (!r || !ids || !logits) return set_err(RINA_ERR_ARG, "forward: bad argument");
-    int rc = r->inf->forward(ids, logits, B, T, start_pos, (hipStream_t)stream);
+    int rc = r->inf->run_forward(ids, logits, B, T, start_pos, (hipStream_t)stream);
     if (rc) set_err(rc, "forward: " + r->inf->last_error());
     return rc;
 }

@@ -62,6 +62,13 @@ struct ForwardBuffers {
     // rows each layer appends, [n_layers][2][max_seq][kv_dim]; host-position
     // forward() calls only
     float* kv_tap = nullptr;
+    // status of the layer forwards since the caller last cleared it: the
+    // first failing C-ABI call's negative status sticks (the reference's
+    // forward_fn returns void, core/layer.h:52)
+    int status = 0;
+    void fail(int rc) {
+        if (rc && !status) status = rc;
+    }
 };
 
 struct BufferManager {

@@ -111,9 +111,13 @@ bool load_rinn(const std::string& path_in, ModelConfig& cfg, TensorMap& tensors,
         t.quant_type = (QuantType)s.quant_type;
         t.n_dim = s.n_dim;
         t.n_elems = 1;
+        // every dim inside the rank positive, the element count far from
+        // int64 overflow (byte sizes are derived from it)
         for (int i = 0; i < s.n_dim; i++) {
+            if (s.shape[i] <= 0 || __builtin_mul_overflow(t.n_elems, (int64_t)s.shape[i], &t.n_elems) ||
+                t.n_elems > ((int64_t)1 << 48))
+                return abort_load("rinn: tensor " + s.name + " has a non-positive or oversized shape");
             t.shape[i] = s.shape[i];
-            t.n_elems *= s.shape[i];
         }
         size_t bytes;
         if (t.quant_type == QuantType::FP32) bytes = (size_t)t.n_elems * sizeof(float);

@@ -21,6 +21,13 @@ struct WeightTensor {
     }
 };
 
+// A layer's init checks every tensor against the element count its config
+// implies (rows x cols, or experts x rows x cols): the kernels index by the
+// config, so a smaller tensor would be read past its end.
+inline bool elems_are(const WeightTensor* t, int64_t n) { return t && n > 0 && t->n_elems == n; }
+// RoPE tables [positions][half]: at least the positions the cache can hold.
+inline bool elems_at_least(const WeightTensor* t, int64_t n) { return t && n > 0 && t->n_elems >= n; }
+
 struct TensorMap {
     std::unordered_map<std::string, WeightTensor> tensors;
 

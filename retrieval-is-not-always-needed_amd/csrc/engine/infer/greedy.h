@@ -13,7 +13,7 @@
 
 struct DeviceGreedyInference : Inference {
     int* d_ids = nullptr;      // [max_seq + 1]
-    int* d_pos = nullptr;      // device position of the last id
+    int* d_pos = nullptr;      // device position of the last id; d_pos[2..3]: this loop's argmax key slot
     int max_seq = 0;
     int vocab = 0;
     int gen_len = 0;           // ids valid in d_ids after the last generate / decode_more
@@ -43,7 +43,21 @@ struct DeviceGreedyInference : Inference {
 
     bool alloc_ids() {
         return hipMalloc(&d_ids, sizeof(int) * (max_seq + 1)) == hipSuccess &&
-               hipMalloc(&d_pos, sizeof(int)) == hipSuccess;
+               hipMalloc(&d_pos, 4 * sizeof(int)) == hipSuccess && hipMemset(d_pos, 0, 4 * sizeof(int)) == hipSuccess;
+    }
+    // argmax with this inference's own key slot: two inferences decoding on
+    // different streams never share it
+    int argmax(hipStream_t s) { return rina_hip_argmax_ws(lm_buffer(), vocab, nullptr, d_ids, d_pos, d_pos + 2, s); }
+
+    // A captured graph holds the activation pointers of its capture: every
+    // ensure_cap() that re-allocates them must drop the graphs, so the next
+    // decode_more() captures again on the new buffers.
+    void drop_graphs() {
+        for (int c = 0; c < 2; c++) {
+            if (graph[c]) (void)hipGraphExecDestroy(graph[c]);
+            graph[c] = nullptr;
+            graph_stream[c] = nullptr;
+        }
     }
 
     // (re)capture decode graph c, valid for device positions <= hint
@@ -68,19 +82,24 @@ struct DeviceGreedyInference : Inference {
     int decode_step(hipStream_t s) {
         int rc = run(d_ids, d_pos, 1, 0, lm_buffer(), true, s);
         if (rc) return rc;
-        return rina_hip_argmax(lm_buffer(), vocab, nullptr, d_ids, d_pos, s);
+        return argmax(s);
     }
 
     int generate(const int* prompt, int n, int steps, int* out, bool use_graph, hipStream_t s,
                  float* decode_ms) override {
         if (n < 1 || steps < 1 || n + steps - 1 > max_seq) { err_ = tag + ": prompt + steps exceed max_seq"; return RINA_ERR_RANGE; }
+        for (int i = 0; i < n; i++)
+            if (prompt[i] < 0 || prompt[i] >= vocab) {
+                err_ = tag + ": prompt id " + std::to_string(prompt[i]) + " outside the vocabulary";
+                return RINA_ERR_ARG;
+            }
         int rc = ensure_cap(n);
         if (rc) return rc;
         if (hipMemcpyAsync(d_ids, prompt, sizeof(int) * n, hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
         int p0 = n - 1;
         if (hipMemcpyAsync(d_pos, &p0, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
         if ((rc = run(d_ids, nullptr, n, 0, lm_buffer(), true, s))) return rc;
-        if ((rc = rina_hip_argmax(lm_buffer(), vocab, nullptr, d_ids, d_pos, s))) return rc;
+        if ((rc = argmax(s))) return rc;
         if (hipStreamSynchronize(s) != hipSuccess) return RINA_ERR_HIP;
         gen_len = n + 1;
         if (hipMemcpyAsync(out, d_ids + n, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return RINA_ERR_HIP;

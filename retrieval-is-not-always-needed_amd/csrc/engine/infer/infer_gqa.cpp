@@ -38,6 +38,15 @@ struct GQAInference : DeviceGreedyInference {
             return fail("gqa: incomplete config");
         layers = build_layers(cfg, w);
         if ((int)layers.size() != cfg.n_layers || layers.empty()) return fail("gqa: layer init failed");
+        wte = w.get("transformer.wte.weight");
+        ln_f = w.get("transformer.ln_f.weight");
+        lm_head = w.get("lm_head.weight");
+        if (!wte) return fail("gqa: transformer.wte.weight missing");
+        // the embedding and the LM head index rows by the config
+        const int64_t vd_rows = (int64_t)cfg.vocab_size * cfg.dim;
+        if (!elems_are(wte, vd_rows)) return fail("gqa: transformer.wte.weight is not [vocab, dim]");
+        if (lm_head && !elems_are(lm_head, vd_rows)) return fail("gqa: lm_head.weight is not [vocab, dim]");
+        if (ln_f && !elems_are(ln_f, cfg.dim)) return fail("gqa: transformer.ln_f.weight is not [dim]");
         // MLP width: the widest w1 of any layer (GQA, SSM or RINA-MLA)
         hd = cfg.hidden_dim;
         for (int l = 0; l < cfg.n_layers; l++) {
@@ -66,15 +75,14 @@ struct GQAInference : DeviceGreedyInference {
         if (!bufs.alloc_attn_ws(rina_hip_gqa_attention_workspace(1, cfg.n_heads, cfg.head_dim, max_seq)))
             return fail("gqa: attention workspace allocation failed");
         if (!alloc_ids()) return fail("gqa: id buffer allocation failed");
-        wte = w.get("transformer.wte.weight");
-        ln_f = w.get("transformer.ln_f.weight");
-        lm_head = w.get("lm_head.weight");
-        if (!wte) return fail("gqa: transformer.wte.weight missing");
         return true;
     }
 
     int ensure_cap(int n) override {
         if (n <= bufs.fwd.cap) return RINA_OK;
+        // the queued work and the captured graphs use the old buffers
+        if (hipDeviceSynchronize() != hipSuccess) return RINA_ERR_HIP;
+        drop_graphs();
         ForwardBuffers keep = bufs.fwd;   // caches survive the re-allocation
         bufs.fwd.kv_cache.data = nullptr;
         bufs.fwd.kv_cache_quant.data = nullptr;
@@ -104,9 +112,10 @@ struct GQAInference : DeviceGreedyInference {
         f.kv_cache.start_pos = start_pos;
         f.kv_cache_quant.start_pos = start_pos;
         f.d_pos = pos_dev;
-        if ((rc = rina_hip_embedding(wte->data, (int)wte->quant_type, ids, pos_dev, f.h, T, cfg.dim, s))) return rc;
+        if ((rc = rina_hip_embedding(wte->data, (int)wte->quant_type, ids, pos_dev, f.h, T, cfg.dim, cfg.vocab_size, s))) return rc;
+        f.status = RINA_OK;
         for (auto& l : layers)
-            if ((rc = l->forward(f.h, f, 1, T, s))) return rc;
+            if ((rc = l->run(f.h, f, 1, T, s))) return rc;
         const WeightTensor* hw = head();
         const float* x = f.h;
         int M = T;
@@ -118,12 +127,14 @@ struct GQAInference : DeviceGreedyInference {
                                      ln_f ? (const float*)ln_f->data : nullptr, 1e-5f, s);
     }
 
-    int forward(const int* ids, float* logits, int B, int T, int start_pos, hipStream_t s) override {
-        if (B != 1) { err_ = "gqa: the KV-cache path decodes one sequence (B == 1)"; return RINA_ERR_ARG; }
-        if (T < 1 || start_pos < 0 || start_pos + T > max_seq) { err_ = "gqa: positions exceed max_seq"; return RINA_ERR_RANGE; }
+    void forward(const int* ids, float* logits, int B, int T, int start_pos, hipStream_t s) override {
+        if (B != 1) return set_status(RINA_ERR_ARG, "gqa: the KV-cache path decodes one sequence (B == 1)");
+        if (T < 1 || start_pos < 0 || start_pos + T > max_seq)
+            return set_status(RINA_ERR_RANGE, "gqa: positions exceed max_seq");
         int rc = ensure_cap(T);
-        if (rc) return rc;
-        return run(ids, nullptr, T, start_pos, logits, false, s);
+        if (rc) return set_status(rc, "gqa: activation buffer allocation failed");
+        rc = run(ids, nullptr, T, start_pos, logits, false, s);
+        set_status(rc, "gqa: a forward launch failed");
     }
 
     int set_kv_tap(float* tap) override {

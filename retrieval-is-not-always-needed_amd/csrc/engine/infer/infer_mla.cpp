@@ -51,6 +51,15 @@ struct MLAInference : DeviceGreedyInference {
         dc = cfg.kv_lora_rank > 0 ? cfg.kv_lora_rank : (cfg.d_c > 0 ? cfg.d_c : 512);
         layers = build_layers(cfg, w);
         if ((int)layers.size() != cfg.n_layers || layers.empty()) return fail("mla: layer init failed");
+        wte = w.get("transformer.wte.weight");
+        ln_f = w.get("transformer.ln_f.weight");
+        lm_head = w.get("lm_head.weight");
+        if (!wte) return fail("mla: transformer.wte.weight missing");
+        // the embedding and the LM head index rows by the config
+        const int64_t vd_rows = (int64_t)cfg.vocab_size * cfg.dim;
+        if (!elems_are(wte, vd_rows)) return fail("mla: transformer.wte.weight is not [vocab, dim]");
+        if (lm_head && !elems_are(lm_head, vd_rows)) return fail("mla: lm_head.weight is not [vocab, dim]");
+        if (ln_f && !elems_are(ln_f, cfg.dim)) return fail("mla: transformer.ln_f.weight is not [dim]");
         for (auto& l : layers) {
             ffn = std::max(ffn, mla_layer_ffn_width(*l));
             scratch = std::max(scratch, l->workspace_per_token(cfg.dim, cfg.n_heads, cfg.head_dim));
@@ -62,15 +71,14 @@ struct MLAInference : DeviceGreedyInference {
         if (!bufs.alloc_attn_ws(rina_hip_mla_attention_workspace(cfg.n_heads, dc, rope, max_seq)))
             return fail("mla: attention workspace allocation failed");
         if (!alloc_ids()) return fail("mla: id buffer allocation failed");
-        wte = w.get("transformer.wte.weight");
-        ln_f = w.get("transformer.ln_f.weight");
-        lm_head = w.get("lm_head.weight");
-        if (!wte) return fail("mla: transformer.wte.weight missing");
         return true;
     }
 
     int ensure_cap(int n) override {
         if (n <= bufs.fwd.cap) return RINA_OK;
+        // the queued work and the captured graphs use the old buffers
+        if (hipDeviceSynchronize() != hipSuccess) return RINA_ERR_HIP;
+        drop_graphs();
         ForwardBuffers keep = bufs.fwd;
         bufs.fwd.mla_cache.data = nullptr;
         bufs.fwd.attn_ws = nullptr;
@@ -93,9 +101,10 @@ struct MLAInference : DeviceGreedyInference {
         f.mla_cache.start_pos = start_pos;
         f.d_pos = pos_dev;
         f.pos_hint = pos_dev ? pos_hint : -1;
-        if ((rc = rina_hip_embedding(wte->data, (int)wte->quant_type, ids, pos_dev, f.h, T, cfg.dim, s))) return rc;
+        if ((rc = rina_hip_embedding(wte->data, (int)wte->quant_type, ids, pos_dev, f.h, T, cfg.dim, cfg.vocab_size, s))) return rc;
+        f.status = RINA_OK;
         for (auto& l : layers)
-            if ((rc = l->forward(f.h, f, 1, T, s))) return rc;
+            if ((rc = l->run(f.h, f, 1, T, s))) return rc;
         const WeightTensor* hw = lm_head ? lm_head : wte;
         const float* x = f.h;
         int M = T;
@@ -106,12 +115,14 @@ struct MLAInference : DeviceGreedyInference {
                                      ln_f ? (const float*)ln_f->data : nullptr, 1e-5f, s);
     }
 
-    int forward(const int* ids, float* logits, int B, int T, int start_pos, hipStream_t s) override {
-        if (B != 1) { err_ = "mla: the cache path decodes one sequence (B == 1)"; return RINA_ERR_ARG; }
-        if (T < 1 || start_pos < 0 || start_pos + T > max_seq) { err_ = "mla: positions exceed max_seq"; return RINA_ERR_RANGE; }
+    void forward(const int* ids, float* logits, int B, int T, int start_pos, hipStream_t s) override {
+        if (B != 1) return set_status(RINA_ERR_ARG, "mla: the cache path decodes one sequence (B == 1)");
+        if (T < 1 || start_pos < 0 || start_pos + T > max_seq)
+            return set_status(RINA_ERR_RANGE, "mla: positions exceed max_seq");
         int rc = ensure_cap(T);
-        if (rc) return rc;
-        return run(ids, nullptr, T, start_pos, logits, false, s);
+        if (rc) return set_status(rc, "mla: activation buffer allocation failed");
+        rc = run(ids, nullptr, T, start_pos, logits, false, s);
+        set_status(rc, "mla: a forward launch failed");
     }
 
     int set_kv_tap(float*) override {

@@ -1433,7 +1433,7 @@ extern "C" int rina_hip_linear_fused_ex(const rina_linear_seg* segs, int nseg, i
     if (pro != RINA_PRO_NONE && (!fused_pro || (norm_out && !direct))) {
         // normalize first (into norm_out when given, else library scratch):
         // prompt rows, unusual shapes
-        float* tmp = norm_out ? norm_out : (float*)rina_scratch((size_t)M * K * 4);
+        float* tmp = norm_out ? norm_out : (float*)rina_scratch((size_t)M * K * 4, as_stream(stream));
         if (!tmp) return RINA_ERR_HIP;
         int rc = pro == RINA_PRO_RMSNORM ? rina_hip_rms_norm(input, tmp, nw, M, K, eps, stream)
                                          : rina_hip_layer_norm(input, tmp, nw, M, K, eps, stream);
@@ -1488,7 +1488,7 @@ extern "C" int rina_hip_linear(const void* weight, int qt, const float* input, f
     bool alias = ib < oe && ob < ie;
     float* dst = output;
     if (alias) {
-        dst = (float*)rina_scratch((size_t)M * N * 4);
+        dst = (float*)rina_scratch((size_t)M * N * 4, st);
         if (!dst) return RINA_ERR_HIP;
     }
     rina_linear_seg seg{weight, nullptr, dst, N};

@@ -3,6 +3,7 @@
 #include "rina_common.hpp"
 #include "kv_formats.hpp"
 #include <mutex>
+#include <vector>
 
 namespace {
 
@@ -69,12 +70,17 @@ __global__ void rope_kernel(float* x, const float* ct, const float* st, int T, i
 }
 
 // ops/embedding.cu:6-230: row lookup with per-format dequant; Q2_K rows are
-// row-aligned (ceil(d/256) blocks per row, ops/embedding.cu:80-81)
-__global__ void embedding_kernel(const uint8_t* w, int qt, const int* ids, const int* d_pos, float* out, int d) {
+// row-aligned (ceil(d/256) blocks per row, ops/embedding.cu:80-81).  With
+// vocab > 0 an id outside [0, vocab) is clamped into it, so a bad id read
+// from device memory never indexes past the table (the reference reads it
+// unchecked; host prompts are rejected before launch by the engine).
+__global__ void embedding_kernel(const uint8_t* w, int qt, const int* ids, const int* d_pos, float* out, int d,
+                                 int vocab) {
     const int t = blockIdx.x;
     const int off = d_pos ? *d_pos : 0;
     int id = ids[off + t];
     if (id < 0) id = 0;
+    if (vocab > 0 && id >= vocab) id = vocab - 1;
     float* o = out + (int64_t)t * d;
     const uint8_t* row;
     if (qt == RINA_QT_Q4_0) row = w + (int64_t)id * (d / 32) * 18;
@@ -99,12 +105,14 @@ __global__ void saxpy_kernel(float* d, const float* s, float p, int64_t n) {
 
 // Greedy argmax (main.cpp:139-146): strict ">" from -1e10, lowest index on
 // ties.  Candidates are packed into one 64-bit key (order-preserving float
-// bits, then the complemented index) and merged with a 64-bit atomicMax;
-// the key slot is a device global that the finishing kernel clears again.
-__device__ unsigned long long g_argmax_key = 0ull;
+// bits, then the complemented index) and merged with a 64-bit atomicMax
+// into a key slot that the finishing kernel reads and clears again.  -0 is
+// keyed as +0: under ">" the two are equal, so the lower index must win.
+__device__ unsigned long long g_argmax_key = 0ull;   // slot of rina_hip_argmax (one per device)
 
 __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
     uint32_t b = __float_as_uint(v);
+    if (b == 0x80000000u) b = 0u;
     uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
 }
@@ -115,7 +123,7 @@ __device__ __forceinline__ unsigned long long cand(float v, int i) { return v > 
 
 // A few workgroups (one 64-bit atomic each, after a wave + LDS reduction)
 // cover x with 16-byte loads; many same-address atomics serialize.
-__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* x, int n) {
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* x, int n, unsigned long long* key) {
     __shared__ unsigned long long red[4];
     unsigned long long best = 0ull;
     const int tid = threadIdx.x;
@@ -133,13 +141,13 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* x, int
     __syncthreads();
     if (tid == 0) {
         best = umax64(umax64(red[0], red[1]), umax64(red[2], red[3]));
-        if (best) atomicMax(&g_argmax_key, best);
+        if (best) atomicMax(key, best);
     }
 }
 
-__global__ void argmax_finish_kernel(int* out_idx, int* ids_out, int* d_pos) {
-    unsigned long long k = g_argmax_key;
-    g_argmax_key = 0ull;
+__global__ void argmax_finish_kernel(int* out_idx, int* ids_out, int* d_pos, unsigned long long* key) {
+    unsigned long long k = *key;
+    *key = 0ull;
     int idx = k ? (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : 0;
     if (out_idx) *out_idx = idx;
     if (d_pos) {
@@ -153,11 +161,23 @@ unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
 struct DevState {
     int cus = 0;
-    void* scratch = nullptr;
-    size_t scratch_bytes = 0;
 };
 DevState g_dev[64];
 std::mutex g_mu;
+
+// Library scratch, one buffer per (device, stream): work on different
+// streams never shares it, and work on one stream is ordered.  A buffer
+// that must grow is replaced by one of at least twice its size; the old
+// one may still be read by queued work, so it is kept (retired) until the
+// process ends: at most log2 of the largest request buffers per stream.
+struct ScratchSlot {
+    int dev;
+    hipStream_t st;
+    void* p;
+    size_t bytes;
+};
+std::vector<ScratchSlot> g_scratch;
+std::vector<void*> g_retired;
 
 }  // namespace
 
@@ -172,19 +192,25 @@ int rina_num_cus() {
     return g_dev[dev].cus;
 }
 
-void* rina_scratch(size_t bytes) {
+void* rina_scratch(size_t bytes, hipStream_t st) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
     std::lock_guard<std::mutex> lk(g_mu);
-    DevState& s = g_dev[dev];
-    if (s.scratch_bytes < bytes) {
-        // the previous buffer may still be read by queued work: keep it alive
+    for (ScratchSlot& s : g_scratch) {
+        if (s.dev != dev || s.st != st) continue;
+        if (s.bytes >= bytes) return s.p;
+        size_t nb = bytes > 2 * s.bytes ? bytes : 2 * s.bytes;
         void* p = nullptr;
-        if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-        s.scratch = p;
-        s.scratch_bytes = bytes;
+        if (hipMalloc(&p, nb) != hipSuccess) return nullptr;
+        g_retired.push_back(s.p);
+        s.p = p;
+        s.bytes = nb;
+        return p;
     }
-    return s.scratch;
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    g_scratch.push_back({dev, st, p, bytes});
+    return p;
 }
 
 extern "C" int rina_hip_rms_norm(const float* x, float* out, const float* w, int n, int d, float eps, void* stream) {
@@ -212,13 +238,13 @@ extern "C" int rina_hip_rope(float* x, const float* ct, const float* st, int T, 
 }
 
 extern "C" int rina_hip_embedding(const void* w, int qt, const int* ids, const int* d_pos, float* out, int n, int d,
-                                  void* stream) {
+                                  int vocab, void* stream) {
     if (!w || !ids || !out || n < 1 || d < 1) return RINA_ERR_ARG;
     if (qt != RINA_QT_FP32 && qt != RINA_QT_Q4_0 && qt != RINA_QT_Q4_0F && qt != RINA_QT_GGML_Q2_K)
         return RINA_ERR_QTYPE;
     if ((qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && d % 32) return RINA_ERR_SHAPE;
     hipLaunchKernelGGL(embedding_kernel, dim3(n), dim3(256), 0, as_stream(stream), (const uint8_t*)w, qt, ids, d_pos,
-                       out, d);
+                       out, d, vocab);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }
@@ -247,16 +273,45 @@ extern "C" int rina_hip_saxpy(float* d, const float* s, float p, int64_t n, void
     return RINA_OK;
 }
 
-extern "C" int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out, int* d_pos, void* stream) {
-    if (!x || n < 1 || (!out_idx && !d_pos)) return RINA_ERR_ARG;
-    hipStream_t st = as_stream(stream);
+namespace {
+int argmax_launch(const float* x, int n, int* out_idx, int* ids_out, int* d_pos, unsigned long long* key,
+                  hipStream_t st) {
     int grid = (n + 1023) / 1024;
     if (grid > 64) grid = 64;
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(grid), dim3(256), 0, st, x, n);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(grid), dim3(256), 0, st, x, n, key);
     RINA_LAUNCH_CHECK();
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, st, out_idx, ids_out, d_pos);
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1), 0, st, out_idx, ids_out, d_pos, key);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
+}
+
+// device address of g_argmax_key, looked up once per device with that
+// device current (host code must never pass the symbol itself)
+unsigned long long* g_key_addr[64];
+std::mutex g_key_mu;
+}  // namespace
+
+extern "C" int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out, int* d_pos, void* stream) {
+    if (!x || n < 1 || (!out_idx && !d_pos)) return RINA_ERR_ARG;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return RINA_ERR_HIP;
+    unsigned long long* key;
+    {
+        std::lock_guard<std::mutex> lk(g_key_mu);
+        if (!g_key_addr[dev]) {
+            void* p = nullptr;
+            if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_argmax_key)) != hipSuccess || !p) return RINA_ERR_HIP;
+            g_key_addr[dev] = (unsigned long long*)p;
+        }
+        key = g_key_addr[dev];
+    }
+    return argmax_launch(x, n, out_idx, ids_out, d_pos, key, as_stream(stream));
+}
+
+extern "C" int rina_hip_argmax_ws(const float* x, int n, int* out_idx, int* ids_out, int* d_pos, void* key_slot,
+                                  void* stream) {
+    if (!x || n < 1 || (!out_idx && !d_pos) || !key_slot || (uintptr_t)key_slot % 8) return RINA_ERR_ARG;
+    return argmax_launch(x, n, out_idx, ids_out, d_pos, (unsigned long long*)key_slot, as_stream(stream));
 }
 
 extern "C" const char* rina_hip_version(void) { return "rina-mi355x hip 0.1 (gfx950)"; }

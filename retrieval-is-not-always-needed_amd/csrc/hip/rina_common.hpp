@@ -161,9 +161,10 @@ static inline hipStream_t as_stream(void* s) { return (hipStream_t)s; }
 // Number of compute units of the current device (cached per device).
 int rina_num_cus();
 
-// Per-device scratch buffer owned by the library (grown on demand, never
-// shrunk).  Used only when a caller aliases input and output.
-void* rina_scratch(size_t bytes);
+// Scratch owned by the library, one buffer per (device, stream), grown on
+// demand and never shrunk.  Used only where a caller aliases input and
+// output, and for a norm that runs before a matvec as its own launch.
+void* rina_scratch(size_t bytes, hipStream_t stream);
 
 __device__ __forceinline__ int read_pos(int start_pos, const int* d_pos) {
     return start_pos + (d_pos ? *d_pos : 0);

@@ -113,3 +113,35 @@ def test_kv_pack_bitexact_from_model(rina, orc, tiny, kv_mode):
             want = orc.kv_quantize(fmt, rows)
             assert np.array_equal(cache[: want.size], want), "layer %d %s" % (layer, "V" if which else "K")
     eng.rina_infer_destroy(inf)
+
+
+def test_graph_recaptured_after_buffer_growth(rina):
+    """A decode graph captured at one activation capacity must not be
+    replayed after a longer prompt re-allocates the activations: generate
+    with a short prompt (graph captured), then with a prompt past the
+    512-row capacity on the same Inference; the tokens equal a fresh
+    Inference's, and a prompt id outside the vocabulary is rejected before
+    anything is launched."""
+    eng = rina.load_engine()
+    sm = synth(rina).SynthLlama(TINY, qt=rina.QT_Q4_0F, seed=5, max_seq=600)
+    try:
+        steps = 6
+        short = [3, 1, 4, 1, 5, 9, 2, 6]
+        long_prompt = list(np.random.default_rng(7).integers(0, TINY["vocab_size"], 530))
+        inf = sm.infer("q8")
+        out = (C.c_int * steps)()
+        rina.check(eng.rina_infer_generate(inf, (C.c_int * len(short))(*short), len(short), steps, out, 1,
+                                           stream(), None), "generate short")
+        first = list(out)
+        rina.check(eng.rina_infer_generate(inf, (C.c_int * len(long_prompt))(*long_prompt), len(long_prompt), steps,
+                                           out, 1, stream(), None), "generate long")
+        reused = list(out)
+        bad = list(short)
+        bad[3] = TINY["vocab_size"]
+        assert eng.rina_infer_generate(inf, (C.c_int * len(bad))(*bad), len(bad), 2, out, 1, stream(), None) == -1
+        assert "outside the vocabulary" in eng.rina_engine_last_error().decode()
+        eng.rina_infer_destroy(inf)
+        assert gen_gpu(rina, sm, "q8", long_prompt, steps, True) == reused
+        assert gen_gpu(rina, sm, "q8", short, steps, True) == first
+    finally:
+        sm.close()

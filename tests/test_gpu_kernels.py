@@ -536,9 +536,15 @@ def test_embedding(rina, orc, qt):
         w = wf if qt == 6 else orc.pack(qt, wf)
     ids = np.array([0, 299, -4, 17, 150], np.int32)
     od = empty(5 * d)
-    ok(hip.rina_hip_embedding(dev(w).data_ptr(), qt, dev(ids).data_ptr(), None, od.data_ptr(), 5, d, stream()))
+    ok(hip.rina_hip_embedding(dev(w).data_ptr(), qt, dev(ids).data_ptr(), None, od.data_ptr(), 5, d, 0, stream()))
     ref = np.zeros((5, d), np.float32)
     orc.load().orc_embedding(w.ctypes.data, qt, ids.ctypes.data, ref.ctypes.data, 5, d)
+    assert np.array_equal(host(od).reshape(5, d), ref)
+    # with the vocabulary bound, ids past the table are clamped to its last row
+    big = np.array([300, 7, 1 << 30, -1, 299], np.int32)
+    ok(hip.rina_hip_embedding(dev(w).data_ptr(), qt, dev(big).data_ptr(), None, od.data_ptr(), 5, d, V, stream()))
+    want = np.clip(big, 0, V - 1).astype(np.int32)
+    orc.load().orc_embedding(w.ctypes.data, qt, want.ctypes.data, ref.ctypes.data, 5, d)
     assert np.array_equal(host(od).reshape(5, d), ref)
 
 
@@ -567,6 +573,28 @@ def test_argmax(rina, orc):
     pos = dev(np.array([4], np.int32))
     ok(hip.rina_hip_argmax(dev(c3).data_ptr(), c3.size, None, ids.data_ptr(), pos.data_ptr(), stream()))
     assert int(host(pos)[0]) == 5 and int(host(ids)[5]) == 100
+
+
+def test_argmax_signed_zero_and_key_slots(rina, orc):
+    """+0 and -0 are equal under the reference's strict ">" (main.cpp:139-146),
+    so the lower index wins either way round; two caller key slots give each
+    call its own answer."""
+    hip = rina.load_hip()
+    cases = [np.array([-0.0, 0.0, -1.0], np.float32), np.array([0.0, -0.0], np.float32),
+             np.array([-3.0, -0.0, -1.0, 0.0], np.float32), np.full(2000, -0.0, np.float32)]
+    slots = empty(4, "int32")   # two 8-byte slots, zero
+    for i, a in enumerate(cases):
+        want = orc.load().orc_argmax(a.ctypes.data, a.size)
+        out = empty(1, "int32")
+        ok(hip.rina_hip_argmax(dev(a).data_ptr(), a.size, out.data_ptr(), None, None, stream()))
+        assert int(host(out)[0]) == want, (a[:4], want)
+        ok(hip.rina_hip_argmax_ws(dev(a).data_ptr(), a.size, out.data_ptr(), None, None,
+                                  slots.data_ptr() + 8 * (i % 2), stream()))
+        assert int(host(out)[0]) == want
+    assert not host(slots).any()   # each call leaves its slot zero
+    bad = hip.rina_hip_argmax_ws(dev(cases[0]).data_ptr(), 3, empty(1, "int32").data_ptr(), None, None,
+                                 slots.data_ptr() + 4, stream())
+    assert bad == -1   # misaligned slot rejected before launch
 
 
 @pytest.mark.parametrize("qt", [7, 5, 10, 6])

@@ -339,3 +339,46 @@ def test_mla_engine_full_width_greedy(rina, orc):
         assert list(out) == ref
     finally:
         sm.close()
+
+
+def test_mla_graph_recaptured_after_buffer_growth(rina, orc):
+    """The MLA Inference starts with 64 activation rows: a graph captured
+    after a short prompt must be dropped when a 70-token prompt grows them.
+    Tokens after the long prompt equal a fresh Inference's and the oracle's."""
+    synth = importlib.import_module("rina_amd.synth")
+    max_seq = 96
+    tensors, qts, mats = mt.build(seed=11, max_pos=max_seq)
+    up = {}
+    for nm, arr in tensors.items():
+        shp = list(shape_of(nm, arr, qts[nm]))
+        if shp[-1] == -1:
+            c = mt.CFG
+            shp[-1] = {"w_kv_b": c["dc"], "w_o": c["n_heads"] * c["v_dim"], "w2": c["dense_ffn"],
+                       "down_exps": c["expert_ffn"], "down_shexp": c["shared_ffn"]}.get(nm.split(".")[-2], c["dim"])
+        up[nm] = (qts[nm], tuple(shp), arr)
+    hm = synth.HostModel(header(max_seq), up)
+    try:
+        eng = rina.load_engine()
+        steps = 5
+        short = [3, 1, 4, 1, 5]
+        long_prompt = [int(x) for x in np.random.default_rng(2).integers(0, mt.CFG["vocab_size"], 70)]
+        out = (C.c_int * steps)()
+
+        def gen(inf, prompt):
+            rina.check(eng.rina_infer_generate(inf, (C.c_int * len(prompt))(*prompt), len(prompt), steps, out, 1,
+                                               stream(), None), "generate")
+            return list(out)
+
+        inf = hm.infer("mla", max_seq=max_seq)
+        gen(inf, short)
+        reused = gen(inf, long_prompt)
+        eng.rina_infer_destroy(inf)
+        fresh = hm.infer("mla", max_seq=max_seq)
+        assert gen(fresh, long_prompt) == reused
+        eng.rina_infer_destroy(fresh)
+        m, hold = orc.mla_from_tensors(mt.CFG, tensors, qts, max_seq)
+        ref = orc.mla_generate(m, long_prompt, steps)
+        orc.load().orc_mla_destroy(m)
+        assert reused == ref
+    finally:
+        hm.close()

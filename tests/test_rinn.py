@@ -87,7 +87,8 @@ def _write(path, cfg, tens, corrupt=None):
             corrupt(f)
 
 
-@pytest.mark.parametrize("case", ["missing", "magic", "index_count", "data_past_end", "qtype"])
+@pytest.mark.parametrize("case", ["missing", "magic", "index_count", "data_past_end", "qtype", "negative_dim",
+                                  "zero_dim", "overflow"])
 def test_load_errors(tmp_path, case):
     rina = load_pkg()
     eng = rina.load_engine()
@@ -95,7 +96,9 @@ def test_load_errors(tmp_path, case):
     tens = sample_tensors()
     path = str(tmp_path / "m.rinn")
     want = {"missing": "cannot open", "magic": "bad magic", "index_count": "tensor count",
-            "data_past_end": "past the end", "qtype": "unsupported quant_type"}[case]
+            "data_past_end": "past the end", "qtype": "unsupported quant_type",
+            "negative_dim": "non-positive or oversized", "zero_dim": "non-positive or oversized",
+            "overflow": "non-positive or oversized"}[case]
     if case == "magic":
         _write(path, cfg, tens, lambda f: f.write(b"RINX"))
     elif case == "index_count":
@@ -105,6 +108,14 @@ def test_load_errors(tmp_path, case):
         _write(path, cfg, [("transformer.wte.weight", (5000, 7000), QT_FP32, tens[0][3])] + tens[1:])
     elif case == "qtype":
         _write(path, cfg, [("transformer.h.0.x.weight", (256,), 10, np.zeros(84, np.uint8))] + tens)
+    elif case == "negative_dim":
+        # [-5, -7] has a positive product: the reader must look at each dim
+        _write(path, cfg, [("transformer.wte.weight", (-5, -7), QT_FP32, tens[0][3])] + tens[1:])
+    elif case == "zero_dim":
+        _write(path, cfg, [("transformer.wte.weight", (5, 0, 7), QT_FP32, tens[0][3])] + tens[1:])
+    elif case == "overflow":
+        big = (1 << 31) - 1
+        _write(path, cfg, [("transformer.wte.weight", (big, big, big, big), QT_FP32, tens[0][3])] + tens[1:])
     m = eng.rina_model_load(path.encode())
     assert not m
     assert want in eng.rina_engine_last_error().decode()
@@ -115,3 +126,68 @@ def test_load_directory_form_needs_weights_rinn(tmp_path):
     eng = rina.load_engine()
     assert not eng.rina_model_load(str(tmp_path).encode())          # a directory without weights.rinn
     assert "weights.rinn" in eng.rina_engine_last_error().decode()
+
+
+def _tiny_header(**kw):
+    h = {"name": "llama-tiny", "dim": 64, "n_layers": 1, "n_heads": 2, "n_kv_heads": 1, "head_dim": 32,
+         "vocab_size": 50, "max_seq_len": 16, "hidden_dim": 128, "layers": [{"type": "standard_attention"}]}
+    h.update(kw)
+    return h
+
+
+def _add_fake(eng, m, name, qt, shape):
+    """Register a tensor at a fake device address: no kernel reads it on the
+    CPU, the engine only borrows the pointer."""
+    import ctypes as C
+    shp = (C.c_int64 * len(shape))(*shape)
+    return eng.rina_model_add_tensor(m, name.encode(), qt, len(shape), shp, C.c_void_p(0x1000))
+
+
+def test_add_tensor_rejects_bad_shapes():
+    import json
+    eng = load_pkg().load_engine()
+    m = eng.rina_model_create(json.dumps(_tiny_header()).encode())
+    assert m
+    try:
+        for shape in ((-4, 16), (4, 0), (0,), (1 << 40, 1 << 20)):
+            assert _add_fake(eng, m, "transformer.wte.weight", QT_FP32, shape) == -1
+            assert "shape" in eng.rina_engine_last_error().decode()
+        assert _add_fake(eng, m, "transformer.wte.weight", QT_FP32, (50, 64)) == 0
+    finally:
+        eng.rina_model_destroy(m)
+
+
+@pytest.mark.parametrize("bad", [None, "transformer.h.0.attn.w_k.weight", "transformer.h.0.mlp.w2.weight",
+                                 "transformer.h.0.attn.rope.cos", "transformer.wte.weight"])
+def test_layer_init_checks_shapes(bad):
+    """A tensor smaller than its config implies fails Inference init (the
+    kernels would read past it); with every shape right, init gets past the
+    layers and fails only at the device allocation (no GPU here)."""
+    import json
+    eng = load_pkg().load_engine()
+    m = eng.rina_model_create(json.dumps(_tiny_header()).encode())
+    d, H, Hkv, dh, hd, V, S = 64, 2, 1, 32, 128, 50, 16
+    shapes = {"transformer.h.0.attn.w_q.weight": (H * dh, d), "transformer.h.0.attn.w_k.weight": (Hkv * dh, d),
+              "transformer.h.0.attn.w_v.weight": (Hkv * dh, d), "transformer.h.0.attn.w_o.weight": (d, H * dh),
+              "transformer.h.0.mlp.w1.weight": (hd, d), "transformer.h.0.mlp.w3.weight": (hd, d),
+              "transformer.h.0.mlp.w2.weight": (d, hd), "transformer.h.0.ln1.weight": (d,),
+              "transformer.h.0.ln2.weight": (d,), "transformer.h.0.attn.rope.cos": (S, dh // 2),
+              "transformer.h.0.attn.rope.sin": (S, dh // 2), "transformer.wte.weight": (V, d),
+              "transformer.ln_f.weight": (d,)}
+    try:
+        for name, shp in shapes.items():
+            if name == bad:
+                shp = (shp[0] - 1,) + tuple(shp[1:])
+            qt = QT_FP32 if ("ln" in name or "rope" in name or "wte" in name) else 7
+            assert _add_fake(eng, m, name, qt, shp) == 0
+        inf = eng.rina_infer_create(m, b"gqa", b"fp32", 0)
+        assert not inf
+        msg = eng.rina_engine_last_error().decode()
+        if bad is None:
+            assert "allocation failed" in msg, msg
+        elif bad == "transformer.wte.weight":
+            assert "wte" in msg, msg
+        else:
+            assert "layer init failed" in msg, msg
+    finally:
+        eng.rina_model_destroy(m)
