@@ -74,6 +74,56 @@ def roofline(bytes_per_launch, seconds, traffic=None):
             "frac": round(a / HBM_PEAK, 4), "traffic": traffic}
 
 
+def plain_read_time(torch, hip, st, nbytes, iters):
+    """Device time (s) of one launch that only streams nbytes from HBM: the
+    rina_hip_read_probe kernel over a ring of buffers larger than the
+    256 MB MALL, best of four grid sizes.  A kernel's ceiling_frac is this
+    time over its own at the same byte count."""
+    n = min(64, max(2, -(-640_000_000 // nbytes)))
+    ring = [torch.empty(nbytes // 4 + 4, device="cuda") for _ in range(n)]
+    sink = torch.empty(8192, device="cuda")
+    best = None
+    for grid in (256, 512, 1024, 2048):
+        t = time_kernel(torch, lambda i=0: hip.rina_hip_read_probe(ring[i % n].data_ptr(), nbytes, grid,
+                                                                   sink.data_ptr(), st), iters)
+        best = t if best is None else min(best, t)
+    del ring
+    return best
+
+
+def with_ceiling(roof, t_kernel, t_plain):
+    roof = dict(roof)
+    roof["plain_read_us"] = round(t_plain * 1e6, 3)
+    roof["ceiling_frac"] = round(t_plain / t_kernel, 4)
+    return roof
+
+
+_hiprt = None
+
+
+def d2h_f32(ptr, n):
+    """n floats of engine-owned device memory to a numpy array."""
+    global _hiprt
+    if _hiprt is None:
+        _hiprt = C.CDLL("libamdhip64.so")
+        _hiprt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        _hiprt.hipMemcpy.restype = C.c_int
+    out = np.empty(n, np.float32)
+    assert _hiprt.hipMemcpy(out.ctypes.data, ptr, n * 4, 2) == 0   # hipMemcpyDeviceToHost
+    return out
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_lm_head_fp32.json")
 COPY_BYTES = 512 << 20          # calibration copy: 512 MiB read + 512 MiB written (> the 256 MB MALL)
 
@@ -174,7 +224,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--no-config4", action="store_true", help="skip the DeepSeek MLA + MoE (config 4) decode line")
     ap.add_argument("--config4-steps", type=int, default=32)
@@ -247,6 +297,17 @@ def main():
                "note": "Q4 linears on v_mfma_f32_16x16x4f32 (fp32 products, fp32 sums); prompt attention "
                        "from position 0 in 64-position blocks (one softmax rescale per block)"}
     log("prefill: %d tokens in %.2f ms (%.0f tok/s)" % (args.prompt, pre_ms[-1], prefill["tokens_per_s"]))
+    # the GPU's K/V rows of the prompt, so the CPU baseline decodes at the
+    # GPU's positions from the same cache
+    cache_rows = []
+    if want_cpu:
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        torch.cuda.synchronize()
+        for layer in range(cfg["n_layers"]):
+            for which in (0, 1):
+                ptr, nb = C.c_void_p(), C.c_size_t()
+                rina.check(eng.rina_infer_kv_region(inf, layer, which, C.byref(ptr), C.byref(nb)), "kv region")
+                cache_rows.append(d2h_f32(ptr.value, args.prompt * kvd))
     eng.rina_infer_destroy(inf)
 
     # ---- dominant kernel: fp32 tied LM head GEMV (128256 x 2048), HIP events on our stream
@@ -258,8 +319,10 @@ def main():
     t_lm = time_kernel(torch, lambda i=0: hip.rina_hip_linear(wte.data_ptr(), rina.QT_FP32, x.data_ptr(), y.data_ptr(),
                                                               1, V, d, st), args.kernel_iters)
     traffic, traffic_detail = committed_traffic()
-    lm_roof = roofline(lm_bytes, t_lm, traffic)
-    log("lm_head fp32 GEMV: %.1f us, %.0f GB/s" % (t_lm * 1e6, lm_bytes / t_lm / 1e9))
+    lm_roof = with_ceiling(roofline(lm_bytes, t_lm, traffic), t_lm,
+                           plain_read_time(torch, hip, st, lm_bytes, max(4, args.kernel_iters // 5)))
+    log("lm_head fp32 GEMV: %.1f us, %.0f GB/s (plain read %.1f us)" %
+        (t_lm * 1e6, lm_bytes / t_lm / 1e9, lm_roof["plain_read_us"]))
 
     # ---- Q4_0F SwiGLU matvec over the model's own layers (ring > MALL)
     hd = cfg["hidden_dim"]
@@ -274,7 +337,7 @@ def main():
                                          rina.EPI_SWIGLU, rina.PRO_NONE, None, 0.0, st)
     t_sw = time_kernel(torch, swiglu, args.kernel_iters)
     sw_bytes = 2 * hd * d // 32 * 20 + d * 4 + hd * 4
-    sw_roof = roofline(sw_bytes, t_sw)
+    sw_roof = with_ceiling(roofline(sw_bytes, t_sw), t_sw, plain_read_time(torch, hip, st, sw_bytes, args.kernel_iters))
     log("Q4_0F W1/W3 SwiGLU matvec: %.1f us, %.0f GB/s" % (t_sw * 1e6, sw_bytes / t_sw / 1e9))
 
     # ---- prompt phase: the same W1/W3 SwiGLU at M = args.prompt rows on the
@@ -305,16 +368,59 @@ def main():
     t_q4 = time_kernel(torch, lambda i=0: hip.rina_hip_linear(ring[i % 64].data_ptr(), rina.QT_Q4_0, x1.data_ptr(),
                                                               y1.data_ptr(), 1, N1, K1, st), args.kernel_iters * 4)
     q4_bytes = N1 * K1 // 32 * 18 + K1 * 4 + N1 * 4
-    q4_roof = roofline(q4_bytes, t_q4)
-    log("config-1 Q4_0 GEMV: %.2f us, %.0f GB/s" % (t_q4 * 1e6, q4_bytes / t_q4 / 1e9))
     del ring
+    q4_roof = with_ceiling(roofline(q4_bytes, t_q4), t_q4, plain_read_time(torch, hip, st, q4_bytes, args.kernel_iters))
+    log("config-1 Q4_0 GEMV: %.2f us, %.0f GB/s (plain read %.2f us)" %
+        (t_q4 * 1e6, q4_bytes / t_q4 / 1e9, q4_roof["plain_read_us"]))
+
+    # ---- decode attention of one layer (RoPE, append, split + combine), the
+    # metric's other kernel: config 2's fp32 cache at position 530 and
+    # config 3's q8 cache at position 4095, over rings of caches larger than
+    # the MALL (as between the layers of a decode step)
+    attn_roofs = {}
+    H, Hkv, dh = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    kvd = Hkv * dh
+    for name, mode, pos, kb, vb in (("decode_attention_fp32_p530", 0, 530, 4.0, 4.0),
+                                    ("decode_attention_q8_p4095", 1, 4095, 34 / 32, 34 / 32)):
+        msq = pos + 8
+        region = int(hip.rina_hip_kv_region_bytes(mode, 0, msq, kvd))
+        nring = min(128, max(2, -(-640_000_000 // (2 * region))))
+        kc = [torch.zeros(region // 4 + 4, device="cuda") for _ in range(nring)]
+        vc = [torch.zeros(region // 4 + 4, device="cuda") for _ in range(nring)]
+        if mode:   # valid q8 blocks: pack random rows once, copy into every ring entry
+            rows = torch.randn(msq * kvd, device="cuda")
+            hip.rina_hip_kv_quantize(rina.KVF_Q8_0, rows.data_ptr(), kc[0].data_ptr(), msq * kvd, st)
+            hip.rina_hip_kv_quantize(rina.KVF_Q8_0, rows.data_ptr(), vc[0].data_ptr(), msq * kvd, st)
+        else:
+            kc[0].normal_()
+            vc[0].normal_()
+        for i in range(1, nring):
+            kc[i].copy_(kc[0])
+            vc[i].copy_(vc[0])
+        cos, sin = synth.make_rope(dh, msq, cfg.get("rope_theta", 500000.0))
+        cd, sd = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+        qa, ka, va = torch.randn(H * dh, device="cuda"), torch.randn(kvd, device="cuda"), torch.randn(kvd, device="cuda")
+        oa = torch.empty(H * dh, device="cuda")
+        wsb = int(hip.rina_hip_gqa_attention_workspace(1, H, dh, msq))
+        wsa = torch.empty(wsb // 4 + 4, device="cuda")
+        t_at = time_kernel(torch, lambda i=0: hip.rina_hip_gqa_decode_attention(
+            qa.data_ptr(), ka.data_ptr(), va.data_ptr(), cd.data_ptr(), sd.data_ptr(), cd.data_ptr(), sd.data_ptr(),
+            kc[i % nring].data_ptr(), vc[i % nring].data_ptr(), mode, H, Hkv, dh, pos, None, msq, oa.data_ptr(), None,
+            wsa.data_ptr(), wsb, st), args.kernel_iters)
+        at_bytes = int(pos * kvd * (kb + vb)) + (2 * H * dh + 2 * kvd) * 4
+        attn_roofs[name] = dict(with_ceiling(roofline(at_bytes, t_at), t_at,
+                                             plain_read_time(torch, hip, st, at_bytes, args.kernel_iters)),
+                                bytes_per_launch=at_bytes, avg_us=round(t_at * 1e6, 3),
+                                note="RoPE + append + split-sequence attention + chunk merge, two launches")
+        log("%s: %.2f us, %.0f GB/s" % (name, t_at * 1e6, at_bytes / t_at / 1e9))
+        del kc, vc
 
     # ---- config 4: DeepSeek-V2-Lite-shaped MLA + MoE decode, random Q2_K weights
     cfg4 = None
     if not args.no_config4:
         t4 = time.time()
-        p4, s4 = 32, args.config4_steps
-        ds = synth.SynthDeepSeek(seed=1, max_seq=max(2048, p4 + s4 + 8))   # context 2048
+        p4, s4 = 2040, args.config4_steps   # context 2048: decode steps at positions 2041..
+        ds = synth.SynthDeepSeek(seed=1, max_seq=p4 + s4 + 8)
         log("config 4 model built in %.1fs" % (time.time() - t4))
         inf4 = ds.infer()
         pr4 = np.random.default_rng(4).integers(0, ds.cfg["vocab_size"], p4).astype(np.int32)
@@ -331,7 +437,9 @@ def main():
         b4 = ds.bytes_per_token(p4 + 1 + s4 // 2)
         cfg4 = {"workload": "DeepSeek-V2-Lite-shaped MLA + MoE decode: 27 layers (1 dense + 26 MoE, 64 experts top-6 "
                             "of 1408, 2 shared), d 2048, 16 heads, kv_lora_rank 512, rope 64, vocab 102400, random "
-                            "Q2_K weights, latent fp32 cache of 2048 positions, %d-token prompt, greedy" % p4,
+                            "zero-mean Q2_K weights, latent fp32 cache, %d-token seeded prompt (prefill untimed), "
+                            "greedy steps at positions %d..%d" % (p4, p4 + 1, p4 + s4),
+                "latent_kv_bytes_per_token": ds.cfg["n_layers"] * (p4 + 1 + s4 // 2) * (ds.cfg["dc"] + ds.cfg["rope"]) * 4,
                 "tokens_per_s": round(s4 / w4, 2), "ms_per_step": round(w4 * 1e3 / s4, 4), "steps": s4,
                 "bytes_per_token": b4, "hbm_gbps": round(b4 * s4 / w4 / 1e9, 1),
                 "hbm_frac": round(b4 * s4 / w4 / HBM_PEAK, 4), "tokens_head": list(first4) + list(out4)[:6]}
@@ -343,8 +451,8 @@ def main():
     # ---- config 5: RINA Gen6 Jamba hybrid, 64-token prompt then 128 greedy steps
     cfg5 = None
     if not args.no_config5:
-        p5, s5 = 64, 128
-        jm = synth.SynthJamba(seed=1, max_seq=max(2048, p5 + s5 + 8))   # context 2048
+        p5, s5 = 1900, 128   # context 2048: steps at positions 1901..2028
+        jm = synth.SynthJamba(seed=1, max_seq=2048)
         inf5 = jm.infer()
         pr5 = np.random.default_rng(5).integers(0, jm.cfg["vocab_size"], p5).astype(np.int32)
         # two generated tokens: the second step captures the decode graph
@@ -362,7 +470,8 @@ def main():
         b5 = jm.bytes_per_token(p5 + 1 + s5 // 2)
         cfg5 = {"workload": "RINA Gen6 Jamba hybrid at random init: 640d, 16 layers (12 InertiaWave SSM + 4 RINA-MLA), "
                             "10/5 heads, d_c 160, LayerNorm + SwiGLU 1536, vocab 128256, Q4_0 linears, fp32 tied LM "
-                            "head, context 2048, %d-token prompt, %d greedy steps" % (p5, s5),
+                            "head, context 2048, %d-token seeded prompt (prefill untimed), %d greedy steps at "
+                            "positions %d..%d" % (p5, s5, p5 + 1, p5 + s5),
                 "tokens_per_s": round(s5 / w5, 2), "ms_per_step": round(w5 * 1e3 / s5, 4), "steps": s5,
                 "bytes_per_token": b5, "hbm_gbps": round(b5 * s5 / w5 / 1e9, 1),
                 "hbm_frac": round(b5 * s5 / w5 / HBM_PEAK, 4), "tokens_head": list(first5) + list(out5)[:7]}
@@ -408,29 +517,59 @@ def main():
                             "%d..%d), Q4_0F linears, fp32 tied LM head, KV cache q8 / q4 / q2k_q1v" % (n3 + 2, n3 + 1 + s3),
                 "steps": s3, "modes": modes}
 
-    # ---- CPU baseline: the oracle (scalar C restatement) decoding the same model
+    # ---- CPU baseline: the oracle (scalar C restatement of the reference's
+    # loops) decoding the same model at the GPU's positions: it takes the
+    # GPU's prompt K/V rows and first token, then decodes greedily; timed on
+    # the job's CPU share (all of it) and on one core.
     cpu = None
     if want_cpu:
         sys.path.insert(0, ROOT)
         import oracle
-        nthreads = min(os.cpu_count() or 1, 16)
-        m, hold = oracle.gqa_from_tensors(cfg, sm.host, sm.qt, 64, "fp32", nthreads)
+        try:
+            share = len(os.sched_getaffinity(0))
+        except AttributeError:
+            share = os.cpu_count() or 1
+        cores = max(1, min(share, 16))   # this pool gives one GPU job a 16-core CPU share
         L = oracle.load()
-        p8 = np.ascontiguousarray(prompt[:8])
-        lg = np.zeros(V, np.float32)
-        L.orc_gqa_forward(m, p8.ctypes.data, 8, 0, lg.ctypes.data, 1)
-        tok = np.array([int(np.argmax(lg))], np.int32)
-        tc = time.perf_counter()
-        for s in range(args.cpu_steps):
-            L.orc_gqa_forward(m, tok.ctypes.data, 1, 8 + s, lg.ctypes.data, 1)
-            tok[0] = L.orc_argmax(lg.ctypes.data, V)
-        dt = time.perf_counter() - tc
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        ms_cpu = args.prompt + 16
+
+        def cpu_model_at_prompt(nthreads):
+            m, hold = oracle.gqa_from_tensors(cfg, sm.host, sm.qt, ms_cpu, "fp32", nthreads)
+            for layer in range(cfg["n_layers"]):
+                for which in (0, 1):
+                    onb = C.c_size_t()
+                    optr = L.orc_gqa_cache(m, layer, which, C.byref(onb))
+                    src = cache_rows[2 * layer + which]
+                    C.memmove(optr, src.ctypes.data, src.nbytes)
+            return m, hold
+
+        def decode(m, steps):
+            lg = np.zeros(V, np.float32)
+            tok = np.array([tokens[0]], np.int32)
+            ids = []
+            tc = time.perf_counter()
+            for k in range(steps):
+                L.orc_gqa_forward(m, tok.ctypes.data, 1, args.prompt + k, lg.ctypes.data, 1)
+                tok[0] = L.orc_argmax(lg.ctypes.data, V)
+                ids.append(int(tok[0]))
+            return time.perf_counter() - tc, ids
+
+        m, hold = cpu_model_at_prompt(cores)
+        dt, ids_cpu = decode(m, args.cpu_steps)
         L.orc_gqa_destroy(m)
-        cpu = {"value": round(args.cpu_steps / dt, 3), "unit": "tokens/s", "cores": nthreads, "kind": "port",
-               "sample": "%d greedy decode steps of the same model at positions 8..%d after an 8-token prefill "
-                         "(weights dominate: 1.66 GB/token; the p~550 fp32 KV adds 36 MB/token)"
-                         % (args.cpu_steps, 8 + args.cpu_steps - 1)}
-        log("cpu oracle: %.3f tok/s on %d threads" % (cpu["value"], nthreads))
+        m1, hold1 = cpu_model_at_prompt(1)
+        dt1, _ = decode(m1, 1)
+        L.orc_gqa_destroy(m1)
+        cpu = {"value": round(args.cpu_steps / dt, 4), "unit": "tokens/s", "cores": cores, "kind": "port",
+               "value_1core": round(1.0 / dt1, 4), "cpu_model": cpu_model(), "host_cores_visible": os.cpu_count(),
+               "matches_gpu_tokens": ids_cpu == tokens[1:1 + args.cpu_steps],
+               "sample": "%d greedy decode steps (and 1 step on one core) of the same config-2 model at the GPU's "
+                         "positions %d..%d, the oracle starting from the GPU's %d prompt K/V rows and first token "
+                         "(1.66 GB of weights and ~34 MB of fp32 KV per token)"
+                         % (args.cpu_steps, args.prompt, args.prompt + args.cpu_steps - 1, args.prompt)}
+        log("cpu oracle: %.3f tok/s on %d threads, %.3f tok/s on 1 (%s)" %
+            (cpu["value"], cores, cpu["value_1core"], cpu["cpu_model"]))
 
     per_token = sm.weight_bytes_per_token() + cfg["n_layers"] * 2 * (args.prompt + args.warmup + args.steps // 2) * \
         cfg["n_kv_heads"] * cfg["head_dim"] * 4
@@ -458,6 +597,7 @@ def main():
             "config1_q4_0_gemv_8192x2048": dict(q4_roof, bytes_per_launch=q4_bytes, avg_us=round(t_q4 * 1e6, 3)),
             "prefill_q4_0f_swiglu_m%d" % Mp: dict(swp_roof, flop_per_launch=swp_flop, avg_us=round(t_swp * 1e6, 2),
                                                   kernel="gemm_mfma_kernel (v_mfma_f32_16x16x4f32)"),
+            **attn_roofs,
         },
         "decode_hbm_gbps": round(per_token * tok_s / 1e9, 1),
         "decode_hbm_frac": round(per_token * tok_s / HBM_PEAK, 4),

@@ -385,6 +385,13 @@ int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out,
 int rina_hip_argmax_ws(const float* x, int n, int* out_idx, int* ids_out,
                        int* d_pos, void* key_slot, void* stream);
 
+/* Measurement helper, no counterpart in the reference: one launch of
+ * `grid` 256-thread workgroups that stream-reads bytes (rounded down to
+ * 16) of src (16-byte aligned) and writes grid floats to sink.  Its time
+ * is the plain-read ceiling the benchmark sets next to each matvec of the
+ * same byte count. */
+int rina_hip_read_probe(const void* src, int64_t bytes, int grid, float* sink, void* stream);
+
 /* Library version / self-description. */
 const char* rina_hip_version(void);
 

@@ -115,6 +115,8 @@ def load(build=True):
         "orc_mla_forward": (I32, [VP, VP, I32, I32, VP, I32]),
         "orc_mla_generate": (I32, [VP, VP, I32, I32, VP]),
         "orc_mla_cache": (VP, [VP, I32, I32]),
+        "orc_mla_load_latent": (I32, [VP, I32, VP, I32]),
+        "orc_mla_set_latent_tap": (None, [VP, VP]),
     }
     for n, (r, a) in sigs.items():
         f = getattr(L, n)

@@ -206,6 +206,41 @@ static inline float q2k_value(const uint8_t* w, int64_t elem) {
     return fmaf(scale_val, (float)q, -min_val);  /* exact products: one rounding */
 }
 
+/* Elements e0 .. e0+n-1 of the flat Q2_K stream, q2k_value's arithmetic
+ * with each block's fp16 fields and 16 scale / min products formed once. */
+static void q2k_range(const uint8_t* w, int64_t e0, int64_t n, float* out) {
+    int64_t e = e0;
+    const int64_t end = e0 + n;
+    while (e < end) {
+        const int64_t blk = e / 256;
+        const int in0 = (int)(e - blk * 256);
+        const int in1 = end - blk * 256 < 256 ? (int)(end - blk * 256) : 256;
+        const uint8_t* bd = w + blk * 84;
+        if (in0 == 0 && in1 == 256) {
+            const float dall = ld_f16(bd + 80), dmin = ld_f16(bd + 82);
+            float sv[16], mv[16];
+            for (int i = 0; i < 16; i++) {
+                sv[i] = dall * (float)(bd[i] & 0xF);
+                mv[i] = dmin * (float)(bd[i] >> 4);
+            }
+            /* the same elements in runs of 16 that share one scale byte */
+            for (int page = 0; page < 2; page++)
+                for (int g = 0; g < 4; g++)
+                    for (int half = 0; half < 2; half++) {
+                        const int is = 8 * page + half + 2 * g;
+                        const float sc = sv[is], mn = -mv[is];
+                        const uint8_t* qs = bd + 16 + page * 32 + half * 16;
+                        float* o = out + page * 128 + g * 32 + half * 16;
+                        for (int l = 0; l < 16; l++) o[l] = fmaf(sc, (float)((qs[l] >> (2 * g)) & 3), mn);
+                    }
+            out += 256;
+        } else {
+            for (int j = in0; j < in1; j++) *out++ = q2k_value(w, blk * 256 + j);
+        }
+        e = blk * 256 + in1;
+    }
+}
+
 static inline float q4_value(const uint8_t* blk, int i, float scale, int off) {
     int q = (blk[off + (i >> 1)] >> ((i & 1) << 2)) & 0xF;
     return (float)(q - 7) * scale;
@@ -227,7 +262,7 @@ void orc_dequant_weights(const void* wv, int qt, int64_t n, float* out) {
             }
             break;
         case ORC_GGML_Q2_K:
-            for (int64_t e = 0; e < n; e++) out[e] = q2k_value(w, e);
+            q2k_range(w, 0, n, out);
             break;
         default:
             memcpy(out, wv, (size_t)n * 4);
@@ -269,8 +304,7 @@ static void weight_row(const uint8_t* w, int qt, int64_t n, int K, float* row) {
             break;
         }
         case ORC_GGML_Q2_K: {
-            int64_t e0 = n * (int64_t)K;
-            for (int i = 0; i < K; i++) row[i] = q2k_value(w, e0 + i);
+            q2k_range(w, n * (int64_t)K, K, row);
             break;
         }
         default:
@@ -290,8 +324,38 @@ static void* lin_worker(void* arg) {
     lin_job* j = (lin_job*)arg;
     int64_t per = ((int64_t)j->N + j->nt - 1) / j->nt;
     int64_t a = per * j->t, b = a + per < j->N ? a + per : j->N;
-    float* row = (float*)malloc((size_t)j->K * 4);
     const int K = j->K;
+    if (j->M == 1) {
+        /* four rows at a time: four independent chains, each in k order */
+        float* rows = (float*)malloc((size_t)K * 4 * 4);
+        const float* x = j->in;
+        for (int64_t n = a; n < b; n += 4) {
+            const int nr = b - n < 4 ? (int)(b - n) : 4;
+            for (int r = 0; r < nr; r++) weight_row(j->w, j->qt, n + r, K, rows + (size_t)r * K);
+            if (nr == 4) {
+                float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+                const float *r0 = rows, *r1 = rows + K, *r2 = rows + 2 * (size_t)K, *r3 = rows + 3 * (size_t)K;
+                for (int k = 0; k < K; k++) {
+                    const float xv = x[k];
+                    a0 = fmaf(r0[k], xv, a0);
+                    a1 = fmaf(r1[k], xv, a1);
+                    a2 = fmaf(r2[k], xv, a2);
+                    a3 = fmaf(r3[k], xv, a3);
+                }
+                j->out[n] = a0; j->out[n + 1] = a1; j->out[n + 2] = a2; j->out[n + 3] = a3;
+            } else {
+                for (int r = 0; r < nr; r++) {
+                    float acc = 0.f;
+                    const float* rr = rows + (size_t)r * K;
+                    for (int k = 0; k < K; k++) acc = fmaf(rr[k], x[k], acc);
+                    j->out[n + r] = acc;
+                }
+            }
+        }
+        free(rows);
+        return NULL;
+    }
+    float* row = (float*)malloc((size_t)j->K * 4);
     for (int64_t n = a; n < b; n++) {
         weight_row(j->w, j->qt, n, K, row);
         for (int m0 = 0; m0 < j->M; m0 += 8) {
@@ -807,7 +871,10 @@ struct orc_mla {
     orc_mla_layer_w* layers;
     float* cache;      /* [L][max_seq*(rope + H*nope + H*v)] */
     size_t per_layer;
+    float* latent_tap; /* optional [L][max_seq][dc + rope]: records of the rows forward() stores */
 };
+
+void orc_mla_set_latent_tap(orc_mla* m, float* tap) { m->latent_tap = tap; }
 
 orc_mla* orc_mla_create(const orc_mla_cfg* cfg) {
     orc_mla* m = (orc_mla*)calloc(1, sizeof(orc_mla));
@@ -836,6 +903,34 @@ const float* orc_mla_cache(orc_mla* m, int layer, int which) {
     return base + (size_t)c->max_seq * c->n_heads * c->nope;
 }
 
+/* Positions 0..n_pos-1 of one layer's cache from latent records
+ * [c (dc) | k_pe (rope)] (the c of a record is RMSNorm(c_kv)*k_norm, the
+ * k_pe is already rotated): the same rows orc_mla_forward stores for those
+ * positions (deepseek_mla_layer.cu:196,221-228): k_pe as is, and
+ * [K_nope | V] = W_kv_b c through orc_linear. */
+int orc_mla_load_latent(orc_mla* m, int layer, const float* rec, int n_pos) {
+    const orc_mla_cfg* c = &m->c;
+    if (layer < 0 || layer >= c->n_layers || n_pos < 0 || n_pos > c->max_seq) return -3;
+    const int H = c->n_heads, nope = c->nope, rope = c->rope, vd = c->v_dim, dc = c->dc, R = dc + rope;
+    const orc_mla_layer_w* L = &c->layers[layer];
+    if (!n_pos) return 0;
+    float* Cn = (float*)malloc((size_t)n_pos * dc * 4);
+    float* KVB = (float*)malloc((size_t)n_pos * H * (nope + vd) * 4);
+    for (int p = 0; p < n_pos; p++) memcpy(Cn + (size_t)p * dc, rec + (size_t)p * R, (size_t)dc * 4);
+    int rc = orc_linear(L->w_kv_b, L->qt_kv_b, Cn, KVB, n_pos, H * (nope + vd), dc, c->nthreads);
+    float* kpe_c = (float*)orc_mla_cache(m, layer, 0);
+    float* kn_c = (float*)orc_mla_cache(m, layer, 1);
+    float* v_c = (float*)orc_mla_cache(m, layer, 2);
+    for (int p = 0; p < n_pos && !rc; p++) {
+        memcpy(kpe_c + (size_t)p * rope, rec + (size_t)p * R + dc, (size_t)rope * 4);
+        memcpy(kn_c + (size_t)p * H * nope, KVB + (size_t)p * H * (nope + vd), (size_t)H * nope * 4);
+        memcpy(v_c + (size_t)p * H * vd, KVB + (size_t)p * H * (nope + vd) + (size_t)H * nope, (size_t)H * vd * 4);
+    }
+    free(Cn);
+    free(KVB);
+    return rc;
+}
+
 /* SwiGLU block: out[d] = W_down(silu(W_gate x) * (W_up x)) */
 static void swiglu_rows(const void* wg, const void* wu, int qt_gu, const void* wd, int qt_d,
                         const float* x, float* out, int T, int d, int hid, int nt) {
@@ -846,6 +941,41 @@ static void swiglu_rows(const void* wg, const void* wu, int qt_gu, const void* w
     orc_silu_mul(g, g, u, T * hid);
     orc_linear(wd, qt_d, g, out, T, d, hid, nt);
     free(g); free(u);
+}
+
+typedef struct {
+    const float *Q, *kn_c, *kpe_c, *v_c;
+    float* att;
+    int H, nope, rope, vd, T, start_pos, w, nw;
+    float *Kh, *Vh;    /* NULL: the worker allocates its own */
+    int ms;
+} mla_head_job;
+
+/* heads w, w + nw, ... of one layer's attention (orc_mla_forward) */
+static void* mla_head_worker(void* arg) {
+    mla_head_job* j = (mla_head_job*)arg;
+    const int H = j->H, nope = j->nope, rope = j->rope, vd = j->vd, dq = nope + rope;
+    float* Kh = j->Kh ? j->Kh : (float*)malloc((size_t)j->ms * dq * 4);
+    float* Vh = j->Vh ? j->Vh : (float*)malloc((size_t)j->ms * vd * 4);
+    float qv[1024];
+    const int last = j->start_pos + j->T;
+    for (int hh = j->w; hh < H; hh += j->nw) {
+        for (int p = 0; p < last; p++) {
+            memcpy(Kh + (size_t)p * dq, j->kn_c + (size_t)p * H * nope + (size_t)hh * nope, (size_t)nope * 4);
+            memcpy(Kh + (size_t)p * dq + nope, j->kpe_c + (size_t)p * rope, (size_t)rope * 4);
+            memcpy(Vh + (size_t)p * vd, j->v_c + (size_t)p * H * vd + (size_t)hh * vd, (size_t)vd * 4);
+        }
+        for (int t = 0; t < j->T; t++) {
+            const float* qrow = j->Q + (size_t)t * H * dq;
+            memcpy(qv, qrow + (size_t)hh * nope, (size_t)nope * 4);
+            memcpy(qv + nope, qrow + (size_t)H * nope + (size_t)hh * rope, (size_t)rope * 4);
+            orc_attn_rows(qv, dq, Kh, dq, Vh, vd, j->att + (size_t)t * H * vd + (size_t)hh * vd, vd,
+                          j->start_pos + t, 1, dq, vd);
+        }
+    }
+    if (!j->Kh) free(Kh);
+    if (!j->Vh) free(Vh);
+    return NULL;
 }
 
 int orc_mla_forward(orc_mla* m, const int* ids, int T, int start_pos, float* logits, int last_only) {
@@ -863,7 +993,6 @@ int orc_mla_forward(orc_mla* m, const int* ids, int T, int start_pos, float* log
     float* tmp = (float*)malloc((size_t)T * d * 4);
     float* Kh = (float*)malloc((size_t)ms * dq * 4);
     float* Vh = (float*)malloc((size_t)ms * vd * 4);
-    float qv[1024];
     orc_embedding(c->wte, c->qt_wte, ids, h, T, d);
     for (int l = 0; l < c->n_layers; l++) {
         const orc_mla_layer_w* L = &c->layers[l];
@@ -886,25 +1015,30 @@ int orc_mla_forward(orc_mla* m, const int* ids, int T, int start_pos, float* log
                 orc_rope_neox(kpe, L->rope_cos, L->rope_sin, 1, 1, rope, pos);
             }
             memcpy(kpe_c + (size_t)pos * rope, kpe, (size_t)rope * 4);
+            if (m->latent_tap) {
+                float* r = m->latent_tap + ((size_t)l * ms + pos) * (dc + rope);
+                memcpy(r, Cn + (size_t)t * dc, (size_t)dc * 4);
+                memcpy(r + dc, kpe, (size_t)rope * 4);
+            }
             memcpy(kn_c + (size_t)pos * H * nope, KVB + (size_t)t * H * (nope + vd), (size_t)H * nope * 4);
             memcpy(v_c + (size_t)pos * H * vd, KVB + (size_t)t * H * (nope + vd) + (size_t)H * nope,
                    (size_t)H * vd * 4);
         }
-        /* attention per head over keys 0..pos: K = [K_nope | k_pe], V, scale rsqrt(dq) */
-        for (int hh = 0; hh < H; hh++) {
-            const int last = start_pos + T;
-            for (int j = 0; j < last; j++) {
-                memcpy(Kh + (size_t)j * dq, kn_c + (size_t)j * H * nope + (size_t)hh * nope, (size_t)nope * 4);
-                memcpy(Kh + (size_t)j * dq + nope, kpe_c + (size_t)j * rope, (size_t)rope * 4);
-                memcpy(Vh + (size_t)j * vd, v_c + (size_t)j * H * vd + (size_t)hh * vd, (size_t)vd * 4);
+        /* attention per head over keys 0..pos: K = [K_nope | k_pe], V, scale
+         * rsqrt(dq); heads are independent and run on the worker threads */
+        {
+            mla_head_job jobs[64];
+            pthread_t th[64];
+            int nth = nt > 0 ? nt : orc_num_threads();
+            if (nth > H) nth = H;
+            if (nth > 64) nth = 64;
+            for (int w = 0; w < nth; w++) {
+                jobs[w] = (mla_head_job){Q, kn_c, kpe_c, v_c, att, H, nope, rope, vd, T, start_pos, w, nth,
+                                         w == 0 ? Kh : NULL, w == 0 ? Vh : NULL, ms};
+                if (w) pthread_create(&th[w], NULL, mla_head_worker, &jobs[w]);
             }
-            for (int t = 0; t < T; t++) {
-                const float* qrow = Q + (size_t)t * H * dq;
-                memcpy(qv, qrow + (size_t)hh * nope, (size_t)nope * 4);
-                memcpy(qv + nope, qrow + (size_t)H * nope + (size_t)hh * rope, (size_t)rope * 4);
-                orc_attn_rows(qv, dq, Kh, dq, Vh, vd, att + (size_t)t * H * vd + (size_t)hh * vd, vd,
-                              start_pos + t, 1, dq, vd);
-            }
+            mla_head_worker(&jobs[0]);
+            for (int w = 1; w < nth; w++) pthread_join(th[w], NULL);
         }
         orc_linear(L->w_o, L->qt_o, att, tmp, T, d, H * vd, nt);               /* :271 (out of place) */
         orc_add(h, h, tmp, T * d);

@@ -203,6 +203,14 @@ int      orc_mla_generate(orc_mla* m, const int* prompt, int n_prompt, int steps
 /* the expanded cache of one layer: k_pe [max_seq][rope], k_nope
  * [max_seq][H*nope], v [max_seq][H*v] (which: 0, 1, 2) */
 const float* orc_mla_cache(orc_mla* m, int layer, int which);
+/* Load cache positions 0..n_pos-1 of one layer from latent records
+ * rec [n_pos][dc + rope] = [RMSNorm(c_kv)*k_norm | RoPE(k_pe)] (the GPU
+ * engine's cache layout): k_pe copied, K_nope and V expanded through
+ * W_kv_b exactly as orc_mla_forward stores its own rows. */
+int orc_mla_load_latent(orc_mla* m, int layer, const float* rec, int n_pos);
+/* Test hook: tap [n_layers][max_seq][dc + rope] receives the latent record
+ * of every row orc_mla_forward stores (NULL: off). */
+void orc_mla_set_latent_tap(orc_mla* m, float* tap);
 
 /* ---- RINA Jamba hybrid (SSM + RINA-MLA layers, GQAInference) -------- */
 enum { ORC_JAMBA_SSM = 0, ORC_JAMBA_RMLA = 1 };

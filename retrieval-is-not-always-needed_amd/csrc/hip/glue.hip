@@ -157,6 +157,27 @@ __global__ void argmax_finish_kernel(int* out_idx, int* ids_out, int* d_pos, uns
     }
 }
 
+// Streaming-read probe: every lane sums 16-byte non-temporal loads of its
+// grid-stride slice, four in flight; one float per workgroup is written so
+// the loads cannot be dropped.  Measures what a plain read of `bytes`
+// costs in one launch (the ceiling a matvec of the same size could reach).
+__global__ __launch_bounds__(256) void read_probe_kernel(const f32x4* src, int64_t n4, float* sink) {
+    __shared__ float red[4];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    float acc = 0.f;
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+        const f32x4 a = gld_nt(src + i), b = gld_nt(src + i + stride), c = gld_nt(src + i + 2 * stride),
+                    d = gld_nt(src + i + 3 * stride);
+        acc += (a.x + b.y) + (c.z + d.w);
+    }
+    for (; i < n4; i += stride) acc += gld_nt(src + i).x;
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
 struct DevState {
@@ -312,6 +333,14 @@ extern "C" int rina_hip_argmax_ws(const float* x, int n, int* out_idx, int* ids_
                                   void* stream) {
     if (!x || n < 1 || (!out_idx && !d_pos) || !key_slot || (uintptr_t)key_slot % 8) return RINA_ERR_ARG;
     return argmax_launch(x, n, out_idx, ids_out, d_pos, (unsigned long long*)key_slot, as_stream(stream));
+}
+
+extern "C" int rina_hip_read_probe(const void* src, int64_t bytes, int grid, float* sink, void* stream) {
+    if (!src || !sink || bytes < 16 || grid < 1 || (uintptr_t)src % 16) return RINA_ERR_ARG;
+    hipLaunchKernelGGL(read_probe_kernel, dim3(grid), dim3(256), 0, as_stream(stream), (const f32x4*)src, bytes / 16,
+                       sink);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
 }
 
 extern "C" const char* rina_hip_version(void) { return "rina-mi355x hip 0.1 (gfx950)"; }

@@ -33,18 +33,29 @@ def normal(seed, n, std):
     return (np.random.default_rng(seed).standard_normal(n, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
 
+def q2k_scales(target_std):
+    """fp16 (d, dmin) of the zero-mean Q2_K blocks below: with the min nibble
+    equal to the scale nibble sc and dmin = 1.5 d, an element is
+    d*sc*q - 1.5*d*sc = d*sc*(q - 1.5), symmetric around 0 for uniform
+    2-bit q.  Its rms over uniform sc in 0..15 is d*sqrt(77.5*1.25) = 9.84 d."""
+    d = np.float16(target_std / 9.84)
+    return d, np.float16(np.float32(d) * np.float32(1.5))
+
+
 def random_q2k(seed, n_elems, target_std=0.02):
-    """Random valid Q2_K blocks (84 B / 256 values): random 4-bit scale and
-    min nibbles, random 2-bit q, fp16 d / dmin sized so the values have
-    roughly target_std spread (the reference ships no Q2_K quantizer)."""
+    """Random valid Q2_K blocks (84 B / 256 values) with zero-mean values:
+    random 4-bit scale nibbles, each sub-block's min nibble equal to its
+    scale nibble, random 2-bit q, fp16 d / dmin from q2k_scales (the
+    reference ships no Q2_K quantizer).  Uniform independent min nibbles
+    would give every weight a mean of about +0.6 of its spread, and a random
+    model built from them emits the same token at every step."""
     nb = (n_elems + 255) // 256
     rng = np.random.default_rng(seed)
     blk = np.zeros((nb, 84), np.uint8)
-    blk[:, 0:16] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    sc = rng.integers(0, 16, (nb, 16), dtype=np.uint8)
+    blk[:, 0:16] = sc | (sc << 4)
     blk[:, 16:80] = rng.integers(0, 256, (nb, 64), dtype=np.uint8)
-    # value = d*sc*q - dmin*m, sc,m in 0..15, q in 0..3: std ~ d*7.5*1.1
-    d = np.float16(target_std / 8.0)
-    dmin = np.float16(target_std / 16.0)
+    d, dmin = q2k_scales(target_std)
     blk[:, 80:82] = np.frombuffer(np.array([d], np.float16).tobytes(), np.uint8)
     blk[:, 82:84] = np.frombuffer(np.array([dmin], np.float16).tobytes(), np.uint8)
     return blk.reshape(-1)
@@ -265,13 +276,17 @@ DSV2_LITE = dict(name="deepseek-v2-lite", dim=2048, n_layers=27, n_heads=16, nop
 
 
 def q2k_device(n_elems, seed, std=0.02):
-    """Random valid Q2_K blocks generated on the device (see random_q2k)."""
+    """Random valid zero-mean Q2_K blocks generated on the device (the rule
+    of random_q2k)."""
     torch = _torch()
     nb = (n_elems + 255) // 256
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     blk = torch.randint(0, 256, (nb, 84), dtype=torch.uint8, device="cuda", generator=g)
-    dd = np.frombuffer(np.array([std / 8.0, std / 16.0], np.float16).tobytes(), np.uint8)
+    sc = blk[:, 0:16] & 15
+    blk[:, 0:16] = sc | (sc << 4)
+    d, dmin = q2k_scales(std)
+    dd = np.frombuffer(np.array([d, dmin], np.float16).tobytes(), np.uint8)
     blk[:, 80:84] = torch.from_numpy(dd.copy()).cuda()
     return blk.reshape(-1)
 

@@ -13,11 +13,17 @@ CFG = dict(dim=256, n_layers=3, n_heads=4, nope=32, rope=16, v_dim=32, dc=64, vo
 
 
 def q2k_random(r, n, std=0.05):
+    """Zero-mean Q2_K blocks: min nibble = scale nibble, dmin = 1.5 d, so an
+    element is d*sc*(q - 1.5) (the rule of rina_amd.synth.random_q2k)."""
     nb = (n + 255) // 256
     blk = np.zeros((nb, 84), np.uint8)
     blk[:, 0:80] = r.integers(0, 256, (nb, 80), dtype=np.uint8)
-    blk[:, 80:82] = np.frombuffer(np.array([std / 8], np.float16).tobytes(), np.uint8)
-    blk[:, 82:84] = np.frombuffer(np.array([std / 16], np.float16).tobytes(), np.uint8)
+    sc = blk[:, 0:16] & 15
+    blk[:, 0:16] = sc | (sc << 4)
+    d = np.float16(std / 9.84)
+    dmin = np.float16(np.float32(d) * np.float32(1.5))
+    blk[:, 80:82] = np.frombuffer(np.array([d], np.float16).tobytes(), np.uint8)
+    blk[:, 82:84] = np.frombuffer(np.array([dmin], np.float16).tobytes(), np.uint8)
     return blk.reshape(-1)
 
 
@@ -62,7 +68,7 @@ def build(seed=11, max_pos=64, cfg=CFG):
             q2(p + "mlp.w2.weight", d, hd)
             q2(p + "mlp.w3.weight", hd, d)
         else:
-            f32(p + "mlp.gate_inp.weight", r.standard_normal((E, d)) * 0.5)
+            f32(p + "mlp.gate_inp.weight", r.standard_normal((E, d)) * 0.06)
             q2(p + "mlp.gate_exps.weight", F, d, E)
             q2(p + "mlp.up_exps.weight", F, d, E)
             q2(p + "mlp.down_exps.weight", d, F, E)

@@ -66,3 +66,39 @@ def test_tiny_mla_greedy_matches_float64(orc):
         ids.append(int(top[0]))
     assert got == ids[4:]
     orc.load().orc_mla_destroy(m)
+
+
+def test_load_latent_reproduces_the_forward_cache(orc):
+    """orc_mla_load_latent, fed the latent records a prefill stored, gives
+    a second model the same expanded cache: every cached float equal and the
+    next decode step's logits equal bit for bit.  A wrong record offset, a
+    swapped K_nope / V half or a missing k_pe rotation fails here."""
+    L = orc.load()
+    max_seq = 32
+    c = mt.CFG
+    R = c["dc"] + c["rope"]
+    m, hold, _ = _model(orc, 11, max_seq)
+    m2, hold2, _ = _model(orc, 11, max_seq)
+    tap = np.zeros((c["n_layers"], max_seq, R), np.float32)
+    L.orc_mla_set_latent_tap(m, tap.ctypes.data)
+    ids = np.array([5, 17, 3, 90, 42, 7, 11, 60, 2], np.int32)
+    n = len(ids) - 1
+    lg = np.zeros(c["vocab_size"], np.float32)
+    assert L.orc_mla_forward(m, ids.ctypes.data, n, 0, lg.ctypes.data, 1) == 0
+    L.orc_mla_set_latent_tap(m, None)
+    assert np.any(tap[:, :n] != 0) and not np.any(tap[:, n:])
+    for layer in range(c["n_layers"]):
+        assert L.orc_mla_load_latent(m2, layer, tap[layer].ctypes.data, n) == 0
+        sizes = (max_seq * c["rope"], max_seq * c["n_heads"] * c["nope"], max_seq * c["n_heads"] * c["v_dim"])
+        for which, sz in enumerate(sizes):
+            a = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_float * sz).from_address(L.orc_mla_cache(m, layer, which)))
+            b = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_float * sz).from_address(L.orc_mla_cache(m2, layer, which)))
+            assert np.array_equal(a, b), (layer, which)
+    lg1 = np.zeros_like(lg)
+    lg2 = np.zeros_like(lg)
+    assert L.orc_mla_forward(m, ids[n:].ctypes.data, 1, n, lg1.ctypes.data, 1) == 0
+    assert L.orc_mla_forward(m2, ids[n:].ctypes.data, 1, n, lg2.ctypes.data, 1) == 0
+    assert np.array_equal(lg1, lg2)
+    assert L.orc_mla_load_latent(m2, c["n_layers"], tap[0].ctypes.data, n) != 0   # bad layer rejected
+    L.orc_mla_destroy(m)
+    L.orc_mla_destroy(m2)
