@@ -655,11 +655,44 @@ void orc_attn_rows(const float* q, int ldq, const float* k, int ldk,
     }
 }
 
+typedef struct {
+    const float *q, *ek, *ev;
+    float* out;
+    int H, rep, dh, kvd, start_pos, T, w, nw;
+} gqa_head_job;
+
+/* heads w, w + nw, ... of orc_gqa_attention (heads are independent) */
+static void* gqa_head_worker(void* arg) {
+    gqa_head_job* j = (gqa_head_job*)arg;
+    for (int h = j->w; h < j->H; h += j->nw) {
+        int kvh = h / j->rep;   /* build_qkv_fp32.cu:16 */
+        orc_attn_rows(j->q + (int64_t)h * j->dh, j->H * j->dh, j->ek + (int64_t)kvh * j->dh, j->kvd,
+                      j->ev + (int64_t)kvh * j->dh, j->kvd, j->out + (int64_t)h * j->dh, j->H * j->dh,
+                      j->start_pos, j->T, j->dh, j->dh);
+    }
+    return NULL;
+}
+
+static void gqa_attention_nt(const float* q, const float* kcur, const float* vcur,
+                             const float* k_cache, const float* v_cache,
+                             const uint8_t* kq, const uint8_t* vq, int mode, int pre_rope,
+                             const float* rkc, const float* rks,
+                             int T, int start_pos, int H, int Hkv, int dh, float* out, int nt);
+
 void orc_gqa_attention(const float* q, const float* kcur, const float* vcur,
                        const float* k_cache, const float* v_cache,
                        const uint8_t* kq, const uint8_t* vq, int mode, int pre_rope,
                        const float* rkc, const float* rks,
                        int T, int start_pos, int H, int Hkv, int dh, float* out) {
+    gqa_attention_nt(q, kcur, vcur, k_cache, v_cache, kq, vq, mode, pre_rope, rkc, rks, T, start_pos, H, Hkv, dh, out,
+                     1);
+}
+
+static void gqa_attention_nt(const float* q, const float* kcur, const float* vcur,
+                             const float* k_cache, const float* v_cache,
+                             const uint8_t* kq, const uint8_t* vq, int mode, int pre_rope,
+                             const float* rkc, const float* rks,
+                             int T, int start_pos, int H, int Hkv, int dh, float* out, int nt) {
     int kvd = Hkv * dh;
     int total = start_pos + T;
     /* ext_k / ext_v of gqa_layer.cu:204-244: cached rows [0,start_pos) in fp32,
@@ -681,12 +714,15 @@ void orc_gqa_attention(const float* q, const float* kcur, const float* vcur,
     memcpy(ek + (size_t)start_pos * kvd, kcur, (size_t)T * kvd * 4);
     memcpy(ev + (size_t)start_pos * kvd, vcur, (size_t)T * kvd * 4);
     int rep = H / Hkv;
-    for (int h = 0; h < H; h++) {
-        int kvh = h / rep;   /* build_qkv_fp32.cu:16 */
-        orc_attn_rows(q + (int64_t)h * dh, H * dh, ek + (int64_t)kvh * dh, kvd,
-                      ev + (int64_t)kvh * dh, kvd, out + (int64_t)h * dh, H * dh,
-                      start_pos, T, dh, dh);
+    gqa_head_job jobs[64];
+    pthread_t th[64];
+    int nw = nt < 1 ? 1 : nt > H ? H : nt > 64 ? 64 : nt;
+    for (int w = 0; w < nw; w++) {
+        jobs[w] = (gqa_head_job){q, ek, ev, out, H, rep, dh, kvd, start_pos, T, w, nw};
+        if (w) pthread_create(&th[w], NULL, gqa_head_worker, &jobs[w]);
     }
+    gqa_head_worker(&jobs[0]);
+    for (int w = 1; w < nw; w++) pthread_join(th[w], NULL);
     free(ek);
     free(ev);
 }
@@ -793,15 +829,15 @@ int orc_gqa_forward(orc_gqa* m, const int* ids, int T, int start_pos, float* log
             size_t off = (size_t)start_pos * kvd / 32;
             orc_kv_quantize(m->kf, kc, ck + off * m->kbb, (int64_t)T * kvd);
             orc_kv_quantize(m->vf, v, cv + off * m->vbb, (int64_t)T * kvd);
-            orc_gqa_attention(q, k, v, NULL, NULL, ck, cv, c->kv_mode, c->pre_rope,
-                              L->rope_k_cos, L->rope_k_sin, T, start_pos, H, Hkv, dh, att);
+            gqa_attention_nt(q, k, v, NULL, NULL, ck, cv, c->kv_mode, c->pre_rope,
+                             L->rope_k_cos, L->rope_k_sin, T, start_pos, H, Hkv, dh, att, nt > 0 ? nt : orc_num_threads());
         } else {
             float* ck = (float*)orc_gqa_cache(m, l, 0, NULL);
             float* cv = (float*)orc_gqa_cache(m, l, 1, NULL);
             memcpy(ck + (size_t)start_pos * kvd, kc, (size_t)T * kvd * 4);
             memcpy(cv + (size_t)start_pos * kvd, v, (size_t)T * kvd * 4);
-            orc_gqa_attention(q, k, v, ck, cv, NULL, NULL, 0, c->pre_rope,
-                              L->rope_k_cos, L->rope_k_sin, T, start_pos, H, Hkv, dh, att);
+            gqa_attention_nt(q, k, v, ck, cv, NULL, NULL, 0, c->pre_rope,
+                             L->rope_k_cos, L->rope_k_sin, T, start_pos, H, Hkv, dh, att, nt > 0 ? nt : orc_num_threads());
         }
         orc_linear(L->w_o, L->qt_o, att, a, T, d, H * dh, nt);   /* out of place */
         orc_add(h, h, a, T * d);
@@ -1214,6 +1250,29 @@ static void rope_hf_row(float* row, const float* ct, const float* st, int d, int
 }
 
 /* one RINA-MLA layer on token rows [T, d] at positions start_pos.. (rina_mla_layer.cu:65-98) */
+typedef struct {
+    const float *q, *qr, *kc, *vc;
+    float* att;
+    int H, Hkv, dh, dhr, T, start_pos, w, nw;
+} rmla_rows_job;
+
+/* query rows t = w, w + nw, ... of the RINA-MLA attention: every head of
+ * the row over keys 0..start_pos + t (flash_fp32 semantics) */
+static void* rmla_rows_worker(void* arg) {
+    rmla_rows_job* j = (rmla_rows_job*)arg;
+    const int H = j->H, Hkv = j->Hkv, dh = j->dh, dhr = j->dhr, dq = dh + dhr, rep = H / Hkv;
+    float qv[512];
+    for (int t = j->w; t < j->T; t += j->nw)
+        for (int hh = 0; hh < H; hh++) {
+            const int kv = hh / rep;
+            memcpy(qv, j->q + ((size_t)t * H + hh) * dh, (size_t)dh * 4);
+            memcpy(qv + dh, j->qr + ((size_t)t * H + hh) * dhr, (size_t)dhr * 4);
+            orc_attn_rows(qv, dq, j->kc + (size_t)kv * dq, Hkv * dq, j->vc + (size_t)kv * dh, Hkv * dh,
+                          j->att + ((size_t)t * H + hh) * dh, dh, j->start_pos + t, 1, dq, dh);
+        }
+    return NULL;
+}
+
 static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
     const orc_jamba_cfg* c = &m->c;
     const orc_jamba_layer_w* L = &c->layers[l];
@@ -1228,7 +1287,6 @@ static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
     float* kr = (float*)malloc((size_t)T * Hkv * dhr * 4);
     float* att = (float*)malloc((size_t)T * H * dh * 4);
     float* tmp = (float*)malloc((size_t)T * d * 4);
-    float qv[512];
     memcpy(a, h, (size_t)T * d * 4);
     orc_layer_norm(a, L->ln1, T, d, 1e-5f);                                    /* :70 */
     orc_linear(L->w_dq, L->qt, a, cq, T, dc, d, nt);                            /* :72 w_dqkv */
@@ -1252,15 +1310,18 @@ static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
         }
         memcpy(m->vc[l] + (size_t)pos * Hkv * dh, v + (size_t)t * Hkv * dh, (size_t)Hkv * dh * 4);
     }
-    const int rep = H / Hkv;
-    for (int t = 0; t < T; t++) {
-        for (int hh = 0; hh < H; hh++) {
-            const int kv = hh / rep;
-            memcpy(qv, q + ((size_t)t * H + hh) * dh, (size_t)dh * 4);
-            memcpy(qv + dh, qr + ((size_t)t * H + hh) * dhr, (size_t)dhr * 4);
-            orc_attn_rows(qv, dq, m->kc[l] + (size_t)kv * dq, Hkv * dq, m->vc[l] + (size_t)kv * dh, Hkv * dh,
-                          att + ((size_t)t * H + hh) * dh, dh, start_pos + t, 1, dq, dh);   /* flash_fp32 */
+    {   /* query rows are independent: rows t = w, w + nw, ... per worker */
+        rmla_rows_job jobs[64];
+        pthread_t th[64];
+        int nw = nt > 0 ? nt : orc_num_threads();
+        if (nw > T) nw = T;
+        if (nw > 64) nw = 64;
+        for (int w = 0; w < nw; w++) {
+            jobs[w] = (rmla_rows_job){q, qr, m->kc[l], m->vc[l], att, H, Hkv, dh, dhr, T, start_pos, w, nw};
+            if (w) pthread_create(&th[w], NULL, rmla_rows_worker, &jobs[w]);
         }
+        rmla_rows_worker(&jobs[0]);
+        for (int w = 1; w < nw; w++) pthread_join(th[w], NULL);
     }
     orc_linear(L->c_proj, L->qt, att, tmp, T, d, H * dh, nt);                   /* :87 (out of place) */
     orc_add(h, h, tmp, T * d);

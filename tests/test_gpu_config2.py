@@ -59,3 +59,60 @@ def test_config2_greedy_64_steps(rina, orc):
         assert got[1:] == ref
     finally:
         sm.close()
+
+
+def test_config2_prompt_rows_full_shape(rina, orc):
+    """The prompt path at the full config-2 shape: a 96-token prefill (Q4_0F
+    matmuls on the matrix cores, prompt attention from position 0) against
+    the oracle's own prefill of the same tokens.  Layer 0's 96 appended K
+    (post-RoPE) and V rows agree per row within 1e-5; layer l's within
+    1e-5*sqrt(l+1), the growth of independent per-layer rounding
+    differences (measured: 1.9e-6 at layer 0 rising to 1.3e-5 at layer 15).
+    The last row's logits agree within 1e-5 and the first greedy token is
+    the same with a top-2 margin above twice that tolerance."""
+    import torch
+    from _util import REL_TOL, assert_close, empty, host
+    synth = importlib.import_module("rina_amd.synth")
+    n, S = 96, 128
+    sm = synth.SynthLlama(synth.LLAMA_1B, qt=rina.QT_Q4_0F, seed=1, max_seq=S, keep_host=True)
+    try:
+        eng = rina.load_engine()
+        c = sm.cfg
+        L, kvd, V = c["n_layers"], c["n_kv_heads"] * c["head_dim"], c["vocab_size"]
+        inf = sm.infer("fp32", S)
+        tap = torch.zeros(L * 2 * S * kvd, dtype=torch.float32, device="cuda")
+        rina.check(eng.rina_infer_set_kv_tap(inf, tap.data_ptr()), "tap")
+        prompt = np.random.default_rng(3).integers(0, V, n).astype(np.int32)
+        lg = empty(n * V)
+        rina.check(eng.rina_infer_forward(inf, torch.from_numpy(prompt).cuda().data_ptr(), lg.data_ptr(), 1, n, 0,
+                                          stream()), "prefill")
+        got_last = host(lg).reshape(n, V)[n - 1].copy()
+        tp = tap.cpu().numpy().reshape(L, 2, S, kvd)
+        eng.rina_infer_destroy(inf)
+        m, hold = orc.gqa_from_tensors(c, sm.host, sm.qt, S, "fp32", min(os.cpu_count() or 1, 16))
+        Lo = orc.load()
+        ref = np.zeros(V, np.float32)
+        assert Lo.orc_gqa_forward(m, prompt.ctypes.data, n, 0, ref.ctypes.data, 1) == 0
+        worst = np.zeros((L, 2))
+        for layer in range(L):
+            for which in (0, 1):
+                onb = C.c_size_t()
+                optr = Lo.orc_gqa_cache(m, layer, which, C.byref(onb))
+                want = np.ctypeslib.as_array((C.c_float * (n * kvd)).from_address(optr)).reshape(n, kvd)
+                gotr = tp[layer, which, :n]
+                err = np.max(np.abs(gotr - want), axis=1) / np.maximum(np.max(np.abs(want), axis=1), 1e-30)
+                worst[layer, which] = err.max()
+        Lo.orc_gqa_destroy(m)
+        print("per-row K/V error by layer:", " ".join("%d:%.1e/%.1e" % (l, worst[l, 0], worst[l, 1]) for l in range(L)))
+        # layer 0's rows are one layer's outputs (norm, prompt matmul, RoPE):
+        # 1e-5 per row.  Deeper rows carry the fp32 rounding differences of
+        # every layer below (the oracle sums serially, the matrix cores in
+        # tiles), which add like independent errors: 1e-5 * sqrt(l + 1).
+        bound = REL_TOL * np.sqrt(np.arange(1, L + 1))[:, None]
+        assert np.all(worst <= bound), worst
+        assert_close(got_last, ref, what="prefill logits, last row")
+        top = np.argsort(ref)[::-1][:2]
+        assert (ref[top[0]] - ref[top[1]]) / np.max(np.abs(ref)) > 2 * REL_TOL
+        assert int(np.argmax(got_last)) == int(top[0])
+    finally:
+        sm.close()

@@ -1,11 +1,12 @@
 """Config 3: the Llama-3.2-1B-shaped model at context 4096 with the KV cache
-in q8, q4 and q2k_q1v.  The GPU prefills a 4090-token seeded prompt and
-decodes greedily; every K/V row the model appended is re-packed by the
-oracle and compared with the cache bytes (bit-exact), and the oracle,
-started from those same cache rows and the first generated token, decodes
-the same tokens at ~4096 positions (its own prefill of 4090 tokens on the
-CPU would take hours; the first token comes from the prefill, which
-attends over the fp32 rows, not the packed cache)."""
+in q8, q4 and q2k_q1v.  The GPU prefills a 4032-token seeded prompt and
+decodes 64 greedy steps (positions 4032..4095); every K/V row the model
+appended is re-packed by the oracle and compared with the cache bytes
+(bit-exact), and the oracle, started from those same cache rows and the
+first generated token, decodes the same 64 tokens (its own prefill of 4032
+tokens on the CPU would take hours; the first token comes from the
+prefill, which attends over the fp32 rows, not the packed cache).  Every
+step's top-2 logit margin must clear twice the 1e-5 tolerance."""
 import ctypes as C
 import importlib
 import os
@@ -13,12 +14,12 @@ import os
 import numpy as np
 import pytest
 
-from _util import d2h, stream
+from _util import REL_TOL, d2h, stream
 
 pytestmark = pytest.mark.gpu
 
-N_PROMPT = 4090
-STEPS = 6
+N_PROMPT = 4032
+STEPS = 65          # the prefill's token, then 64 decode steps
 MAX_SEQ = 4104
 
 
@@ -62,13 +63,17 @@ def test_ctx4096_packs_and_greedy(rina, orc, llama, kv_mode):
             C.memmove(optr, cache.ctypes.data, keep)
     eng.rina_infer_destroy(inf)
     lg = np.zeros(V, np.float32)
-    ref = []
+    ref, margins = [], []
     tok, pos = got[0], N_PROMPT
     for s in range(STEPS - 1):
         t = np.array([tok], np.int32)
         assert Lo.orc_gqa_forward(m, t.ctypes.data, 1, pos, lg.ctypes.data, 1) == 0
+        top = np.argsort(lg)[::-1][:2]
+        margins.append(float(lg[top[0]] - lg[top[1]]) / float(np.max(np.abs(lg))))
         tok = Lo.orc_argmax(lg.ctypes.data, V)
         ref.append(tok)
         pos += 1
     Lo.orc_gqa_destroy(m)
-    assert got[1:] == ref
+    assert got[1:] == ref, "first divergence at step %d" % next(i for i in range(STEPS - 1) if got[1 + i] != ref[i])
+    assert min(margins) > 2 * REL_TOL, "near tie at step %d (%.2e)" % (int(np.argmin(margins)), min(margins))
+    assert len(set(got)) >= 16

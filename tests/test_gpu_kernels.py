@@ -670,3 +670,47 @@ def test_linear_prefill_segments(rina, orc, qt, Ns, epi):
     for i, n in enumerate(Ns):
         ref = orc.linear(ws[i], qt, x, n, K).astype(np.float64) + (y0[i] if epi == 1 else 0.0)
         assert_close(host(ys[i]).reshape(M, n), ref, what="segment %d of %s" % (i, Ns))
+
+
+@pytest.mark.parametrize("qt", [5, 7, 10, 6])
+@pytest.mark.parametrize("N,K", [(2048, 2048), (512, 8192), (1024, 1408)])
+def test_linear_outlier_activations(rina, orc, qt, N, K):
+    """Activation columns carrying 1e4x outliers (the decode matvec holds x
+    to 22 bits of each 32-value column's maximum, weakest when one value of
+    a column dwarfs the rest).  Per element, the error against a float64
+    matvec of the same dequantized weights must stay within 1e-5 of the
+    element's magnitude scale sum_k |w_ik x_k| (the bound fp32 accumulation
+    itself obeys); the oracle's fp32 result is checked the same way, and the
+    largest error relative to |y_i| is reported."""
+    if qt in (5, 7) and K % 32:
+        pytest.skip("Q4 rows need K % 32 == 0")
+    hip = rina.load_hip()
+    r = rng(qt * 7 + K)
+    x = r.standard_normal(K).astype(np.float32)
+    cols = K // 32
+    hot = r.choice(cols, max(1, cols // 8), replace=False)
+    for cidx in hot:                       # one 1e4x value in every eighth column
+        x[cidx * 32 + int(r.integers(32))] = np.float32(1e4 * (1 if r.integers(2) else -1))
+    x[:32] = np.float32(1e4) * r.standard_normal(32).astype(np.float32)   # a column of outliers only
+    if qt == 10:
+        import importlib
+        w = importlib.import_module("rina_amd.synth").random_q2k(K, N * K)
+    elif qt == 6:
+        w = (r.standard_normal(N * K) * 0.02).astype(np.float32)
+    else:
+        w = orc.pack(qt, (r.standard_normal(N * K) * 0.02).astype(np.float32))
+    W = orc.dequant(qt, w, N * K).reshape(N, K).astype(np.float64)
+    ref64 = W @ x.astype(np.float64)
+    scale = np.abs(W) @ np.abs(x.astype(np.float64))
+    yd = empty(N)
+    ok(hip.rina_hip_linear(dev(w).data_ptr(), qt, dev(x).data_ptr(), yd.data_ptr(), 1, N, K, stream()), "linear")
+    got = host(yd).astype(np.float64)
+    ora = orc.linear(w, qt, x, N, K)[0].astype(np.float64)
+    e_gpu = np.abs(got - ref64) / scale
+    e_ora = np.abs(ora - ref64) / scale
+    rel_y = np.abs(got - ref64) / np.maximum(np.abs(ref64), 1e-30)
+    print("qt %d N %d K %d: max |err|/sum|wx| gpu %.2e oracle %.2e; max |err|/|y| gpu %.2e (median %.2e)"
+          % (qt, N, K, e_gpu.max(), e_ora.max(), rel_y.max(), np.median(rel_y)))
+    assert e_ora.max() <= REL_TOL
+    assert e_gpu.max() <= REL_TOL, "element %d: %.3e" % (int(e_gpu.argmax()), e_gpu.max())
+    assert_close(got, ora, what="outlier matvec vs oracle")
