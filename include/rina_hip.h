@@ -206,6 +206,26 @@ int rina_hip_gqa_decode_attention(const float* q, const float* k, const float* v
                                   void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* rina_hip_gqa_decode_attention without a workspace argument, and it
+ * allocates nothing: no counterpart in the reference; it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The chunk partials live in a
+ * library-owned device array of rina_hip_noalloc_scratch_bytes() (1 MiB)
+ * per device, held until the process ends; a call whose partials need more
+ * (rina_hip_gqa_attention_workspace(1, H, 64, max_seq) bytes, e.g. more
+ * than 62 query heads) returns RINA_ERR_WORKSPACE before launching.  All
+ * calls on one device share that array: calls that overlap on one device
+ * (different streams) race.  The first call on each device looks the array
+ * up; make it outside graph capture. */
+size_t rina_hip_noalloc_scratch_bytes(void);
+int rina_hip_gqa_decode_attention_noalloc(const float* q, const float* k, const float* v,
+                                          const float* rope_q_cos, const float* rope_q_sin,
+                                          const float* rope_k_cos, const float* rope_k_sin,
+                                          void* cache_k, void* cache_v, int mode, int H,
+                                          int Hkv, int dh, int start_pos, const int* d_pos,
+                                          int max_seq, float* out, float* k_rot_out,
+                                          void* stream);
+
 /* ====================================================================== */
 /* DeepSeek MLA (latent cache) and MoE                                     */
 /* ====================================================================== */

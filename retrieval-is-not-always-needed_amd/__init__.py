@@ -48,6 +48,9 @@ _HIP_SIGS = {
                                      VP, SZ, VP]),
     "rina_hip_gqa_decode_attention": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, I32, I32, VP, I32,
                                             VP, VP, VP, SZ, VP]),
+    "rina_hip_noalloc_scratch_bytes": (SZ, []),
+    "rina_hip_gqa_decode_attention_noalloc": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, I32, I32, VP,
+                                                    I32, VP, VP, VP]),
     "rina_hip_mla_attention_workspace": (SZ, [I32, I32, I32, I32]),
     "rina_hip_mla_cache_bytes": (SZ, [I32, I32, I32]),
     "rina_hip_mla_decode_attention": (I32, [VP, VP, VP, F32, VP, VP, VP, I32, VP, I32, I32, I32, I32, I32, I32, VP,

@@ -22,6 +22,7 @@
 // (the workgroup holding that position), replacing the separate append launch.
 #include "rina_common.hpp"
 #include "kv_formats.hpp"
+#include <mutex>
 
 namespace {
 
@@ -814,6 +815,57 @@ extern "C" int rina_hip_gqa_decode_attention(const float* q, const float* k, con
     sa.mode = mode; sa.H = H; sa.Hkv = Hkv; sa.start_pos = start_pos; sa.max_seq = max_seq; sa.d_pos = d_pos;
     sa.scale = 1.0f / sqrtf((float)dh);
     return launch_split_mode<true>(sa, H / Hkv, ws_bytes, workspace, as_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode attention.  The chunk partials (m, l, O) that the
+// caller's workspace holds for rina_hip_gqa_decode_attention live here in a
+// file-scope device array instead: kNoAllocScratchBytes per device, held
+// until the process ends.  Nothing in it has to start at zero (the combine
+// reads only the chunks the split kernel of the same call wrote).  Host code
+// never passes the array's name (a host-side stand-in); it looks up the
+// array's device address once per device, with that device current, and
+// passes that.  Every call on one device shares the array: calls that
+// overlap on one device (two streams) race.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)1 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+void* g_scratch_addr[64];
+std::mutex g_scratch_mu;
+
+int noalloc_scratch(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return RINA_ERR_HIP;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RINA_ERR_HIP;
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return RINA_OK;
+}
+}  // namespace
+
+extern "C" size_t rina_hip_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int rina_hip_gqa_decode_attention_noalloc(const float* q, const float* k, const float* v,
+                                                     const float* rope_q_cos, const float* rope_q_sin,
+                                                     const float* rope_k_cos, const float* rope_k_sin, void* cache_k,
+                                                     void* cache_v, int mode, int H, int Hkv, int dh, int start_pos,
+                                                     const int* d_pos, int max_seq, float* out, float* k_rot_out,
+                                                     void* stream) {
+    if (H < 1 || max_seq < 1) return RINA_ERR_ARG;
+    const size_t need = rina_hip_gqa_attention_workspace(1, H, dh, max_seq);
+    if (need > kNoAllocScratchBytes) return RINA_ERR_WORKSPACE;
+    void* ws = nullptr;
+    const int rc = noalloc_scratch(&ws);
+    if (rc) return rc;
+    return rina_hip_gqa_decode_attention(q, k, v, rope_q_cos, rope_q_sin, rope_k_cos, rope_k_sin, cache_k, cache_v,
+                                         mode, H, Hkv, dh, start_pos, d_pos, max_seq, out, k_rot_out, ws,
+                                         kNoAllocScratchBytes, stream);
 }
 
 extern "C" size_t rina_hip_dq_attention_workspace(int H, int dq, int max_pos) {
