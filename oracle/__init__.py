@@ -72,9 +72,10 @@ def load(build=True):
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(SO) and build:
+    so = os.environ.get("RINA_ORACLE_SO") or SO     # a sanitizer build of the same source, for tests
+    if so == SO and not os.path.exists(SO) and build:
         subprocess.run(["make", "-s", "-C", HERE], check=True)
-    L = C.CDLL(SO)
+    L = C.CDLL(so)
     sigs = {
         "orc_f32_to_f16": (C.c_uint16, [F32]),
         "orc_f32_to_f16_trunc": (C.c_uint16, [F32]),

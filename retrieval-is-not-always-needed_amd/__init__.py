@@ -112,7 +112,8 @@ def hip_path():
 
 
 def engine_path():
-    return os.path.join(LIB_DIR, "librina_engine.so")
+    # RINA_ENGINE_SO: the sanitizer build of the same host sources (tests)
+    return os.environ.get("RINA_ENGINE_SO") or os.path.join(LIB_DIR, "librina_engine.so")
 
 
 def load_hip():

@@ -70,6 +70,37 @@ def build_oracle():
     _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")])
 
 
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
+
+
+def build_sanitized(jobs=None):
+    """AddressSanitizer + UBSan builds of the host code: the engine's C++
+    (g++, no HIP sources; linked against the uninstrumented librina_hip.so)
+    into _build/asan/librina_engine.so and the oracle into
+    oracle/build/asan/librina_oracle.so.  Used by tests/test_sanitizers.py
+    through RINA_ENGINE_SO / RINA_ORACLE_SO."""
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    out = os.path.join(OBJ, "asan")
+    os.makedirs(out, exist_ok=True)
+    srcs = []
+    for d, _, fs in os.walk(ENG_SRC):
+        srcs += [os.path.join(d, f) for f in fs if f.endswith(".cpp")]
+    srcs.sort()
+    cmds = []
+    for s in srcs:
+        o = os.path.join(out, os.path.relpath(s, ENG_SRC).replace(os.sep, "_")[:-4] + ".o")
+        cmds.append(["g++"] + CXX_FLAGS + SAN_FLAGS + ["-I", INC, "-I", ENG_SRC, "-I", os.path.join(ROCM, "include"),
+                                                      "-c", s, "-o", o])
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        list(ex.map(_run, cmds))
+    so = os.path.join(out, "librina_engine.so")
+    _run(["g++", "-shared", "-fsanitize=address,undefined", "-o", so] + [c[-1] for c in cmds] +
+         ["-L", LIB, "-lrina_hip", "-Wl,-rpath," + LIB, "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+          "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+    _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "asan"])
+    return so, os.path.join(ROOT, "oracle", "build", "asan", "librina_oracle.so")
+
+
 def build(verbose=False, jobs=None):
     jobs = jobs or min(8, os.cpu_count() or 4)
     os.makedirs(OBJ, exist_ok=True)
