@@ -355,6 +355,32 @@ int rina_hip_dq_decode_attention(const float* qa, const float* qb, const float* 
                                  const int* d_pos, int max_seq, float* out, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* rina_hip_dq_decode_attention with the cache form chosen by kv_mode:
+ *   RINA_KV_FP32     cache_k [max_seq][Hkv][da+db] fp32, cache_v
+ *                    [max_seq][Hkv][dv] fp32, cache_kr unused;
+ *   RINA_KV_Q2K_Q1V  the q2 K / q1 V cache of the reference's RINA-MLA in
+ *                    q2k_q1v mode (rina/model_jamba_qw2.py:175-177): cache_k
+ *                    holds the key content part [max_seq][Hkv][da/32] as
+ *                    q2_1 blocks, cache_kr the RoPE'd key part
+ *                    [max_seq][Hkv][db] fp32 (training keeps it unquantized),
+ *                    cache_v the values [max_seq][Hkv][dv/32] as 6-byte q1_0
+ *                    records; da == 64, dv == 64.  The block codecs are
+ *                    kernels/quantize.cu:74-185's (rina_hip_kv_quantize).
+ * Positions before pos0 are read from the cache (dequantized), the current
+ * position from the fp32 rows, which are then appended (packed), as the
+ * GQA composition does (arch/gqa/gqa_layer.cu:192-270).
+ * rina_hip_dq_kv_region_bytes gives each region's size: part 0 cache_k,
+ * 1 cache_v, 2 cache_kr. */
+size_t rina_hip_dq_kv_region_bytes(int kv_mode, int part, int max_seq, int Hkv, int da, int db, int dv);
+int rina_hip_dq_decode_attention_kv(const float* qa, const float* qb, const float* ka,
+                                    const float* kb, const float* v, const float* rope_q_cos,
+                                    const float* rope_q_sin, const float* rope_k_cos,
+                                    const float* rope_k_sin, int kv_mode, void* cache_k,
+                                    void* cache_v, float* cache_kr, int H, int Hkv, int da,
+                                    int db, int dv, int start_pos, const int* d_pos, int max_seq,
+                                    float* out, void* workspace, size_t workspace_bytes,
+                                    void* stream);
+
 /* ====================================================================== */
 /* Per-token glue                                                          */
 /* ====================================================================== */

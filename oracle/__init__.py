@@ -62,7 +62,7 @@ class JambaCfg(C.Structure):
     _fields_ = [("dim", I32), ("n_layers", I32), ("n_heads", I32), ("n_kv_heads", I32), ("head_dim", I32),
                 ("dhr", I32), ("dc", I32), ("ssm_steps", I32), ("hidden", I32), ("vocab", I32), ("max_seq", I32),
                 ("nthreads", I32), ("wte", VP), ("qt_wte", I32), ("ln_f", VP), ("lm_head", VP), ("qt_lm", I32),
-                ("layers", C.POINTER(JambaLayerW))]
+                ("layers", C.POINTER(JambaLayerW)), ("rmla_kv_mode", I32)]
 
 
 _lib = None
@@ -111,6 +111,8 @@ def load(build=True):
         "orc_jamba_forward": (I32, [VP, VP, I32, I32, VP, I32]),
         "orc_jamba_generate": (I32, [VP, VP, I32, I32, VP]),
         "orc_jamba_generate_recompute": (I32, [VP, VP, I32, I32, VP]),
+        "orc_jamba_packed_cache": (VP, [VP, I32, I32]),
+        "orc_jamba_fp32_cache": (VP, [VP, I32, I32]),
         "orc_mla_create": (VP, [C.POINTER(MLACfg)]),
         "orc_mla_destroy": (None, [VP]),
         "orc_mla_forward": (I32, [VP, VP, I32, I32, VP, I32]),
@@ -310,11 +312,12 @@ def mla_generate(m, prompt, steps):
 JAMBA_SSM_TYPES = ("inertia_wave_ssm", "ssm")
 
 
-def jamba_from_tensors(cfg, tensors, layer_types, qt, max_seq, nthreads=0):
+def jamba_from_tensors(cfg, tensors, layer_types, qt, max_seq, nthreads=0, kv_mode="fp32"):
     """Oracle RINA Jamba model over host tensors (reference names).  cfg:
     dim, n_layers, n_heads, n_kv_heads, head_dim, d_h_r, d_c, ssm_steps,
     hidden_dim, vocab_size; layer_types: per-layer type strings; qt: quant
-    type of every linear.  Returns (handle, keepalive)."""
+    type of every linear; kv_mode: the RINA-MLA cache form ("fp32" or
+    "q2k_q1v").  Returns (handle, keepalive)."""
     hold = []
 
     def h(name):
@@ -351,7 +354,7 @@ def jamba_from_tensors(cfg, tensors, layer_types, qt, max_seq, nthreads=0):
                  head_dim=cfg["head_dim"], dhr=cfg["d_h_r"], dc=cfg["d_c"], ssm_steps=cfg["ssm_steps"],
                  hidden=cfg["hidden_dim"], vocab=cfg["vocab_size"], max_seq=max_seq, nthreads=nthreads,
                  wte=h("transformer.wte.weight"), qt_wte=FP32, ln_f=h("transformer.ln_f.weight"),
-                 lm_head=h("lm_head.weight"), qt_lm=FP32, layers=lw)
+                 lm_head=h("lm_head.weight"), qt_lm=FP32, layers=lw, rmla_kv_mode=KV_MODES[kv_mode])
     m = load().orc_jamba_create(C.byref(c))
     return m, (hold, lw, c)
 

@@ -1151,7 +1151,19 @@ struct orc_jamba {
     float** wcs;     /* SSM layers: [H*dh] weighted cumulative memory */
     float** kc;      /* RMLA layers: [max_seq][Hkv*(dh+dhr)] */
     float** vc;      /* RMLA layers: [max_seq][Hkv*dh] */
+    uint8_t** kq;    /* rmla_kv_mode q2k_q1v: key content q2_1 [max_seq][Hkv][dh/32] blocks */
+    uint8_t** vq;    /* rmla_kv_mode q2k_q1v: value q1_0 [max_seq][Hkv][dh/32] records */
 };
+
+const float* orc_jamba_fp32_cache(orc_jamba* m, int layer, int which) {
+    if (layer < 0 || layer >= m->c.n_layers || m->layers[layer].type == ORC_JAMBA_SSM) return NULL;
+    return which ? m->vc[layer] : m->kc[layer];
+}
+
+const uint8_t* orc_jamba_packed_cache(orc_jamba* m, int layer, int part) {
+    if (layer < 0 || layer >= m->c.n_layers || m->c.rmla_kv_mode != ORC_KV_Q2K_Q1V || !m->kq) return NULL;
+    return part == 0 ? m->kq[layer] : part == 1 ? m->vq[layer] : NULL;
+}
 
 orc_jamba* orc_jamba_create(const orc_jamba_cfg* cfg) {
     orc_jamba* m = (orc_jamba*)calloc(1, sizeof(orc_jamba));
@@ -1174,13 +1186,25 @@ orc_jamba* orc_jamba_create(const orc_jamba_cfg* cfg) {
             m->vc[l] = (float*)calloc((size_t)cfg->max_seq * Hkv * dh, 4);
         }
     }
+    if (cfg->rmla_kv_mode == ORC_KV_Q2K_Q1V) {
+        m->kq = (uint8_t**)calloc(L, sizeof(uint8_t*));
+        m->vq = (uint8_t**)calloc(L, sizeof(uint8_t*));
+        for (int l = 0; l < L; l++)
+            if (m->layers[l].type != ORC_JAMBA_SSM) {
+                m->kq[l] = (uint8_t*)calloc((size_t)cfg->max_seq * Hkv * (dh / 32), 10);
+                m->vq[l] = (uint8_t*)calloc((size_t)cfg->max_seq * Hkv * (dh / 32), 6);
+            }
+    }
     return m;
 }
 
 void orc_jamba_destroy(orc_jamba* m) {
     if (!m) return;
-    for (int l = 0; l < m->c.n_layers; l++) { free(m->lcs[l]); free(m->wcs[l]); free(m->kc[l]); free(m->vc[l]); }
-    free(m->lcs); free(m->wcs); free(m->kc); free(m->vc); free(m->layers);
+    for (int l = 0; l < m->c.n_layers; l++) {
+        free(m->lcs[l]); free(m->wcs[l]); free(m->kc[l]); free(m->vc[l]);
+        if (m->kq) { free(m->kq[l]); free(m->vq[l]); }
+    }
+    free(m->lcs); free(m->wcs); free(m->kc); free(m->vc); free(m->kq); free(m->vq); free(m->layers);
     free(m);
 }
 
@@ -1296,6 +1320,13 @@ static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
     orc_linear(L->w_k2v, L->qt, k, v, T, Hkv * dh, Hkv * dh, nt);               /* :77 */
     orc_linear(L->w_qr, L->qt, a, qr, T, H * dhr, d, nt);                       /* :78 */
     orc_linear(L->w_kr, L->qt, a, kr, T, Hkv * dhr, d, nt);                     /* :79 */
+    /* q2k_q1v cache: position p attends to positions < p through the packed
+     * cache (key content and values dequantized; the RoPE part is kept fp32)
+     * and to itself through its fp32 rows, as the GQA composition reads its
+     * quantized cache (gqa_layer.cu:203-245).  Rows go in one at a time, so a
+     * T-row call equals T single-row calls. */
+    const int qkv = c->rmla_kv_mode == ORC_KV_Q2K_Q1V;
+    const int rep_q = H / Hkv;
     for (int t = 0; t < T; t++) {
         const int pos = start_pos + t;
         if (L->rope_q_cos)
@@ -1309,8 +1340,32 @@ static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
             memcpy(krow + hh * dq + dh, kr + ((size_t)t * Hkv + hh) * dhr, (size_t)dhr * 4);
         }
         memcpy(m->vc[l] + (size_t)pos * Hkv * dh, v + (size_t)t * Hkv * dh, (size_t)Hkv * dh * 4);
+        if (qkv) {
+            /* quantize-on-append of the fp32 rows (kernels/quantize.cu:74-185) */
+            for (int hh = 0; hh < Hkv; hh++) {
+                const size_t r = (size_t)pos * Hkv + hh;
+                orc_kv_quantize(ORC_KVF_Q2_1, k + ((size_t)t * Hkv + hh) * dh, m->kq[l] + r * (dh / 32) * 10, dh);
+                orc_kv_quantize(ORC_KVF_Q1_0, v + ((size_t)t * Hkv + hh) * dh, m->vq[l] + r * (dh / 32) * 6, dh);
+            }
+            /* this row's attention: earlier rows already hold their packed
+             * values, this one its fp32 values */
+            float qv[512];
+            for (int hh = 0; hh < H; hh++) {
+                const int kv = hh / rep_q;
+                memcpy(qv, q + ((size_t)t * H + hh) * dh, (size_t)dh * 4);
+                memcpy(qv + dh, qr + ((size_t)t * H + hh) * dhr, (size_t)dhr * 4);
+                orc_attn_rows(qv, dq, m->kc[l] + (size_t)kv * dq, Hkv * dq, m->vc[l] + (size_t)kv * dh, Hkv * dh,
+                              att + ((size_t)t * H + hh) * dh, dh, pos, 1, dq, dh);
+            }
+            /* from now on the row is read through the packed cache */
+            for (int hh = 0; hh < Hkv; hh++) {
+                const size_t r = (size_t)pos * Hkv + hh;
+                orc_kv_dequant(ORC_KVF_Q2_1, m->kq[l] + r * (dh / 32) * 10, m->kc[l] + r * dq, dh);
+                orc_kv_dequant(ORC_KVF_Q1_0, m->vq[l] + r * (dh / 32) * 6, m->vc[l] + r * dh, dh);
+            }
+        }
     }
-    {   /* query rows are independent: rows t = w, w + nw, ... per worker */
+    if (!qkv) {   /* query rows are independent: rows t = w, w + nw, ... per worker */
         rmla_rows_job jobs[64];
         pthread_t th[64];
         int nw = nt > 0 ? nt : orc_num_threads();

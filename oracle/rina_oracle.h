@@ -241,6 +241,10 @@ typedef struct {
     const float* ln_f;                  /* LayerNorm */
     const void* lm_head; int qt_lm;     /* NULL -> tied to wte */
     const orc_jamba_layer_w* layers;
+    /* RINA-MLA cache form: ORC_KV_FP32, or ORC_KV_Q2K_Q1V (the key content
+     * part packed as q2_1, the RoPE part kept fp32, values as q1_0;
+     * rina/model_jamba_qw2.py:175-177); head_dim == 64 for the latter */
+    int rmla_kv_mode;
 } orc_jamba_cfg;
 
 typedef struct orc_jamba orc_jamba;
@@ -260,6 +264,14 @@ int        orc_jamba_forward(orc_jamba* m, const int* ids, int T, int start_pos,
 int        orc_jamba_generate(orc_jamba* m, const int* prompt, int n_prompt, int steps, int* out_ids);
 /* greedy decode with the reference's full recompute at every step */
 int        orc_jamba_generate_recompute(orc_jamba* m, const int* prompt, int n_prompt, int steps, int* out_ids);
+/* packed RINA-MLA cache of layer l (rmla_kv_mode ORC_KV_Q2K_Q1V): part 0 the
+ * key content q2_1 blocks [max_seq][Hkv][head_dim/32], 1 the value q1_0
+ * records [max_seq][Hkv][head_dim/32]; NULL otherwise */
+const uint8_t* orc_jamba_packed_cache(orc_jamba* m, int layer, int part);
+/* fp32 rows of a RINA-MLA layer's cache as attention reads them: which 0
+ * keys [max_seq][Hkv][head_dim + dhr], 1 values [max_seq][Hkv][head_dim]
+ * (q2k_q1v mode: past rows hold their dequantized packs) */
+const float* orc_jamba_fp32_cache(orc_jamba* m, int layer, int which);
 
 int orc_num_threads(void);
 

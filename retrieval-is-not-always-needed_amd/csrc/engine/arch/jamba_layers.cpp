@@ -172,7 +172,12 @@ struct RMLAImpl {
     const void *w_dqkv = nullptr, *w_uq = nullptr, *w_uk = nullptr, *w_k2v = nullptr, *w_qr = nullptr,
                *w_kr = nullptr, *c_proj = nullptr;
     MLPPart mlp;
-    float *ck = nullptr, *cv = nullptr;        // fp32 K [max_seq][Hkv][dh+dhr], V [max_seq][Hkv][dh]
+    // K / V cache: fp32 K [max_seq][Hkv][dh+dhr] and V [max_seq][Hkv][dh]
+    // (kv_mode RINA_KV_FP32), or the q2k_q1v form: q2_1 key content, fp32
+    // RoPE part (kr), q1_0 values (rina_hip_dq_decode_attention_kv)
+    int kv_mode = RINA_KV_FP32;
+    void *ck = nullptr, *cv = nullptr;
+    float* ckr = nullptr;
     float* scratch = nullptr;                  // cq | qr | kr | q | k | v | att
     void* ws = nullptr;
     size_t ws_bytes = 0;
@@ -180,6 +185,7 @@ struct RMLAImpl {
     ~RMLAImpl() {
         if (ck) (void)hipFree(ck);
         if (cv) (void)hipFree(cv);
+        if (ckr) (void)hipFree(ckr);
         if (scratch) (void)hipFree(scratch);
         if (ws) (void)hipFree(ws);
     }
@@ -214,8 +220,17 @@ struct RMLAImpl {
         qt = (int)L.qt;
         ws_bytes = rina_hip_dq_attention_workspace(H, dh + dhr, max_seq);
         const size_t sc = (size_t)dc + H * dhr + Hkv * dhr + H * dh + 2 * Hkv * dh + H * dh;
-        return dev_alloc(&ck, (size_t)max_seq * Hkv * (dh + dhr)) && dev_alloc(&cv, (size_t)max_seq * Hkv * dh) &&
-               dev_alloc(&scratch, sc) && dev_alloc((uint8_t**)&ws, ws_bytes);
+        // the model's kv_quant_mode: "fp32" (or none) or "q2k_q1v" (q2 K / q1 V,
+        // rina/model_jamba_qw2.py:175-177); other modes have no RINA-MLA form
+        const int mode = cfg.kv_quant_mode.empty() ? RINA_KV_FP32 : kv_mode_from_name(cfg.kv_quant_mode.c_str());
+        if (mode != RINA_KV_FP32 && mode != RINA_KV_Q2K_Q1V) return false;
+        kv_mode = mode;
+        const size_t kb = rina_hip_dq_kv_region_bytes(mode, 0, max_seq, Hkv, dh, dhr, dh);
+        const size_t vb = rina_hip_dq_kv_region_bytes(mode, 1, max_seq, Hkv, dh, dhr, dh);
+        const size_t rb = rina_hip_dq_kv_region_bytes(mode, 2, max_seq, Hkv, dh, dhr, dh);
+        if (!kb || !vb) return false;
+        return dev_alloc((uint8_t**)&ck, kb) && dev_alloc((uint8_t**)&cv, vb) &&
+               (!rb || dev_alloc((uint8_t**)&ckr, rb)) && dev_alloc(&scratch, sc) && dev_alloc((uint8_t**)&ws, ws_bytes);
     }
 
     int forward(float* h, ForwardBuffers& b, int T, hipStream_t s) {
@@ -238,8 +253,8 @@ struct RMLAImpl {
             CK(rina_hip_linear_fused(s2, 2, qt, cq, 1, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
             rina_linear_seg s3{w_k2v, nullptr, v, Hkv * dh};
             CK(rina_hip_linear_fused(&s3, 1, qt, k, 1, Hkv * dh, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
-            CK(rina_hip_dq_decode_attention(q, qr, k, kr, v, rqc, rqs, rkc, rks, ck, cv, H, Hkv, dh, dhr, dh,
-                                            start_pos + t, b.d_pos, max_seq, att, ws, ws_bytes, s));
+            CK(rina_hip_dq_decode_attention_kv(q, qr, k, kr, v, rqc, rqs, rkc, rks, kv_mode, ck, cv, ckr, H, Hkv, dh,
+                                               dhr, dh, start_pos + t, b.d_pos, max_seq, att, ws, ws_bytes, s));
             rina_linear_seg so{c_proj, nullptr, ht, d};
             CK(rina_hip_linear_fused(&so, 1, qt, att, 1, H * dh, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
             CK(mlp.run(ht, b, d, qt, s));

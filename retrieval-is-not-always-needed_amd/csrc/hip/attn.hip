@@ -415,12 +415,31 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(SplitArgs a) {
 struct DqArgs {
     const float *qa, *qb, *ka, *kb, *v;
     const float *qc, *qs, *kc, *ks;     // HF RoPE tables [max_seq][db/2] (NULL: none)
-    float* ck;                          // [max_seq][Hkv][dq]
-    float* cv;                          // [max_seq][Hkv][dv]
+    float* ck;                          // fp32 cache: [max_seq][Hkv][dq]
+    float* cv;                          // fp32 cache: [max_seq][Hkv][dv]
+    uint8_t* ckq;                       // q2k_q1v: key content, q2_1 blocks [max_seq][Hkv][da/32]
+    float* ckr;                         // q2k_q1v: key RoPE part, fp32 [max_seq][Hkv][db]
+    uint8_t* cvq;                       // q2k_q1v: values, q1_0 records [max_seq][Hkv][dv/32]
     int H, Hkv, da, db, dv, start_pos, max_seq;
     const int* d_pos;
     float scale;
 };
+
+// Dim `lane` (< 64) of a q2_1-packed 64-value row / a q1_0-packed 64-value
+// row (two 32-value blocks each): kernels/quantize.cu:106-133, :160-185.
+__device__ __forceinline__ float q2_1_dim(const uint8_t* row, int lane) {
+    const uint8_t* b = row + (lane >> 5) * 10;
+    const int i = lane & 31;
+    const float s = f16_to_f32(kvq::ld16(b));
+    return (float)((int)((b[2 + (i >> 2)] >> ((i & 3) * 2)) & 3) - 1) * s;
+}
+__device__ __forceinline__ float q1_0_dim(const uint8_t* row, int lane) {
+    const uint8_t* b = row + (lane >> 5) * 6;
+    const int i = lane & 31;
+    const float s = f16_to_f32(kvq::ld16(b));
+    const uint32_t half = kvq::ld16(b + 2 + ((i >> 4) << 1));
+    return ((half >> (i & 15)) & 1u) ? s : -s;
+}
 
 constexpr int kDqChunk = 32;
 
@@ -444,9 +463,13 @@ __device__ __forceinline__ float dq_dim(const float* xa, const float* xb, const 
     return i < da ? va : vb;
 }
 
+// QKV: 0 = fp32 caches; 1 = the q2k_q1v cache (key content q2_1, key RoPE
+// part fp32, values q1_0; da == 64, dv == 64)
+template <int QKV>
 __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     __shared__ float s_o[4][64];
     __shared__ float s_m[4], s_l[4];
+    __shared__ float s_row[2][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;
@@ -477,10 +500,16 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     for (int i = 0; i < PW; i++) {
         const int pp = wave + 4 * i;
         const int64_t jp = j0 + (pp < ncv ? pp : 0);
-        const float* kr = a.ck + (jp * a.Hkv + kvh) * dq;
-        k0[i] = gld(kr + lane);
-        k1[i] = lane + 64 < dq ? gld(kr + lane + 64) : 0.f;
-        vv[i] = gld(a.cv + (jp * a.Hkv + kvh) * a.dv + lane);
+        if (QKV == 0) {
+            const float* kr = a.ck + (jp * a.Hkv + kvh) * dq;
+            k0[i] = gld(kr + lane);
+            k1[i] = lane + 64 < dq ? gld(kr + lane + 64) : 0.f;
+            vv[i] = gld(a.cv + (jp * a.Hkv + kvh) * a.dv + lane);
+        } else {
+            k0[i] = q2_1_dim(a.ckq + (jp * a.Hkv + kvh) * 20, lane);
+            k1[i] = lane < a.db ? gld(a.ckr + (jp * a.Hkv + kvh) * a.db + lane) : 0.f;
+            vv[i] = q1_0_dim(a.cvq + (jp * a.Hkv + kvh) * 12, lane);
+        }
     }
     // scores in base-2 units (the partials the combine kernel merges)
     const float sc2 = a.scale * 1.44269504088896341f;
@@ -500,11 +529,27 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     }
     // append at pos0 by the KV head's first query head (no workgroup of
     // this launch reads that row)
-    if (has_cur && h % rep == 0 && wave == 0) {
+    if (QKV == 0 && has_cur && h % rep == 0 && wave == 0) {
         float* kd = a.ck + ((int64_t)pos0 * a.Hkv + kvh) * dq;
         gst(kd + lane, kc0);
         if (lane + 64 < dq) gst(kd + lane + 64, kc1);
         gst(a.cv + ((int64_t)pos0 * a.Hkv + kvh) * a.dv + lane, vc);
+    }
+    if (QKV == 1 && has_cur && h % rep == 0) {
+        // the current key content and value rows packed with the KV cache's
+        // block codec (the same code as rina_hip_kv_quantize), the RoPE part
+        // stored as is
+        if (wave == 0) {
+            s_row[0][lane] = kc0;
+            s_row[1][lane] = vc;
+            if (lane < a.db) gst(a.ckr + ((int64_t)pos0 * a.Hkv + kvh) * a.db + lane, kc1);
+        }
+        __syncthreads();
+        if (wave == 0 && (lane & 31) == 0) {
+            const int b = lane >> 5;
+            kvq::quantize_block(RINA_KVF_Q2_1, &s_row[0][32 * b], a.ckq + ((int64_t)pos0 * a.Hkv + kvh) * 20 + 10 * b);
+            kvq::quantize_block(RINA_KVF_Q1_0, &s_row[1][32 * b], a.cvq + ((int64_t)pos0 * a.Hkv + kvh) * 12 + 6 * b);
+        }
     }
     s_o[wave][lane] = o;
     if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
@@ -875,17 +920,21 @@ extern "C" size_t rina_hip_dq_attention_workspace(int H, int dq, int max_pos) {
     return nch * H * (2 + 64) * sizeof(float);
 }
 
-extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, const float* ka, const float* kb,
-                                            const float* v, const float* rope_q_cos, const float* rope_q_sin,
-                                            const float* rope_k_cos, const float* rope_k_sin, float* cache_k,
-                                            float* cache_v, int H, int Hkv, int da, int db, int dv, int start_pos,
-                                            const int* d_pos, int max_seq, float* out, void* workspace,
-                                            size_t ws_bytes, void* stream) {
-    if (!qa || !ka || !v || !cache_k || !cache_v || !out || H < 1 || Hkv < 1 || da < 1 || db < 0 || max_seq < 1)
-        return RINA_ERR_ARG;
+namespace {
+int dq_attention(const float* qa, const float* qb, const float* ka, const float* kb, const float* v,
+                 const float* rope_q_cos, const float* rope_q_sin, const float* rope_k_cos, const float* rope_k_sin,
+                 int kv_mode, float* cache_k, float* cache_v, uint8_t* cache_kc, float* cache_kr, uint8_t* cache_vq,
+                 int H, int Hkv, int da, int db, int dv, int start_pos, const int* d_pos, int max_seq, float* out,
+                 void* workspace, size_t ws_bytes, hipStream_t st) {
+    if (!qa || !ka || !v || !out || H < 1 || Hkv < 1 || da < 1 || db < 0 || max_seq < 1) return RINA_ERR_ARG;
     if (db > 0 && (!qb || !kb)) return RINA_ERR_ARG;
+    if (kv_mode == RINA_KV_FP32 && (!cache_k || !cache_v)) return RINA_ERR_ARG;
+    if (kv_mode == RINA_KV_Q2K_Q1V && (!cache_kc || !cache_vq || (db > 0 && !cache_kr))) return RINA_ERR_ARG;
+    if (kv_mode != RINA_KV_FP32 && kv_mode != RINA_KV_Q2K_Q1V) return RINA_ERR_QTYPE;
     if ((!rope_q_cos) != (!rope_q_sin) || (!rope_k_cos) != (!rope_k_sin)) return RINA_ERR_ARG;
     if (H % Hkv || dv != 64 || da + db > 128 || da + db < 64 || db % 2) return RINA_ERR_SHAPE;
+    if (kv_mode == RINA_KV_Q2K_Q1V && (da != 64 || db > 64 || ((uintptr_t)cache_kc | (uintptr_t)cache_vq) % 2))
+        return RINA_ERR_SHAPE;
     if (!d_pos && (start_pos < 0 || start_pos >= max_seq)) return RINA_ERR_RANGE;
     const int max_pos = d_pos ? max_seq : start_pos + 1;
     const int nch = (max_pos + kDqChunk - 1) / kDqChunk;
@@ -895,7 +944,7 @@ extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, co
     DqArgs a{};
     a.qa = qa; a.qb = qb; a.ka = ka; a.kb = kb; a.v = v;
     a.qc = rope_q_cos; a.qs = rope_q_sin; a.kc = rope_k_cos; a.ks = rope_k_sin;
-    a.ck = cache_k; a.cv = cache_v;
+    a.ck = cache_k; a.cv = cache_v; a.ckq = cache_kc; a.ckr = cache_kr; a.cvq = cache_vq;
     a.H = H; a.Hkv = Hkv; a.da = da; a.db = db; a.dv = dv;
     a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos;
     a.scale = 1.0f / sqrtf((float)(da + db));
@@ -904,12 +953,48 @@ extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, co
     p.ws_l = p.ws_m + (size_t)nch * H;
     p.ws_o = p.ws_l + (size_t)nch * H;
     p.out = out; p.H = H; p.start_pos = start_pos; p.max_seq = max_seq; p.d_pos = d_pos; p.chunk = kDqChunk;
-    hipStream_t st = as_stream(stream);
     // chunks padded to the 8 XCDs: the query heads of one chunk share its
     // cache rows in one L2 (padding workgroups start past max_seq and return)
-    hipLaunchKernelGGL(dq_split_kernel, dim3((nch + 7) / 8 * 8, H), dim3(256), 0, st, a, p);
+    const dim3 grid((nch + 7) / 8 * 8, H);
+    if (kv_mode == RINA_KV_FP32) hipLaunchKernelGGL(dq_split_kernel<0>, grid, dim3(256), 0, st, a, p);
+    else hipLaunchKernelGGL(dq_split_kernel<1>, grid, dim3(256), 0, st, a, p);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(attn_combine_kernel, dim3(H), dim3(256), 0, st, p);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
+}
+}  // namespace
+
+extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, const float* ka, const float* kb,
+                                            const float* v, const float* rope_q_cos, const float* rope_q_sin,
+                                            const float* rope_k_cos, const float* rope_k_sin, float* cache_k,
+                                            float* cache_v, int H, int Hkv, int da, int db, int dv, int start_pos,
+                                            const int* d_pos, int max_seq, float* out, void* workspace,
+                                            size_t ws_bytes, void* stream) {
+    return dq_attention(qa, qb, ka, kb, v, rope_q_cos, rope_q_sin, rope_k_cos, rope_k_sin, RINA_KV_FP32, cache_k,
+                        cache_v, nullptr, nullptr, nullptr, H, Hkv, da, db, dv, start_pos, d_pos, max_seq, out,
+                        workspace, ws_bytes, as_stream(stream));
+}
+
+extern "C" size_t rina_hip_dq_kv_region_bytes(int kv_mode, int part, int max_seq, int Hkv, int da, int db, int dv) {
+    if (max_seq < 1 || Hkv < 1 || da < 1 || db < 0 || dv < 1 || part < 0 || part > 2) return 0;
+    const size_t rows = (size_t)max_seq * Hkv;
+    if (kv_mode == RINA_KV_FP32) return part == 0 ? rows * (da + db) * 4 : part == 1 ? rows * dv * 4 : 0;
+    if (kv_mode != RINA_KV_Q2K_Q1V || da % 32 || dv % 32) return 0;
+    return part == 0 ? rows * (da / 32) * 10 : part == 1 ? rows * (dv / 32) * 6 : rows * db * 4;
+}
+
+extern "C" int rina_hip_dq_decode_attention_kv(const float* qa, const float* qb, const float* ka, const float* kb,
+                                               const float* v, const float* rope_q_cos, const float* rope_q_sin,
+                                               const float* rope_k_cos, const float* rope_k_sin, int kv_mode,
+                                               void* cache_k, void* cache_v, float* cache_kr, int H, int Hkv,
+                                               int da, int db, int dv, int start_pos, const int* d_pos, int max_seq,
+                                               float* out, void* workspace, size_t ws_bytes, void* stream) {
+    if (kv_mode == RINA_KV_FP32)
+        return dq_attention(qa, qb, ka, kb, v, rope_q_cos, rope_q_sin, rope_k_cos, rope_k_sin, kv_mode,
+                            (float*)cache_k, (float*)cache_v, nullptr, nullptr, nullptr, H, Hkv, da, db, dv, start_pos,
+                            d_pos, max_seq, out, workspace, ws_bytes, as_stream(stream));
+    return dq_attention(qa, qb, ka, kb, v, rope_q_cos, rope_q_sin, rope_k_cos, rope_k_sin, kv_mode, nullptr, nullptr,
+                        (uint8_t*)cache_k, cache_kr, (uint8_t*)cache_v, H, Hkv, da, db, dv, start_pos, d_pos, max_seq,
+                        out, workspace, ws_bytes, as_stream(stream));
 }

@@ -410,7 +410,7 @@ class SynthJamba:
     RINA-MLA layers with Q4_0 linears packed on the device, LayerNorm, fp32
     tied embedding / LM head, HF RoPE tables."""
 
-    def __init__(self, cfg=JAMBA, seed=1, max_seq=2048, keep_host=False, std=0.02):
+    def __init__(self, cfg=JAMBA, seed=1, max_seq=2048, keep_host=False, std=0.02, kv_mode="fp32"):
         torch = _torch()
         c = self.cfg = dict(cfg)
         self.max_seq = max_seq
@@ -420,7 +420,8 @@ class SynthJamba:
                                          c["hidden_dim"], c["vocab_size"])
         header = {"name": c["name"], "dim": d, "n_layers": c["n_layers"], "n_heads": H, "n_kv_heads": Hkv,
                   "head_dim": dh, "d_h_r": dhr, "d_c": dc, "ssm_steps": c["ssm_steps"], "vocab_size": V,
-                  "max_seq_len": max_seq, "hidden_dim": hd, "layers": [{"type": t} for t in self.types]}
+                  "max_seq_len": max_seq, "hidden_dim": hd, "kv_quant_mode": kv_mode,
+                  "layers": [{"type": t} for t in self.types]}
         eng = load_engine()
         self._eng = eng
         self.arena = DeviceArena()

@@ -78,8 +78,12 @@ def rope_hf(x, cos, sin):
     return y
 
 
-def forward(mats, ids, cfg=CFG, types=TYPES):
-    """float64 logits of the last row, full recompute over ids"""
+def forward(mats, ids, cfg=CFG, types=TYPES, history=None):
+    """float64 logits of the last row, full recompute over ids.  history:
+    layer -> (K content [T, Hkv, dh], V [T, Hkv, dh]) that position tt's
+    attention reads for positions < tt instead of the computed rows (the
+    q2k_q1v RINA-MLA cache: earlier positions dequantized, the own position
+    from its computed rows; the RoPE part never quantized)."""
     c = cfg
     d, H, Hkv, dh, dhr = c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["d_h_r"]
     T = len(ids)
@@ -111,12 +115,15 @@ def forward(mats, ids, cfg=CFG, types=TYPES):
                          mats[p + "path.rope.sin"])
             att = np.zeros((T, H, dh))
             rep = H // Hkv
+            kh, vh = (k, v) if history is None or l not in history else history[l]
             for tt in range(T):
                 for hh in range(H):
                     g = hh // rep
                     qq = np.concatenate([q[tt, hh], qr[tt, hh]])
-                    K = np.concatenate([k[: tt + 1, g], kr[: tt + 1, g]], axis=1)
-                    att[tt, hh] = nr.softmax_attn(qq, K, v[: tt + 1, g], 1 / np.sqrt(dh + dhr))
+                    kc_rows = np.concatenate([kh[:tt, g], k[tt:tt + 1, g]], axis=0)
+                    v_rows = np.concatenate([vh[:tt, g], v[tt:tt + 1, g]], axis=0)
+                    K = np.concatenate([kc_rows, kr[: tt + 1, g]], axis=1)
+                    att[tt, hh] = nr.softmax_attn(qq, K, v_rows, 1 / np.sqrt(dh + dhr))
             h = h + att.reshape(T, H * dh) @ mats[p + "path.c_proj.weight"].T
         a = ln(h, mats[p + "ln2.weight"])
         g = a @ mats[p + "mlp.w1.weight"].T

@@ -194,3 +194,176 @@ def test_jamba_config5_full_context_128_steps(rina, orc):
         assert len(set(got)) >= 16
     finally:
         sm.close()
+
+
+@pytest.mark.parametrize("P,use_dpos", [(0, False), (9, False), (70, True), (300, False)])
+@pytest.mark.parametrize("H,Hkv,db", [(10, 5, 32), (4, 2, 16)])
+def test_dq_decode_attention_q2k_q1v(rina, orc, P, use_dpos, H, Hkv, db):
+    """The q2 K / q1 V RINA-MLA cache: earlier positions are read through
+    their packs (key content q2_1, values q1_0, the RoPE part fp32), the
+    current one from its fp32 rows, which are appended packed: the appended
+    bytes equal the KV packers' (bit-exact), the RoPE part is stored as
+    rotated, no other position changes, and the output is within 1e-5 of a
+    float64 softmax over that history."""
+    hip = rina.load_hip()
+    da, dv = 64, 64
+    dq = da + db
+    max_seq = P + 5
+    r = rng(P + H + db + 1000)
+    ckf = r.standard_normal((max_seq, Hkv, da)).astype(np.float32)    # history before packing
+    cvf = r.standard_normal((max_seq, Hkv, dv)).astype(np.float32)
+    ckr = r.standard_normal((max_seq, Hkv, db)).astype(np.float32)
+    ckq = orc.kv_quantize(3, ckf.reshape(-1))
+    cvq = orc.kv_quantize(4, cvf.reshape(-1))
+    Kc = orc.kv_dequant(3, ckq, ckf.size).reshape(max_seq, Hkv, da).astype(np.float64)
+    Vh = orc.kv_dequant(4, cvq, cvf.size).reshape(max_seq, Hkv, dv).astype(np.float64)
+    qa = r.standard_normal((H, da)).astype(np.float32)
+    qb = r.standard_normal((H, db)).astype(np.float32)
+    ka = r.standard_normal((Hkv, da)).astype(np.float32)
+    kb = r.standard_normal((Hkv, db)).astype(np.float32)
+    v = r.standard_normal((Hkv, dv)).astype(np.float32)
+    ang = np.outer(np.arange(max_seq), 1.0 / 10000 ** (np.arange(0, db, 2) / db)).astype(np.float32)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+    def rope(x):   # HF pairs at position P, reference fma form in fp32
+        c, s = cos[P], sin[P]
+        y = x.copy()
+        x0, x1 = x[..., 0::2], x[..., 1::2]
+        y[..., 0::2] = (x0.astype(np.float64) * c - (x1 * s).astype(np.float32)).astype(np.float32)
+        y[..., 1::2] = (x0.astype(np.float64) * s + (x1 * c).astype(np.float32)).astype(np.float32)
+        return y
+
+    qf = np.concatenate([qa, rope(qb)], axis=1).astype(np.float64)
+    krot = rope(kb)
+    K = np.concatenate([Kc, ckr.astype(np.float64)], axis=2)
+    V = Vh.copy()
+    K[P] = np.concatenate([ka, krot], axis=1)
+    V[P] = v
+    rep = H // Hkv
+    ref = np.concatenate([nr.softmax_attn(qf[h], K[: P + 1, h // rep], V[: P + 1, h // rep], 1 / np.sqrt(dq))
+                          for h in range(H)])
+    wsb = hip.rina_hip_dq_attention_workspace(H, dq, max_seq)
+    ws = empty(wsb, "uint8")
+    for part, arr in ((0, ckq), (1, cvq), (2, ckr)):
+        assert hip.rina_hip_dq_kv_region_bytes(5, part, max_seq, Hkv, da, db, dv) == arr.nbytes
+    ckd, cvd, krd = dev(ckq), dev(cvq), dev(ckr)
+    od = empty(H * dv)
+    cd, sd = dev(cos), dev(sin)
+    pos = dev(np.array([P], np.int32)) if use_dpos else None
+    ok(hip.rina_hip_dq_decode_attention_kv(dev(qa).data_ptr(), dev(qb).data_ptr(), dev(ka).data_ptr(),
+                                           dev(kb).data_ptr(), dev(v).data_ptr(), cd.data_ptr(), sd.data_ptr(),
+                                           cd.data_ptr(), sd.data_ptr(), 5, ckd.data_ptr(), cvd.data_ptr(),
+                                           krd.data_ptr(), H, Hkv, da, db, dv, 0 if use_dpos else P,
+                                           pos.data_ptr() if use_dpos else None, max_seq, od.data_ptr(),
+                                           ws.data_ptr(), wsb, stream()), "dq attention q2k_q1v")
+    assert_close(host(od), ref, what="dq attention q2k_q1v P %d" % P)
+    gk, gv, gr = host(ckd), host(cvd), host(krd).reshape(max_seq, Hkv, db)
+    kbytes, vbytes = Hkv * (da // 32) * 10, Hkv * (dv // 32) * 6
+    assert np.array_equal(gk[P * kbytes:(P + 1) * kbytes], orc.kv_quantize(3, ka.reshape(-1)))
+    assert np.array_equal(gv[P * vbytes:(P + 1) * vbytes], orc.kv_quantize(4, v.reshape(-1)))
+    assert np.max(np.abs(gr[P] - krot)) <= 2e-6 * np.max(np.abs(krot))
+    keep = np.ones(max_seq, bool)
+    keep[P] = False
+    assert np.array_equal(gk.reshape(max_seq, -1)[keep], ckq.reshape(max_seq, -1)[keep])
+    assert np.array_equal(gv.reshape(max_seq, -1)[keep], cvq.reshape(max_seq, -1)[keep])
+    assert np.array_equal(gr[keep], ckr[keep])
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_jamba_q2k_q1v_cache_greedy(rina, orc, use_graph):
+    """The tiny hybrid with the q2 K / q1 V RINA-MLA cache: the engine's
+    greedy tokens equal the oracle's in the same cache mode, and so do the
+    logits of a prefill and of three host-position decode steps (1e-5),
+    which differ from the fp32-cache model's by far more (the packed
+    history is what the steps read)."""
+    import torch
+    synth = importlib.import_module("rina_amd.synth")
+    max_seq = 48
+    tensors, mats, shapes = jt.build(orc, seed=21, max_pos=max_seq)
+    qts = {n: (6 if a.dtype == np.float32 else jt.Q4_0) for n, a in tensors.items()}
+    up = {n: (qts[n], shapes[n], tensors[n]) for n in tensors}
+    hdr = header(max_seq)
+    hdr["kv_quant_mode"] = "q2k_q1v"
+    hm = synth.HostModel(hdr, up)
+    try:
+        eng = rina.load_engine()
+        inf = hm.infer("gqa", max_seq=max_seq)
+        prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+        steps = 20
+        out = (C.c_int * steps)()
+        rina.check(eng.rina_infer_generate(inf, (C.c_int * len(prompt))(*prompt), len(prompt), steps, out,
+                                           1 if use_graph else 0, stream(), None), "generate")
+        eng.rina_infer_destroy(inf)
+        m, hold = orc.jamba_from_tensors(jt.CFG, tensors, jt.TYPES, jt.Q4_0, max_seq, kv_mode="q2k_q1v")
+        ref = orc.jamba_generate(m, prompt, steps)
+        orc.load().orc_jamba_destroy(m)
+        assert list(out) == ref
+        # logits: prefill of 6 tokens, then 3 decode steps at host positions
+        L = orc.load()
+        V = jt.CFG["vocab_size"]
+        mq, hq = orc.jamba_from_tensors(jt.CFG, tensors, jt.TYPES, jt.Q4_0, max_seq, kv_mode="q2k_q1v")
+        mf, hf = orc.jamba_from_tensors(jt.CFG, tensors, jt.TYPES, jt.Q4_0, max_seq)
+        inf = hm.infer("gqa", max_seq=max_seq)
+        ids = np.array([5, 17, 3, 90, 42, 7], np.int32)
+        lg = empty(len(ids) * V)
+        rina.check(eng.rina_infer_forward(inf, torch.from_numpy(ids).cuda().data_ptr(), lg.data_ptr(), 1, len(ids), 0,
+                                          stream()), "forward")
+        rq, rf = np.zeros(V, np.float32), np.zeros(V, np.float32)
+        L.orc_jamba_forward(mq, ids.ctypes.data, len(ids), 0, rq.ctypes.data, 1)
+        L.orc_jamba_forward(mf, ids.ctypes.data, len(ids), 0, rf.ctypes.data, 1)
+        assert_close(host(lg).reshape(len(ids), V)[-1], rq, what="q2k_q1v prefill logits")
+        far = 0.0
+        for t, nxt in enumerate([11, 64, 2]):
+            x = np.array([nxt], np.int32)
+            rina.check(eng.rina_infer_forward(inf, torch.from_numpy(x).cuda().data_ptr(), lg.data_ptr(), 1, 1, 6 + t,
+                                              stream()), "decode")
+            L.orc_jamba_forward(mq, x.ctypes.data, 1, 6 + t, rq.ctypes.data, 1)
+            L.orc_jamba_forward(mf, x.ctypes.data, 1, 6 + t, rf.ctypes.data, 1)
+            assert_close(host(lg)[:V], rq, what="q2k_q1v decode logits %d" % t)
+            far = max(far, float(np.max(np.abs(rq - rf)) / np.max(np.abs(rf))))
+        eng.rina_infer_destroy(inf)
+        L.orc_jamba_destroy(mq)
+        L.orc_jamba_destroy(mf)
+        assert far > 1e-3, far
+    finally:
+        hm.close()
+
+
+def test_jamba_config5_q2k_q1v_cache(rina, orc):
+    """Config 5's "q2 K / q1 V cache": the full Jamba shape with the packed
+    RINA-MLA cache, a 300-token prompt and 64 greedy steps, identical to the
+    oracle in the same mode (its own prefill), with varied tokens and every
+    step's top-2 margin above twice the 1e-5 tolerance."""
+    synth = importlib.import_module("rina_amd.synth")
+    n_prompt, steps, max_seq = 300, 64, 384
+    sm = synth.SynthJamba(seed=3, max_seq=max_seq, keep_host=True, kv_mode="q2k_q1v")
+    try:
+        eng = rina.load_engine()
+        V = sm.cfg["vocab_size"]
+        prompt = np.random.default_rng(7).integers(0, V, n_prompt).astype(np.int32)
+        inf = sm.infer()
+        out = (C.c_int * (steps + 1))()
+        rina.check(eng.rina_infer_generate(inf, prompt.ctypes.data_as(C.POINTER(C.c_int)), n_prompt, steps + 1, out,
+                                           1, stream(), None), "generate")
+        eng.rina_infer_destroy(inf)
+        got = list(out)
+        m, hold = orc.jamba_from_tensors(sm.cfg, sm.host, sm.types, jt.Q4_0, max_seq, min(os.cpu_count() or 1, 16),
+                                         kv_mode="q2k_q1v")
+        L = orc.load()
+        lg = np.zeros(V, np.float32)
+        ref, margins = [], []
+        ids, T, pos = prompt, n_prompt, 0
+        for s in range(steps + 1):
+            assert L.orc_jamba_forward(m, ids.ctypes.data, T, pos, lg.ctypes.data, 1) == 0
+            top = np.argsort(lg)[::-1][:2]
+            margins.append(float(lg[top[0]] - lg[top[1]]) / float(np.max(np.abs(lg))))
+            tok = L.orc_argmax(lg.ctypes.data, V)
+            ref.append(tok)
+            pos += T
+            ids, T = np.array([tok], np.int32), 1
+        L.orc_jamba_destroy(m)
+        assert got == ref, "first divergence at step %d" % next(i for i in range(steps + 1) if got[i] != ref[i])
+        assert min(margins) > 2 * REL_TOL
+        assert len(set(got)) >= 16
+    finally:
+        sm.close()
