@@ -1007,22 +1007,39 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MfmaArgs ma) {
     const bool xok = sr < BM && m0 + sr < a.M, wok = n0 + sr < a.N;
     const float* xrow = a.x + (int64_t)(xok ? m0 + sr : 0) * a.K + 8 * sq;
     const int64_t wrow = (int64_t)(wok ? n0 + sr : 0) * nb * BB;
+    // Q2_K (flat element order): values 8 sq .. 8 sq + 7 of the row's block b
+    // are elements e = row K + 32 b + 8 sq, inside one 256-value block and
+    // one shift group g of one 128-value page (row starts and b are
+    // multiples of 32): qs bytes 16 + 32 page + 8 sq .. + 7, scale byte
+    // 8 page + sq / 2 + 2 g, fp16 d / dmin at 80 / 82
+    const int64_t erow = (int64_t)(wok ? n0 + sr : 0) * a.K + 8 * sq;
     f32x4 xr0, xr1;
-    uint32_t wsc[NMAT], wnb[NMAT];
+    uint32_t wsc[NMAT], wnb[NMAT], wq1[NMAT], wdd[NMAT];
     auto load_blk = [&](int b) {
         const f32x4* xp = (const f32x4*)(xrow + 32 * b);
         xr0 = gld(xp);
         xr1 = gld(xp + 1);
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            const uint8_t* bp = (m ? a.w2 : a.w) + wrow + (int64_t)b * BB;
-            if constexpr (FMT == FMT_Q4_0F) {
-                wsc[m] = gld((const uint32_t*)bp);
-                wnb[m] = gld((const uint32_t*)(bp + 4 + 4 * sq));
+            if constexpr (FMT == FMT_Q2_K) {
+                const int64_t e = erow + 32 * b;
+                const uint8_t* bd = (m ? a.w2 : a.w) + (e >> 8) * 84;
+                const int inb = (int)(e & 255), page = inb >> 7, g = (inb & 127) >> 5;
+                const int is = 8 * page + (sq >> 1) + 2 * g;
+                wnb[m] = gld((const uint32_t*)(bd + 16 + 32 * page + 8 * sq));
+                wq1[m] = gld((const uint32_t*)(bd + 20 + 32 * page + 8 * sq));
+                wsc[m] = ((gld((const uint32_t*)(bd + (is & ~3))) >> (8 * (is & 3))) & 0xFF) | ((uint32_t)(2 * g) << 8);
+                wdd[m] = gld((const uint32_t*)(bd + 80));
             } else {
-                wsc[m] = gld((const uint16_t*)bp);
-                wnb[m] = (uint32_t)gld((const uint16_t*)(bp + 2 + 4 * sq)) |
-                         ((uint32_t)gld((const uint16_t*)(bp + 4 + 4 * sq)) << 16);
+                const uint8_t* bp = (m ? a.w2 : a.w) + wrow + (int64_t)b * BB;
+                if constexpr (FMT == FMT_Q4_0F) {
+                    wsc[m] = gld((const uint32_t*)bp);
+                    wnb[m] = gld((const uint32_t*)(bp + 4 + 4 * sq));
+                } else {
+                    wsc[m] = gld((const uint16_t*)bp);
+                    wnb[m] = (uint32_t)gld((const uint16_t*)(bp + 2 + 4 * sq)) |
+                             ((uint32_t)gld((const uint16_t*)(bp + 4 + 4 * sq)) << 16);
+                }
             }
         }
     };
@@ -1035,10 +1052,22 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MfmaArgs ma) {
         }
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            const float sc = FMT == FMT_Q4_0F ? __uint_as_float(wsc[m]) : f16_to_f32((uint16_t)wsc[m]);
+            if constexpr (FMT == FMT_Q2_K) {
+                // ops/linear.cu:413-431: d * (sc & 15) * q - dmin * (sc >> 4)
+                const uint32_t sc = wsc[m] & 0xFF, sh = wsc[m] >> 8;
+                const float dv = f16_to_f32((uint16_t)(wdd[m] & 0xFFFF)), mv = f16_to_f32((uint16_t)(wdd[m] >> 16));
+                const float scale = dv * (float)(sc & 0xF), mn = mv * (float)(sc >> 4);
 #pragma unroll
-            for (int t = 0; t < 8; t++)
-                ws[m][8 * sq + t][sr] = wok ? (float)((int)((wnb[m] >> (4 * t)) & 0xF) - 7) * sc : 0.f;
+                for (int t = 0; t < 8; t++) {
+                    const uint32_t qb = ((t < 4 ? wnb[m] : wq1[m]) >> (8 * (t & 3))) & 0xFF;
+                    ws[m][8 * sq + t][sr] = wok ? fmaf(scale, (float)((qb >> sh) & 3), -mn) : 0.f;
+                }
+            } else {
+                const float sc = FMT == FMT_Q4_0F ? __uint_as_float(wsc[m]) : f16_to_f32((uint16_t)wsc[m]);
+#pragma unroll
+                for (int t = 0; t < 8; t++)
+                    ws[m][8 * sq + t][sr] = wok ? (float)((int)((wnb[m] >> (4 * t)) & 0xF) - 7) * sc : 0.f;
+            }
         }
     };
     const int wm = (wave >> 1) * 16 * MI, wn = (wave & 1) * 32;
@@ -1351,7 +1380,8 @@ int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int e
 }
 
 bool mfma_ok(int qt, const float* x, int M, int K) {
-    return M >= 16 && (qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F) && K % 32 == 0 && (uintptr_t)x % 16 == 0;
+    return M >= 16 && (qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F || qt == RINA_QT_GGML_Q2_K) && K % 32 == 0 &&
+           (uintptr_t)x % 16 == 0;
 }
 
 // Matrix-core prompt matmul over up to 3 segments sharing x (one launch).
@@ -1379,6 +1409,9 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     if (qt == RINA_QT_Q4_0F) {
         if (two) MFMA_LAUNCH(FMT_Q4_0F, 2);
         else MFMA_LAUNCH(FMT_Q4_0F, 1);
+    } else if (qt == RINA_QT_GGML_Q2_K) {
+        if (two) MFMA_LAUNCH(FMT_Q2_K, 2);
+        else MFMA_LAUNCH(FMT_Q2_K, 1);
     } else {
         if (two) MFMA_LAUNCH(FMT_Q4_0, 2);
         else MFMA_LAUNCH(FMT_Q4_0, 1);
@@ -1388,8 +1421,8 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
 }
 
 int gemm_tiled(const rina_linear_seg& seg, int qt, const float* x, int M, int K, int epi, hipStream_t st) {
-    // matrix cores for prompt-sized M and Q4 weights (K % 32 == 0, x rows
-    // 16-byte aligned; weight rows are 4-byte aligned for Q4_0F)
+    // matrix cores for prompt-sized M and Q4 / Q2_K weights (K % 32 == 0, x
+    // rows 16-byte aligned; weights 4-byte aligned)
     if (mfma_ok(qt, x, M, K)) return gemm_mfma(&seg, 1, qt, x, M, K, epi, st);
     GemmArgs a{(const uint8_t*)seg.weight, epi == RINA_EPI_SWIGLU ? (const uint8_t*)seg.weight2 : nullptr,
                x, seg.out, M, seg.N, K, qt, epi};

@@ -622,18 +622,28 @@ def test_linear_norm_prologue(rina, orc, qt, pro, M, K):
     assert_close(host(y).reshape(M, N), orc.linear(w, qt, xn, N, K), what="prologue %d qt %d" % (pro, qt))
 
 
-@pytest.mark.parametrize("qt", [5, 7])
+def _prefill_weights(orc, qt, r, n):
+    if qt == 10:   # zero-mean Q2_K blocks (flat element order; rows may straddle blocks)
+        import importlib
+        return importlib.import_module("rina_amd.synth").random_q2k(int(r.integers(1 << 30)), n)
+    return orc.pack(qt, (r.standard_normal(n) * 0.02).astype(np.float32))
+
+
+@pytest.mark.parametrize("qt", [5, 7, 10])
 @pytest.mark.parametrize("M,N,K", [(16, 64, 32), (100, 200, 512), (64, 2048, 2048), (130, 77, 320), (512, 96, 1024),
-                                   (520, 4096, 64)])   # the last one takes 64-row tiles, the others 32-row tiles
+                                   (520, 4096, 64),    # 64-row tiles; the others take 32-row tiles
+                                   (48, 1408, 2048), (100, 2048, 1408), (33, 96, 10944)])   # DeepSeek-V2-Lite rows
 @pytest.mark.parametrize("epi", [0, 1, 2])
 def test_linear_prefill_mfma(rina, orc, qt, M, N, K, epi):
     """Prompt-sized M on the matrix-core path: store, residual add and
     SiLU*up epilogues against the oracle's per-row matvec (fp32 products of
-    the dequantized weights, fp32 sums)."""
+    the dequantized weights, fp32 sums).  Q2_K rows in flat element order
+    (K = 320, 1408, 10944 straddle 256-value blocks) are the M > 1 analogue
+    of the fused Q2_K kernel (ops/linear.cu:445-483)."""
     hip = rina.load_hip()
     r = rng(M * 7 + N + K + qt * 3 + epi)
-    w = orc.pack(qt, (r.standard_normal(N * K) * 0.02).astype(np.float32))
-    w3 = orc.pack(qt, (r.standard_normal(N * K) * 0.02).astype(np.float32))
+    w = _prefill_weights(orc, qt, r, N * K)
+    w3 = _prefill_weights(orc, qt, r, N * K)
     x = r.standard_normal((M, K)).astype(np.float32)
     y0 = r.standard_normal((M, N)).astype(np.float32)
     y = dev(y0)
@@ -651,7 +661,7 @@ def test_linear_prefill_mfma(rina, orc, qt, M, N, K, epi):
     assert_close(host(y).reshape(M, N), ref, what="prefill q%d epi %d %s" % (qt, epi, (M, N, K)))
 
 
-@pytest.mark.parametrize("qt", [5, 7])
+@pytest.mark.parametrize("qt", [5, 7, 10])
 @pytest.mark.parametrize("Ns,epi", [((256, 64, 64), 0), ((100, 37), 1), ((2048, 512, 512), 0)])
 def test_linear_prefill_segments(rina, orc, qt, Ns, epi):
     """Several weight segments on one prompt (q / k / v) in one matrix-core
@@ -659,7 +669,7 @@ def test_linear_prefill_segments(rina, orc, qt, Ns, epi):
     hip = rina.load_hip()
     r = rng(sum(Ns) + qt + epi)
     M, K = 100, 512
-    ws = [orc.pack(qt, (r.standard_normal(n * K) * 0.02).astype(np.float32)) for n in Ns]
+    ws = [_prefill_weights(orc, qt, r, n * K) for n in Ns]
     x = r.standard_normal((M, K)).astype(np.float32)
     y0 = [r.standard_normal((M, n)).astype(np.float32) for n in Ns]
     ys = [dev(y) for y in y0]
