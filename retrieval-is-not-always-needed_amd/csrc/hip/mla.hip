@@ -10,10 +10,13 @@
 // expanded K/V) and folds W_kb into the query and W_vb after the softmax:
 //   q_lat_h = W_kb_h^T q_nope_h,  s_j = (q_lat_h . c_j + q_rope_h . kpe_j) scale,
 //   o_h = W_vb_h (sum_j p_j c_j).
-// Short contexts: one launch (mla_fused_kernel).  Longer ones: three
-// launches, prep (q_lat, rotated q_rope, latent append at pos0), split
-// (chunk partials over positions, one workgroup per chunk and head), out
-// (chunk merge and W_vb per head).
+// Short contexts: one launch (mla_fused_kernel).  Longer ones at the
+// DeepSeek-V2 shape: two launches, mla_chunk_kernel (per chunk of positions
+// and head: q_lat, the chunk's softmax partial and W_vb applied to it) and
+// mla_combine_kernel (chunk merge per head).  Other shapes: three launches,
+// prep (q_lat, rotated q_rope, latent append at pos0), split (chunk
+// partials over positions, one workgroup per chunk and head), out (chunk
+// merge and W_vb per head).
 //
 // MoE: device top-k (no host round trip), a gathered SiLU*up matvec over the
 // selected experts, and the down projection that accumulates the experts in
@@ -129,13 +132,31 @@ struct MlaArgs {
     float* ws_l;
     float* ws_o;           // [nchunk][H][dc]
     int H, nope, rope, v, dc, start_pos, max_seq, chunk;
+    int nslot;             // > 0: chunk workgroups; chunk length from the position count (chunk_of)
     const int* d_pos;
     float scale;
 };
 
-constexpr int kMlaChunk = 32;          // positions per split workgroup (8 per wave)
+constexpr int kSplitWaves = 8;         // waves per split workgroup
+constexpr int kMlaChunk = 8 * kSplitWaves;   // positions per split block (8 per wave)
+constexpr int kMlaMaxChunks = 64;      // chunk partials the out kernel merges (host: chunk length adapts)
+constexpr int kPrepRows = 4;           // W_kb rows per prep thread: nope <= 4 * 256 / (dc / 64)
 constexpr int kMaxRecLanes = 10;       // record floats per lane: dc + rope <= 640
 constexpr int kMaxOutLanes = 8;        // latent dims per lane: dc <= 512
+
+// positions per chunk when L positions are dealt to nslot chunk
+// workgroups in whole units of gran positions: as few units per chunk as
+// fill the slots (the merging kernel derives the same chunks)
+__device__ __forceinline__ int dyn_chunk(int L, int nslot, int gran) {
+    const int nt = (L + gran - 1) / gran;
+    return gran * ((nt + nslot - 1) / nslot);
+}
+
+// a.nslot > 0: chunks follow the position count (a.chunk is the unit);
+// else a.chunk positions per chunk
+__device__ __forceinline__ int chunk_of(const MlaArgs& a, int L) {
+    return a.nslot > 0 ? dyn_chunk(L, a.nslot, a.chunk) : a.chunk;
+}
 
 // NeoX rotation of pair (i, i+rope/2) at table row pos, reference fma form
 __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& o0, float& o1) {
@@ -155,27 +176,46 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
     const int R = a.dc + a.rope, hr = a.rope / 2;
     if (blockIdx.x == (unsigned)a.H) {
         if (blockIdx.y) return;
-        float ss = 0.f;
-        for (int k = tid; k < a.dc; k += 256) {
-            const float x = gld(a.kva + k);
-            ss = fmaf(x, x, ss);
-        }
+        // the record [RMSNorm(c_kv) * k_norm | RoPE(k_pe)]: every input is
+        // loaded up front (one memory round trip), dc <= 512, rope / 2 <= 256
+        const int k0 = tid < a.dc ? tid : 0, k1 = tid + 256 < a.dc ? tid + 256 : 0, jr = tid < hr ? tid : 0;
+        const float x0 = gld(a.kva + k0), x1 = gld(a.kva + k1);
+        const float n0 = gld(a.k_norm + k0), n1 = gld(a.k_norm + k1);
+        float p0 = gld(a.kva + a.dc + jr), p1 = gld(a.kva + a.dc + (hr ? jr + hr : 0));
+        const float* tc = a.rc ? a.rc : a.kva;
+        const float* ts = a.rs ? a.rs : a.kva;
+        const float cc = gld(tc + (a.rc ? (int64_t)pos * hr + jr : 0)), sn = gld(ts + (a.rs ? (int64_t)pos * hr + jr : 0));
+        float ss = (tid < a.dc ? x0 * x0 : 0.f);
+        ss = fmaf(tid + 256 < a.dc ? x1 : 0.f, tid + 256 < a.dc ? x1 : 0.f, ss);
         ss = wave_sum(ss);
         if ((tid & 63) == 0) s_red[tid >> 6] = ss;
         __syncthreads();
         const float inv = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)a.dc + a.eps);
         float* rec = a.cache + (int64_t)pos * R;
-        for (int k = tid; k < a.dc; k += 256) gst(rec + k, gld(a.kva + k) * inv * gld(a.k_norm + k));
-        for (int j = tid; j < hr; j += 256) {
-            float x0 = gld(a.kva + a.dc + j), x1 = gld(a.kva + a.dc + j + hr);
-            if (a.rc) rope_pair(x0, x1, gld(a.rc + (int64_t)pos * hr + j), gld(a.rs + (int64_t)pos * hr + j), x0, x1);
-            gst(rec + a.dc + j, x0);
-            gst(rec + a.dc + j + hr, x1);
+        if (tid < a.dc) gst(rec + tid, x0 * inv * n0);
+        if (tid + 256 < a.dc) gst(rec + tid + 256, x1 * inv * n1);
+        if (tid < hr) {
+            if (a.rc) rope_pair(p0, p1, cc, sn, p0, p1);
+            gst(rec + a.dc + tid, p0);
+            gst(rec + a.dc + tid + hr, p1);
         }
         return;
     }
     const int h = blockIdx.x;
     float* qo = a.ws_q + (int64_t)h * R;
+    // q_lat[k] = sum_i q_nope[i] W[h*nope + i][k] for this workgroup's column
+    // quarter: thread = (row slice, 16-column unit).  The thread's weight
+    // units (at most kPrepRows rows; the host checks) are loaded before
+    // q_nope is staged, so one memory round trip covers both.
+    const int ncu = a.dc / 64;
+    const int RS = 256 / ncu;
+    const int cu = blockIdx.y * ncu + tid % ncu, rsl = tid / ncu;
+    float w[kPrepRows][16];
+#pragma unroll
+    for (int j = 0; j < kPrepRows; j++) {
+        const int i = rsl + j * RS < a.nope ? rsl + j * RS : a.nope - 1;
+        load_unit16(a.wkvb, a.qt, ((int64_t)h * a.nope + i) * a.dc + 16 * cu, w[j]);
+    }
     stage_lds(s_q, a.q + (int64_t)h * a.nope, a.nope);
     for (int j = tid; j < hr && blockIdx.y == 0; j += 256) {
         const float* qr = a.q + (int64_t)a.H * a.nope + (int64_t)h * a.rope;
@@ -185,21 +225,15 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
         gst(qo + a.dc + j + hr, x1);
     }
     __syncthreads();
-    // q_lat[k] = sum_i q_nope[i] W[h*nope + i][k] for this workgroup's column
-    // quarter: thread = (row slice, 16-column unit)
-    const int ncu = a.dc / 64;
-    const int RS = 256 / ncu;
-    const int cu = blockIdx.y * ncu + tid % ncu, rsl = tid / ncu;
     float acc[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) acc[j] = 0.f;
-#pragma unroll 4
-    for (int i = rsl; i < a.nope; i += RS) {
-        float w[16];
-        load_unit16(a.wkvb, a.qt, ((int64_t)h * a.nope + i) * a.dc + 16 * cu, w);
-        const float qi = s_q[i];
 #pragma unroll
-        for (int j = 0; j < 16; j++) acc[j] = fmaf(qi, w[j], acc[j]);
+    for (int jr = 0; jr < kPrepRows; jr++) {
+        const int i = rsl + jr * RS;
+        const float qi = i < a.nope ? s_q[i] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[j] = fmaf(qi, w[jr][j], acc[j]);
     }
     const int cw = a.dc / 4;                      // columns of this workgroup
 #pragma unroll
@@ -212,52 +246,71 @@ __global__ __launch_bounds__(256) void mla_prep_kernel(MlaArgs a) {
     }
 }
 
-// grid (nchunk, H): each wave takes 8 positions of the chunk (loads issued
-// together), lanes cover the record's dims; online softmax per wave, waves
-// merged in LDS, chunk partials (m, l, sum p c) written.
-__global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
-    __shared__ float s_o[4][512];
-    __shared__ float s_m[4], s_l[4];
+// grid (nchunk, H): the workgroup walks its chunk (a.chunk positions, a
+// multiple of kMlaChunk) in blocks of kMlaChunk; each wave takes 8 positions
+// of a block (loads issued together), lanes cover the record's dims.  Per
+// block: the wave's 8 scores first (independent dot products and
+// reductions), then one softmax update (maximum, rescale, weights; base-2
+// units).  Waves merged in LDS, chunk partials (m, l, sum p c) written.
+__global__ __launch_bounds__(64 * kSplitWaves) void mla_split_kernel(MlaArgs a) {
+    __shared__ float s_o[kSplitWaves][512];
+    __shared__ float s_m[kSplitWaves], s_l[kSplitWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;
     const int L = pos0 + 1, c = blockIdx.x, h = blockIdx.y;
-    const int j0 = c * kMlaChunk;
-    if (j0 >= L) return;
-    const int ncv = min(kMlaChunk, L - j0);
+    const int jc = c * a.chunk;
+    if (jc >= L) return;
+    const int jend = min(jc + a.chunk, L);
     const int R = a.dc + a.rope;
     const float* qh = a.ws_q + (int64_t)h * R;
     float qv[kMaxRecLanes];
 #pragma unroll
     for (int j = 0; j < kMaxRecLanes; j++) qv[j] = (lane + 64 * j < R) ? gld(qh + lane + 64 * j) : 0.f;
-    // this wave's positions: j0 + wave + 4 i (past the chunk end: the chunk's
-    // first position, masked below)
-    constexpr int PW = kMlaChunk / 4;
-    float kv[PW][kMaxRecLanes];
-#pragma unroll
-    for (int i = 0; i < PW; i++) {
-        const int p = wave + 4 * i;
-        const float* rec = a.cache + (int64_t)(j0 + (p < ncv ? p : 0)) * R;
-#pragma unroll
-        for (int j = 0; j < kMaxRecLanes; j++) kv[i][j] = (lane + 64 * j < R) ? gld(rec + lane + 64 * j) : 0.f;
-    }
+    const float sc2 = a.scale * 1.44269504088896341f;
+    constexpr int PW = kMlaChunk / kSplitWaves;
     float m = -INFINITY, l = 0.f, o[kMaxOutLanes];
 #pragma unroll
     for (int j = 0; j < kMaxOutLanes; j++) o[j] = 0.f;
+    for (int j0 = jc; j0 < jend; j0 += kMlaChunk) {
+        const int ncv = min(kMlaChunk, jend - j0);
+        // this wave's positions: j0 + wave + kSplitWaves i (past the block
+        // end: its first position, masked below)
+        float kv[PW][kMaxRecLanes];
 #pragma unroll
-    for (int i = 0; i < PW; i++) {
-        float dot = 0.f;
+        for (int i = 0; i < PW; i++) {
+            const int p = wave + kSplitWaves * i;
+            const float* rec = a.cache + (int64_t)(j0 + (p < ncv ? p : 0)) * R;
 #pragma unroll
-        for (int j = 0; j < kMaxRecLanes; j++) dot = fmaf(qv[j], kv[i][j], dot);
-        const float s = wave_sum(dot) * a.scale;
-        if (wave + 4 * i < ncv) {
-            const float mn = fmaxf(m, s);
-            const float al = expf(m - mn), pe = expf(s - mn);
-            l = fmaf(l, al, pe);
-#pragma unroll
-            for (int j = 0; j < kMaxOutLanes; j++) o[j] = fmaf(o[j], al, pe * kv[i][j]);
-            m = mn;
+            for (int j = 0; j < kMaxRecLanes; j++) kv[i][j] = (lane + 64 * j < R) ? gld(rec + lane + 64 * j) : 0.f;
         }
+        float dot[PW];
+#pragma unroll
+        for (int i = 0; i < PW; i++) {
+            float d = 0.f;
+#pragma unroll
+            for (int j = 0; j < kMaxRecLanes; j++) d = fmaf(qv[j], kv[i][j], d);
+            dot[i] = d;
+        }
+#pragma unroll
+        for (int i = 0; i < PW; i++) dot[i] = wave_sum(dot[i]) * sc2;
+        float mb = m;
+#pragma unroll
+        for (int i = 0; i < PW; i++)
+            if (wave + kSplitWaves * i < ncv) mb = fmaxf(mb, dot[i]);
+        if (mb == -INFINITY) continue;                     // no position of this wave in the block
+        const float al = __builtin_amdgcn_exp2f(m - mb);   // 0 while m is -inf
+        l *= al;
+#pragma unroll
+        for (int j = 0; j < kMaxOutLanes; j++) o[j] *= al;
+#pragma unroll
+        for (int i = 0; i < PW; i++) {
+            const float pe = wave + kSplitWaves * i < ncv ? __builtin_amdgcn_exp2f(dot[i] - mb) : 0.f;
+            l += pe;
+#pragma unroll
+            for (int j = 0; j < kMaxOutLanes; j++) o[j] = fmaf(pe, kv[i][j], o[j]);
+        }
+        m = mb;
     }
 #pragma unroll
     for (int j = 0; j < kMaxOutLanes; j++)
@@ -266,21 +319,31 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
     __syncthreads();
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w]);
-    float aw[4];
+    for (int w = 0; w < kSplitWaves; w++) M = fmaxf(M, s_m[w]);
+    float aw[kSplitWaves];
 #pragma unroll
-    for (int w = 0; w < 4; w++) aw[w] = s_m[w] == -INFINITY ? 0.f : expf(s_m[w] - M);
+    for (int w = 0; w < kSplitWaves; w++) aw[w] = s_m[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w] - M);
     float* wo = a.ws_o + ((int64_t)c * a.H + h) * a.dc;
-    for (int k = tid; k < a.dc; k += 256)
-        gst(wo + k, ((s_o[0][k] * aw[0] + s_o[1][k] * aw[1]) + (s_o[2][k] * aw[2] + s_o[3][k] * aw[3])));
+    for (int k = tid; k < a.dc; k += 64 * kSplitWaves) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kSplitWaves; w++) t = fmaf(s_o[w][k], aw[w], t);
+        gst(wo + k, t);
+    }
     if (tid == 0) {
+        float lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < kSplitWaves; w++) lt = fmaf(s_l[w], aw[w], lt);
         gst(a.ws_m + (int64_t)c * a.H + h, M);
-        gst(a.ws_l + (int64_t)c * a.H + h, (s_l[0] * aw[0] + s_l[1] * aw[1]) + (s_l[2] * aw[2] + s_l[3] * aw[3]));
+        gst(a.ws_l + (int64_t)c * a.H + h, lt);
     }
 }
 
 // grid (H, v/16): merge the chunks of head h into o_lat (every workgroup of
-// the head repeats this small merge), then 16 rows of out_h = W_vb_h o_lat
+// the head repeats this small merge), then 16 rows of out_h = W_vb_h o_lat,
+// 4 per wave.  Every load the workgroup needs (its W_vb units, the chunk
+// maxima / sums and both latent values of each chunk for this thread) is
+// issued at entry: one memory round trip, then LDS work.
 __global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
     __shared__ float s_w[256];
     __shared__ __align__(16) float s_lat[512];
@@ -288,38 +351,67 @@ __global__ __launch_bounds__(256) void mla_out_kernel(MlaArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;
-    const int nch = pos0 / kMlaChunk + 1;
+    const int nch = pos0 / chunk_of(a, pos0 + 1) + 1;      // <= kMlaMaxChunks
     const int h = blockIdx.x;
+    // this wave's 4 rows (v % 4 == 0; rows past v: a clamped row, not stored)
+    const int i0 = 16 * blockIdx.y + 4 * wave;
+    const bool rows_ok = i0 < a.v;
+    const int64_t row0 = (int64_t)a.H * a.nope + (int64_t)h * a.v + (rows_ok ? i0 : 0);
+    const int units = a.dc / 16, ul = lane < units ? lane : 0;   // dc <= 1024: one unit per lane
+    float wv[4][16];
+#pragma unroll
+    for (int r = 0; r < 4; r++) load_unit16(a.wkvb, a.qt, (row0 + r) * a.dc + 16 * ul, wv[r]);
     const float mc = tid < nch ? gld(a.ws_m + (int64_t)tid * a.H + h) : -INFINITY;
     const float lc = tid < nch ? gld(a.ws_l + (int64_t)tid * a.H + h) : 0.f;
+    const int k0 = tid < a.dc ? tid : 0, k1 = tid + 256 < a.dc ? tid + 256 : 0;
+    float v0[kMlaMaxChunks], v1[kMlaMaxChunks];
+#pragma unroll
+    for (int cc = 0; cc < kMlaMaxChunks; cc++) {
+        const float* po = a.ws_o + ((int64_t)(cc < nch ? cc : nch - 1) * a.H + h) * a.dc;
+        v0[cc] = gld(po + k0);
+        v1[cc] = gld(po + k1);
+    }
     const float mw = wave_max(mc);
     if (lane == 0) s_red[wave] = mw;
     __syncthreads();
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    const float w = tid < nch ? expf(mc - M) : 0.f;
+    const float w = tid < nch ? __builtin_amdgcn_exp2f(mc - M) : 0.f;   // partial maxima in base-2 units
     s_w[tid] = w;
     const float lw = wave_sum(w * lc);
     __syncthreads();
     if (lane == 0) s_red[4 + wave] = lw;
     __syncthreads();
     const float inv_l = 1.0f / ((s_red[4] + s_red[5]) + (s_red[6] + s_red[7]));
-    for (int k = tid; k < a.dc; k += 256) {
-        float acc = 0.f;
-#pragma unroll 8
-        for (int cc = 0; cc < nch; cc++) acc = fmaf(gld(a.ws_o + ((int64_t)cc * a.H + h) * a.dc + k), s_w[cc], acc);
-        s_lat[k] = acc * inv_l;
+    // o_lat = sum_c w_c O_c / sum_c w_c l_c (weight 0 past nch)
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < kMlaMaxChunks; cc++) {
+        acc0 = fmaf(v0[cc], s_w[cc], acc0);
+        acc1 = fmaf(v1[cc], s_w[cc], acc1);
     }
+    if (tid < a.dc) s_lat[tid] = acc0 * inv_l;
+    if (tid + 256 < a.dc) s_lat[tid + 256] = acc1 * inv_l;
     __syncthreads();
-    // out rows: 4 per wave at a time (v % 4 == 0)
-    const int64_t row0 = (int64_t)a.H * a.nope + (int64_t)h * a.v;
-    for (int i = 16 * blockIdx.y + 4 * wave; i < min(a.v, 16 * (int)blockIdx.y + 16); i += 16) {
-        const uint8_t* const w4[4] = {a.wkvb, a.wkvb, a.wkvb, a.wkvb};
-        const int64_t r4[4] = {row0 + i, row0 + i + 1, row0 + i + 2, row0 + i + 3};
-        const float* const x4[4] = {s_lat, s_lat, s_lat, s_lat};
-        float o4[4];
-        rows_dot<4>(w4, a.qt, r4, a.dc, x4, lane, o4);
-        if (lane < 4) gst(a.out + (int64_t)h * a.v + i + lane, lane == 0 ? o4[0] : lane == 1 ? o4[1] : lane == 2 ? o4[2] : o4[3]);
+    float o4[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float acc = 0.f;
+        if (lane < units) {
+            // 16-byte LDS reads of the lane's 16-value slice
+            const f32x4* xr = (const f32x4*)(s_lat + 16 * lane);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 xv = xr[q];
+                acc = fmaf(wv[r][4 * q], xv.x, acc);
+                acc = fmaf(wv[r][4 * q + 1], xv.y, acc);
+                acc = fmaf(wv[r][4 * q + 2], xv.z, acc);
+                acc = fmaf(wv[r][4 * q + 3], xv.w, acc);
+            }
+        }
+        o4[r] = wave_sum(acc);
     }
+    if (rows_ok && lane < 4)
+        gst(a.out + (int64_t)h * a.v + i0 + lane, lane == 0 ? o4[0] : lane == 1 ? o4[1] : lane == 2 ? o4[2] : o4[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -347,6 +439,7 @@ constexpr int kFusedPw = 4;                   // positions per wave per block
 constexpr int kFusedBlock = 16 * kFusedPw;
 constexpr int kFusedY = 4;                    // workgroups per head
 constexpr int kFusedMaxPos = 256;
+constexpr int kChunkTarget = 16;              // chunks of the two-launch path (mla_chunk_kernel)
 
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -661,6 +754,243 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Longer contexts at the DeepSeek-V2 shape: two launches.
+// mla_chunk_kernel, grid (chunks padded to the 8 XCDs, H), 1024 threads:
+// every workgroup forms q_lat_h and the current record as mla_fused_kernel
+// does, scores only its chunk of positions (blocks of 64, 4 per wave),
+// merges its 16 waves into the unnormalized latent partial
+// sum_p 2^(s_p - M_c) c_p and applies all of W_vb_h to it (the merge over
+// chunks is linear in that partial).  It writes (M_c, l_c, W_vb_h partial)
+// per chunk; mla_combine_kernel merges the chunks of each head.  The
+// workgroup whose chunk holds pos0 of head 0 stores the record.
+// The grid has nslot = min(kChunkTarget, max_pos / 64) chunk slots per head;
+// the chunk length is derived from the position count at run time (whole
+// 64-position blocks, as few per chunk as fill the slots), so a replayed
+// graph uses all its slots at every position.  Every chunk workgroup repeats
+// q_lat and W_vb_h, and the heads of a chunk each stream its records, so 16
+// chunks per head measured best (fewer leave CUs idle, more repeat the fixed
+// work).
+// ---------------------------------------------------------------------------
+template <int QT>
+__global__ __launch_bounds__(1024) void mla_chunk_kernel(MlaArgs a) {
+    __shared__ __align__(16) float s_part[kFusedRs * kFusedDc];   // W_kb partials, then wave partials
+    __shared__ __align__(16) float s_q[kFusedR];                  // q_lat | rotated q_rope
+    __shared__ __align__(16) float s_rec[kFusedR];                // the new record
+    __shared__ __align__(16) float s_lat[kFusedDc];
+    __shared__ float s_qn[128];
+    __shared__ float s_m[16], s_l[16], s_red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos0 = read_pos(a.start_pos, a.d_pos);
+    if (pos0 < 0 || pos0 >= a.max_seq) return;
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int L = pos0 + 1, chunk = chunk_of(a, L), jc = c * chunk;
+    if (jc >= L) return;                                          // padding / chunks past pos0
+    const int jend = min(jc + chunk, L);
+    const bool has_cur = pos0 < jend;                             // this chunk holds pos0
+    const int R = kFusedR, hr = kFusedRope / 2;
+    const int cu = tid & (kFusedNcu - 1), rs = tid / kFusedNcu;
+    // small loads first (as mla_fused_kernel), then the weights, then the
+    // chunk's first block of records
+    const int ti = tid < hr ? tid : 0;
+    const float* qr = a.q + (int64_t)a.H * a.nope + (int64_t)h * kFusedRope;
+    const float qn = gld(a.q + (int64_t)h * a.nope + (tid < a.nope ? tid : 0));
+    float x0 = gld(qr + ti), x1 = gld(qr + ti + hr);
+    float k0 = gld(a.kva + kFusedDc + ti), k1 = gld(a.kva + kFusedDc + ti + hr);
+    float rc = 1.f, rsn = 0.f;
+    if (a.rc) { rc = gld(a.rc + (int64_t)pos0 * hr + ti); rsn = gld(a.rs + (int64_t)pos0 * hr + ti); }
+    const float cx = gld(a.kva + (tid & (kFusedDc - 1))), cn = gld(a.k_norm + (tid & (kFusedDc - 1)));
+    const float cx2 = gld(a.kva + (tid & 255) + 256);
+    __builtin_amdgcn_sched_barrier(0);
+    RawUnit wk[4], wv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int i = rs + kFusedRs * r;
+        raw_issue<QT>(wk[r], a.wkvb, ((int64_t)h * a.nope + (i < a.nope ? i : 0)) * kFusedDc + 16 * cu);
+    }
+    // W_vb_h rows rs + 32 r (rows past v re-read row 0, never stored)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int vr = rs + kFusedRs * r;
+        raw_issue<QT>(wv[r], a.wkvb, ((int64_t)a.H * a.nope + (int64_t)h * a.v + (vr < a.v ? vr : 0)) * kFusedDc +
+                                     16 * cu);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float kv[kFusedPw][kFusedRec];
+    fused_load_block(kv, a.cache, jc, wave, pos0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < a.nope) s_qn[tid] = qn;
+    if (tid < hr) {
+        if (a.rc) {
+            rope_pair(x0, x1, rc, rsn, x0, x1);
+            rope_pair(k0, k1, rc, rsn, k0, k1);
+        }
+        s_q[kFusedDc + tid] = x0;
+        s_q[kFusedDc + tid + hr] = x1;
+        s_rec[kFusedDc + tid] = k0;
+        s_rec[kFusedDc + tid + hr] = k1;
+        if (h == 0 && has_cur) {
+            float* rec = a.cache + (int64_t)pos0 * R;
+            gst(rec + kFusedDc + tid, k0);
+            gst(rec + kFusedDc + tid + hr, k1);
+        }
+    }
+    if (tid < 256) {
+        const float ss = wave_sum(fmaf(cx2, cx2, fmaf(cx, cx, 0.f)));
+        if (lane == 0) s_red[wave] = ss;
+    }
+    __syncthreads();
+    {
+        float acc[16], bias = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[j] = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int i = rs + kFusedRs * r;
+            raw_fold<QT>(wk[r], i < a.nope ? s_qn[i] : 0.f, acc, bias);
+        }
+        f32x4* dst = (f32x4*)(s_part + rs * kFusedDc + 16 * cu);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            dst[q] = f32x4{acc[4 * q] - bias, acc[4 * q + 1] - bias, acc[4 * q + 2] - bias, acc[4 * q + 3] - bias};
+    }
+    if (tid < kFusedDc) {
+        const float inv = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)kFusedDc + a.eps);
+        const float v = cx * inv * cn;
+        s_rec[tid] = v;
+        if (h == 0 && has_cur) gst(a.cache + (int64_t)pos0 * R + tid, v);
+    }
+    __syncthreads();
+    if (tid < kFusedDc) {
+        float t = 0.f;
+#pragma unroll 8
+        for (int r = 0; r < kFusedRs; r++) t += s_part[r * kFusedDc + tid];
+        s_q[tid] = t;
+    }
+    __syncthreads();
+    float qv[kFusedRec];
+#pragma unroll
+    for (int j = 0; j < kFusedRec; j++) qv[j] = s_q[lane + 64 * j];
+    const float sc2 = a.scale * 1.44269504088896341f;
+    float m = -INFINITY, l = 0.f, o[kFusedDc / 64];
+#pragma unroll
+    for (int j = 0; j < kFusedDc / 64; j++) o[j] = 0.f;
+    for (int blk = jc; blk < jend; blk += kFusedBlock) {
+        // the next block's records go out before this block is scored
+        const bool more = blk + kFusedBlock < jend;           // uniform
+        float kn[kFusedPw][kFusedRec];
+        if (more) fused_load_block(kn, a.cache, blk + kFusedBlock, wave, pos0, lane);
+        float sv[kFusedPw];
+        float mb = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kFusedPw; i++) {
+            const int p = blk + wave + 16 * i;
+            sv[i] = -INFINITY;
+            if (p < jend) {
+                if (p == pos0) {
+#pragma unroll
+                    for (int j = 0; j < kFusedRec; j++) kv[i][j] = s_rec[lane + 64 * j];
+                }
+                float dot = 0.f;
+#pragma unroll
+                for (int j = 0; j < kFusedRec; j++) dot = fmaf(qv[j], kv[i][j], dot);
+                sv[i] = wave_sum(dot) * sc2;
+                mb = fmaxf(mb, sv[i]);
+            }
+        }
+        if (mb != -INFINITY) {
+            const float mn = fmaxf(m, mb), al = __builtin_amdgcn_exp2f(m - mn);
+            l *= al;
+#pragma unroll
+            for (int j = 0; j < kFusedDc / 64; j++) o[j] *= al;
+            m = mn;
+#pragma unroll
+            for (int i = 0; i < kFusedPw; i++) {
+                if (sv[i] == -INFINITY) continue;
+                const float pe = __builtin_amdgcn_exp2f(sv[i] - mn);
+                l += pe;
+#pragma unroll
+                for (int j = 0; j < kFusedDc / 64; j++) o[j] = fmaf(pe, kv[i][j], o[j]);
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < kFusedPw; i++)
+#pragma unroll
+                for (int j = 0; j < kFusedRec; j++) kv[i][j] = kn[i][j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kFusedDc / 64; j++) s_part[wave * kFusedDc + lane + 64 * j] = o[j];
+    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+    __syncthreads();
+    // merge of the 16 waves: the chunk's maximum, its sum and the
+    // unnormalized latent partial
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 16; w++) M = fmaxf(M, s_m[w]);
+    if (tid < kFusedDc) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; w++) {
+            const float mw = s_m[w];
+            t = fmaf(mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M), s_part[w * kFusedDc + tid], t);
+        }
+        s_lat[tid] = t;
+    }
+    if (tid == 0) {
+        float den = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; w++) den = fmaf(s_m[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w] - M), s_l[w], den);
+        gst(a.ws_m + (int64_t)c * a.H + h, M);
+        gst(a.ws_l + (int64_t)c * a.H + h, den);
+    }
+    __syncthreads();
+    // W_vb_h rows rs + 32 r: the 32 units of a row are lanes 0..31 or 32..63
+    float* wo = a.ws_o + ((int64_t)c * a.H + h) * a.v;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int vr = rs + kFusedRs * r;
+        float pv = raw_dot<QT>(wv[r], s_lat + 16 * cu);
+        pv = sum16(pv);
+        pv += dpp_rows<0x142, 0xA>(pv);   // row_bcast:15: lane 31 = lanes 0..31, lane 63 = lanes 32..63
+        if (vr < a.v && (lane & 31) == 31) gst(wo + vr, pv);
+    }
+}
+
+// grid H, v threads (v <= 128): out_h = sum_c 2^(M_c - M) W_vb_h partial_c /
+// sum_c 2^(M_c - M) l_c over the chunks holding positions 0..pos0 (<= 64),
+// every chunk's value of this thread loaded at once
+__global__ __launch_bounds__(128) void mla_combine_kernel(MlaArgs a) {
+    __shared__ float s_w[kMlaMaxChunks];
+    __shared__ float s_red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos0 = read_pos(a.start_pos, a.d_pos);
+    if (pos0 < 0 || pos0 >= a.max_seq) return;
+    const int nch = pos0 / chunk_of(a, pos0 + 1) + 1, h = blockIdx.x;
+    const int t = tid < a.v ? tid : 0;
+    float ov[kMlaMaxChunks];
+#pragma unroll
+    for (int cc = 0; cc < kMlaMaxChunks; cc++) ov[cc] = gld(a.ws_o + ((int64_t)(cc < nch ? cc : nch - 1) * a.H + h) * a.v + t);
+    const float mc = tid < nch ? gld(a.ws_m + (int64_t)tid * a.H + h) : -INFINITY;
+    const float lc = tid < nch ? gld(a.ws_l + (int64_t)tid * a.H + h) : 0.f;
+    const float mw = wave_max(mc);
+    if (lane == 0) s_red[wave] = mw;
+    __syncthreads();
+    const float M = fmaxf(s_red[0], s_red[1]);
+    const float w = tid < nch ? __builtin_amdgcn_exp2f(mc - M) : 0.f;
+    if (tid < kMlaMaxChunks) s_w[tid] = w;
+    const float lw = wave_sum(w * lc);
+    __syncthreads();
+    if (lane == 0) s_red[2 + wave] = lw;
+    __syncthreads();
+    const float den = s_red[2] + s_red[3];
+    float acc = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < kMlaMaxChunks; cc++) acc = fmaf(ov[cc], s_w[cc], acc);
+    if (tid < a.v) gst(a.out + (int64_t)h * a.v + tid, acc / den);
+}
+
+// ---------------------------------------------------------------------------
 // MoE
 // ---------------------------------------------------------------------------
 
@@ -794,7 +1124,22 @@ bool unit_qt(int qt) {
     return qt == RINA_QT_GGML_Q2_K || qt == RINA_QT_Q4_0 || qt == RINA_QT_Q4_0F || qt == RINA_QT_FP32;
 }
 
-int mla_nchunk(int max_pos) { return (max_pos + kMlaChunk - 1) / kMlaChunk; }
+// positions per split workgroup: a multiple of kMlaChunk that keeps the
+// chunk count at most kMlaMaxChunks (the out kernel merges them at once)
+int mla_chunk_len(int max_pos) {
+    const int blocks = (max_pos + kMlaChunk - 1) / kMlaChunk;
+    return kMlaChunk * ((blocks + kMlaMaxChunks - 1) / kMlaMaxChunks);
+}
+int mla_nchunk(int max_pos) {
+    const int cl = mla_chunk_len(max_pos);
+    return (max_pos + cl - 1) / cl;
+}
+// chunk partials the workspace holds: the most the split kernel
+// (mla_nchunk) or the chunk kernel (at most kChunkTarget chunks of whole
+// 64-position blocks) uses for up to max_pos positions
+int mla_ws_chunks(int max_pos) {
+    return std::min(kMlaMaxChunks, (max_pos + kMlaChunk - 1) / kMlaChunk);
+}
 
 // shapes mla_fused_kernel is built for (the DeepSeek-V2 latent width)
 bool mla_fused_ok(int qt, int nope, int rope, int v, int dc) {
@@ -806,7 +1151,9 @@ bool mla_fused_ok(int qt, int nope, int rope, int v, int dc) {
 
 extern "C" size_t rina_hip_mla_attention_workspace(int H, int dc, int rope, int max_pos) {
     if (H < 1 || dc < 1 || max_pos < 1) return 0;
-    const size_t nch = (size_t)mla_nchunk(max_pos);
+    // the most chunks any call with up to max_pos positions uses (a shorter
+    // cache can take more, shorter chunks)
+    const size_t nch = (size_t)mla_ws_chunks(max_pos);
     return ((size_t)H * (dc + rope) + nch * H * (2 + (size_t)dc)) * sizeof(float);
 }
 
@@ -823,8 +1170,8 @@ extern "C" int rina_hip_mla_decode_attention_ex(const float* q, const float* kva
         return RINA_ERR_ARG;
     if (!unit_qt(qt_kv_b)) return RINA_ERR_QTYPE;
     if ((!rope_cos) != (!rope_sin)) return RINA_ERR_ARG;
-    if (dc % 64 || dc > 512 || rope % 2 || rope < 0 || dc + rope > 64 * kMaxRecLanes || nope > 512 || v_dim % 4 ||
-        mla_nchunk(max_seq) > 256 || (256 % (dc / 64)))
+    if (dc % 64 || dc > 512 || rope % 2 || rope < 0 || dc + rope > 64 * kMaxRecLanes || v_dim % 4 ||
+        (256 % (dc / 64)) || nope > kPrepRows * (256 / (dc / 64)) || max_seq > 32768)
         return RINA_ERR_SHAPE;
     if (!d_pos && (start_pos < 0 || start_pos >= max_seq)) return RINA_ERR_RANGE;
     if (((uintptr_t)w_kv_b | (uintptr_t)q | (uintptr_t)cache) % 16 || (uintptr_t)w_kv_b % 4) return RINA_ERR_SHAPE;
@@ -835,9 +1182,9 @@ extern "C" int rina_hip_mla_decode_attention_ex(const float* q, const float* kva
     a.q = q; a.kva = kva; a.k_norm = k_norm; a.eps = eps; a.rc = rope_cos; a.rs = rope_sin;
     a.wkvb = (const uint8_t*)w_kv_b; a.qt = qt_kv_b; a.cache = cache; a.out = out;
     a.H = H; a.nope = nope; a.rope = rope; a.v = v_dim; a.dc = dc;
-    a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos; a.chunk = kMlaChunk;
+    a.start_pos = start_pos; a.max_seq = max_seq; a.d_pos = d_pos; a.chunk = mla_chunk_len(max_pos);
     a.scale = 1.0f / sqrtf((float)(nope + rope));
-    const int nch = mla_nchunk(max_pos);
+    const int nch = mla_ws_chunks(max_pos);
     a.ws_q = (float*)workspace;
     a.ws_m = a.ws_q + (size_t)H * (dc + rope);
     a.ws_l = a.ws_m + (size_t)nch * H;
@@ -854,12 +1201,30 @@ extern "C" int rina_hip_mla_decode_attention_ex(const float* q, const float* kva
         RINA_LAUNCH_CHECK();
         return RINA_OK;
     }
+    if (mla_fused_ok(qt_kv_b, nope, rope, v_dim, dc)) {
+        // about kChunkTarget chunks of whole 64-position blocks (fewer
+        // while the positions are few): every chunk workgroup repeats
+        // q_lat and W_vb, so fewer, longer chunks win once a workgroup per
+        // CU is reached
+        a.chunk = kFusedBlock;
+        a.nslot = std::min(kChunkTarget, (max_pos + kFusedBlock - 1) / kFusedBlock);
+        const int ncc = a.nslot;
+        const dim3 grid((ncc + 7) / 8 * 8, H);
+        if (qt_kv_b == RINA_QT_GGML_Q2_K) hipLaunchKernelGGL(mla_chunk_kernel<RINA_QT_GGML_Q2_K>, grid, dim3(1024), 0, st, a);
+        else if (qt_kv_b == RINA_QT_Q4_0F) hipLaunchKernelGGL(mla_chunk_kernel<RINA_QT_Q4_0F>, grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL(mla_chunk_kernel<RINA_QT_Q4_0>, grid, dim3(1024), 0, st, a);
+        RINA_LAUNCH_CHECK();
+        hipLaunchKernelGGL(mla_combine_kernel, dim3(H), dim3(128), 0, st, a);
+        RINA_LAUNCH_CHECK();
+        return RINA_OK;
+    }
     hipLaunchKernelGGL(mla_prep_kernel, dim3(H + 1, 4), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
     // chunks padded to the 8 XCDs: every head of a chunk reads the same
     // latent records, fetched into one L2 (padding workgroups start past
     // max_seq and return)
-    hipLaunchKernelGGL(mla_split_kernel, dim3((nch + 7) / 8 * 8, H), dim3(256), 0, st, a);
+    const int nsp = mla_nchunk(max_pos);
+    hipLaunchKernelGGL(mla_split_kernel, dim3((nsp + 7) / 8 * 8, H), dim3(64 * kSplitWaves), 0, st, a);
     RINA_LAUNCH_CHECK();
     hipLaunchKernelGGL(mla_out_kernel, dim3(H, (v_dim + 15) / 16), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();

@@ -38,11 +38,16 @@ def weight(orc, qt, rows, cols, r):
 @pytest.mark.parametrize("qt", [Q2K, Q4F, Q40])
 # (position, device position, pos_hint, minimum max_seq).  At the
 # DeepSeek-V2-Lite shape: one-launch path below 256 positions (one and
-# several 64-position blocks, a device position past its hint), three-launch
-# path at 300 positions and for a device position with no usable bound.
+# several 64-position blocks, a device position past its hint); above it the
+# chunk + combine launches, whose chunks follow the position count: 257
+# (5 slots, the last chunk 2 positions), 300, 700 (11 one-block chunks),
+# 1100 with a 4100-position cache (16 slots, 9 chunks of two blocks) and a
+# device position with no usable bound.  The tiny shape takes the
+# three-launch path above 256.
 @pytest.mark.parametrize("P,use_dpos,hint,min_seq", [(0, False, -1, 0), (5, False, -1, 0), (40, True, -1, 0),
                                                      (40, True, -1, 400), (40, True, 63, 400), (100, False, -1, 0),
-                                                     (200, True, 10, 0), (300, False, -1, 0)])
+                                                     (200, True, 10, 0), (257, True, -1, 0), (300, False, -1, 0),
+                                                     (700, False, -1, 0), (1100, True, -1, 4100)])
 def test_mla_decode_attention(rina, orc, shape, qt, P, use_dpos, hint, min_seq):
     hip = rina.load_hip()
     L = orc.load()
