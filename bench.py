@@ -216,6 +216,71 @@ def committed_traffic():
         return None, None
 
 
+def config4_kernel_roofs(torch, hip, rina, synth, st, pos, iters):
+    """Live device times of config 4's two largest per-layer stages at its
+    decode context, over rings larger than the 256 MB MALL (as between the
+    layers of a decode step): the latent attention at position `pos`
+    (RMSNorm + RoPE append, q_lat, softmax over pos+1 latent records, W_vb)
+    and the MoE block (router, top-6 of 64, shared + routed gate/up, down)."""
+    H, nope, rope, vd, dc, d = 16, 128, 64, 128, 512, 2048
+    E, K, F, S = 64, 6, 1408, 2816
+    R = dc + rope
+    q2b = lambda n: n // 256 * 84
+    out = {}
+    ms = pos + 8
+    nr = 64                                   # 64 x (4.7 MB cache + 0.7 MB W_kv_b) > MALL
+    caches = [torch.randn(ms * R, device="cuda") for _ in range(nr)]
+    wkvb = [synth.q2k_device(H * (nope + vd) * dc, 100 + i) for i in range(nr)]
+    q = torch.randn(H * (nope + rope), device="cuda")
+    kva = torch.randn(R, device="cuda")
+    kn = torch.ones(dc, device="cuda")
+    cos, sin = synth.make_rope(rope, ms, 10000.0)
+    cd, sd = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    o = torch.empty(H * vd, device="cuda")
+    pd = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    wsb = int(hip.rina_hip_mla_attention_workspace(H, dc, rope, ms))
+    ws = torch.empty(wsb // 4 + 4, device="cuda")
+    t = time_kernel(torch, lambda i=0: hip.rina_hip_mla_decode_attention_ex(
+        q.data_ptr(), kva.data_ptr(), kn.data_ptr(), 1e-5, cd.data_ptr(), sd.data_ptr(), wkvb[i % nr].data_ptr(),
+        rina.QT_Q2_K, caches[i % nr].data_ptr(), H, nope, rope, vd, dc, 0, pd.data_ptr(), ms, ms - 1,
+        o.data_ptr(), ws.data_ptr(), wsb, st), iters)
+    nb = (pos + 1) * R * 4 + q2b(H * (nope + vd) * dc) + (H * (nope + rope) + R + H * vd) * 4
+    out["decode_mla_latent_p%d" % pos] = dict(
+        with_ceiling(roofline(nb, t), t, plain_read_time(torch, hip, st, nb, iters)), bytes_per_launch=nb,
+        avg_us=round(t * 1e6, 3), note="config 4 latent attention, device position (graph replay): "
+                                       "mla_chunk_kernel + mla_combine_kernel")
+    log("config-4 latent attention at %d: %.2f us" % (pos, t * 1e6))
+    del caches, wkvb
+    # MoE block: 4 layers' weights (4 x 187 MB), h updated in place by every
+    # call, so the selected experts change from call to call
+    nl = 4
+    lay = [dict(wr=torch.randn(E * d, device="cuda") * 0.02, sg=synth.q2k_device(S * d, 10 * l + 1),
+                su=synth.q2k_device(S * d, 10 * l + 2), sd=synth.q2k_device(d * S, 10 * l + 3),
+                wg=synth.q2k_device(E * F * d, 10 * l + 4), wu=synth.q2k_device(E * F * d, 10 * l + 5),
+                wd=synth.q2k_device(E * d * F, 10 * l + 6)) for l in range(nl)]
+    h = torch.randn(d, device="cuda")
+    ln2 = torch.ones(d, device="cuda")
+    wsb = int(hip.rina_hip_moe_block_workspace(d, E, K, F, S))
+    ws = torch.empty(wsb // 4 + 4, device="cuda")
+    sgu, sdn = q2b(F * d), q2b(d * F)
+    def moe(i=0):
+        w = lay[i % nl]
+        return hip.rina_hip_moe_block(h.data_ptr(), ln2.data_ptr(), 1e-5, w["wr"].data_ptr(), rina.QT_FP32,
+                                      w["sg"].data_ptr(), w["su"].data_ptr(), w["sd"].data_ptr(), S,
+                                      w["wg"].data_ptr(), w["wu"].data_ptr(), w["wd"].data_ptr(), rina.QT_Q2_K,
+                                      sgu, sdn, E, K, d, F, ws.data_ptr(), wsb, st)
+    t = time_kernel(torch, moe, iters)
+    nb = E * d * 4 + 3 * q2b(S * d) + 3 * K * q2b(F * d) + 2 * d * 4
+    out["decode_moe_block_q2k"] = dict(
+        with_ceiling(roofline(nb, t), t, plain_read_time(torch, hip, st, nb, iters)), bytes_per_launch=nb,
+        avg_us=round(t * 1e6, 3), note="config 4 MoE block (64 experts, top-6 of 1408, 2 shared): "
+                                       "moe_router_kernel + moe_gate_up_q2_kernel + moe_down_q2_kernel")
+    log("config-4 MoE block: %.2f us" % (t * 1e6))
+    del lay
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -447,6 +512,7 @@ def main():
         ds.close()
         del ds
         torch.cuda.empty_cache()
+        attn_roofs.update(config4_kernel_roofs(torch, hip, rina, synth, st, p4, args.kernel_iters))
 
     # ---- config 5: RINA Gen6 Jamba hybrid, 64-token prompt then 128 greedy steps
     cfg5 = None
