@@ -352,7 +352,7 @@ def attention_case(rina, orc, mode, P, T, H=32, Hkv=8, dh=64, pre_rope=0, use_dp
 
 
 @pytest.mark.parametrize("mode", [0, 1, 2, 3, 4, 5])
-@pytest.mark.parametrize("P", [0, 1, 31, 32, 33, 100, 543])
+@pytest.mark.parametrize("P", [0, 1, 31, 32, 33, 100, 543, 1000])
 def test_attention_decode(rina, orc, mode, P):
     got, ref = attention_case(rina, orc, mode, P, 1)
     assert_close(got, ref, what="decode mode %d pos %d" % (mode, P))
