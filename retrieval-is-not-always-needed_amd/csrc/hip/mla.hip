@@ -12,8 +12,8 @@
 //   o_h = W_vb_h (sum_j p_j c_j).
 // Short contexts: one launch (mla_fused_kernel).  Longer ones at the
 // DeepSeek-V2 shape: two launches, mla_chunk_kernel (per chunk of positions
-// and head: q_lat, the chunk's softmax partial and W_vb applied to it) and
-// mla_combine_kernel (chunk merge per head).  Other shapes: three launches,
+// and head: q_lat and the chunk's softmax partial in latent space) and
+// mla_combine_kernel (chunk merge and W_vb per head).  Other shapes: three launches,
 // prep (q_lat, rotated q_rope, latent append at pos0), split (chunk
 // partials over positions, one workgroup per chunk and head), out (chunk
 // merge and W_vb per head).
@@ -757,26 +757,25 @@ __global__ __launch_bounds__(1024) void mla_fused_kernel(MlaArgs a) {
 // Longer contexts at the DeepSeek-V2 shape: two launches.
 // mla_chunk_kernel, grid (chunks padded to the 8 XCDs, H), 1024 threads:
 // every workgroup forms q_lat_h and the current record as mla_fused_kernel
-// does, scores only its chunk of positions (blocks of 64, 4 per wave),
+// does, scores only its chunk of positions (blocks of 64, 4 per wave) and
 // merges its 16 waves into the unnormalized latent partial
-// sum_p 2^(s_p - M_c) c_p and applies all of W_vb_h to it (the merge over
-// chunks is linear in that partial).  It writes (M_c, l_c, W_vb_h partial)
-// per chunk; mla_combine_kernel merges the chunks of each head.  The
-// workgroup whose chunk holds pos0 of head 0 stores the record.
+// sum_p 2^(s_p - M_c) c_p.  It writes (M_c, l_c, partial) per chunk;
+// mla_combine_kernel merges the chunks of each head and applies W_vb_h once
+// (applying it per chunk cost every chunk workgroup 1.6 us and the
+// registers that made the kernel spill).  The workgroup whose chunk holds
+// pos0 of head 0 stores the record.
 // The grid has nslot = min(kChunkTarget, max_pos / 64) chunk slots per head;
 // the chunk length is derived from the position count at run time (whole
 // 64-position blocks, as few per chunk as fill the slots), so a replayed
 // graph uses all its slots at every position.  Every chunk workgroup repeats
-// q_lat and W_vb_h, and the heads of a chunk each stream its records, so 16
-// chunks per head measured best (fewer leave CUs idle, more repeat the fixed
-// work).
+// q_lat, and the heads of a chunk each stream its records, so 16 chunks per
+// head measured best (fewer leave CUs idle, more repeat the fixed work).
 // ---------------------------------------------------------------------------
 template <int QT>
 __global__ __launch_bounds__(1024) void mla_chunk_kernel(MlaArgs a) {
     __shared__ __align__(16) float s_part[kFusedRs * kFusedDc];   // W_kb partials, then wave partials
     __shared__ __align__(16) float s_q[kFusedR];                  // q_lat | rotated q_rope
     __shared__ __align__(16) float s_rec[kFusedR];                // the new record
-    __shared__ __align__(16) float s_lat[kFusedDc];
     __shared__ float s_qn[128];
     __shared__ float s_m[16], s_l[16], s_red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -801,18 +800,11 @@ __global__ __launch_bounds__(1024) void mla_chunk_kernel(MlaArgs a) {
     const float cx = gld(a.kva + (tid & (kFusedDc - 1))), cn = gld(a.k_norm + (tid & (kFusedDc - 1)));
     const float cx2 = gld(a.kva + (tid & 255) + 256);
     __builtin_amdgcn_sched_barrier(0);
-    RawUnit wk[4], wv[4];
+    RawUnit wk[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int i = rs + kFusedRs * r;
         raw_issue<QT>(wk[r], a.wkvb, ((int64_t)h * a.nope + (i < a.nope ? i : 0)) * kFusedDc + 16 * cu);
-    }
-    // W_vb_h rows rs + 32 r (rows past v re-read row 0, never stored)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int vr = rs + kFusedRs * r;
-        raw_issue<QT>(wv[r], a.wkvb, ((int64_t)a.H * a.nope + (int64_t)h * a.v + (vr < a.v ? vr : 0)) * kFusedDc +
-                                     16 * cu);
     }
     __builtin_amdgcn_sched_barrier(0);
     float kv[kFusedPw][kFusedRec];
@@ -924,7 +916,7 @@ __global__ __launch_bounds__(1024) void mla_chunk_kernel(MlaArgs a) {
     if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
     __syncthreads();
     // merge of the 16 waves: the chunk's maximum, its sum and the
-    // unnormalized latent partial
+    // unnormalized latent partial, written for the combine kernel
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < 16; w++) M = fmaxf(M, s_m[w]);
@@ -935,7 +927,7 @@ __global__ __launch_bounds__(1024) void mla_chunk_kernel(MlaArgs a) {
             const float mw = s_m[w];
             t = fmaf(mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M), s_part[w * kFusedDc + tid], t);
         }
-        s_lat[tid] = t;
+        gst(a.ws_o + ((int64_t)c * a.H + h) * kFusedDc + tid, t);
     }
     if (tid == 0) {
         float den = 0.f;
@@ -944,50 +936,69 @@ __global__ __launch_bounds__(1024) void mla_chunk_kernel(MlaArgs a) {
         gst(a.ws_m + (int64_t)c * a.H + h, M);
         gst(a.ws_l + (int64_t)c * a.H + h, den);
     }
-    __syncthreads();
-    // W_vb_h rows rs + 32 r: the 32 units of a row are lanes 0..31 or 32..63
-    float* wo = a.ws_o + ((int64_t)c * a.H + h) * a.v;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int vr = rs + kFusedRs * r;
-        float pv = raw_dot<QT>(wv[r], s_lat + 16 * cu);
-        pv = sum16(pv);
-        pv += dpp_rows<0x142, 0xA>(pv);   // row_bcast:15: lane 31 = lanes 0..31, lane 63 = lanes 32..63
-        if (vr < a.v && (lane & 31) == 31) gst(wo + vr, pv);
-    }
 }
 
-// grid H, v threads (v <= 128): out_h = sum_c 2^(M_c - M) W_vb_h partial_c /
-// sum_c 2^(M_c - M) l_c over the chunks holding positions 0..pos0 (<= 64),
-// every chunk's value of this thread loaded at once
-__global__ __launch_bounds__(128) void mla_combine_kernel(MlaArgs a) {
-    __shared__ float s_w[kMlaMaxChunks];
-    __shared__ float s_red[4];
+// grid (H, v/16), 256 threads: the chunk merge of head h,
+// o_lat = sum_c 2^(M_c - M) partial_c / sum_c 2^(M_c - M) l_c over the
+// chunks holding positions 0..pos0 (at most kChunkTarget), then 16 rows of
+// out_h = W_vb_h o_lat, 4 per wave.  Thread = (float4 column tid & 127,
+// chunk parity tid >> 7): 8 16-byte partial loads, the chunk maxima / sums
+// and four W_vb units per thread, all issued at entry (one round trip).
+// Every workgroup of the head repeats the small merge.
+template <int QT>
+__global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
+    __shared__ float s_w[kChunkTarget];
+    __shared__ __align__(16) f32x4 s_half[kFusedDc / 4];
+    __shared__ __align__(16) float s_lat[kFusedDc];
+    __shared__ float s_red[8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;
-    const int nch = pos0 / chunk_of(a, pos0 + 1) + 1, h = blockIdx.x;
-    const int t = tid < a.v ? tid : 0;
-    float ov[kMlaMaxChunks];
+    const int nch = pos0 / chunk_of(a, pos0 + 1) + 1;       // <= kChunkTarget
+    const int h = blockIdx.x;
+    // this wave's 4 rows (v % 4 == 0; rows past v: a clamped row, not stored)
+    const int i0 = 16 * blockIdx.y + 4 * wave;
+    const bool rows_ok = i0 < a.v;
+    const int64_t row0 = (int64_t)a.H * a.nope + (int64_t)h * a.v + (rows_ok ? i0 : 0);
+    const int ul = lane & (kFusedNcu - 1);                     // lanes 32..63 repeat lanes 0..31's unit, summed as 0
+    RawUnit wv[4];
 #pragma unroll
-    for (int cc = 0; cc < kMlaMaxChunks; cc++) ov[cc] = gld(a.ws_o + ((int64_t)(cc < nch ? cc : nch - 1) * a.H + h) * a.v + t);
+    for (int r = 0; r < 4; r++) raw_issue<QT>(wv[r], a.wkvb, (row0 + r) * kFusedDc + 16 * ul);
+    const int t4 = tid & 127, cp = tid >> 7;
+    f32x4 pv[kChunkTarget / 2];
+#pragma unroll
+    for (int i = 0; i < kChunkTarget / 2; i++) {
+        const int cc = 2 * i + cp < nch ? 2 * i + cp : nch - 1;
+        pv[i] = gld((const f32x4*)(a.ws_o + ((int64_t)cc * a.H + h) * kFusedDc) + t4);
+    }
     const float mc = tid < nch ? gld(a.ws_m + (int64_t)tid * a.H + h) : -INFINITY;
     const float lc = tid < nch ? gld(a.ws_l + (int64_t)tid * a.H + h) : 0.f;
     const float mw = wave_max(mc);
     if (lane == 0) s_red[wave] = mw;
     __syncthreads();
-    const float M = fmaxf(s_red[0], s_red[1]);
-    const float w = tid < nch ? __builtin_amdgcn_exp2f(mc - M) : 0.f;
-    if (tid < kMlaMaxChunks) s_w[tid] = w;
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float w = tid < nch ? __builtin_amdgcn_exp2f(mc - M) : 0.f;   // partial maxima in base-2 units
+    if (tid < kChunkTarget) s_w[tid] = w;
     const float lw = wave_sum(w * lc);
     __syncthreads();
-    if (lane == 0) s_red[2 + wave] = lw;
-    __syncthreads();
-    const float den = s_red[2] + s_red[3];
-    float acc = 0.f;
+    if (lane == 0) s_red[4 + wave] = lw;
+    // each parity's chunks (weight 0 past nch), then the two parities
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int cc = 0; cc < kMlaMaxChunks; cc++) acc = fmaf(ov[cc], s_w[cc], acc);
-    if (tid < a.v) gst(a.out + (int64_t)h * a.v + tid, acc / den);
+    for (int i = 0; i < kChunkTarget / 2; i++) acc += pv[i] * s_w[2 * i + cp];
+    if (cp) s_half[t4] = acc;
+    __syncthreads();
+    const float inv_l = 1.0f / ((s_red[4] + s_red[5]) + (s_red[6] + s_red[7]));
+    if (!cp) *(f32x4*)(s_lat + 4 * t4) = (acc + s_half[t4]) * inv_l;
+    __syncthreads();
+    float o4[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float pr = raw_dot<QT>(wv[r], s_lat + 16 * ul);
+        o4[r] = wave_sum(lane < kFusedNcu ? pr : 0.f);
+    }
+    if (rows_ok && lane < 4)
+        gst(a.out + (int64_t)h * a.v + i0 + lane, lane == 0 ? o4[0] : lane == 1 ? o4[1] : lane == 2 ? o4[2] : o4[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1214,7 +1225,10 @@ extern "C" int rina_hip_mla_decode_attention_ex(const float* q, const float* kva
         else if (qt_kv_b == RINA_QT_Q4_0F) hipLaunchKernelGGL(mla_chunk_kernel<RINA_QT_Q4_0F>, grid, dim3(1024), 0, st, a);
         else hipLaunchKernelGGL(mla_chunk_kernel<RINA_QT_Q4_0>, grid, dim3(1024), 0, st, a);
         RINA_LAUNCH_CHECK();
-        hipLaunchKernelGGL(mla_combine_kernel, dim3(H), dim3(128), 0, st, a);
+        const dim3 cgrid(H, (v_dim + 15) / 16);
+        if (qt_kv_b == RINA_QT_GGML_Q2_K) hipLaunchKernelGGL(mla_combine_kernel<RINA_QT_GGML_Q2_K>, cgrid, dim3(256), 0, st, a);
+        else if (qt_kv_b == RINA_QT_Q4_0F) hipLaunchKernelGGL(mla_combine_kernel<RINA_QT_Q4_0F>, cgrid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL(mla_combine_kernel<RINA_QT_Q4_0>, cgrid, dim3(256), 0, st, a);
         RINA_LAUNCH_CHECK();
         return RINA_OK;
     }
