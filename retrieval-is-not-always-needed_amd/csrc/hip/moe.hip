@@ -344,25 +344,32 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     const int i = blockIdx.x * 8 + wave;           // grid covers d rows exactly once
     const bool row_on = i < a.d;
     const int ir = row_on ? i : 0;
-    const float inv_f = 1.0f / (float)fcols;
 
     // G and the selected experts / probabilities load together (one round
-    // trip); the weight addresses need the expert ids
+    // trip); the weight addresses need the expert ids.  Lane j < k holds
+    // slot j's expert and probability; a column's slot is read from that
+    // lane (ds_bpermute, every lane active) instead of a select chain.
     GStage gs;
     stage_g_load(a.G, ncol, gs);
-    int sid[16];
-    float spr[16];
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        sid[j] = j < a.k ? __builtin_amdgcn_readfirstlane(gld(a.ids + j)) : -1;
-        spr[j] = j < a.k ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gld(a.probs + j)))) : 0.f;
-    }
+    const int my_id = lane < a.k ? gld(a.ids + lane) : -1;
+    const float my_pr = lane < a.k ? gld(a.probs + lane) : 0.f;
+    // floor(t / fcols) for 0 <= t < 2^16 / 128: t * ceil(2^16 / fcols) >> 16,
+    // then one correction step each way
+    const uint32_t magic = (65536u + (uint32_t)fcols - 1u) / (uint32_t)fcols;
     Q2Col c[kDnRounds];
     float wt[kDnRounds];
     int col[kDnRounds];
 #pragma unroll
     for (int r = 0; r < kDnRounds; r++) {
         const int cc = 64 * r + lane;
+        const int t = cc - scols;                  // routed column index (negative: a shared column)
+        const int tt = t < 0 ? 0 : t;
+        int j = (int)(((uint32_t)tt * magic) >> 16);
+        j -= j * fcols > tt;
+        j += (j + 1) * fcols <= tt;
+        j = j < a.k ? j : a.k - 1;
+        const int e = __shfl(my_id, j);
+        const float pj = __shfl(my_pr, j);
         const uint8_t* w = a.sd;
         uint32_t e0 = 0;
         float f = 0.f;
@@ -370,23 +377,10 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
             if (cc < scols) {
                 e0 = (uint32_t)ir * (uint32_t)a.S + 32u * cc;
                 f = 1.0f;
-            } else {
-                const int t = cc - scols;
-                int j = (int)((float)t * inv_f);       // t < 512: exact after one correction each way
-                j -= j * fcols > t;
-                j += (j + 1) * fcols <= t;
-                int e = -1;
-                float pj = 0.f;
-#pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    e = j == q ? sid[q] : e;
-                    pj = j == q ? spr[q] : pj;
-                }
-                if (e >= 0 && e < a.E) {
-                    w = a.wd + (int64_t)e * a.stride_dn;
-                    e0 = (uint32_t)ir * (uint32_t)a.F + 32u * (uint32_t)(t - j * fcols);
-                    f = pj;
-                }
+            } else if (e >= 0 && e < a.E) {
+                w = a.wd + (int64_t)e * a.stride_dn;
+                e0 = (uint32_t)ir * (uint32_t)a.F + 32u * (uint32_t)(t - j * fcols);
+                f = pj;
             }
         }
         wt[r] = f;
