@@ -293,6 +293,9 @@ def main():
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--no-config4", action="store_true", help="skip the DeepSeek MLA + MoE (config 4) decode line")
     ap.add_argument("--config4-steps", type=int, default=32)
+    ap.add_argument("--config4-prompt", type=int, default=2040,
+                    help="config 4 prompt length (decode context); shorter for counter runs, where every dispatch "
+                         "of the per-token prompt path is serialized")
     ap.add_argument("--no-config5", action="store_true", help="skip the RINA Jamba (config 5) decode line")
     ap.add_argument("--no-config3", action="store_true", help="skip the context-4096 quantized-KV (config 3) line")
     ap.add_argument("--config3-steps", type=int, default=8)
@@ -484,7 +487,7 @@ def main():
     cfg4 = None
     if not args.no_config4:
         t4 = time.time()
-        p4, s4 = 2040, args.config4_steps   # context 2048: decode steps at positions 2041..
+        p4, s4 = args.config4_prompt, args.config4_steps   # context 2048: decode steps at positions 2041..
         ds = synth.SynthDeepSeek(seed=1, max_seq=p4 + s4 + 8)
         log("config 4 model built in %.1fs" % (time.time() - t4))
         inf4 = ds.infer()
