@@ -974,6 +974,12 @@ constexpr int kMfmaLd = 80;
 
 // Up to 3 weight segments sharing x (q / k / v) in one launch: column
 // tiles t0[s] .. of segment s, in order.
+// XCD-aware tile order: workgroups go to the 8 XCDs round-robin in linear
+// order, so workgroup id serves XCD id % 8.  The x rows are split into xa
+// parts and the weight columns into xb parts (xa * xb = 8); XCD x takes
+// m-tiles of part x / xb and n-tiles of part x % xb, so each L2 fetches
+// 1/xa of the activation tiles and 1/xb of the weight tiles (the host
+// picks the split with the fewest bytes fetched).
 struct MfmaArgs {
     GemmArgs g;                  // g.w / g.w2 / g.y / g.N: segment 0
     const uint8_t* w[3];
@@ -981,6 +987,9 @@ struct MfmaArgs {
     int N[3];
     int t0[3];
     int nseg;
+    int mt, nt;                  // m-tiles, n-tiles
+    int xb;                      // weight parts (8 / xb activation parts)
+    int mpp, npp;                // m-tiles, n-tiles per part
 };
 
 template <int FMT, int NMAT, int BM>
@@ -991,15 +1000,20 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MfmaArgs ma) {
     __shared__ float ws[NMAT][32][kMfmaLd];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // this workgroup's tile: XCD id % 8 owns activation part (id % 8) / xb
+    // and weight part (id % 8) % xb
+    const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+    const int mm = k / ma.npp, nn = k - mm * ma.npp;
+    const int by = (xcd / ma.xb) * ma.mpp + mm, bx = (xcd % ma.xb) * ma.npp + nn;
+    if (mm >= ma.mpp || by >= ma.mt || bx >= ma.nt) return;   // padding of the split
     // this workgroup's segment (wave-uniform selects, no indexed argument reads)
     GemmArgs a = ma.g;
-    const int bx = blockIdx.x;
     const int sg = (ma.nseg > 1 && bx >= ma.t0[1]) + (ma.nseg > 2 && bx >= ma.t0[2]);
     a.w = sg == 0 ? ma.w[0] : sg == 1 ? ma.w[1] : ma.w[2];
     a.y = sg == 0 ? ma.y[0] : sg == 1 ? ma.y[1] : ma.y[2];
     a.N = sg == 0 ? ma.N[0] : sg == 1 ? ma.N[1] : ma.N[2];
     const int tb = sg == 0 ? ma.t0[0] : sg == 1 ? ma.t0[1] : ma.t0[2];
-    const int m0 = blockIdx.y * BM, n0 = (bx - tb) * 64;
+    const int m0 = by * BM, n0 = (bx - tb) * 64;
     const int nb = a.K / 32;
     // staging: thread t takes row t / 4 of the x tile (rows < BM) and of
     // each weight tile, values 8 (t % 4) .. 8 (t % 4) + 7 of the block
@@ -1402,7 +1416,20 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     const bool two = epi == RINA_EPI_SWIGLU;
     const int64_t t64 = (int64_t)tiles * ((M + 63) / 64);
     const bool half = t64 < 2LL * rina_num_cus();        // 32-row tiles: more workgroups in flight
-    const dim3 g(tiles, half ? (M + 31) / 32 : (M + 63) / 64);
+    ma.mt = half ? (M + 31) / 32 : (M + 63) / 64;
+    ma.nt = tiles;
+    // bytes the 8 L2s fetch for a split of x into 8 / xb parts and the
+    // weights into xb parts: xb * (x bytes) + (8 / xb) * (weight bytes)
+    const double xbytes = 4.0 * M * K;
+    const double wbytes = (two ? 2.0 : 1.0) * 64.0 * tiles * K *
+                          (qt == RINA_QT_Q4_0F ? 20.0 / 32 : qt == RINA_QT_GGML_Q2_K ? 84.0 / 256 : 18.0 / 32);
+    int best = 1;
+    for (int xb = 2; xb <= 8; xb *= 2)
+        if (xb * xbytes + (8 / xb) * wbytes < best * xbytes + (8 / best) * wbytes) best = xb;
+    ma.xb = best;
+    ma.mpp = (ma.mt + 8 / best - 1) / (8 / best);
+    ma.npp = (tiles + best - 1) / best;
+    const dim3 g(8 * ma.mpp * ma.npp);
 #define MFMA_LAUNCH(F, NM) \
     do { if (half) hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 32>), g, dim3(256), 0, st, ma); \
          else hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 64>), g, dim3(256), 0, st, ma); } while (0)
