@@ -350,16 +350,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
                 gst((float*)a.ck + row + tid, s_k[tid]);
                 gst((float*)a.cv + row + tid, s_v[tid]);
             }
-        } else if (tid < 4 * HG) {              // HG heads x 2 blocks x {K, V}
-            const bool isv = tid >= 2 * HG;
-            const int b = isv ? tid - 2 * HG : tid;
-            float vals[32];
-            const float* src = (isv ? s_v : s_k) + b * 32;
-#pragma unroll
-            for (int i = 0; i < 32; i++) vals[i] = src[i];
-            const int64_t blk = row / 32 + b;
-            if (isv) kvq::quantize_block(VF, vals, a.cv + blk * VBB);
-            else kvq::quantize_block(KF, vals, a.ck + blk * KBB);
+        } else if (tid < 2 * HG * DH) {
+            // one value per thread, a half wave per 32-value block; K fills
+            // the first HG*DH threads (whole waves), V the next
+            const bool isv = tid >= HG * DH;
+            const int e = isv ? tid - HG * DH : tid;
+            const int64_t blk = row / 32 + e / 32;
+            if (isv) kvq::quantize_block_lanes(VF, s_v[e], a.cv + blk * VBB);
+            else kvq::quantize_block_lanes(KF, s_k[e], a.ck + blk * KBB);
         }
         if (a.k_rot_out && tid < HG * DH) gst(a.k_rot_out + (int64_t)hg0 * DH + tid, s_k[tid]);
     }
@@ -469,7 +467,6 @@ template <int QKV>
 __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     __shared__ float s_o[4][64];
     __shared__ float s_m[4], s_l[4];
-    __shared__ float s_row[2][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;
@@ -537,18 +534,14 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     }
     if (QKV == 1 && has_cur && h % rep == 0) {
         // the current key content and value rows packed with the KV cache's
-        // block codec (the same code as rina_hip_kv_quantize), the RoPE part
-        // stored as is
+        // block codec (the same bytes as rina_hip_kv_quantize), the RoPE part
+        // stored as is; lane d of wave 0 holds dim d of both rows, a half
+        // wave per 32-value block
         if (wave == 0) {
-            s_row[0][lane] = kc0;
-            s_row[1][lane] = vc;
-            if (lane < a.db) gst(a.ckr + ((int64_t)pos0 * a.Hkv + kvh) * a.db + lane, kc1);
-        }
-        __syncthreads();
-        if (wave == 0 && (lane & 31) == 0) {
             const int b = lane >> 5;
-            kvq::quantize_block(RINA_KVF_Q2_1, &s_row[0][32 * b], a.ckq + ((int64_t)pos0 * a.Hkv + kvh) * 20 + 10 * b);
-            kvq::quantize_block(RINA_KVF_Q1_0, &s_row[1][32 * b], a.cvq + ((int64_t)pos0 * a.Hkv + kvh) * 12 + 6 * b);
+            if (lane < a.db) gst(a.ckr + ((int64_t)pos0 * a.Hkv + kvh) * a.db + lane, kc1);
+            kvq::quantize_block_lanes(RINA_KVF_Q2_1, kc0, a.ckq + ((int64_t)pos0 * a.Hkv + kvh) * 20 + 10 * b);
+            kvq::quantize_block_lanes(RINA_KVF_Q1_0, vc, a.cvq + ((int64_t)pos0 * a.Hkv + kvh) * 12 + 6 * b);
         }
     }
     s_o[wave][lane] = o;

@@ -166,17 +166,17 @@ __global__ __launch_bounds__(256) void rope_append_kernel(AppendArgs a) {
     }
     int kf, vf;
     kvq::mode_formats(a.mode, kf, vf);
-    const int nbk = kvd / 32;
-    const int64_t b0 = (int64_t)pos * nbk;
-    for (int j = tid; j < 2 * nbk; j += blockDim.x) {
-        float vals[32];
-        bool isv = j >= nbk;
-        int b = isv ? j - nbk : j;
-        const float* src = isv ? vrow + b * 32 : kc_src + b * 32;
-#pragma unroll
-        for (int i = 0; i < 32; i++) vals[i] = src[i];
-        if (isv) kvq::quantize_block(vf, vals, a.cv + (b0 + b) * kvq::block_bytes(vf));
-        else kvq::quantize_block(kf, vals, a.ck + (b0 + b) * kvq::block_bytes(kf));
+    const int64_t b0 = (int64_t)pos * (kvd / 32);
+    // one value per thread, a half wave per 32-value block: 2*kvd is a
+    // multiple of 64 and blockDim.x of 256, so every wave runs the loop's
+    // iterations whole, and kvd is a multiple of 32, so no half wave holds
+    // both K and V
+    for (int e = tid; e < 2 * kvd; e += blockDim.x) {
+        const bool isv = e >= kvd;
+        const int i = isv ? e - kvd : e;
+        const int64_t b = b0 + i / 32;
+        if (isv) kvq::quantize_block_lanes(vf, vrow[i], a.cv + b * kvq::block_bytes(vf));
+        else kvq::quantize_block_lanes(kf, kc_src[i], a.ck + b * kvq::block_bytes(kf));
     }
 }
 

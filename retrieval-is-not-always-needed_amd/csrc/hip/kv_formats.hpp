@@ -86,6 +86,62 @@ __device__ inline void quantize_block(int fmt, const float* v, uint8_t* o) {
     }
 }
 
+// The same block quantized by a 32-lane half wave: lane (__lane_id() & 31) = i
+// holds element i, all 32 lanes are active and pass the same fmt and o.
+// The amax comes from a butterfly max (NaN and -0 enter as 0, as they
+// drop out of the serial scan above), each lane applies quantize_block's
+// per-element arithmetic to its own value (the same fp32 division and
+// roundf), and the codes are OR-gathered into the 16-bit words the serial
+// form stores, so the record bytes are identical.  Used where one thread
+// per block would leave the rest of the workgroup idle (the decode appends).
+__device__ inline void quantize_block_lanes(int fmt, float v, uint8_t* o) {
+    const int i = (int)(__lane_id() & 31);
+    const float av = fabsf(v);
+    float amax = av > 0.f ? av : 0.f;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+    if (fmt == RINA_KVF_Q8_0) {
+        float scale = amax / 127.0f;
+        if (scale < 1e-10f) scale = 1e-10f;
+        int q = (int)roundf(v / scale);
+        q = min(max(q, -127), 127);
+        uint32_t w = (uint32_t)(q & 0xFF) << (8 * (i & 1));
+        w |= __shfl_xor(w, 1, 32);
+        if (i == 0) st16(o, f32_to_f16_rne(scale));
+        if ((i & 1) == 0) st16(o + 2 + i, w);
+    } else if (fmt == RINA_KVF_Q4_0) {
+        float scale = amax / 7.0f;
+        if (scale < 1e-10f) scale = 1e-10f;
+        int q = (int)roundf(v / scale);
+        q = min(max(q, -7), 7) + 7;
+        uint32_t w = (uint32_t)(q & 0xF) << (4 * (i & 3));
+        w |= __shfl_xor(w, 1, 32);
+        w |= __shfl_xor(w, 2, 32);
+        if (i == 0) st16(o, f32_to_f16_rne(scale));
+        if ((i & 3) == 0) st16(o + 2 + i / 2, w);
+    } else if (fmt == RINA_KVF_Q2_1) {
+        uint32_t c = 0;
+        if (amax > 1e-10f) {
+            int q = (int)roundf(v / amax);
+            c = (uint32_t)((min(max(q, -1), 1) + 1) & 3);
+        }
+        uint32_t w = c << (2 * (i & 7));
+        w |= __shfl_xor(w, 1, 32);
+        w |= __shfl_xor(w, 2, 32);
+        w |= __shfl_xor(w, 4, 32);
+        if (i == 0) st16(o, f32_to_f16_rne(amax));
+        if ((i & 7) == 0) st16(o + 2 + i / 4, w);
+    } else {  // RINA_KVF_Q1_0
+        uint32_t w = (amax > 1e-10f && v > 0.0f ? 1u : 0u) << (i & 15);
+        w |= __shfl_xor(w, 1, 32);
+        w |= __shfl_xor(w, 2, 32);
+        w |= __shfl_xor(w, 4, 32);
+        w |= __shfl_xor(w, 8, 32);
+        if (i == 0) st16(o, f32_to_f16_rne(amax));
+        if ((i & 15) == 0) st16(o + 2 + i / 8, w);
+    }
+}
+
 // Element i of one block (kernels/quantize.cu:106-295).
 __device__ __forceinline__ float dequant_one(int fmt, const uint8_t* b, int i) {
     float s = f16_to_f32(ld16(b));

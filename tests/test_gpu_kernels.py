@@ -384,6 +384,101 @@ def test_attention_other_shapes(rina, orc, H, Hkv, dh):
     assert_close(got, ref, what="shape %s" % ((H, Hkv, dh),))
 
 
+def edge_row(r, n, t):
+    """n values (n % 32 == 0) made of 32-value blocks on the quantizers'
+    edges, in an order and power-of-two scale that depend on t: all zeros;
+    -0 with values under the 1e-10 scale clamp; exact roundf ties on the q8
+    grid (amax 127, scale 1), the q4 grid (amax 7) and the q2_1 grid (amax 2,
+    v / amax = +-0.5); one outlier over normals; plain normals."""
+    blocks = [np.zeros(32),
+              np.concatenate([[-0.0, 1e-12, -3e-11], np.full(29, -0.0)]),
+              np.array([127.0] + [(j % 9 - 4) + 0.5 for j in range(31)]),
+              np.array([7.0] + [(j % 7 - 3) + 0.5 for j in range(31)]),
+              np.array([2.0] + [(-1.0) ** j for j in range(31)]),
+              np.concatenate([[3e5], r.standard_normal(31)]),
+              r.standard_normal(32)]
+    out = [blocks[(t + 3 * b) % len(blocks)] * 2.0 ** ((t + b) % 5 - 2) for b in range(n // 32)]
+    return np.concatenate(out).astype(np.float32)
+
+
+def gpu_kv_quantize(hip, fmt, x):
+    """rina_hip_kv_quantize: one thread packs each 32-value block."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = empty(x.size // 32 * nr.KV_BB[fmt], "uint8")
+    ok(hip.rina_hip_kv_quantize(fmt, dev(x).data_ptr(), out.data_ptr(), x.size, stream()), "kv_quantize")
+    return host(out)
+
+
+@pytest.mark.parametrize("mode", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("pre_rope,Hkv,dh", [(1, 4, 64), (0, 4, 64), (1, 3, 32), (0, 3, 32)])
+def test_rope_append_cache_bytes(rina, orc, mode, pre_rope, Hkv, dh):
+    """The records rope_append writes (a half wave packs each block) are the
+    bytes of rina_hip_kv_quantize (one thread per block) on the same rows,
+    inf and NaN included, and the oracle's bytes on the finite rows; with
+    3 x 32 dims a wave holds K blocks in one half and V blocks in the other."""
+    hip = rina.load_hip()
+    H, T, P, max_seq = 2 * Hkv, 4, 6, 16
+    kvd = Hkv * dh
+    r = rng(300 + 10 * mode + pre_rope + Hkv)
+    k = np.stack([edge_row(r, kvd, t) for t in range(T)])
+    v = np.stack([edge_row(r, kvd, t + 2) for t in range(T)])
+    k[3, 5], k[3, 40], v[3, 70], v[3, kvd - 3] = np.inf, np.nan, -np.inf, np.nan
+    q = r.standard_normal((T, H * dh)).astype(np.float32)
+    cos, sin = rope_tables(dh, max_seq)
+    ck = empty(hip.rina_hip_kv_region_bytes(mode, 0, max_seq, kvd), "uint8")
+    cv = empty(hip.rina_hip_kv_region_bytes(mode, 1, max_seq, kvd), "uint8")
+    kd = dev(k)
+    cd, sd = dev(cos), dev(sin)
+    ok(hip.rina_hip_rope_append(dev(q).data_ptr(), kd.data_ptr(), dev(v).data_ptr(), cd.data_ptr(), sd.data_ptr(),
+                                cd.data_ptr(), sd.data_ptr(), ck.data_ptr(), cv.data_ptr(), mode, pre_rope, T, H, Hkv,
+                                dh, P, None, max_seq, stream()), "rope_append")
+    kf, vf = orc.kv_mode_formats(mode)
+    ks = k if pre_rope else host(kd).reshape(T, kvd)      # the cache holds raw keys under pre_rope
+    kb, vb = kvd // 32 * nr.KV_BB[kf], kvd // 32 * nr.KV_BB[vf]
+    gk, gv = host(ck)[P * kb:(P + T) * kb], host(cv)[P * vb:(P + T) * vb]
+    assert np.array_equal(gk, gpu_kv_quantize(hip, kf, ks))
+    assert np.array_equal(gv, gpu_kv_quantize(hip, vf, v))
+    assert np.array_equal(gk[:3 * kb], orc.kv_quantize(kf, ks[:3]))
+    assert np.array_equal(gv[:3 * vb], orc.kv_quantize(vf, v[:3]))
+
+
+@pytest.mark.parametrize("mode", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("P,H,Hkv", [(0, 32, 8), (45, 32, 8), (0, 10, 5), (300, 16, 16)])
+def test_decode_attention_fused_edge_blocks(rina, orc, mode, P, H, Hkv):
+    """The fused decode append packs the current K / V row with a half wave
+    per block: on blocks at the quantizers' edges its records equal the
+    oracle's bytes for the rotated key row the call returns and the value
+    row, and no other cache row changes."""
+    hip = rina.load_hip()
+    dh = 64
+    kvd = Hkv * dh
+    max_seq = P + 3
+    r = rng(500 + 10 * mode + P + H)
+    kc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    vc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    q = r.standard_normal(H * dh).astype(np.float32)
+    k, v = edge_row(r, kvd, P), edge_row(r, kvd, P + 1)
+    cos, sin = rope_tables(dh, max_seq)
+    kf, vf = orc.kv_mode_formats(mode)
+    ckb, cvb = orc.kv_quantize(kf, kc), orc.kv_quantize(vf, vc)
+    ws_bytes = hip.rina_hip_gqa_attention_workspace(1, H, dh, max_seq)
+    ws = empty(ws_bytes, "uint8")
+    ckd, cvd = dev(ckb), dev(cvb)
+    od, krot = empty(H * dh), empty(kvd)
+    cd, sd = dev(cos), dev(sin)
+    ok(hip.rina_hip_gqa_decode_attention(dev(q).data_ptr(), dev(k).data_ptr(), dev(v).data_ptr(), cd.data_ptr(),
+                                         sd.data_ptr(), cd.data_ptr(), sd.data_ptr(), ckd.data_ptr(), cvd.data_ptr(),
+                                         mode, H, Hkv, dh, P, None, max_seq, od.data_ptr(), krot.data_ptr(),
+                                         ws.data_ptr(), ws_bytes, stream()), "decode attention")
+    kr = host(krot)
+    if P == 0:        # cos 1, sin 0: the rotation leaves the edge blocks as they are
+        assert np.array_equal(kr, k)
+    want_k, want_v = kc.copy(), vc.copy()
+    want_k[P], want_v[P] = kr, v
+    assert np.array_equal(host(ckd), orc.kv_quantize(kf, want_k))
+    assert np.array_equal(host(cvd), orc.kv_quantize(vf, want_v))
+
+
 @pytest.mark.parametrize("mode", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("P,H,Hkv,use_dpos", [(0, 32, 8, False), (37, 32, 8, False), (543, 32, 8, True),
                                               (1500, 32, 8, False), (70, 10, 5, False), (16, 8, 8, True),
