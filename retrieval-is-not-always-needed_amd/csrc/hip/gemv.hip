@@ -1177,10 +1177,12 @@ int launch_direct(GemvArgs& a, hipStream_t st) {
     constexpr int RPI = 4 / WPR;
     int cus = rina_num_cus();
     int wgs = (a.total_tiles + RPI - 1) / RPI;
-    // workgroups resident per CU at this register count (Q2_K, 4 rows, one
-    // matrix: 89 VGPRs and 28.7 KB of LDS leave room for 5; the LM head
-    // 102400 x 2048 measured 32.5 / 31.5 / 30.8 us at 3 / 4 / 5)
-    int per_cu = FMT == FMT_Q2_K ? (RB >= 4 ? (NMAT == 2 ? 2 : 5) : 4) : (RB >= 8 ? 2 : RB == 4 ? 3 : 4);
+    // workgroups per CU (measured): Q2_K with 4 rows and one matrix (89
+    // VGPRs, 28.7 KB of LDS) takes 5, the LM head 102400 x 2048 measured
+    // 32.5 / 31.5 / 30.8 us at 3 / 4 / 5; Q4 with 1-4 rows per wave takes 3
+    // (config 1 8192 x 2048 at 2 rows: 4.42 us at 4, 4.28 at 3; SwiGLU
+    // 8192 x 2048 at 1 row: 7.33 / 6.44 us), 8 rows take 2
+    int per_cu = FMT == FMT_Q2_K ? (RB >= 4 ? (NMAT == 2 ? 2 : 5) : 4) : (RB >= 8 ? 2 : 3);
     int grid = wgs < cus * per_cu ? wgs : cus * per_cu;
     hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB, NS>), dim3(grid), dim3(kWG), 0, st, a);
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
@@ -1279,6 +1281,13 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
         }
         int rb = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : 8;
         if (fmt == FMT_Q2_K && rb > 4) rb = 4;   // 8 rows measured slower (LM head 32 -> 35 us)
+        // Q4 rows of at most 4096 values: more workgroups with fewer rows
+        // each (config 1 8192 x 2048: 4 -> 2 rows per wave, 5.06 -> 4.28 us;
+        // SwiGLU 8192 x 2048: 2 -> 1 row, 7.22 -> 6.44 us, 3 workgroups per CU)
+        if (fmt != FMT_Q2_K && wpr < 4) {
+            const int cap = nmat == 2 ? 1 : 2;
+            if (rb > cap) rb = cap;
+        }
         a.R = rows;
         a.total_tiles = (rows + rb - 1) / rb;
         if (fmt == FMT_Q2_K)
