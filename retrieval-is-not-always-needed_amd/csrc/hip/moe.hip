@@ -14,6 +14,8 @@
 //               by the probabilities, then one reduction: the same terms as
 //               the reference's shared matvec + saxpy chain, summed in
 //               another order).  G is digitized into LDS per workgroup.
+#include <type_traits>
+
 #include "q2k_col.hpp"
 
 namespace {
@@ -332,8 +334,13 @@ __device__ __forceinline__ void read_rec(const uint32_t* rc, DCols<FMT_Q2_K>& xc
 // no lane idles on a short expert row; each column's product is weighted by
 // its source's probability (1 for the shared FFN) and one wave reduction
 // gives the row.  The loads go out before the workgroup digitizes G.
+// QUAD (shared and expert widths multiples of 128): a quad's four lanes
+// hold the four columns of one half page, so each lane loads 8 of its 32
+// qs bytes and the quad exchanges them (Q2ColQ) instead of every lane
+// loading all 32.
 constexpr int kDnRounds = 8;   // columns per lane: (shared + k * ffn) / 32 <= 512
 
+template <bool QUAD>
 __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     extern __shared__ __align__(16) uint32_t s_rec[];   // [n / 32][kRec]
     const int tid = threadIdx.x, lane = tid & 63;
@@ -356,7 +363,7 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     // floor(t / fcols) for 0 <= t < 2^16 / 128: t * ceil(2^16 / fcols) >> 16,
     // then one correction step each way
     const uint32_t magic = (65536u + (uint32_t)fcols - 1u) / (uint32_t)fcols;
-    Q2Col c[kDnRounds];
+    typename std::conditional<QUAD, Q2ColQ, Q2Col>::type c[kDnRounds];
     float wt[kDnRounds];
     int col[kDnRounds];
 #pragma unroll
@@ -385,7 +392,8 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
         }
         wt[r] = f;
         col[r] = cc < ncol ? cc : 0;
-        q2_col_issue32(w, e0, c[r]);
+        if constexpr (QUAD) q2_colq_issue32(w, e0, c[r]);
+        else q2_col_issue32(w, e0, c[r]);
     }
     stage_g_digits(gs, ncol, s_rec);
     __syncthreads();
@@ -394,11 +402,14 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     float acc = 0.f;
 #pragma unroll
     for (int r = 0; r < kDnRounds; r++) {
-        if (r >= rounds) break;
+        if (r >= rounds) break;                    // wave-uniform
+        Q2Col cx;
+        if constexpr (QUAD) q2_colq_expand(c[r], cx);   // every lane of the quad takes part
+        else cx = c[r];
         if (wt[r] != 0.f) {
             DCols<FMT_Q2_K> xc;
             read_rec(s_rec + col[r] * kRec, xc);
-            acc = fmaf(wt[r], q2_col(c[r], xc), acc);
+            acc = fmaf(wt[r], q2_col(cx, xc), acc);
         }
     }
     acc = wave_sum(acc);
@@ -455,7 +466,11 @@ extern "C" int rina_hip_moe_block(float* h, const float* ln2, float eps, const v
     if (g1 > cus * 3) g1 = cus * 3;
     hipLaunchKernelGGL(moe_gate_up_q2_kernel, dim3(g1), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
-    hipLaunchKernelGGL(moe_down_q2_kernel, dim3((d + 7) / 8), dim3(512), lds, st, a);
+    // quad column loads when every source's columns come in whole half pages
+    if (S % 128 == 0 && F % 128 == 0)
+        hipLaunchKernelGGL(moe_down_q2_kernel<true>, dim3((d + 7) / 8), dim3(512), lds, st, a);
+    else
+        hipLaunchKernelGGL(moe_down_q2_kernel<false>, dim3((d + 7) / 8), dim3(512), lds, st, a);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }

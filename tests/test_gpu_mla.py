@@ -163,7 +163,10 @@ def test_moe_ffn_vs_float64(rina, orc, d, F, E, k, qt):
 
 
 @pytest.mark.parametrize("d,F,S,E,k", [(2048, 1408, 2816, 64, 6), (256, 64, 128, 8, 3), (512, 96, 192, 16, 4),
-                                       (1024, 2048, 64, 32, 2)])
+                                       (1024, 2048, 64, 32, 2),
+                                       # shared and expert widths multiples of 128 (the down
+                                       # kernel's quad column loads)
+                                       (256, 128, 256, 8, 3), (512, 256, 128, 16, 4)])
 def test_moe_block_vs_float64(rina, orc, d, F, S, E, k):
     """Fused MoE block (norm, router, top-k, shared + routed experts, residual)
     against a float64 restatement of forward_moe; selected ids and probs
