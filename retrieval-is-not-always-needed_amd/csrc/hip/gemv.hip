@@ -395,7 +395,7 @@ struct DirectBlkQ2 {
     // repeated bytes (W_o 2048 x 2048: 3.7 vs 4.4 us)
     static constexpr bool QUAD = RB >= 4;
     uint32_t qs[RB][2][QUAD ? 2 : 8];
-    uint32_t sm[RB][2];     // scale bytes of halves 0 and 1 (low 16 bits)
+    uint32_t sm[RB][2];     // dword holding the scale bytes of halves 0 and 1 (q2_sm16)
     uint32_t dd[RB][2];     // d | dmin << 16
     int sh[RB];             // 2g
     int seg[RB], row[RB];
@@ -501,14 +501,14 @@ __device__ __forceinline__ void direct_issue(const GemvArgs& a, const Segs& S, i
                 Q2ColQ c;
                 q2_colq_load(S.wt(sg, m) + off, page, g, c);
                 b.qs[i][m][0] = c.q[0]; b.qs[i][m][1] = c.q[1];
-                b.sm[i][m] = c.sm & 0xFFFFu;
+                b.sm[i][m] = c.sm;
                 b.dd[i][m] = c.dd;
             } else {
                 Q2Col c;
                 q2_col_load(S.wt(sg, m) + off, page, g, c);
 #pragma unroll
                 for (int z = 0; z < 8; z++) b.qs[i][m][z] = c.qs[z];
-                b.sm[i][m] = c.sm & 0xFFFFu;
+                b.sm[i][m] = c.sm;
                 b.dd[i][m] = c.dd;
             }
         }
@@ -541,13 +541,13 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S,
                 Q2Col c;
                 if constexpr (DirectBlkQ2<RB>::QUAD) {
                     // the quad exchange runs on every lane, outside the row test
-                    const Q2ColQ cq{{cur.qs[i][m][0], cur.qs[i][m][1]}, 0u, 0u};
+                    const Q2ColQ cq{{cur.qs[i][m][0], cur.qs[i][m][1]}, 0u, 0u, 0u};
                     q2_colq_expand(cq, c);
                 } else {
 #pragma unroll
                     for (int z = 0; z < 8; z++) c.qs[z] = cur.qs[i][m][z];
                 }
-                part[i][m] = wave_sum(cur.ok[i] ? q2_col(c.qs, cur.sm[i][m], cur.dd[i][m], cur.sh[i], xc) : 0.f);
+                part[i][m] = wave_sum(cur.ok[i] ? q2_col(c.qs, q2_sm16(cur.sm[i][m], cur.sh[i]), cur.dd[i][m], cur.sh[i], xc) : 0.f);
             }
             else
                 part[i][m] = wave_sum((cur.ok[i] ? cur.sc[i][m] : 0.f) * xc.xe[0] * q4_dot(cur.nib[i][m], xc, 0));

@@ -198,8 +198,9 @@ __device__ __forceinline__ void gu_consume(const MoeBlkArgs& a, const DCols<FMT_
     }
 }
 
-// Every wave selects the experts itself (no barrier before its first weight
-// loads); the loads are in flight while the workgroup digitizes a2.
+// Every wave with routed rows selects the experts itself (no barrier before
+// its first weight loads); the loads are in flight while the workgroup
+// digitizes a2.
 __global__ __launch_bounds__(256) void moe_gate_up_q2_kernel(MoeBlkArgs a) {
     __shared__ PrepLds prep;
     __shared__ int s_ids_w[4][16];
@@ -211,14 +212,21 @@ __global__ __launch_bounds__(256) void moe_gate_up_q2_kernel(MoeBlkArgs a) {
     PrepRaw<4, RINA_PRO_NONE> raw;
     wg_prep_load<4, RINA_PRO_NONE>(src, raw);
     const int* s_ids = s_ids_w[wave];
-    topk_wave(a, s_ids_w[wave], s_pr_w[wave], s_tmp_w[wave], blockIdx.x == 0 && wave == 0);
     const bool active = lane < a.d / 32;
     const int R = a.S + a.k * a.F;
     const int ngrp = (R + kGuRB - 1) / kGuRB;
     const int step = gridDim.x * 4;
     int grp = blockIdx.x * 4 + wave;
+    const bool publish = blockIdx.x == 0 && wave == 0;
+    // a wave whose only row group holds shared-FFN rows needs no expert ids:
+    // its weight loads go out at once, during the other waves' logits round
+    // trip (wave 0 of workgroup 0 still publishes the selection)
+    const bool shared_only = (grp + 1) * kGuRB <= a.S && grp + step >= ngrp && !publish;
+    // (one issue site for both: separate copies of the loads leave the
+    // load-counter waits after the join counting the wrong loads)
+    if (!shared_only) topk_wave(a, s_ids_w[wave], s_pr_w[wave], s_tmp_w[wave], publish);
     GuBlk A, B;
-    gu_issue(a, s_ids, grp < ngrp ? grp : 0, R, active && grp < ngrp, A);
+    gu_issue(a, s_ids, grp < ngrp ? grp : 0, R, active && grp < ngrp, A);   // rows < S do not read s_ids
     wg_prep_x<FMT_Q2_K, 4, RINA_PRO_NONE>(src, raw, prep);
     DCols<FMT_Q2_K> xc;
     read_cols<FMT_Q2_K>(prep, lane, active, xc);

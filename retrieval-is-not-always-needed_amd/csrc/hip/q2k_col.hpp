@@ -170,19 +170,28 @@ __device__ __forceinline__ float q2_col(const uint32_t (&qs)[8], uint32_t sm, ui
 
 // The loads of one 32-value Q2_K column starting at flat element e0 of the
 // weight stream w (e0 % 32 == 0): the page's qs bytes, the two half scale
-// bytes and the block's d / dmin.
+// bytes and the block's d / dmin.  The fields hold loaded dwords as they
+// are (the field shift sh comes from the address; the scale pair is cut
+// out of its dword where it is used): arithmetic on a loaded value at issue,
+// also the zero extension of a 16-bit load, makes the wave wait for that
+// load there.
 struct Q2Col {
     uint32_t qs[8];
-    uint32_t sm;    // half scale bytes (bits 0-15) | 2g << 16
+    uint32_t sm;    // dword holding the two half scale bytes (q2_sm16)
     uint32_t dd;
+    uint32_t sh;    // 2g: shift of the column's 2-bit field in each qs byte
 };
+
+// the column's half scale bytes from the dword at 8 page + 4 (g / 2)
+__device__ __forceinline__ uint32_t q2_sm16(uint32_t smw, uint32_t sh) { return smw >> (8 * (sh & 2)); }
 
 __device__ __forceinline__ void q2_col_load(const uint8_t* bp, int page, int g, Q2Col& c) {
     const u32x4_a4 q0 = gld_nt_a4(bp + 16 + 32 * page), q1 = gld_nt_a4(bp + 32 + 32 * page);
     c.qs[0] = q0.x; c.qs[1] = q0.y; c.qs[2] = q0.z; c.qs[3] = q0.w;
     c.qs[4] = q1.x; c.qs[5] = q1.y; c.qs[6] = q1.z; c.qs[7] = q1.w;
-    c.sm = (uint32_t)gld_nt((const uint16_t*)(bp + 8 * page + 2 * g)) | ((uint32_t)(2 * g) << 16);
+    c.sm = gld_nt((const uint32_t*)(bp + 8 * page + 4 * (g >> 1)));
     c.dd = gld_nt((const uint32_t*)(bp + 80));
+    c.sh = (uint32_t)(2 * g);
 }
 
 __device__ __forceinline__ void q2_col_issue(const uint8_t* w, int64_t e0, Q2Col& c) {
@@ -198,7 +207,7 @@ __device__ __forceinline__ void q2_col_issue32(const uint8_t* w, uint32_t e0, Q2
 }
 
 __device__ __forceinline__ float q2_col(const Q2Col& c, const DCols<FMT_Q2_K>& xc) {
-    return q2_col(c.qs, c.sm & 0xFFFFu, c.dd, (int)(c.sm >> 16), xc);
+    return q2_col(c.qs, q2_sm16(c.sm, c.sh), c.dd, (int)c.sh, xc);
 }
 
 // Quad form of the column loads.  When lane u holds column u of a row
@@ -210,8 +219,9 @@ __device__ __forceinline__ float q2_col(const Q2Col& c, const DCols<FMT_Q2_K>& x
 // lanes of a quad must be active at the exchange.
 struct Q2ColQ {
     uint32_t q[2];  // qs bytes 8t .. 8t + 7 of the half page, t = lane & 3
-    uint32_t sm;    // as Q2Col::sm
+    uint32_t sm;    // as Q2Col
     uint32_t dd;
+    uint32_t sh;
 };
 
 __device__ __forceinline__ void q2_colq_load(const uint8_t* bp, int page, int g, Q2ColQ& c) {
@@ -219,8 +229,9 @@ __device__ __forceinline__ void q2_colq_load(const uint8_t* bp, int page, int g,
     const u32x2_a4 q = __builtin_nontemporal_load(
         (const __attribute__((address_space(1))) u32x2_a4*)(bp + 16 + 32 * page + 8 * (threadIdx.x & 3)));
     c.q[0] = q.x; c.q[1] = q.y;
-    c.sm = (uint32_t)gld_nt((const uint16_t*)(bp + 8 * page + 2 * g)) | ((uint32_t)(2 * g) << 16);
+    c.sm = gld_nt((const uint32_t*)(bp + 8 * page + 4 * (g >> 1)));
     c.dd = gld_nt((const uint32_t*)(bp + 80));
+    c.sh = (uint32_t)(2 * g);
 }
 
 __device__ __forceinline__ void q2_colq_issue32(const uint8_t* w, uint32_t e0, Q2ColQ& c) {
@@ -246,6 +257,7 @@ __device__ __forceinline__ void q2_colq_expand(const Q2ColQ& c, Q2Col& o) {
     o.qs[6] = quad_bcast<3>(c.q[0]); o.qs[7] = quad_bcast<3>(c.q[1]);
     o.sm = c.sm;
     o.dd = c.dd;
+    o.sh = c.sh;
 }
 
 // Digits of one 32-value column in the Q2_K (natural) order with the fp32
