@@ -111,10 +111,9 @@ __global__ __launch_bounds__(256) void moe_router_kernel(MoeBlkArgs a) {
 // among equal ones, and fill the slots from the top.  The normalizer is
 // summed in expert order as the reference's loop does (the exponentials of
 // experts >= E are exact zeros).  s_tmp: 64 floats of the wave's own LDS.
-__device__ __forceinline__ void topk_wave(const MoeBlkArgs& a, int* s_ids, float* s_pr, float* s_tmp,
+__device__ __forceinline__ void topk_wave(const MoeBlkArgs& a, float x, int* s_ids, float* s_pr, float* s_tmp,
                                           bool publish) {
     const int lane = threadIdx.x & 63;
-    const float x = lane < a.E ? gld(a.logits + lane) : -INFINITY;
     const float mx = wave_max(x);
     const float ex = lane < a.E ? expf(x - mx) : 0.f;
     s_tmp[lane] = ex;
@@ -208,9 +207,6 @@ __global__ __launch_bounds__(256) void moe_gate_up_q2_kernel(MoeBlkArgs a) {
     __shared__ __align__(16) float s_tmp_w[4][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const PrepSrc src{a.a2, nullptr, a.d, 0.f};
-    PrepRaw<4, RINA_PRO_NONE> raw;
-    wg_prep_load<4, RINA_PRO_NONE>(src, raw);
     const int* s_ids = s_ids_w[wave];
     const bool active = lane < a.d / 32;
     const int R = a.S + a.k * a.F;
@@ -222,9 +218,15 @@ __global__ __launch_bounds__(256) void moe_gate_up_q2_kernel(MoeBlkArgs a) {
     // its weight loads go out at once, during the other waves' logits round
     // trip (wave 0 of workgroup 0 still publishes the selection)
     const bool shared_only = (grp + 1) * kGuRB <= a.S && grp + step >= ngrp && !publish;
+    // the logits before a2 (loads complete in issue order: the top-k waits
+    // for the logits alone)
+    const float lg = !shared_only && lane < a.E ? gld(a.logits + lane) : -INFINITY;
+    const PrepSrc src{a.a2, nullptr, a.d, 0.f};
+    PrepRaw<4, RINA_PRO_NONE> raw;
+    wg_prep_load<4, RINA_PRO_NONE>(src, raw);
     // (one issue site for both: separate copies of the loads leave the
     // load-counter waits after the join counting the wrong loads)
-    if (!shared_only) topk_wave(a, s_ids_w[wave], s_pr_w[wave], s_tmp_w[wave], publish);
+    if (!shared_only) topk_wave(a, lg, s_ids_w[wave], s_pr_w[wave], s_tmp_w[wave], publish);
     GuBlk A, B;
     gu_issue(a, s_ids, grp < ngrp ? grp : 0, R, active && grp < ngrp, A);   // rows < S do not read s_ids
     wg_prep_x<FMT_Q2_K, 4, RINA_PRO_NONE>(src, raw, prep);
@@ -271,16 +273,17 @@ struct GStage {
     f32x4 v[kStageRounds][2];
 };
 
+// Every lane loads (columns past ncol read column 0, which stage_g_digits
+// never stores): loads under a branch leave the load-counter waits after it
+// waiting for every load in flight.
 __device__ __forceinline__ void stage_g_load(const float* G, int ncol, GStage& g) {
     const int tid = threadIdx.x, j = tid & 3;
-    const int rounds = (ncol + 127) / 128;
 #pragma unroll
     for (int r = 0; r < kStageRounds; r++) {
         const int c = (tid >> 2) + 128 * r;
-        const bool on = c < ncol && r < rounds;
-        const f32x4* src = (const f32x4*)(G + 32 * (on ? c : 0) + 8 * j);
-        g.v[r][0] = on ? gld(src) : f32x4{0.f, 0.f, 0.f, 0.f};
-        g.v[r][1] = on ? gld(src + 1) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4* src = (const f32x4*)(G + 32 * (c < ncol ? c : 0) + 8 * j);
+        g.v[r][0] = gld(src);
+        g.v[r][1] = gld(src + 1);
     }
 }
 
@@ -360,14 +363,16 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     const bool row_on = i < a.d;
     const int ir = row_on ? i : 0;
 
-    // G and the selected experts / probabilities load together (one round
+    // the selected experts / probabilities and G load together (one round
     // trip); the weight addresses need the expert ids.  Lane j < k holds
     // slot j's expert and probability; a column's slot is read from that
     // lane (ds_bpermute, every lane active) instead of a select chain.
-    GStage gs;
-    stage_g_load(a.G, ncol, gs);
+    // (ids first: loads complete in issue order, so the addresses wait for
+    // the ids alone)
     const int my_id = lane < a.k ? gld(a.ids + lane) : -1;
     const float my_pr = lane < a.k ? gld(a.probs + lane) : 0.f;
+    GStage gs;
+    stage_g_load(a.G, ncol, gs);
     // floor(t / fcols) for 0 <= t < 2^16 / 128: t * ceil(2^16 / fcols) >> 16,
     // then one correction step each way
     const uint32_t magic = (65536u + (uint32_t)fcols - 1u) / (uint32_t)fcols;
