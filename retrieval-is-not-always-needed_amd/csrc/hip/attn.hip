@@ -168,28 +168,34 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     const int wslot = wave * PPW + slot;
 
     // query rows (and the current K/V row) first: cache hits, consumed while
-    // the chunk's K/V loads are in flight
+    // the chunk's K/V loads are in flight.  The query-side loads sit under no
+    // branch (without RoPE tables the query rows stand in for them, unused):
+    // loads under a branch can leave register copies at the join that wait
+    // for them there, before the cache loads are issued.  The current row is
+    // read by the workgroup that holds it only (a uniform branch).
     float qraw[REP][8], qpair[REP][8], tc[8], ts[8];
     float kown[8], kpair[8], kc8[8], ks8[8], vcur[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) kown[i] = vcur[i] = 0.f;
+    const bool qrope = FUSED && a.qc, krope = FUSED && a.kc;
+    const int64_t toff = (int64_t)pos0 * 32 + (dim0 & 31);
 #pragma unroll
     for (int r = 0; r < REP; r++) {
         const float* qh = a.q + (int64_t)(kvh * REP + r) * DH;
         ld8f(qh + dim0, qraw[r]);
-        if (FUSED && a.qc) ld8f(qh + (dim0 ^ 32), qpair[r]);
+        if constexpr (FUSED) ld8f(qh + (dim0 ^ 32), qpair[r]);
     }
-    if (FUSED && a.qc) {
-        ld8f(a.qc + (int64_t)pos0 * 32 + (dim0 & 31), tc);
-        ld8f(a.qs + (int64_t)pos0 * 32 + (dim0 & 31), ts);
+    if constexpr (FUSED) {
+        ld8f(qrope ? a.qc + toff : a.q, tc);
+        ld8f(qrope ? a.qs + toff : a.q, ts);
     }
+#pragma unroll
+    for (int i = 0; i < 8; i++) kown[i] = vcur[i] = kpair[i] = kc8[i] = ks8[i] = 0.f;
     if (has_cur) {
         ld8f(a.kcur + voff, kown);
         ld8f(a.vcur + voff, vcur);
-        if (FUSED && a.kc) {
+        if constexpr (FUSED) {
             ld8f(a.kcur + (int64_t)kvh * DH + (dim0 ^ 32), kpair);
-            ld8f(a.kc + (int64_t)pos0 * 32 + (dim0 & 31), kc8);
-            ld8f(a.ks + (int64_t)pos0 * 32 + (dim0 & 31), ks8);
+            ld8f(krope ? a.kc + toff : a.kcur, kc8);
+            ld8f(krope ? a.ks + toff : a.kcur, ks8);
         }
     }
 
@@ -212,7 +218,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     const float qsc = a.scale * 1.44269504088896341f;
 #pragma unroll
     for (int r = 0; r < REP; r++) {
-        if (FUSED && a.qc) rope8(dim0, qraw[r], qpair[r], tc, ts, qv[r]);
+        if (qrope) rope8(dim0, qraw[r], qpair[r], tc, ts, qv[r]);
         else {
 #pragma unroll
             for (int i = 0; i < 8; i++) qv[r][i] = qraw[r][i];
@@ -220,13 +226,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; i++) qv[r][i] *= qsc;
     }
-    float kcur[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (has_cur) {
-        if (FUSED && a.kc) rope8(dim0, kown, kpair, kc8, ks8, kcur);
-        else {
+    float kcur[8];                                  // used only where has_cur
+    if (krope) rope8(dim0, kown, kpair, kc8, ks8, kcur);
+    else {
 #pragma unroll
-            for (int i = 0; i < 8; i++) kcur[i] = kown[i];
-        }
+        for (int i = 0; i < 8; i++) kcur[i] = kown[i];
     }
 
     float ov[REP][8], m_run[REP], l_run[REP];
