@@ -362,7 +362,8 @@ def main():
         pre_ms.append((time.perf_counter() - t_p) * 1e3)
     prefill = {"prompt": args.prompt, "ms": round(pre_ms[-1], 3),
                "tokens_per_s": round(args.prompt / (pre_ms[-1] / 1e3), 1),
-               "note": "Q4 linears on v_mfma_f32_16x16x4f32 (fp32 products, fp32 sums); prompt attention "
+               "note": "Q4 linears on v_mfma_f32_16x16x32_bf16 with x split exactly into three bf16 parts "
+                       "(fp32 products, fp32 sums); prompt attention "
                        "from position 0 in 64-position blocks (one softmax rescale per block)"}
     log("prefill: %d tokens in %.2f ms (%.0f tok/s)" % (args.prompt, pre_ms[-1], prefill["tokens_per_s"]))
     # the GPU's K/V rows of the prompt, so the CPU baseline decodes at the
@@ -409,7 +410,10 @@ def main():
     log("Q4_0F W1/W3 SwiGLU matvec: %.1f us, %.0f GB/s" % (t_sw * 1e6, sw_bytes / t_sw / 1e9))
 
     # ---- prompt phase: the same W1/W3 SwiGLU at M = args.prompt rows on the
-    # matrix cores (fp32 MFMA peak), HIP events on our stream
+    # matrix cores, HIP events on our stream.  The kernel forms fp32 products
+    # from three bf16 MFMAs each (x split exactly into three bf16 parts), so
+    # its peak in fp32-product flop is the dense bf16 peak / 3 (2500 / 3
+    # TFLOP/s); the flop counted are the algorithmic 2 per multiply-add.
     Mp = args.prompt
     xp = torch.randn(Mp * d, device="cuda")
     gp = torch.empty(Mp * hd, device="cuda")
@@ -420,8 +424,10 @@ def main():
                                          rina.EPI_SWIGLU, rina.PRO_NONE, None, 0.0, st)
     t_swp = time_kernel(torch, swiglu_p, 8, replays=2)
     swp_flop = 2 * 2 * Mp * hd * d
-    swp_roof = {"bound": "mfma", "achieved": round(swp_flop / t_swp / 1e12, 2), "peak": 157.3, "unit": "TFLOP/s",
-                "frac": round(swp_flop / t_swp / 157.3e12, 4), "traffic": None}
+    swp_peak = 2500.0 / 3
+    swp_roof = {"bound": "mfma", "achieved": round(swp_flop / t_swp / 1e12, 2), "peak": round(swp_peak, 1),
+                "unit": "TFLOP/s", "frac": round(swp_flop / t_swp / (swp_peak * 1e12), 4), "traffic": None,
+                "fp32_mfma_frac": round(swp_flop / t_swp / 157.3e12, 4)}
     log("prompt W1/W3 SwiGLU (M %d): %.1f us, %.1f TFLOP/s" % (Mp, t_swp * 1e6, swp_flop / t_swp / 1e12))
     del xp, gp
 
@@ -665,7 +671,8 @@ def main():
             "q4_0f_swiglu_w1w3": dict(sw_roof, bytes_per_launch=sw_bytes, avg_us=round(t_sw * 1e6, 2)),
             "config1_q4_0_gemv_8192x2048": dict(q4_roof, bytes_per_launch=q4_bytes, avg_us=round(t_q4 * 1e6, 3)),
             "prefill_q4_0f_swiglu_m%d" % Mp: dict(swp_roof, flop_per_launch=swp_flop, avg_us=round(t_swp * 1e6, 2),
-                                                  kernel="gemm_mfma_kernel (v_mfma_f32_16x16x4f32)"),
+                                                  kernel="gemm_bf3_kernel (v_mfma_f32_16x16x32_bf16, "
+                                                         "three per fp32 product)"),
             **attn_roofs,
         },
         "decode_hbm_gbps": round(per_token * tok_s / 1e9, 1),

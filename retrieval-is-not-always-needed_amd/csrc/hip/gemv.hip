@@ -1132,6 +1132,165 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MfmaArgs ma) {
             }
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// the high halves of two fp32 bit patterns as one dword of two bf16 (a's in
+// the low half)
+__device__ __forceinline__ uint32_t hi16_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+// x0, x1 split exactly into three bf16 parts each, x = h + m + l: h is x cut
+// to its top 8 significant bits, m the remainder cut the same way, l the
+// rest (at most 8 significant bits, so exact); packed as two-value dwords
+__device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& ph, uint32_t& pm, uint32_t& pl) {
+    const uint32_t u0 = __float_as_uint(x0), u1 = __float_as_uint(x1);
+    ph = hi16_pair(u0, u1);
+    const float r0 = x0 - __uint_as_float(u0 & 0xFFFF0000u), r1 = x1 - __uint_as_float(u1 & 0xFFFF0000u);
+    const uint32_t v0 = __float_as_uint(r0), v1 = __float_as_uint(r1);
+    pm = hi16_pair(v0, v1);
+    const float s0 = r0 - __uint_as_float(v0 & 0xFFFF0000u), s1 = r1 - __uint_as_float(v1 & 0xFFFF0000u);
+    pl = hi16_pair(__float_as_uint(s0), __float_as_uint(s1));
+}
+
+// Prompt matmul for Q4_0 / Q4_0F weights on the bf16 matrix cores, with fp32
+// products and sums.  Every x value is split exactly into three bf16 parts,
+// x = h + m + l (8 significant bits each: the two remainders are exact in
+// fp32), and a weight value q - 7 is a small integer, exact in bf16, so
+// v_mfma_f32_16x16x32_bf16 forms the exact products of the fp32 x with the
+// integer weights and sums them in fp32.  Per 32-value block and 16x16 tile
+// three MFMAs (l, m, h into one accumulator), then one fp32 fma with the
+// block scale of the tile column.  Tiles, XCD order, segments, staging
+// (thread t: row t / 4, values 8 (t % 4) .. + 7 of the block) and epilogues
+// as gemm_mfma_kernel.  LDS rows of 40 bf16 keep the 16-byte fragment reads
+// of 16 rows on distinct banks.  Fragment layout (16x16x32): lane l holds
+// A[l % 16][8 (l / 16) .. + 7], B[8 (l / 16) .. + 7][l % 16] and
+// D[4 (l / 16) + e][l % 16].
+template <int FMT, int NMAT, int BM>
+__global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
+    constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
+    constexpr int MI = BM / 32;                    // MFMA tiles per wave along M
+    constexpr int LD = 40;
+    __shared__ __align__(16) uint16_t xs[3][BM][LD];
+    __shared__ __align__(16) uint16_t ws[NMAT][64][LD];
+    __shared__ float wsc_s[NMAT][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+    const int mm = k / ma.npp, nn = k - mm * ma.npp;
+    const int by = (xcd / ma.xb) * ma.mpp + mm, bx = (xcd % ma.xb) * ma.npp + nn;
+    if (mm >= ma.mpp || by >= ma.mt || bx >= ma.nt) return;   // padding of the split
+    GemmArgs a = ma.g;
+    const int sg = (ma.nseg > 1 && bx >= ma.t0[1]) + (ma.nseg > 2 && bx >= ma.t0[2]);
+    a.w = sg == 0 ? ma.w[0] : sg == 1 ? ma.w[1] : ma.w[2];
+    a.y = sg == 0 ? ma.y[0] : sg == 1 ? ma.y[1] : ma.y[2];
+    a.N = sg == 0 ? ma.N[0] : sg == 1 ? ma.N[1] : ma.N[2];
+    const int tb = sg == 0 ? ma.t0[0] : sg == 1 ? ma.t0[1] : ma.t0[2];
+    const int m0 = by * BM, n0 = (bx - tb) * 64;
+    const int nb = a.K / 32;
+    const int sr = tid >> 2, sq = tid & 3;
+    const bool xok = sr < BM && m0 + sr < a.M, wok = n0 + sr < a.N;
+    const float* xrow = a.x + (int64_t)(xok ? m0 + sr : 0) * a.K + 8 * sq;
+    const int64_t wrow = (int64_t)(wok ? n0 + sr : 0) * nb * BB;
+    f32x4 xr0, xr1;
+    uint32_t wsc[NMAT], wnb[NMAT];
+    auto load_blk = [&](int b) {
+        const f32x4* xp = (const f32x4*)(xrow + 32 * b);
+        xr0 = gld(xp);
+        xr1 = gld(xp + 1);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            const uint8_t* bp = (m ? a.w2 : a.w) + wrow + (int64_t)b * BB;
+            if constexpr (FMT == FMT_Q4_0F) {
+                wsc[m] = gld((const uint32_t*)bp);
+                wnb[m] = gld((const uint32_t*)(bp + 4 + 4 * sq));
+            } else {
+                wsc[m] = gld((const uint16_t*)bp);
+                wnb[m] = (uint32_t)gld((const uint16_t*)(bp + 2 + 4 * sq)) |
+                         ((uint32_t)gld((const uint16_t*)(bp + 4 + 4 * sq)) << 16);
+            }
+        }
+    };
+    // value 8 sq + t of the block is nibble t of wnb (byte t / 2, low nibble for even t)
+    auto store_blk = [&]() {
+        if (sr < BM) {
+            const float xv[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
+            uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+            for (int t = 0; t < 8; t += 2)
+                split3_pair(xok ? xv[t] : 0.f, xok ? xv[t + 1] : 0.f, ph[t >> 1], pm[t >> 1], pl[t >> 1]);
+            *(u32x4*)&xs[0][sr][8 * sq] = u32x4{ph[0], ph[1], ph[2], ph[3]};
+            *(u32x4*)&xs[1][sr][8 * sq] = u32x4{pm[0], pm[1], pm[2], pm[3]};
+            *(u32x4*)&xs[2][sr][8 * sq] = u32x4{pl[0], pl[1], pl[2], pl[3]};
+        }
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            // q - 7 as bf16, a small integer (exact): nibble t of wnb is byte
+            // t / 2 of lo (even t) or hi (odd t)
+            const uint32_t lo = and_opaque(wnb[m], 0x0F0F0F0Fu), hi = and_opaque(wnb[m] >> 4, 0x0F0F0F0Fu);
+            uint32_t pw[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float f0 = (float)((lo >> (8 * j)) & 0xFF) - 7.0f, f1 = (float)((hi >> (8 * j)) & 0xFF) - 7.0f;
+                pw[j] = wok ? hi16_pair(__float_as_uint(f0), __float_as_uint(f1)) : 0u;
+            }
+            *(u32x4*)&ws[m][sr][8 * sq] = u32x4{pw[0], pw[1], pw[2], pw[3]};
+            if (sq == 0) {
+                const float sc = FMT == FMT_Q4_0F ? __uint_as_float(wsc[m]) : f16_to_f32((uint16_t)wsc[m]);
+                wsc_s[m][sr] = wok ? sc : 0.f;
+            }
+        }
+    };
+    const int wm = (wave >> 1) * 16 * MI, wn = (wave & 1) * 32;
+    const int fr = lane & 15, fk = lane >> 4;
+    f32x4m acc[NMAT][MI][2];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[m][i][j] = f32x4m{0.f, 0.f, 0.f, 0.f};
+    load_blk(0);
+    for (int b = 0; b < nb; b++) {
+        __syncthreads();                           // the previous block's fragments are read
+        store_blk();
+        __syncthreads();
+        load_blk(b + 1 < nb ? b + 1 : b);          // unconditional: the last block reloads itself
+        bf16x8 af[3][MI];
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+#pragma unroll
+            for (int i = 0; i < MI; i++) af[p][i] = *(const bf16x8*)&xs[p][wm + 16 * i + fr][8 * fk];
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const bf16x8 bf = *(const bf16x8*)&ws[m][wn + 16 * j + fr][8 * fk];
+                const float sc = wsc_s[m][wn + 16 * j + fr];
+#pragma unroll
+                for (int i = 0; i < MI; i++) {
+                    f32x4m d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[2][i], bf, f32x4m{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][i], bf, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][i], bf, d, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[m][i][j][e] = fmaf(sc, d[e], acc[m][i][j][e]);
+                }
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int row = m0 + wm + 16 * i + 4 * fk + e, col = n0 + wn + 16 * j + fr;
+                if (row >= a.M || col >= a.N) continue;
+                float* y = a.y + (int64_t)row * a.N + col;
+                const float v0 = acc[0][i][j][e];
+                if (NMAT == 2) *y = silu_mul(v0, acc[NMAT - 1][i][j][e]);
+                else if (a.epi == RINA_EPI_ADD) *y = *y + v0;
+                else *y = v0;
+            }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -1441,18 +1600,20 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     ma.mpp = (ma.mt + 8 / best - 1) / (8 / best);
     ma.npp = (tiles + best - 1) / best;
     const dim3 g(8 * ma.mpp * ma.npp);
-#define MFMA_LAUNCH(F, NM) \
-    do { if (half) hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 32>), g, dim3(256), 0, st, ma); \
-         else hipLaunchKernelGGL((gemm_mfma_kernel<F, NM, 64>), g, dim3(256), 0, st, ma); } while (0)
+#define MFMA_LAUNCH(KN, F, NM) \
+    do { if (half) hipLaunchKernelGGL((KN<F, NM, 32>), g, dim3(256), 0, st, ma); \
+         else hipLaunchKernelGGL((KN<F, NM, 64>), g, dim3(256), 0, st, ma); } while (0)
+    // Q4 weights: bf16 matrix cores on exact three-part splits of x; Q2_K
+    // (weights d sc q - dmin m, not small integers): fp32 matrix cores
     if (qt == RINA_QT_Q4_0F) {
-        if (two) MFMA_LAUNCH(FMT_Q4_0F, 2);
-        else MFMA_LAUNCH(FMT_Q4_0F, 1);
+        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 2);
+        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 1);
     } else if (qt == RINA_QT_GGML_Q2_K) {
-        if (two) MFMA_LAUNCH(FMT_Q2_K, 2);
-        else MFMA_LAUNCH(FMT_Q2_K, 1);
+        if (two) MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 2);
+        else MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 1);
     } else {
-        if (two) MFMA_LAUNCH(FMT_Q4_0, 2);
-        else MFMA_LAUNCH(FMT_Q4_0, 1);
+        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 2);
+        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 1);
     }
 #undef MFMA_LAUNCH
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
