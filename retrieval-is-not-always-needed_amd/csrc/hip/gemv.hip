@@ -1160,18 +1160,22 @@ __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& ph, ui
 // three MFMAs (l, m, h into one accumulator), then one fp32 fma with the
 // block scale of the tile column.  Tiles, XCD order, segments, staging
 // (thread t: row t / 4, values 8 (t % 4) .. + 7 of the block) and epilogues
-// as gemm_mfma_kernel.  LDS rows of 40 bf16 keep the 16-byte fragment reads
-// of 16 rows on distinct banks.  Fragment layout (16x16x32): lane l holds
+// as gemm_mfma_kernel.  LDS rows of (32 * KB + 8) bf16 keep the 16-byte
+// fragment reads of 16 rows on distinct banks.  Fragment layout (16x16x32): lane l holds
 // A[l % 16][8 (l / 16) .. + 7], B[8 (l / 16) .. + 7][l % 16] and
 // D[4 (l / 16) + e][l % 16].
 template <int FMT, int NMAT, int BM>
 __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
     constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
     constexpr int MI = BM / 32;                    // MFMA tiles per wave along M
-    constexpr int LD = 40;
+    // 32-value blocks per LDS stage: two halve the barriers of the one-matrix
+    // launches; the paired SwiGLU tile keeps one (its registers would cut
+    // occupancy to 3 waves per SIMD)
+    constexpr int KB = NMAT == 2 ? 1 : 4;
+    constexpr int LD = 32 * KB + 8;
     __shared__ __align__(16) uint16_t xs[3][BM][LD];
     __shared__ __align__(16) uint16_t ws[NMAT][64][LD];
-    __shared__ float wsc_s[NMAT][64];
+    __shared__ float wsc_s[NMAT][KB][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
@@ -1185,57 +1189,74 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
     a.N = sg == 0 ? ma.N[0] : sg == 1 ? ma.N[1] : ma.N[2];
     const int tb = sg == 0 ? ma.t0[0] : sg == 1 ? ma.t0[1] : ma.t0[2];
     const int m0 = by * BM, n0 = (bx - tb) * 64;
-    const int nb = a.K / 32;
+    const int nb = a.K / 32, nst = (nb + KB - 1) / KB;
     const int sr = tid >> 2, sq = tid & 3;
     const bool xok = sr < BM && m0 + sr < a.M, wok = n0 + sr < a.N;
     const float* xrow = a.x + (int64_t)(xok ? m0 + sr : 0) * a.K + 8 * sq;
     const int64_t wrow = (int64_t)(wok ? n0 + sr : 0) * nb * BB;
-    f32x4 xr0, xr1;
-    uint32_t wsc[NMAT], wnb[NMAT];
-    auto load_blk = [&](int b) {
-        const f32x4* xp = (const f32x4*)(xrow + 32 * b);
-        xr0 = gld(xp);
-        xr1 = gld(xp + 1);
+    // register sets holding one stage's loads each; with two, a stage's loads
+    // are issued two stages before they are stored to LDS
+    struct Stage {
+        f32x4 xr[KB][2];
+        uint32_t wsc[KB][NMAT], wnb[KB][NMAT];
+    };
+    Stage r0, r1;
+    // stage st: blocks KB st .. KB st + KB - 1 (past nb: block nb - 1 again,
+    // stored as zeros)
+    auto load_stage = [&](Stage& r, int st) {
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-            const uint8_t* bp = (m ? a.w2 : a.w) + wrow + (int64_t)b * BB;
-            if constexpr (FMT == FMT_Q4_0F) {
-                wsc[m] = gld((const uint32_t*)bp);
-                wnb[m] = gld((const uint32_t*)(bp + 4 + 4 * sq));
-            } else {
-                wsc[m] = gld((const uint16_t*)bp);
-                wnb[m] = (uint32_t)gld((const uint16_t*)(bp + 2 + 4 * sq)) |
-                         ((uint32_t)gld((const uint16_t*)(bp + 4 + 4 * sq)) << 16);
+        for (int kb = 0; kb < KB; kb++) {
+            const int b = min(KB * st + kb, nb - 1);
+            const f32x4* xp = (const f32x4*)(xrow + 32 * b);
+            r.xr[kb][0] = gld(xp);
+            r.xr[kb][1] = gld(xp + 1);
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                const uint8_t* bp = (m ? a.w2 : a.w) + wrow + (int64_t)b * BB;
+                if constexpr (FMT == FMT_Q4_0F) {
+                    r.wsc[kb][m] = gld((const uint32_t*)bp);
+                    r.wnb[kb][m] = gld((const uint32_t*)(bp + 4 + 4 * sq));
+                } else {
+                    r.wsc[kb][m] = gld((const uint16_t*)bp);
+                    r.wnb[kb][m] = (uint32_t)gld((const uint16_t*)(bp + 2 + 4 * sq)) |
+                                 ((uint32_t)gld((const uint16_t*)(bp + 4 + 4 * sq)) << 16);
+                }
             }
         }
     };
-    // value 8 sq + t of the block is nibble t of wnb (byte t / 2, low nibble for even t)
-    auto store_blk = [&]() {
-        if (sr < BM) {
-            const float xv[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
-            uint32_t ph[4], pm[4], pl[4];
+    // value 8 sq + t of a block is nibble t of wnb (byte t / 2, low nibble for even t)
+    auto store_stage = [&](const Stage& r, int st) {
 #pragma unroll
-            for (int t = 0; t < 8; t += 2)
-                split3_pair(xok ? xv[t] : 0.f, xok ? xv[t + 1] : 0.f, ph[t >> 1], pm[t >> 1], pl[t >> 1]);
-            *(u32x4*)&xs[0][sr][8 * sq] = u32x4{ph[0], ph[1], ph[2], ph[3]};
-            *(u32x4*)&xs[1][sr][8 * sq] = u32x4{pm[0], pm[1], pm[2], pm[3]};
-            *(u32x4*)&xs[2][sr][8 * sq] = u32x4{pl[0], pl[1], pl[2], pl[3]};
-        }
+        for (int kb = 0; kb < KB; kb++) {
+            const bool bok = KB * st + kb < nb;
+            if (sr < BM) {
+                const float xv[8] = {r.xr[kb][0].x, r.xr[kb][0].y, r.xr[kb][0].z, r.xr[kb][0].w,
+                                     r.xr[kb][1].x, r.xr[kb][1].y, r.xr[kb][1].z, r.xr[kb][1].w};
+                const bool on = xok && bok;
+                uint32_t ph[4], pm[4], pl[4];
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-            // q - 7 as bf16, a small integer (exact): nibble t of wnb is byte
-            // t / 2 of lo (even t) or hi (odd t)
-            const uint32_t lo = and_opaque(wnb[m], 0x0F0F0F0Fu), hi = and_opaque(wnb[m] >> 4, 0x0F0F0F0Fu);
-            uint32_t pw[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float f0 = (float)((lo >> (8 * j)) & 0xFF) - 7.0f, f1 = (float)((hi >> (8 * j)) & 0xFF) - 7.0f;
-                pw[j] = wok ? hi16_pair(__float_as_uint(f0), __float_as_uint(f1)) : 0u;
+                for (int t = 0; t < 8; t += 2)
+                    split3_pair(on ? xv[t] : 0.f, on ? xv[t + 1] : 0.f, ph[t >> 1], pm[t >> 1], pl[t >> 1]);
+                *(u32x4*)&xs[0][sr][32 * kb + 8 * sq] = u32x4{ph[0], ph[1], ph[2], ph[3]};
+                *(u32x4*)&xs[1][sr][32 * kb + 8 * sq] = u32x4{pm[0], pm[1], pm[2], pm[3]};
+                *(u32x4*)&xs[2][sr][32 * kb + 8 * sq] = u32x4{pl[0], pl[1], pl[2], pl[3]};
             }
-            *(u32x4*)&ws[m][sr][8 * sq] = u32x4{pw[0], pw[1], pw[2], pw[3]};
-            if (sq == 0) {
-                const float sc = FMT == FMT_Q4_0F ? __uint_as_float(wsc[m]) : f16_to_f32((uint16_t)wsc[m]);
-                wsc_s[m][sr] = wok ? sc : 0.f;
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                // q - 7 as bf16, a small integer (exact): nibble t of wnb is
+                // byte t / 2 of lo (even t) or hi (odd t)
+                const uint32_t lo = and_opaque(r.wnb[kb][m], 0x0F0F0F0Fu), hi = and_opaque(r.wnb[kb][m] >> 4, 0x0F0F0F0Fu);
+                uint32_t pw[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float f0 = (float)((lo >> (8 * j)) & 0xFF) - 7.0f, f1 = (float)((hi >> (8 * j)) & 0xFF) - 7.0f;
+                    pw[j] = wok && bok ? hi16_pair(__float_as_uint(f0), __float_as_uint(f1)) : 0u;
+                }
+                *(u32x4*)&ws[m][sr][32 * kb + 8 * sq] = u32x4{pw[0], pw[1], pw[2], pw[3]};
+                if (sq == 0) {
+                    const float sc = FMT == FMT_Q4_0F ? __uint_as_float(r.wsc[kb][m]) : f16_to_f32((uint16_t)r.wsc[kb][m]);
+                    wsc_s[m][kb][sr] = wok && bok ? sc : 0.f;
+                }
             }
         }
     };
@@ -1248,32 +1269,58 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
         for (int i = 0; i < MI; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++) acc[m][i][j] = f32x4m{0.f, 0.f, 0.f, 0.f};
-    load_blk(0);
-    for (int b = 0; b < nb; b++) {
-        __syncthreads();                           // the previous block's fragments are read
-        store_blk();
-        __syncthreads();
-        load_blk(b + 1 < nb ? b + 1 : b);          // unconditional: the last block reloads itself
-        bf16x8 af[3][MI];
+    auto compute_stage = [&]() {
 #pragma unroll
-        for (int p = 0; p < 3; p++)
+        for (int kb = 0; kb < KB; kb++) {
+            bf16x8 af[3][MI];
 #pragma unroll
-            for (int i = 0; i < MI; i++) af[p][i] = *(const bf16x8*)&xs[p][wm + 16 * i + fr][8 * fk];
+            for (int p = 0; p < 3; p++)
 #pragma unroll
-        for (int m = 0; m < NMAT; m++)
+                for (int i = 0; i < MI; i++) af[p][i] = *(const bf16x8*)&xs[p][wm + 16 * i + fr][32 * kb + 8 * fk];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const bf16x8 bf = *(const bf16x8*)&ws[m][wn + 16 * j + fr][8 * fk];
-                const float sc = wsc_s[m][wn + 16 * j + fr];
+            for (int m = 0; m < NMAT; m++)
 #pragma unroll
-                for (int i = 0; i < MI; i++) {
-                    f32x4m d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[2][i], bf, f32x4m{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][i], bf, d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][i], bf, d, 0, 0, 0);
+                for (int j = 0; j < 2; j++) {
+                    const bf16x8 bf = *(const bf16x8*)&ws[m][wn + 16 * j + fr][32 * kb + 8 * fk];
+                    const float sc = wsc_s[m][kb][wn + 16 * j + fr];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[m][i][j][e] = fmaf(sc, d[e], acc[m][i][j][e]);
+                    for (int i = 0; i < MI; i++) {
+                        f32x4m d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[2][i], bf, f32x4m{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[1][i], bf, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[0][i], bf, d, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[m][i][j][e] = fmaf(sc, d[e], acc[m][i][j][e]);
+                    }
                 }
-            }
+        }
+    };
+    load_stage(r0, 0);
+    if constexpr (NMAT == 1) {
+        // stages in pairs, unconditionally: with nst odd the last pair's
+        // second stage lies past nb, is stored as zeros and adds sc 0 times d 0
+        load_stage(r1, 1);
+        for (int st = 0; st < nst; st += 2) {
+            __syncthreads();                       // the previous stage's fragments are read
+            store_stage(r0, st);
+            __syncthreads();
+            load_stage(r0, st + 2);
+            compute_stage();
+            __syncthreads();
+            store_stage(r1, st + 1);
+            __syncthreads();
+            load_stage(r1, st + 3);
+            compute_stage();
+        }
+    } else {
+        // the paired SwiGLU tile keeps one register set (a second would cut
+        // occupancy from 5 to 3 waves per SIMD, which costs it more)
+        for (int st = 0; st < nst; st++) {
+            __syncthreads();
+            store_stage(r0, st);
+            __syncthreads();
+            load_stage(r0, st + 1);                // past the end: block nb - 1, not stored
+            compute_stage();
+        }
     }
 #pragma unroll
     for (int i = 0; i < MI; i++)
