@@ -363,8 +363,8 @@ def main():
     prefill = {"prompt": args.prompt, "ms": round(pre_ms[-1], 3),
                "tokens_per_s": round(args.prompt / (pre_ms[-1] / 1e3), 1),
                "note": "Q4 linears on v_mfma_f32_16x16x32_bf16 with x split exactly into three bf16 parts "
-                       "(fp32 products, fp32 sums); prompt attention "
-                       "from position 0 in 64-position blocks (one softmax rescale per block)"}
+                       "(fp32 products, fp32 sums); prompt attention from position 0 on "
+                       "v_mfma_f32_16x16x4f32 in 64-position blocks (one softmax rescale per block)"}
     log("prefill: %d tokens in %.2f ms (%.0f tok/s)" % (args.prompt, pre_ms[-1], prefill["tokens_per_s"]))
     # the GPU's K/V rows of the prompt, so the CPU baseline decodes at the
     # GPU's positions from the same cache

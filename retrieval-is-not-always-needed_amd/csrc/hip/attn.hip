@@ -663,6 +663,130 @@ __global__ __launch_bounds__(64) void attn_prompt_kernel(AttnArgs a) {
     for (int i = 0; i < nq; i++) a.out[((int64_t)(t0 + i) * a.H + h) * DH + lane] = s_o[i][lane] / s_l[i];
 }
 
+// The same prompt attention on the matrix cores (v_mfma_f32_16x16x4f32: fp32
+// products, fp32 sums), for query heads in groups of 4 that share a KV head
+// (H / Hkv a multiple of 4).  A workgroup of 4 waves takes one group and 16
+// query rows, wave w query head 4 blockIdx.x + w; the 64-position K and V
+// blocks are staged once per workgroup in LDS (the next block's loads in
+// registers while the current one is multiplied).  Per block a wave forms
+// S^T = K Q^T (4 tiles of 16 keys x 16 rows, 16 steps of 4 dims each: lane
+// l's A value is key l % 16 of the tile at dim 16 (l / 16) + step, its B
+// value the query row l % 16 at that dim), so a lane holds 16 scores of
+// one query row (keys 16 kt + 4 (l / 16) + e), the row maximum and sum take
+// two cross-lane steps, and those scores are directly the B operand of
+// O^T += V^T P^T (step 4 kt + e uses key 16 kt + 4 (l / 16) + e; A value:
+// dim 4 (l % 16) + dt of that key for output tile dt).  A lane ends with
+// dims 16 (l / 16) .. + 15 of its row.  Base-2 softmax units and the
+// per-block rescale as in attn_prompt_kernel.
+__global__ __launch_bounds__(256) void attn_prompt_mfma_kernel(AttnArgs a) {
+    constexpr int DH = 64, LDK = DH + 4;
+    __shared__ __align__(16) float s_k[64][LDK];
+    __shared__ __align__(16) float s_v[64][LDK];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ntile = (a.T + kPromptRows - 1) / kPromptRows;
+    const int t0 = (ntile - 1 - (int)blockIdx.y) * kPromptRows;   // longest row tiles first
+    const int h = 4 * (int)blockIdx.x + w;
+    const int kvh = 4 * (int)blockIdx.x / (a.H / a.Hkv);
+    const int kvd = a.Hkv * DH;
+    const int tmax = min(t0 + kPromptRows, a.T) - 1;
+    const int fr = lane & 15, g = lane >> 4;
+    const int row = t0 + fr;
+    const float qsc = a.scale * 1.44269504088896341f;
+    float qv[16];                                   // row fr (clamped), dims 16 g .. 16 g + 15
+    {
+        const f32x4* qp = (const f32x4*)(a.q + ((int64_t)min(row, a.T - 1) * a.H + h) * DH + 16 * g);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f32x4 v = gld(qp + i);
+            qv[4 * i] = v.x * qsc; qv[4 * i + 1] = v.y * qsc; qv[4 * i + 2] = v.z * qsc; qv[4 * i + 3] = v.w * qsc;
+        }
+    }
+    // staging: thread tid moves dims 16 (tid % 4) .. + 15 of key j0 + tid / 4
+    // (clamped to tmax: such keys are masked)
+    const int sk = tid >> 2, sq = tid & 3;
+    f32x4 kr[4], vr[4];
+    auto load_blk = [&](int j0) {
+        const int64_t off = (int64_t)min(j0 + sk, tmax) * kvd + kvh * DH + 16 * sq;
+        const f32x4* kp = (const f32x4*)(a.kcur + off);
+        const f32x4* vp = (const f32x4*)(a.vcur + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            kr[i] = gld(kp + i);
+            vr[i] = gld(vp + i);
+        }
+    };
+    f32x4 o[4];                                     // O^T tile dt: dims 16 g + 4 e + dt of row fr
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    load_blk(0);
+    for (int j0 = 0; j0 <= tmax; j0 += 64) {
+        __syncthreads();                            // the previous block's operands are read
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            *(f32x4*)&s_k[sk][16 * sq + 4 * i] = kr[i];
+            *(f32x4*)&s_v[sk][16 * sq + 4 * i] = vr[i];
+        }
+        __syncthreads();
+        load_blk(j0 + 64 <= tmax ? j0 + 64 : j0);   // unconditional: the last block reloads itself
+        f32x4 s[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            f32x4 kv[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) kv[kt] = *(const f32x4*)&s_k[16 * kt + fr][16 * g + 4 * q4];
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kt][c], qv[4 * q4 + c], s[kt], 0, 0, 0);
+        }
+        // causal mask, then the row's maximum over the lanes l % 16 == fr
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (j0 + 16 * kt + 4 * g + e > row) s[kt][e] = -INFINITY;
+                mx = fmaxf(mx, s[kt][e]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);              // finite: key j0 <= every row of the tile
+        const float al = __builtin_amdgcn_exp2f(m - mn);
+        float ps = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                s[kt][e] = __builtin_amdgcn_exp2f(s[kt][e] - mn);
+                ps += s[kt][e];
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = fmaf(l, al, ps);
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[dt] *= al;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const f32x4 vv = *(const f32x4*)&s_v[16 * kt + 4 * g + e][4 * fr];
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[dt], s[kt][e], o[dt], 0, 0, 0);
+            }
+    }
+    if (row < a.T) {
+        f32x4* op = (f32x4*)(a.out + ((int64_t)row * a.H + h) * DH + 16 * g);
+#pragma unroll
+        for (int e = 0; e < 4; e++) gst(op + e, f32x4{o[0][e] / l, o[1][e] / l, o[2][e] / l, o[3][e] / l});
+    }
+}
+
 __global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs a, int kf, int vf) {
     const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
@@ -824,7 +948,11 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
     a.scale = 1.0f / sqrtf((float)dh);
     // a prompt from position 0 reads only the current rows
     if (T > 1 && !d_pos && start_pos == 0 && dh == 64 && ((uintptr_t)kcur % 16 == 0)) {
-        hipLaunchKernelGGL(attn_prompt_kernel, dim3(H, (T + kPromptRows - 1) / kPromptRows), dim3(64), 0, st, a);
+        const int ntile = (T + kPromptRows - 1) / kPromptRows;
+        if (rep % 4 == 0 && ((uintptr_t)q | (uintptr_t)vcur | (uintptr_t)out) % 16 == 0)
+            hipLaunchKernelGGL(attn_prompt_mfma_kernel, dim3(H / 4, ntile), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL(attn_prompt_kernel, dim3(H, ntile), dim3(64), 0, st, a);
         RINA_LAUNCH_CHECK();
         return RINA_OK;
     }

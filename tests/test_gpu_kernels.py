@@ -370,10 +370,13 @@ def test_attention_multi_row(rina, orc, mode, P, T):
     assert_close(got, ref, what="rows mode %d P %d T %d" % (mode, P, T))
 
 
-@pytest.mark.parametrize("T,H,Hkv", [(100, 32, 8), (300, 32, 8), (129, 10, 5), (64, 8, 8)])
+@pytest.mark.parametrize("T,H,Hkv", [(100, 32, 8), (300, 32, 8), (512, 32, 8), (17, 8, 2), (250, 16, 2),
+                                     (129, 10, 5), (64, 8, 8)])
 def test_attention_prompt_from_zero(rina, orc, T, H, Hkv):
-    """Prompt rows from position 0 (the block-softmax prompt kernel): several
-    64-position blocks, ragged row groups, causal against the oracle."""
+    """Prompt rows from position 0: several 64-position blocks, ragged row
+    groups, causal against the oracle.  H / Hkv a multiple of 4 takes the
+    matrix-core kernel (config 2's 512 x 32 / 8 among them), the others the
+    one-wave block kernel."""
     got, ref = attention_case(rina, orc, 0, 0, T, H=H, Hkv=Hkv)
     assert_close(got, ref, what="prompt T %d H %d/%d" % (T, H, Hkv))
 
