@@ -22,6 +22,7 @@
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWG = 256;
@@ -1190,14 +1191,19 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
     const int tb = sg == 0 ? ma.t0[0] : sg == 1 ? ma.t0[1] : ma.t0[2];
     const int m0 = by * BM, n0 = (bx - tb) * 64;
     const int nb = a.K / 32, nst = (nb + KB - 1) / KB;
+    // x staging: every thread splits XV values of one row per block (XT
+    // threads per row), so the split work is spread over all four waves;
+    // weight staging: thread tid takes values 8 sq .. 8 sq + 7 of column sr
+    constexpr int XV = BM / 8, XT = 32 / XV;
+    const int xsr = tid / XT, xsq = tid % XT;
     const int sr = tid >> 2, sq = tid & 3;
-    const bool xok = sr < BM && m0 + sr < a.M, wok = n0 + sr < a.N;
-    const float* xrow = a.x + (int64_t)(xok ? m0 + sr : 0) * a.K + 8 * sq;
+    const bool xok = m0 + xsr < a.M, wok = n0 + sr < a.N;
+    const float* xrow = a.x + (int64_t)(xok ? m0 + xsr : 0) * a.K + XV * xsq;
     const int64_t wrow = (int64_t)(wok ? n0 + sr : 0) * nb * BB;
     // register sets holding one stage's loads each; with two, a stage's loads
     // are issued two stages before they are stored to LDS
     struct Stage {
-        f32x4 xr[KB][2];
+        f32x4 xr[KB][XV / 4];
         uint32_t wsc[KB][NMAT], wnb[KB][NMAT];
     };
     Stage r0, r1;
@@ -1208,8 +1214,8 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
         for (int kb = 0; kb < KB; kb++) {
             const int b = min(KB * st + kb, nb - 1);
             const f32x4* xp = (const f32x4*)(xrow + 32 * b);
-            r.xr[kb][0] = gld(xp);
-            r.xr[kb][1] = gld(xp + 1);
+#pragma unroll
+            for (int v = 0; v < XV / 4; v++) r.xr[kb][v] = gld(xp + v);
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
                 const uint8_t* bp = (m ? a.w2 : a.w) + wrow + (int64_t)b * BB;
@@ -1229,17 +1235,30 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) {
             const bool bok = KB * st + kb < nb;
-            if (sr < BM) {
-                const float xv[8] = {r.xr[kb][0].x, r.xr[kb][0].y, r.xr[kb][0].z, r.xr[kb][0].w,
-                                     r.xr[kb][1].x, r.xr[kb][1].y, r.xr[kb][1].z, r.xr[kb][1].w};
-                const bool on = xok && bok;
-                uint32_t ph[4], pm[4], pl[4];
+            {
+                float xv[XV];
 #pragma unroll
-                for (int t = 0; t < 8; t += 2)
+                for (int v = 0; v < XV / 4; v++) {
+                    xv[4 * v] = r.xr[kb][v].x; xv[4 * v + 1] = r.xr[kb][v].y;
+                    xv[4 * v + 2] = r.xr[kb][v].z; xv[4 * v + 3] = r.xr[kb][v].w;
+                }
+                const bool on = xok && bok;
+                uint32_t ph[XV / 2], pm[XV / 2], pl[XV / 2];
+#pragma unroll
+                for (int t = 0; t < XV; t += 2)
                     split3_pair(on ? xv[t] : 0.f, on ? xv[t + 1] : 0.f, ph[t >> 1], pm[t >> 1], pl[t >> 1]);
-                *(u32x4*)&xs[0][sr][32 * kb + 8 * sq] = u32x4{ph[0], ph[1], ph[2], ph[3]};
-                *(u32x4*)&xs[1][sr][32 * kb + 8 * sq] = u32x4{pm[0], pm[1], pm[2], pm[3]};
-                *(u32x4*)&xs[2][sr][32 * kb + 8 * sq] = u32x4{pl[0], pl[1], pl[2], pl[3]};
+                uint16_t* d0 = &xs[0][xsr][32 * kb + XV * xsq];
+                uint16_t* d1 = &xs[1][xsr][32 * kb + XV * xsq];
+                uint16_t* d2 = &xs[2][xsr][32 * kb + XV * xsq];
+                if constexpr (XV == 8) {
+                    *(u32x4*)d0 = u32x4{ph[0], ph[1], ph[2], ph[3]};
+                    *(u32x4*)d1 = u32x4{pm[0], pm[1], pm[2], pm[3]};
+                    *(u32x4*)d2 = u32x4{pl[0], pl[1], pl[2], pl[3]};
+                } else {
+                    *(u32x2*)d0 = u32x2{ph[0], ph[1]};
+                    *(u32x2*)d1 = u32x2{pm[0], pm[1]};
+                    *(u32x2*)d2 = u32x2{pl[0], pl[1]};
+                }
             }
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
