@@ -130,13 +130,15 @@ __device__ __forceinline__ void rope8(int dim0, const float (&own)[8], const flo
     }
 }
 
-template <int KF, int VF, int HG, int REP, bool FUSED>
-__global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
+template <int KF, int VF, int HG, int REP, bool FUSED, int QS>
+__global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
     constexpr int DH = 64;
     constexpr int LPP = 8 * HG;          // lanes per position record
     constexpr int PPW = 64 / LPP;        // positions per wave step (slots)
     constexpr int GS = 4 * PPW;          // positions per workgroup step
     constexpr int QH = HG * REP;         // query heads in the group
+    constexpr int RL = REP / QS;         // query heads of a KV head per wave: QS wave sets
+                                         // (waves 4 q .. 4 q + 3) share the positions
     constexpr int NS = 4 * PPW;          // softmax slots of the workgroup
     __shared__ __align__(16) float s_o[NS][QH][DH];
     __shared__ __align__(16) float s_m[QH][NS];
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     __shared__ float s_l[QH][NS], s_M[QH];
     __shared__ float s_k[FUSED ? HG * DH : 1], s_v[FUSED ? HG * DH : 1];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, wq = tid >> 8;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
     if (pos0 < 0 || pos0 >= a.max_seq) return;     // capacity guard (host checks host-known positions)
     const int L = pos0 + 1;
@@ -173,13 +175,13 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     // loads under a branch can leave register copies at the join that wait
     // for them there, before the cache loads are issued.  The current row is
     // read by the workgroup that holds it only (a uniform branch).
-    float qraw[REP][8], qpair[REP][8], tc[8], ts[8];
+    float qraw[RL][8], qpair[RL][8], tc[8], ts[8];
     float kown[8], kpair[8], kc8[8], ks8[8], vcur[8];
     const bool qrope = FUSED && a.qc, krope = FUSED && a.kc;
     const int64_t toff = (int64_t)pos0 * 32 + (dim0 & 31);
 #pragma unroll
-    for (int r = 0; r < REP; r++) {
-        const float* qh = a.q + (int64_t)(kvh * REP + r) * DH;
+    for (int r = 0; r < RL; r++) {
+        const float* qh = a.q + (int64_t)(kvh * REP + wq * RL + r) * DH;
         ld8f(qh + dim0, qraw[r]);
         if constexpr (FUSED) ld8f(qh + (dim0 ^ 32), qpair[r]);
     }
@@ -214,10 +216,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
 
     // scores in base-2 units: log2 e and the scale folded into q, so the
     // softmax weights are hardware exp2 values
-    float qv[REP][8];
+    float qv[RL][8];
     const float qsc = a.scale * 1.44269504088896341f;
 #pragma unroll
-    for (int r = 0; r < REP; r++) {
+    for (int r = 0; r < RL; r++) {
         if (qrope) rope8(dim0, qraw[r], qpair[r], tc, ts, qv[r]);
         else {
 #pragma unroll
@@ -233,9 +235,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
         for (int i = 0; i < 8; i++) kcur[i] = kown[i];
     }
 
-    float ov[REP][8], m_run[REP], l_run[REP];
+    float ov[RL][8], m_run[RL], l_run[RL];
 #pragma unroll
-    for (int r = 0; r < REP; r++) {
+    for (int r = 0; r < RL; r++) {
         m_run[r] = -INFINITY;
         l_run[r] = 0.f;
 #pragma unroll
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
             vx[i] = cur ? vcur[i] : vv[i];
         }
 #pragma unroll
-        for (int r = 0; r < REP; r++) {
+        for (int r = 0; r < RL; r++) {
             float p = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) p = fmaf(qv[r][i], kx[i], p);
@@ -292,18 +294,18 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
     // output dim sums the weighted slots
     if ((lig & 7) == 0) {
 #pragma unroll
-        for (int r = 0; r < REP; r++) {
-            s_m[kvl * REP + r][wslot] = m_run[r];
-            s_l[kvl * REP + r][wslot] = l_run[r];
+        for (int r = 0; r < RL; r++) {
+            s_m[kvl * REP + wq * RL + r][wslot] = m_run[r];
+            s_l[kvl * REP + wq * RL + r][wslot] = l_run[r];
         }
     }
 #pragma unroll
-    for (int r = 0; r < REP; r++) {
-        f32x4* dst = (f32x4*)&s_o[wslot][kvl * REP + r][dim0];
+    for (int r = 0; r < RL; r++) {
+        f32x4* dst = (f32x4*)&s_o[wslot][kvl * REP + wq * RL + r][dim0];
         dst[0] = f32x4{ov[r][0], ov[r][1], ov[r][2], ov[r][3]};
         dst[1] = f32x4{ov[r][4], ov[r][5], ov[r][6], ov[r][7]};
     }
-    if (FUSED && has_cur && wave == 0 && lane < LPP) {
+    if (FUSED && has_cur && tid < LPP) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             s_k[kvl * DH + dim0 + i] = kcur[i];
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(SplitArgs a) {
         if (sl == 0) s_M[qh] = M;
     }
     __syncthreads();
-    for (int e = tid; e < QH * DH; e += 256) {
+    for (int e = tid; e < QH * DH; e += 256 * QS) {
         const int qh = e / DH, d = e % DH;
         float o = 0.f;
 #pragma unroll
@@ -868,11 +870,13 @@ int launch_split(SplitArgs a, int rep, size_t ws_bytes, void* ws, hipStream_t st
     // fetched into one L2 (the padding workgroups start past max_seq and
     // return at once)
     dim3 grid((nchunk + 7) / 8 * 8, a.Hkv / HG);
+    // an even head ratio splits a KV head's query heads over two wave sets
+    // (512 threads): half the per-lane chain per position, two waves per SIMD
     switch (rep) {
-        case 1: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 1, FUSED>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 2, FUSED>), grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 4, FUSED>), grid, dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 8, FUSED>), grid, dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 1, FUSED, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 2, FUSED, 2>), grid, dim3(512), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 4, FUSED, 2>), grid, dim3(512), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((attn_split_kernel<KF, VF, HG, 8, FUSED, 2>), grid, dim3(512), 0, st, a); break;
         default: return RINA_ERR_SHAPE;
     }
     if (hipGetLastError() != hipSuccess) return RINA_ERR_HIP;
