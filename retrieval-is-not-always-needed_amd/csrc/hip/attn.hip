@@ -11,7 +11,9 @@
 // kernel gives each workgroup a chunk of positions of HG KV heads (records of
 // a position are contiguous: position-major, heads inside); 8 lanes cover one
 // head's 64 dims (8 values per lane, dequantized in registers) and the REP
-// query heads of that KV head are reduced with DPP inside the 8-lane group.
+// query heads of that KV head are reduced with DPP inside the 8-lane group
+// (with an even REP, two sets of four waves take the same positions and half
+// the query heads each: a shorter chain per lane, two waves per SIMD).
 // Every 8-lane slot keeps its own online softmax over the positions it takes
 // (no barrier in the loop; the next positions' K/V loads are in flight while
 // the current ones are consumed); the slots merge through one LDS exchange,
