@@ -33,6 +33,38 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, float* ou
     for (int i = threadIdx.x; i < d; i += blockDim.x) orow[i] = row[i] * inv * w[i];
 }
 
+// The same RMSNorm for rows of d <= 1024 NV values (d % 4 == 0, 16-byte
+// aligned rows): each thread holds its NV float4 of the row in registers,
+// so the row is read once with 16-byte loads (prompt rows before a matmul).
+template <int NV>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(const float* x, float* out, const float* w, int d, float eps) {
+    __shared__ float red[4];
+    const f32x4* row = (const f32x4*)(x + (int64_t)blockIdx.x * d);
+    f32x4* orow = (f32x4*)(out + (int64_t)blockIdx.x * d);
+    const int n4 = d >> 2;
+    f32x4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int i = threadIdx.x + 256 * k;
+        v[k] = i < n4 ? gld(row + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+        ss = fmaf(v[k].x, v[k].x, ss);
+        ss = fmaf(v[k].y, v[k].y, ss);
+        ss = fmaf(v[k].z, v[k].z, ss);
+        ss = fmaf(v[k].w, v[k].w, ss);
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)d + eps);
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < n4) {
+            const f32x4 g = gld((const f32x4*)w + i);
+            gst(orow + i, f32x4{v[k].x * inv * g.x, v[k].y * inv * g.y, v[k].z * inv * g.z, v[k].w * inv * g.w});
+        }
+    }
+}
+
 // kernels/pytorch_ln_kernel.cu:4-35 (biased variance; two-pass form)
 __global__ __launch_bounds__(256) void layer_norm_kernel(const float* x, float* out, const float* w, int d, float eps) {
     __shared__ float red[4];
@@ -236,7 +268,14 @@ void* rina_scratch(size_t bytes, hipStream_t st) {
 
 extern "C" int rina_hip_rms_norm(const float* x, float* out, const float* w, int n, int d, float eps, void* stream) {
     if (!x || !out || !w || n < 1 || d < 1) return RINA_ERR_ARG;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(256), 0, as_stream(stream), x, out, w, d, eps);
+    const bool vec = d % 4 == 0 && d <= 8192 && (((uintptr_t)x | (uintptr_t)out | (uintptr_t)w) % 16) == 0;
+    const int nv = (d / 4 + 255) / 256;
+    hipStream_t st = as_stream(stream);
+    if (vec && nv <= 1) hipLaunchKernelGGL(rms_norm_vec_kernel<1>, dim3(n), dim3(256), 0, st, x, out, w, d, eps);
+    else if (vec && nv <= 2) hipLaunchKernelGGL(rms_norm_vec_kernel<2>, dim3(n), dim3(256), 0, st, x, out, w, d, eps);
+    else if (vec && nv <= 4) hipLaunchKernelGGL(rms_norm_vec_kernel<4>, dim3(n), dim3(256), 0, st, x, out, w, d, eps);
+    else if (vec) hipLaunchKernelGGL(rms_norm_vec_kernel<8>, dim3(n), dim3(256), 0, st, x, out, w, d, eps);
+    else hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(256), 0, st, x, out, w, d, eps);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }

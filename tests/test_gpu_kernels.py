@@ -587,6 +587,26 @@ def test_attention_pre_rope(rina, orc, mode):
     assert_close(got, ref, what="pre_rope mode %d" % mode)
 
 
+@pytest.mark.parametrize("d", [64, 102, 640, 2048, 3000, 8192, 10000])
+def test_rms_norm_shapes(rina, orc, d):
+    """rina_hip_rms_norm at row widths of each of its launch forms (16-byte
+    loads held in registers for d % 4 == 0 up to 8192, one to eight float4 per
+    thread; the scalar kernel for the others), out of place and in place."""
+    hip = rina.load_hip()
+    L = orc.load()
+    r = rng(d)
+    n = 5
+    x = (r.standard_normal((n, d)) * np.float32(3.0)).astype(np.float32)
+    w = r.uniform(0.5, 1.5, d).astype(np.float32)
+    ref = x.copy()
+    L.orc_rms_norm(ref.ctypes.data, w.ctypes.data, n, d, np.float32(1e-5))
+    xd, od, wd = dev(x), empty(n * d), dev(w)
+    ok(hip.rina_hip_rms_norm(xd.data_ptr(), od.data_ptr(), wd.data_ptr(), n, d, np.float32(1e-5), stream()))
+    assert_close(host(od).reshape(n, d), ref, what="rms_norm d %d" % d)
+    ok(hip.rina_hip_rms_norm(xd.data_ptr(), xd.data_ptr(), wd.data_ptr(), n, d, np.float32(1e-5), stream()))
+    assert_close(host(xd).reshape(n, d), ref, what="rms_norm in place d %d" % d)
+
+
 def test_glue(rina, orc):
     hip = rina.load_hip()
     L = orc.load()
