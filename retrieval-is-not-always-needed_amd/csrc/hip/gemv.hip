@@ -23,6 +23,7 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWG = 256;
@@ -1165,8 +1166,8 @@ __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& ph, ui
 // fragment reads of 16 rows on distinct banks.  Fragment layout (16x16x32): lane l holds
 // A[l % 16][8 (l / 16) .. + 7], B[8 (l / 16) .. + 7][l % 16] and
 // D[4 (l / 16) + e][l % 16].
-template <int FMT, int NMAT, int BM>
-__global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
+template <int FMT, int NMAT, int BM, int WN>
+__global__ __launch_bounds__(128 * WN) void gemm_bf3_kernel(MfmaArgs ma) {
     constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
     constexpr int MI = BM / 32;                    // MFMA tiles per wave along M
     // 32-value blocks per LDS stage: two halve the barriers of the one-matrix
@@ -1174,9 +1175,11 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
     // occupancy to 3 waves per SIMD)
     constexpr int KB = NMAT == 2 ? 1 : 4;
     constexpr int LD = 32 * KB + 8;
+    // WN waves across the tile's columns (32 each) and two down its rows
+    constexpr int BN = 32 * WN, NT = 128 * WN;
     __shared__ __align__(16) uint16_t xs[3][BM][LD];
-    __shared__ __align__(16) uint16_t ws[NMAT][64][LD];
-    __shared__ float wsc_s[NMAT][KB][64];
+    __shared__ __align__(16) uint16_t ws[NMAT][BN][LD];
+    __shared__ float wsc_s[NMAT][KB][BN];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
@@ -1189,12 +1192,12 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
     a.y = sg == 0 ? ma.y[0] : sg == 1 ? ma.y[1] : ma.y[2];
     a.N = sg == 0 ? ma.N[0] : sg == 1 ? ma.N[1] : ma.N[2];
     const int tb = sg == 0 ? ma.t0[0] : sg == 1 ? ma.t0[1] : ma.t0[2];
-    const int m0 = by * BM, n0 = (bx - tb) * 64;
+    const int m0 = by * BM, n0 = (bx - tb) * BN;
     const int nb = a.K / 32, nst = (nb + KB - 1) / KB;
     // x staging: every thread splits XV values of one row per block (XT
     // threads per row), so the split work is spread over all four waves;
     // weight staging: thread tid takes values 8 sq .. 8 sq + 7 of column sr
-    constexpr int XV = BM / 8, XT = 32 / XV;
+    constexpr int XV = BM * 32 / NT, XT = 32 / XV;
     const int xsr = tid / XT, xsq = tid % XT;
     const int sr = tid >> 2, sq = tid & 3;
     const bool xok = m0 + xsr < a.M, wok = n0 + sr < a.N;
@@ -1203,7 +1206,7 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
     // register sets holding one stage's loads each; with two, a stage's loads
     // are issued two stages before they are stored to LDS
     struct Stage {
-        f32x4 xr[KB][XV / 4];
+        float xr[KB][XV];
         uint32_t wsc[KB][NMAT], wnb[KB][NMAT];
     };
     Stage r0, r1;
@@ -1213,9 +1216,17 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) {
             const int b = min(KB * st + kb, nb - 1);
-            const f32x4* xp = (const f32x4*)(xrow + 32 * b);
+            if constexpr (XV >= 4) {
+                const f32x4* xp = (const f32x4*)(xrow + 32 * b);
 #pragma unroll
-            for (int v = 0; v < XV / 4; v++) r.xr[kb][v] = gld(xp + v);
+                for (int v = 0; v < XV / 4; v++) {
+                    const f32x4 t = gld(xp + v);
+                    r.xr[kb][4 * v] = t.x; r.xr[kb][4 * v + 1] = t.y; r.xr[kb][4 * v + 2] = t.z; r.xr[kb][4 * v + 3] = t.w;
+                }
+            } else {
+                const f32x2 t = gld((const f32x2*)(xrow + 32 * b));
+                r.xr[kb][0] = t.x; r.xr[kb][1] = t.y;
+            }
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
                 const uint8_t* bp = (m ? a.w2 : a.w) + wrow + (int64_t)b * BB;
@@ -1238,10 +1249,7 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
             {
                 float xv[XV];
 #pragma unroll
-                for (int v = 0; v < XV / 4; v++) {
-                    xv[4 * v] = r.xr[kb][v].x; xv[4 * v + 1] = r.xr[kb][v].y;
-                    xv[4 * v + 2] = r.xr[kb][v].z; xv[4 * v + 3] = r.xr[kb][v].w;
-                }
+                for (int v = 0; v < XV; v++) xv[v] = r.xr[kb][v];
                 const bool on = xok && bok;
                 uint32_t ph[XV / 2], pm[XV / 2], pl[XV / 2];
 #pragma unroll
@@ -1254,6 +1262,10 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
                     *(u32x4*)d0 = u32x4{ph[0], ph[1], ph[2], ph[3]};
                     *(u32x4*)d1 = u32x4{pm[0], pm[1], pm[2], pm[3]};
                     *(u32x4*)d2 = u32x4{pl[0], pl[1], pl[2], pl[3]};
+                } else if constexpr (XV == 2) {
+                    *(uint32_t*)d0 = ph[0];
+                    *(uint32_t*)d1 = pm[0];
+                    *(uint32_t*)d2 = pl[0];
                 } else {
                     *(u32x2*)d0 = u32x2{ph[0], ph[1]};
                     *(u32x2*)d1 = u32x2{pm[0], pm[1]};
@@ -1279,7 +1291,7 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(MfmaArgs ma) {
             }
         }
     };
-    const int wm = (wave >> 1) * 16 * MI, wn = (wave & 1) * 32;
+    const int wm = (wave / WN) * 16 * MI, wn = (wave % WN) * 32;
     const int fr = lane & 15, fk = lane >> 4;
     f32x4m acc[NMAT][MI][2];
 #pragma unroll
@@ -1640,6 +1652,18 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     ma.g = GemmArgs{(const uint8_t*)segs[0].weight, epi == RINA_EPI_SWIGLU ? (const uint8_t*)segs[0].weight2 : nullptr,
                     x, segs[0].out, M, segs[0].N, K, qt, epi};
     ma.nseg = nseg;
+    const bool two = epi == RINA_EPI_SWIGLU;
+    // one-matrix Q4 launches take 128-column tiles at 32 rows (8 waves: the
+    // x tile's split and staging then serve twice the columns)
+    auto count = [&](int bn) {
+        int t = 0;
+        for (int s = 0; s < nseg; s++) t += (segs[s].N + bn - 1) / bn;
+        return t;
+    };
+    const bool q4 = qt != RINA_QT_GGML_Q2_K;
+    bool half = (int64_t)count(64) * ((M + 63) / 64) < 2LL * rina_num_cus();   // 32-row tiles: more workgroups in flight
+    const bool wide = q4 && !two && half;
+    const int BN = wide ? 128 : 64;
     int tiles = 0;
     for (int s = 0; s < 3; s++) {
         const int ss = s < nseg ? s : 0;
@@ -1647,17 +1671,14 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
         ma.y[s] = segs[ss].out;
         ma.N[s] = segs[ss].N;
         ma.t0[s] = s < nseg ? tiles : 1 << 30;
-        if (s < nseg) tiles += (segs[s].N + 63) / 64;
+        if (s < nseg) tiles += (segs[s].N + BN - 1) / BN;
     }
-    const bool two = epi == RINA_EPI_SWIGLU;
-    const int64_t t64 = (int64_t)tiles * ((M + 63) / 64);
-    const bool half = t64 < 2LL * rina_num_cus();        // 32-row tiles: more workgroups in flight
     ma.mt = half ? (M + 31) / 32 : (M + 63) / 64;
     ma.nt = tiles;
     // bytes the 8 L2s fetch for a split of x into 8 / xb parts and the
     // weights into xb parts: xb * (x bytes) + (8 / xb) * (weight bytes)
     const double xbytes = 4.0 * M * K;
-    const double wbytes = (two ? 2.0 : 1.0) * 64.0 * tiles * K *
+    const double wbytes = (two ? 2.0 : 1.0) * BN * (double)tiles * K *
                           (qt == RINA_QT_Q4_0F ? 20.0 / 32 : qt == RINA_QT_GGML_Q2_K ? 84.0 / 256 : 18.0 / 32);
     int best = 1;
     for (int xb = 2; xb <= 8; xb *= 2)
@@ -1666,20 +1687,23 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     ma.mpp = (ma.mt + 8 / best - 1) / (8 / best);
     ma.npp = (tiles + best - 1) / best;
     const dim3 g(8 * ma.mpp * ma.npp);
-#define MFMA_LAUNCH(KN, F, NM) \
-    do { if (half) hipLaunchKernelGGL((KN<F, NM, 32>), g, dim3(256), 0, st, ma); \
-         else hipLaunchKernelGGL((KN<F, NM, 64>), g, dim3(256), 0, st, ma); } while (0)
+#define MFMA_LAUNCH(KN, F, NM, ...) \
+    do { if (half) hipLaunchKernelGGL((KN<F, NM, 32 __VA_ARGS__>), g, dim3(256), 0, st, ma); \
+         else hipLaunchKernelGGL((KN<F, NM, 64 __VA_ARGS__>), g, dim3(256), 0, st, ma); } while (0)
     // Q4 weights: bf16 matrix cores on exact three-part splits of x; Q2_K
     // (weights d sc q - dmin m, not small integers): fp32 matrix cores
-    if (qt == RINA_QT_Q4_0F) {
-        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 2);
-        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 1);
-    } else if (qt == RINA_QT_GGML_Q2_K) {
+    if (qt == RINA_QT_GGML_Q2_K) {
         if (two) MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 2);
         else MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 1);
+    } else if (wide) {
+        if (qt == RINA_QT_Q4_0F) hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0F, 1, 32, 4>), g, dim3(512), 0, st, ma);
+        else hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0, 1, 32, 4>), g, dim3(512), 0, st, ma);
+    } else if (qt == RINA_QT_Q4_0F) {
+        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 2, , 2);
+        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 1, , 2);
     } else {
-        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 2);
-        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 1);
+        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 2, , 2);
+        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 1, , 2);
     }
 #undef MFMA_LAUNCH
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
