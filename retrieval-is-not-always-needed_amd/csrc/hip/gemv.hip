@@ -1662,7 +1662,7 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     };
     const bool q4 = qt != RINA_QT_GGML_Q2_K;
     bool half = (int64_t)count(64) * ((M + 63) / 64) < 2LL * rina_num_cus();   // 32-row tiles: more workgroups in flight
-    const bool wide = q4 && !two && half;
+    const bool wide = q4 && (two ? !half : half);
     const int BN = wide ? 128 : 64;
     int tiles = 0;
     for (int s = 0; s < 3; s++) {
@@ -1695,6 +1695,9 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     if (qt == RINA_QT_GGML_Q2_K) {
         if (two) MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 2);
         else MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 1);
+    } else if (wide && two) {
+        if (qt == RINA_QT_Q4_0F) hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0F, 2, 64, 4>), g, dim3(512), 0, st, ma);
+        else hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0, 2, 64, 4>), g, dim3(512), 0, st, ma);
     } else if (wide) {
         if (qt == RINA_QT_Q4_0F) hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0F, 1, 32, 4>), g, dim3(512), 0, st, ma);
         else hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0, 1, 32, 4>), g, dim3(512), 0, st, ma);
