@@ -1170,10 +1170,11 @@ template <int FMT, int NMAT, int BM, int WN>
 __global__ __launch_bounds__(128 * WN) void gemm_bf3_kernel(MfmaArgs ma) {
     constexpr int BB = FMT == FMT_Q4_0F ? 20 : 18;
     constexpr int MI = BM / 32;                    // MFMA tiles per wave along M
-    // 32-value blocks per LDS stage: two halve the barriers of the one-matrix
-    // launches; the paired SwiGLU tile keeps one (its registers would cut
-    // occupancy to 3 waves per SIMD)
-    constexpr int KB = NMAT == 2 ? 1 : 4;
+    // 32-value blocks per LDS stage: four cut the barriers of the one-matrix
+    // launches (two at 64 rows, whose LDS would otherwise hold one
+    // workgroup per CU); the paired SwiGLU tile keeps one (its registers
+    // would cut occupancy to 3 waves per SIMD)
+    constexpr int KB = NMAT == 2 ? 1 : BM == 64 ? 2 : 4;
     constexpr int LD = 32 * KB + 8;
     // WN waves across the tile's columns (32 each) and two down its rows
     constexpr int BN = 32 * WN, NT = 128 * WN;
@@ -1653,16 +1654,15 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
                     x, segs[0].out, M, segs[0].N, K, qt, epi};
     ma.nseg = nseg;
     const bool two = epi == RINA_EPI_SWIGLU;
-    // one-matrix Q4 launches take 128-column tiles at 32 rows (8 waves: the
-    // x tile's split and staging then serve twice the columns)
+    // Q4 launches take 128-column tiles (8 waves: the x tile's split and
+    // staging then serve twice the columns); Q2_K 64-column ones
     auto count = [&](int bn) {
         int t = 0;
         for (int s = 0; s < nseg; s++) t += (segs[s].N + bn - 1) / bn;
         return t;
     };
-    const bool q4 = qt != RINA_QT_GGML_Q2_K;
-    bool half = (int64_t)count(64) * ((M + 63) / 64) < 2LL * rina_num_cus();   // 32-row tiles: more workgroups in flight
-    const bool wide = q4 && (two ? !half : half);
+    const bool wide = qt != RINA_QT_GGML_Q2_K;
+    const bool half = (int64_t)count(64) * ((M + 63) / 64) < 2LL * rina_num_cus();   // 32-row tiles: more workgroups in flight
     const int BN = wide ? 128 : 64;
     int tiles = 0;
     for (int s = 0; s < 3; s++) {
@@ -1687,27 +1687,25 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
     ma.mpp = (ma.mt + 8 / best - 1) / (8 / best);
     ma.npp = (tiles + best - 1) / best;
     const dim3 g(8 * ma.mpp * ma.npp);
-#define MFMA_LAUNCH(KN, F, NM, ...) \
-    do { if (half) hipLaunchKernelGGL((KN<F, NM, 32 __VA_ARGS__>), g, dim3(256), 0, st, ma); \
-         else hipLaunchKernelGGL((KN<F, NM, 64 __VA_ARGS__>), g, dim3(256), 0, st, ma); } while (0)
+#define MFMA_LAUNCH(KN, F, NM) \
+    do { if (half) hipLaunchKernelGGL((KN<F, NM, 32>), g, dim3(256), 0, st, ma); \
+         else hipLaunchKernelGGL((KN<F, NM, 64>), g, dim3(256), 0, st, ma); } while (0)
     // Q4 weights: bf16 matrix cores on exact three-part splits of x; Q2_K
     // (weights d sc q - dmin m, not small integers): fp32 matrix cores
+#define BF3_LAUNCH(F, NM) \
+    do { if (half) hipLaunchKernelGGL((gemm_bf3_kernel<F, NM, 32, 4>), g, dim3(512), 0, st, ma); \
+         else hipLaunchKernelGGL((gemm_bf3_kernel<F, NM, 64, 4>), g, dim3(512), 0, st, ma); } while (0)
     if (qt == RINA_QT_GGML_Q2_K) {
         if (two) MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 2);
         else MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 1);
-    } else if (wide && two) {
-        if (qt == RINA_QT_Q4_0F) hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0F, 2, 64, 4>), g, dim3(512), 0, st, ma);
-        else hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0, 2, 64, 4>), g, dim3(512), 0, st, ma);
-    } else if (wide) {
-        if (qt == RINA_QT_Q4_0F) hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0F, 1, 32, 4>), g, dim3(512), 0, st, ma);
-        else hipLaunchKernelGGL((gemm_bf3_kernel<FMT_Q4_0, 1, 32, 4>), g, dim3(512), 0, st, ma);
     } else if (qt == RINA_QT_Q4_0F) {
-        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 2, , 2);
-        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0F, 1, , 2);
+        if (two) BF3_LAUNCH(FMT_Q4_0F, 2);
+        else BF3_LAUNCH(FMT_Q4_0F, 1);
     } else {
-        if (two) MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 2, , 2);
-        else MFMA_LAUNCH(gemm_bf3_kernel, FMT_Q4_0, 1, , 2);
+        if (two) BF3_LAUNCH(FMT_Q4_0, 2);
+        else BF3_LAUNCH(FMT_Q4_0, 1);
     }
+#undef BF3_LAUNCH
 #undef MFMA_LAUNCH
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
