@@ -1160,9 +1160,10 @@ __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& ph, ui
 // v_mfma_f32_16x16x32_bf16 forms the exact products of the fp32 x with the
 // integer weights and sums them in fp32.  Per 32-value block and 16x16 tile
 // three MFMAs (l, m, h into one accumulator), then one fp32 fma with the
-// block scale of the tile column.  Tiles, XCD order, segments, staging
-// (thread t: row t / 4, values 8 (t % 4) .. + 7 of the block) and epilogues
-// as gemm_mfma_kernel.  LDS rows of (32 * KB + 8) bf16 keep the 16-byte
+// block scale of the tile column.  XCD order, segments and epilogues as
+// gemm_mfma_kernel; tiles are BM x 32 WN with 2 WN waves (two down the rows,
+// WN across, each wave 16 MI rows x 32 columns), so one split of an x tile
+// serves 32 WN columns.  LDS rows of (32 * KB + 8) bf16 keep the 16-byte
 // fragment reads of 16 rows on distinct banks.  Fragment layout (16x16x32): lane l holds
 // A[l % 16][8 (l / 16) .. + 7], B[8 (l / 16) .. + 7][l % 16] and
 // D[4 (l / 16) + e][l % 16].
