@@ -1655,15 +1655,19 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
                     x, segs[0].out, M, segs[0].N, K, qt, epi};
     ma.nseg = nseg;
     const bool two = epi == RINA_EPI_SWIGLU;
-    // Q4 launches take 128-column tiles (8 waves: the x tile's split and
-    // staging then serve twice the columns); Q2_K 64-column ones
+    // Q4 launches take 128-column tiles of eight waves (the x tile's split
+    // and staging then serve twice the columns) when those tiles fill the
+    // CUs in whole rounds, else 64-column tiles of four waves (q/k/v at M
+    // 512: 384 wide tiles would leave half the CUs a second one); Q2_K
+    // 64-column tiles
     auto count = [&](int bn) {
         int t = 0;
         for (int s = 0; s < nseg; s++) t += (segs[s].N + bn - 1) / bn;
         return t;
     };
-    const bool wide = qt != RINA_QT_GGML_Q2_K;
     const bool half = (int64_t)count(64) * ((M + 63) / 64) < 2LL * rina_num_cus();   // 32-row tiles: more workgroups in flight
+    const int64_t mtiles = half ? (M + 31) / 32 : (M + 63) / 64;
+    const bool wide = qt != RINA_QT_GGML_Q2_K && mtiles * count(128) % rina_num_cus() == 0;
     const int BN = wide ? 128 : 64;
     int tiles = 0;
     for (int s = 0; s < 3; s++) {
@@ -1693,9 +1697,11 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
          else hipLaunchKernelGGL((KN<F, NM, 64>), g, dim3(256), 0, st, ma); } while (0)
     // Q4 weights: bf16 matrix cores on exact three-part splits of x; Q2_K
     // (weights d sc q - dmin m, not small integers): fp32 matrix cores
+#define BF3_WN(F, NM, WN) \
+    do { if (half) hipLaunchKernelGGL((gemm_bf3_kernel<F, NM, 32, WN>), g, dim3(128 * WN), 0, st, ma); \
+         else hipLaunchKernelGGL((gemm_bf3_kernel<F, NM, 64, WN>), g, dim3(128 * WN), 0, st, ma); } while (0)
 #define BF3_LAUNCH(F, NM) \
-    do { if (half) hipLaunchKernelGGL((gemm_bf3_kernel<F, NM, 32, 4>), g, dim3(512), 0, st, ma); \
-         else hipLaunchKernelGGL((gemm_bf3_kernel<F, NM, 64, 4>), g, dim3(512), 0, st, ma); } while (0)
+    do { if (wide) BF3_WN(F, NM, 4); else BF3_WN(F, NM, 2); } while (0)
     if (qt == RINA_QT_GGML_Q2_K) {
         if (two) MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 2);
         else MFMA_LAUNCH(gemm_mfma_kernel, FMT_Q2_K, 1);
@@ -1707,6 +1713,7 @@ int gemm_mfma(const rina_linear_seg* segs, int nseg, int qt, const float* x, int
         else BF3_LAUNCH(FMT_Q4_0, 1);
     }
 #undef BF3_LAUNCH
+#undef BF3_WN
 #undef MFMA_LAUNCH
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }

@@ -750,6 +750,7 @@ def _prefill_weights(orc, qt, r, n):
 @pytest.mark.parametrize("qt", [5, 7, 10])
 @pytest.mark.parametrize("M,N,K", [(16, 64, 32), (100, 200, 512), (64, 2048, 2048), (130, 77, 320), (512, 96, 1024),
                                    (520, 4096, 64), (256, 8192, 256),    # 64-row tiles; the others take 32-row tiles
+                                   (512, 2048, 512),   # Q4 at 32 rows in 128-column tiles of eight waves (with 256 CUs)
                                    (48, 1408, 2048), (100, 2048, 1408), (33, 96, 10944)])   # DeepSeek-V2-Lite rows
 @pytest.mark.parametrize("epi", [0, 1, 2])
 def test_linear_prefill_mfma(rina, orc, qt, M, N, K, epi):
