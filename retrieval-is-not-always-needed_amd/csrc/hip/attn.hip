@@ -669,31 +669,36 @@ __global__ __launch_bounds__(64) void attn_prompt_kernel(AttnArgs a) {
 
 // The same prompt attention on the matrix cores (v_mfma_f32_16x16x4f32: fp32
 // products, fp32 sums), for query heads in groups of 4 that share a KV head
-// (H / Hkv a multiple of 4).  A workgroup of 4 waves takes one group and 16
-// query rows, wave w query head 4 blockIdx.x + w; the 64-position K and V
-// blocks are staged once per workgroup in LDS (the next block's loads in
-// registers while the current one is multiplied).  Per block a wave forms
-// S^T = K Q^T (4 tiles of 16 keys x 16 rows, 16 steps of 4 dims each: lane
-// l's A value is key l % 16 of the tile at dim 16 (l / 16) + step, its B
-// value the query row l % 16 at that dim), so a lane holds 16 scores of
-// one query row (keys 16 kt + 4 (l / 16) + e), the row maximum and sum take
-// two cross-lane steps, and those scores are directly the B operand of
-// O^T += V^T P^T (step 4 kt + e uses key 16 kt + 4 (l / 16) + e; A value:
-// dim 4 (l % 16) + dt of that key for output tile dt).  A lane ends with
-// dims 16 (l / 16) .. + 15 of its row.  Base-2 softmax units and the
-// per-block rescale as in attn_prompt_kernel.
-__global__ __launch_bounds__(256) void attn_prompt_mfma_kernel(AttnArgs a) {
+// (H / Hkv a multiple of 4).  A workgroup takes one group and 16 query rows
+// with two sets of 4 waves, wave w of a set query head 4 blockIdx.x + w:
+// set 0 takes the even 64-position K/V blocks, set 1 the odd ones, each with
+// its own online softmax, merged at the end through LDS (so the longest row
+// tiles take half as many steps).  A set stages its block once in LDS (the
+// next block's loads in registers while the current one is multiplied).
+// Per block a wave forms S^T = K Q^T (4 tiles of 16 keys x 16 rows, 16 steps
+// of 4 dims each: lane l's A value is key l % 16 of the tile at dim
+// 16 (l / 16) + step, its B value the query row l % 16 at that dim), so a
+// lane holds 16 scores of one query row (keys 16 kt + 4 (l / 16) + e), the
+// row maximum and sum take two cross-lane steps, and those scores are
+// directly the B operand of O^T += V^T P^T (step 4 kt + e uses key
+// 16 kt + 4 (l / 16) + e; A value: dim 4 (l % 16) + dt of that key for
+// output tile dt).  A lane ends with dims 16 (l / 16) .. + 15 of its row.
+// Base-2 softmax units and the per-block rescale as in attn_prompt_kernel.
+__global__ __launch_bounds__(512) void attn_prompt_mfma_kernel(AttnArgs a) {
     constexpr int DH = 64, LDK = DH + 4;
-    __shared__ __align__(16) float s_k[64][LDK];
-    __shared__ __align__(16) float s_v[64][LDK];
+    __shared__ __align__(16) float s_k[2][64][LDK];
+    __shared__ __align__(16) float s_v[2][64][LDK];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ws = __builtin_amdgcn_readfirstlane(tid >> 8);     // wave set: even / odd blocks
+    const int ts = tid & 255;
+    const int w = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
     const int ntile = (a.T + kPromptRows - 1) / kPromptRows;
     const int t0 = (ntile - 1 - (int)blockIdx.y) * kPromptRows;   // longest row tiles first
     const int h = 4 * (int)blockIdx.x + w;
     const int kvh = 4 * (int)blockIdx.x / (a.H / a.Hkv);
     const int kvd = a.Hkv * DH;
     const int tmax = min(t0 + kPromptRows, a.T) - 1;
+    const int nblk = tmax / 64 + 1, npair = (nblk + 1) / 2;
     const int fr = lane & 15, g = lane >> 4;
     const int row = t0 + fr;
     const float qsc = a.scale * 1.44269504088896341f;
@@ -706,9 +711,9 @@ __global__ __launch_bounds__(256) void attn_prompt_mfma_kernel(AttnArgs a) {
             qv[4 * i] = v.x * qsc; qv[4 * i + 1] = v.y * qsc; qv[4 * i + 2] = v.z * qsc; qv[4 * i + 3] = v.w * qsc;
         }
     }
-    // staging: thread tid moves dims 16 (tid % 4) .. + 15 of key j0 + tid / 4
-    // (clamped to tmax: such keys are masked)
-    const int sk = tid >> 2, sq = tid & 3;
+    // staging: thread ts of a set moves dims 16 (ts % 4) .. + 15 of key
+    // j0 + ts / 4 (clamped to tmax: such keys are masked)
+    const int sk = ts >> 2, sq = ts & 3;
     f32x4 kr[4], vr[4];
     auto load_blk = [&](int j0) {
         const int64_t off = (int64_t)min(j0 + sk, tmax) * kvd + kvh * DH + 16 * sq;
@@ -724,16 +729,18 @@ __global__ __launch_bounds__(256) void attn_prompt_mfma_kernel(AttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
-    load_blk(0);
-    for (int j0 = 0; j0 <= tmax; j0 += 64) {
+    load_blk(64 * ws);
+    for (int ip = 0; ip < npair; ip++) {
+        const int j0 = 64 * (2 * ip + ws);          // this set's block; past tmax: none (same for the set)
         __syncthreads();                            // the previous block's operands are read
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            *(f32x4*)&s_k[sk][16 * sq + 4 * i] = kr[i];
-            *(f32x4*)&s_v[sk][16 * sq + 4 * i] = vr[i];
+            *(f32x4*)&s_k[ws][sk][16 * sq + 4 * i] = kr[i];
+            *(f32x4*)&s_v[ws][sk][16 * sq + 4 * i] = vr[i];
         }
         __syncthreads();
-        load_blk(j0 + 64 <= tmax ? j0 + 64 : j0);   // unconditional: the last block reloads itself
+        load_blk(j0 + 128 <= tmax ? j0 + 128 : j0);   // unconditional: the last block reloads itself
+        if (j0 > tmax) continue;
         f32x4 s[4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -741,7 +748,7 @@ __global__ __launch_bounds__(256) void attn_prompt_mfma_kernel(AttnArgs a) {
         for (int q4 = 0; q4 < 4; q4++) {
             f32x4 kv[4];
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++) kv[kt] = *(const f32x4*)&s_k[16 * kt + fr][16 * g + 4 * q4];
+            for (int kt = 0; kt < 4; kt++) kv[kt] = *(const f32x4*)&s_k[ws][16 * kt + fr][16 * g + 4 * q4];
 #pragma unroll
             for (int c = 0; c < 4; c++)
 #pragma unroll
@@ -779,15 +786,39 @@ __global__ __launch_bounds__(256) void attn_prompt_mfma_kernel(AttnArgs a) {
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const f32x4 vv = *(const f32x4*)&s_v[16 * kt + 4 * g + e][4 * fr];
+                const f32x4 vv = *(const f32x4*)&s_v[ws][16 * kt + 4 * g + e][4 * fr];
 #pragma unroll
                 for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[dt], s[kt][e], o[dt], 0, 0, 0);
             }
     }
-    if (row < a.T) {
+    // merge: set 1 leaves (m, l, O) in LDS, set 0 combines (set 0 always
+    // holds block 0, so its maximum is finite; set 1's may be -inf: weight 0)
+    __syncthreads();
+    float* xch = &s_k[0][0][0];                     // 18 floats per set-1 thread
+    if (ws == 1) {
+        float* d = xch + 18 * ts;
+        d[0] = m;
+        d[1] = l;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) *(f32x4*)&d[2 + 4 * dt] = o[dt];
+    }
+    __syncthreads();
+    if (ws == 0 && row < a.T) {
+        const float* d = xch + 18 * ts;
+        const float m1 = d[0], l1 = d[1];
+        const float mm = fmaxf(m, m1);
+        const float a0 = __builtin_amdgcn_exp2f(m - mm), a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+        const float lt = fmaf(l, a0, l1 * a1);
+        f32x4 ot[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const f32x4 o1 = *(const f32x4*)&d[2 + 4 * dt];
+#pragma unroll
+            for (int e = 0; e < 4; e++) ot[dt][e] = fmaf(o[dt][e], a0, o1[e] * a1);
+        }
         f32x4* op = (f32x4*)(a.out + ((int64_t)row * a.H + h) * DH + 16 * g);
 #pragma unroll
-        for (int e = 0; e < 4; e++) gst(op + e, f32x4{o[0][e] / l, o[1][e] / l, o[2][e] / l, o[3][e] / l});
+        for (int e = 0; e < 4; e++) gst(op + e, f32x4{ot[0][e] / lt, ot[1][e] / lt, ot[2][e] / lt, ot[3][e] / lt});
     }
 }
 
@@ -956,7 +987,7 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
     if (T > 1 && !d_pos && start_pos == 0 && dh == 64 && ((uintptr_t)kcur % 16 == 0)) {
         const int ntile = (T + kPromptRows - 1) / kPromptRows;
         if (rep % 4 == 0 && ((uintptr_t)q | (uintptr_t)vcur | (uintptr_t)out) % 16 == 0)
-            hipLaunchKernelGGL(attn_prompt_mfma_kernel, dim3(H / 4, ntile), dim3(256), 0, st, a);
+            hipLaunchKernelGGL(attn_prompt_mfma_kernel, dim3(H / 4, ntile), dim3(512), 0, st, a);
         else
             hipLaunchKernelGGL(attn_prompt_kernel, dim3(H, ntile), dim3(64), 0, st, a);
         RINA_LAUNCH_CHECK();
