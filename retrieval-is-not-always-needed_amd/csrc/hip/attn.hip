@@ -670,10 +670,11 @@ __global__ __launch_bounds__(64) void attn_prompt_kernel(AttnArgs a) {
 // The same prompt attention on the matrix cores (v_mfma_f32_16x16x4f32: fp32
 // products, fp32 sums), for query heads in groups of 4 that share a KV head
 // (H / Hkv a multiple of 4).  A workgroup takes one group and 16 query rows
-// with two sets of 4 waves, wave w of a set query head 4 blockIdx.x + w:
-// set 0 takes the even 64-position K/V blocks, set 1 the odd ones, each with
-// its own online softmax, merged at the end through LDS (so the longest row
-// tiles take half as many steps).  A set stages its block once in LDS (the
+// with NSET sets of 4 waves, wave w of a set query head 4 blockIdx.x + w:
+// set k takes the 64-position K/V blocks k, k + NSET, ..., each with its
+// own online softmax, merged at the end through LDS (so the longest row
+// tiles take 1 / NSET as many steps; launched with two sets, four measured
+// slower).  A set stages its block once in LDS (the
 // next block's loads in registers while the current one is multiplied).
 // Per block a wave forms S^T = K Q^T (4 tiles of 16 keys x 16 rows, 16 steps
 // of 4 dims each: lane l's A value is key l % 16 of the tile at dim
@@ -684,10 +685,11 @@ __global__ __launch_bounds__(64) void attn_prompt_kernel(AttnArgs a) {
 // 16 kt + 4 (l / 16) + e; A value: dim 4 (l % 16) + dt of that key for
 // output tile dt).  A lane ends with dims 16 (l / 16) .. + 15 of its row.
 // Base-2 softmax units and the per-block rescale as in attn_prompt_kernel.
-__global__ __launch_bounds__(512) void attn_prompt_mfma_kernel(AttnArgs a) {
+template <int NSET>
+__global__ __launch_bounds__(256 * NSET) void attn_prompt_mfma_kernel(AttnArgs a) {
     constexpr int DH = 64, LDK = DH + 4;
-    __shared__ __align__(16) float s_k[2][64][LDK];
-    __shared__ __align__(16) float s_v[2][64][LDK];
+    __shared__ __align__(16) float s_k[NSET][64][LDK];
+    __shared__ __align__(16) float s_v[NSET][64][LDK];
     const int tid = threadIdx.x, lane = tid & 63;
     const int ws = __builtin_amdgcn_readfirstlane(tid >> 8);     // wave set: even / odd blocks
     const int ts = tid & 255;
@@ -698,7 +700,7 @@ __global__ __launch_bounds__(512) void attn_prompt_mfma_kernel(AttnArgs a) {
     const int kvh = 4 * (int)blockIdx.x / (a.H / a.Hkv);
     const int kvd = a.Hkv * DH;
     const int tmax = min(t0 + kPromptRows, a.T) - 1;
-    const int nblk = tmax / 64 + 1, npair = (nblk + 1) / 2;
+    const int nblk = tmax / 64 + 1, npair = (nblk + NSET - 1) / NSET;
     const int fr = lane & 15, g = lane >> 4;
     const int row = t0 + fr;
     const float qsc = a.scale * 1.44269504088896341f;
@@ -731,7 +733,7 @@ __global__ __launch_bounds__(512) void attn_prompt_mfma_kernel(AttnArgs a) {
     float m = -INFINITY, l = 0.f;
     load_blk(64 * ws);
     for (int ip = 0; ip < npair; ip++) {
-        const int j0 = 64 * (2 * ip + ws);          // this set's block; past tmax: none (same for the set)
+        const int j0 = 64 * (NSET * ip + ws);       // this set's block; past tmax: none (same for the set)
         __syncthreads();                            // the previous block's operands are read
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -739,7 +741,7 @@ __global__ __launch_bounds__(512) void attn_prompt_mfma_kernel(AttnArgs a) {
             *(f32x4*)&s_v[ws][sk][16 * sq + 4 * i] = vr[i];
         }
         __syncthreads();
-        load_blk(j0 + 128 <= tmax ? j0 + 128 : j0);   // unconditional: the last block reloads itself
+        load_blk(j0 + 64 * NSET <= tmax ? j0 + 64 * NSET : j0);   // unconditional: the last block reloads itself
         if (j0 > tmax) continue;
         f32x4 s[4];
 #pragma unroll
@@ -794,9 +796,9 @@ __global__ __launch_bounds__(512) void attn_prompt_mfma_kernel(AttnArgs a) {
     // merge: set 1 leaves (m, l, O) in LDS, set 0 combines (set 0 always
     // holds block 0, so its maximum is finite; set 1's may be -inf: weight 0)
     __syncthreads();
-    float* xch = &s_k[0][0][0];                     // 18 floats per set-1 thread
-    if (ws == 1) {
-        float* d = xch + 18 * ts;
+    float* xch = &s_k[0][0][0];                     // 18 floats per thread of sets 1 ..
+    if (ws > 0) {
+        float* d = xch + 18 * (256 * (ws - 1) + ts);
         d[0] = m;
         d[1] = l;
 #pragma unroll
@@ -804,17 +806,25 @@ __global__ __launch_bounds__(512) void attn_prompt_mfma_kernel(AttnArgs a) {
     }
     __syncthreads();
     if (ws == 0 && row < a.T) {
-        const float* d = xch + 18 * ts;
-        const float m1 = d[0], l1 = d[1];
-        const float mm = fmaxf(m, m1);
-        const float a0 = __builtin_amdgcn_exp2f(m - mm), a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
-        const float lt = fmaf(l, a0, l1 * a1);
+        float mm = m;
+#pragma unroll
+        for (int k = 1; k < NSET; k++) mm = fmaxf(mm, xch[18 * (256 * (k - 1) + ts)]);
+        const float a0 = __builtin_amdgcn_exp2f(m - mm);
+        float lt = l * a0;
         f32x4 ot[4];
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-            const f32x4 o1 = *(const f32x4*)&d[2 + 4 * dt];
+        for (int dt = 0; dt < 4; dt++) ot[dt] = o[dt] * a0;
 #pragma unroll
-            for (int e = 0; e < 4; e++) ot[dt][e] = fmaf(o[dt][e], a0, o1[e] * a1);
+        for (int k = 1; k < NSET; k++) {
+            const float* d = xch + 18 * (256 * (k - 1) + ts);
+            const float a1 = d[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(d[0] - mm);
+            lt = fmaf(d[1], a1, lt);
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const f32x4 o1 = *(const f32x4*)&d[2 + 4 * dt];
+#pragma unroll
+                for (int e = 0; e < 4; e++) ot[dt][e] = fmaf(o1[e], a1, ot[dt][e]);
+            }
         }
         f32x4* op = (f32x4*)(a.out + ((int64_t)row * a.H + h) * DH + 16 * g);
 #pragma unroll
@@ -987,7 +997,7 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
     if (T > 1 && !d_pos && start_pos == 0 && dh == 64 && ((uintptr_t)kcur % 16 == 0)) {
         const int ntile = (T + kPromptRows - 1) / kPromptRows;
         if (rep % 4 == 0 && ((uintptr_t)q | (uintptr_t)vcur | (uintptr_t)out) % 16 == 0)
-            hipLaunchKernelGGL(attn_prompt_mfma_kernel, dim3(H / 4, ntile), dim3(512), 0, st, a);
+            hipLaunchKernelGGL(attn_prompt_mfma_kernel<2>, dim3(H / 4, ntile), dim3(512), 0, st, a);
         else
             hipLaunchKernelGGL(attn_prompt_kernel, dim3(H, ntile), dim3(64), 0, st, a);
         RINA_LAUNCH_CHECK();
