@@ -1197,7 +1197,7 @@ __global__ __launch_bounds__(128 * WN) void gemm_bf3_kernel(MfmaArgs ma) {
     const int m0 = by * BM, n0 = (bx - tb) * BN;
     const int nb = a.K / 32, nst = (nb + KB - 1) / KB;
     // x staging: every thread splits XV values of one row per block (XT
-    // threads per row), so the split work is spread over all four waves;
+    // threads per row), so the split work is spread over all the waves;
     // weight staging: thread tid takes values 8 sq .. 8 sq + 7 of column sr
     constexpr int XV = BM * 32 / NT, XT = 32 / XV;
     const int xsr = tid / XT, xsq = tid % XT;
