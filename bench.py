@@ -8,10 +8,14 @@ W_o + residual, RMSNorm, W1/W3 + SiLU*up, W2 + residual], final norm, fp32
 LM head, device argmax), replayed as one HIP graph.  The timed region is
 exactly --steps decode steps with all inputs resident in HBM.
 
-Also reported: the dominant kernel's HBM roofline (measured live with HIP
-events on the stream it runs on), the Q4_0F SwiGLU matvec and config 1's
-Q4_0 GEMV over weight rings larger than the 256 MB MALL, and the CPU
-oracle's decode rate on a bounded sample (cpu_baseline).
+The headline roofline is the metric's own kernels: config 2's quant matvecs
+and decode attention over all 16 layers (the layer stack, one graph replay
+per token, HIP events on the stream it runs on), algorithmic bytes per token
+over device time per token.  Also reported: the fp32 LM head, the Q4_0F
+SwiGLU matvec and config 1's Q4_0 GEMV over weight rings larger than the
+256 MB MALL, decode attention and config 4's stages on their own, configs
+3-5 end to end, and the CPU oracle's decode rate on a bounded sample
+(cpu_baseline).
 """
 import argparse
 import ctypes as C
@@ -125,19 +129,25 @@ def cpu_model():
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_lm_head_fp32.json")
+STACK_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode_layers_config2.json")
 COPY_BYTES = 512 << 20          # calibration copy: 512 MiB read + 512 MiB written (> the 256 MB MALL)
+STACK_POS = 543                 # traffic probe of the layer stack: the average config-2 decode position
 
 
-def traffic_probe(iters):
-    """Run under rocprofv3 --pmc: the LM head matvec (128256 x 2048 fp32) and
-    a plain device copy of COPY_BYTES, `iters` launches each."""
+def _probe_setup():
     import torch
     rina = pkg()
     hip = rina.load_hip()
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
-    st = stream.cuda_stream
+    return torch, rina, hip, stream.cuda_stream
+
+
+def traffic_probe(iters):
+    """Run under rocprofv3 --pmc: the LM head matvec (128256 x 2048 fp32) and
+    a plain device copy of COPY_BYTES, `iters` launches each."""
+    torch, rina, hip, st = _probe_setup()
     d, V = 2048, 128256
     w = torch.randn(V * d, device="cuda") * 0.02
     x = torch.randn(d, device="cuda")
@@ -152,47 +162,83 @@ def traffic_probe(iters):
     print("probe done", flush=True)
 
 
-def _pmc_avg(db, counter):
-    """Per-dispatch average of `counter` (KiB) for the LM head kernel and the copy kernel."""
+def traffic_probe_stack(iters):
+    """Run under rocprofv3 --pmc: `iters` tokens of config 2's decode layer
+    stack (LayerStack at STACK_POS) and as many plain copies of COPY_BYTES."""
+    torch, rina, hip, st = _probe_setup()
+    synth = importlib.import_module("rina_amd.synth")
+    sm = synth.SynthLlama(dict(synth.LLAMA_1B), qt=rina.QT_Q4_0F, seed=1, max_seq=STACK_POS + 8)
+    ls = LayerStack(torch, hip, rina, sm, sm.cfg, STACK_POS, st)
+    src = torch.randn(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        ls.token()
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("probe done: %d tokens, %d bytes per token" % (iters, ls.bytes_per_token()), flush=True)
+
+
+STACK_KERNELS = ("gemv_direct_kernel", "attn_split_kernel", "attn_combine_kernel")
+
+
+def _pmc_sum(db, counter, kernels):
+    """Per-dispatch sums of `counter` (KiB): over every dispatch of a kernel
+    whose name contains one of `kernels`, and over the copy kernel's."""
     import sqlite3
     c = sqlite3.connect(db)
     cols = [r[1] for r in c.execute("pragma table_info(counters_collection)")]
     ix = {n: i for i, n in enumerate(cols)}
-    vals = {"lm": [], "copy": []}
+    tot = {"k": 0.0, "copy": 0.0}
+    n = {"k": 0, "copy": 0}
+    per = {}
     for r in c.execute("select * from counters_collection").fetchall():
         if r[ix["counter_name"]] != counter:
             continue
         name = r[ix["kernel_name"]]
-        key = "lm" if "gemv_f32_kernel" in name else "copy" if "copyBuffer" in name else None
+        key = "k" if any(k in name for k in kernels) else "copy" if "copyBuffer" in name else None
         if key:
-            vals[key].append(float(r[ix["value"]]))
-    return {k: (sum(v) / len(v) if v else None) for k, v in vals.items()}, {k: len(v) for k, v in vals.items()}
+            tot[key] += float(r[ix["value"]])
+            n[key] += 1
+            if key == "k":
+                short = next(k for k in kernels if k in name)
+                per[short] = per.get(short, 0.0) + float(r[ix["value"]])
+    return tot, n, per
 
 
-def measure_traffic(iters=10):
-    """Two rocprofv3 --pmc passes over traffic_probe (FETCH_SIZE, then
-    WRITE_SIZE), each counter scaled by its reading on the plain copy of known
-    size; writes TRAFFIC_FILE.  The profiler runs as a child process."""
+def _pmc_runs(probe_flag, iters, kernels):
     import subprocess
     import tempfile
     out = {}
     env = dict(os.environ, TMPDIR="/tmp")
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         d = tempfile.mkdtemp(prefix="rina_pmc_", dir="/tmp")
-        cmd = ["rocprofv3", "--pmc", counter, "-d", d, "-o", "run", "--", sys.executable,
-               os.path.abspath(__file__), "--traffic-probe", str(iters)]
+        cmd = ["timeout", "-s", "KILL", "170", "rocprofv3", "--pmc", counter, "-d", d, "-o", "run", "--",
+               sys.executable, os.path.abspath(__file__), probe_flag, str(iters)]
         log("running: " + " ".join(cmd))
         subprocess.run(cmd, cwd="/tmp", env=env, check=True, timeout=180)
         db = [os.path.join(r, f) for r, _, fs in os.walk(d) for f in fs if f.endswith("_results.db")][0]
-        avg, n = _pmc_avg(db, counter)
-        log("%s KiB/dispatch: %s (dispatches %s)" % (counter, avg, n))
-        factor = COPY_BYTES / (avg["copy"] * 1024.0)       # bytes per counted KiB
-        out[counter] = {"lm_kib": avg["lm"], "copy_kib": avg["copy"], "factor": factor,
-                        "lm_bytes": avg["lm"] * 1024.0 * factor}
+        tot, n, per = _pmc_sum(db, counter, kernels)
+        log("%s KiB: %s (dispatches %s)" % (counter, tot, n))
+        factor = COPY_BYTES / (tot["copy"] / n["copy"] * 1024.0)       # bytes per counted KiB
+        out[counter] = {"kernel_kib_total": tot["k"], "kernel_dispatches": n["k"],
+                        "copy_kib": tot["copy"] / n["copy"], "factor": factor,
+                        "per_kernel_kib_total": per}
+    return out
+
+
+def measure_traffic(iters=10):
+    """rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE, one run each)
+    over two probes: the LM head and config 2's decode layer stack.  Each
+    counter is scaled by its reading on a plain copy of known size in the
+    same run.  Writes TRAFFIC_FILE and STACK_TRAFFIC_FILE.  The profiler runs
+    as a child process."""
+    out = _pmc_runs("--traffic-probe", iters, ("gemv_f32_kernel",))
+    lmb = {c: out[c]["kernel_kib_total"] / out[c]["kernel_dispatches"] * 1024.0 * out[c]["factor"] for c in out}
     lm_alg = 128256 * 2048 * 4 + 2048 * 4 + 128256 * 4
     res = {"kernel": "gemv_f32_kernel (tied LM head 128256x2048 fp32)", "algorithmic_bytes": lm_alg,
-           "fetch_bytes": round(out["FETCH_SIZE"]["lm_bytes"]), "write_bytes": round(out["WRITE_SIZE"]["lm_bytes"]),
-           "hbm_bytes": round(out["FETCH_SIZE"]["lm_bytes"] + out["WRITE_SIZE"]["lm_bytes"]),
+           "fetch_bytes": round(lmb["FETCH_SIZE"]), "write_bytes": round(lmb["WRITE_SIZE"]),
+           "hbm_bytes": round(lmb["FETCH_SIZE"] + lmb["WRITE_SIZE"]),
            "calibration": "plain device copy of %d bytes (reads and writes %d bytes)" % (COPY_BYTES, COPY_BYTES),
            "counters": out, "command": "python bench.py --measure-traffic"}
     res["traffic_over_algorithmic"] = round(res["hbm_bytes"] / lm_alg, 4)
@@ -200,20 +246,159 @@ def measure_traffic(iters=10):
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(res, f, indent=1)
     print(json.dumps(res), flush=True)
+    tokens = 4
+    out = _pmc_runs("--traffic-probe-stack", tokens, STACK_KERNELS)
+    tb = {c: out[c]["kernel_kib_total"] / tokens * 1024.0 * out[c]["factor"] for c in out}
+    pkg()
+    synth = importlib.import_module("rina_amd.synth")
+    alg = 16 * sum(stack_bytes(synth.LLAMA_1B, STACK_POS).values())
+    res = {"kernel": "config-2 decode layer stack (gemv_direct_kernel, attn_split_kernel, attn_combine_kernel; "
+                     "16 layers, fp32 KV at position %d)" % STACK_POS,
+           "algorithmic_bytes": alg, "tokens": tokens,
+           "fetch_bytes": round(tb["FETCH_SIZE"]), "write_bytes": round(tb["WRITE_SIZE"]),
+           "hbm_bytes": round(tb["FETCH_SIZE"] + tb["WRITE_SIZE"]),
+           "calibration": "plain device copy of %d bytes (reads and writes %d bytes)" % (COPY_BYTES, COPY_BYTES),
+           "counters": out, "command": "python bench.py --measure-traffic"}
+    res["traffic_over_algorithmic"] = round(res["hbm_bytes"] / alg, 4)
+    with open(STACK_TRAFFIC_FILE, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res), flush=True)
 
 
-def committed_traffic():
-    """HBM bytes per launch of the LM head from the committed PMC measurement."""
+def committed_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch (per token for the layer stack) from a committed
+    PMC measurement."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             t = json.load(f)
         return t["hbm_bytes"], {
             "fetch_bytes": t["fetch_bytes"], "write_bytes": t["write_bytes"],
             "over_algorithmic": t["traffic_over_algorithmic"],
-            "source": "profiles/traffic_lm_head_fp32.json (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by "
-                      "the same counter on a plain copy of known size)"}
+            "source": "profiles/%s (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by the same counter on a "
+                      "plain copy of known size)" % os.path.basename(path)}
     except (OSError, KeyError, ValueError):
         return None, None
+
+
+STACK_KINDS = ("qkv", "attn", "wo", "w13", "w2")
+STACK_NOTES = {"qkv": "fused q/k/v Q4_0F matvec with the ln1 RMSNorm prologue (N 3072, K 2048)",
+               "attn": "RoPE + fp32 KV append + split-sequence decode attention + chunk merge",
+               "wo": "W_o Q4_0F matvec + residual (N 2048, K 2048)",
+               "w13": "W1/W3 Q4_0F matvec pair with the ln2 RMSNorm prologue and SiLU*up (N 8192, K 2048)",
+               "w2": "W2 Q4_0F matvec + residual (N 2048, K 8192)"}
+
+
+def stack_bytes(cfg, pos):
+    """Algorithmic bytes of one layer's decode launches at position pos
+    (Q4_0F weights, 20 B per 32 values; fp32 activations, norm weights and
+    K/V rows): weights once, every vector read or written once."""
+    d, H, Hkv, dh, hd = cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["hidden_dim"]
+    kvd = Hkv * dh
+    bq = lambda n, k: n * k // 32 * 20
+    return {"qkv": bq(H * dh + 2 * kvd, d) + 2 * d * 4 + (H * dh + 2 * kvd) * 4,
+            "attn": pos * kvd * 8 + (2 * H * dh + 2 * kvd) * 4,
+            "wo": bq(d, H * dh) + H * dh * 4 + 2 * d * 4,
+            "w13": 2 * bq(hd, d) + 2 * d * 4 + hd * 4,
+            "w2": bq(d, hd) + hd * 4 + 2 * d * 4}
+
+
+class LayerStack:
+    """Config 2's decode layers, issued through the C-ABI exactly as
+    gqa_layer.cpp's decode step issues them, over the model's own 16 layers
+    of weights (608 MB, larger than the 256 MB MALL): per layer the quant
+    matvecs and the decode attention, the launches the metric names.  The
+    embedding, the fp32 LM head and the argmax are not part of it.  Each
+    layer has its own fp32 K/V cache filled with N(0,1) rows; the attention
+    appends at host position `pos` and reads positions 0..pos."""
+
+    def __init__(self, torch, hip, rina, sm, cfg, pos, st):
+        self.hip, self.rina, self.st, self.pos = hip, rina, st, pos
+        d, H, Hkv, dh, hd, L = (cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["hidden_dim"],
+                                cfg["n_layers"])
+        self.d, self.H, self.Hkv, self.dh, self.hd, self.L = d, H, Hkv, dh, hd, L
+        kvd = Hkv * dh
+        self.msq = pos + 8
+        self.kc = [torch.randn(self.msq * kvd, device="cuda") for _ in range(L)]
+        self.vc = [torch.randn(self.msq * kvd, device="cuda") for _ in range(L)]
+        self.h = torch.randn(d, device="cuda")
+        self.q, self.k, self.v = (torch.empty(n, device="cuda") for n in (H * dh, kvd, kvd))
+        self.a, self.g = torch.empty(H * dh, device="cuda"), torch.empty(hd, device="cuda")
+        self.wsb = int(hip.rina_hip_gqa_attention_workspace(1, H, dh, self.msq))
+        self.ws = torch.empty(self.wsb // 4 + 4, device="cuda")
+        W = lambda l, n: sm.dev["transformer.h.%d.%s" % (l, n)].data_ptr()
+        LS = rina.LinearSeg
+        self.lay = []
+        for l in range(L):
+            self.lay.append(dict(
+                qkv=(LS * 3)(LS(W(l, "attn.w_q.weight"), None, self.q.data_ptr(), H * dh),
+                             LS(W(l, "attn.w_k.weight"), None, self.k.data_ptr(), kvd),
+                             LS(W(l, "attn.w_v.weight"), None, self.v.data_ptr(), kvd)),
+                wo=LS(W(l, "attn.w_o.weight"), None, self.h.data_ptr(), d),
+                w13=LS(W(l, "mlp.w1.weight"), W(l, "mlp.w3.weight"), self.g.data_ptr(), hd),
+                w2=LS(W(l, "mlp.w2.weight"), None, self.h.data_ptr(), d),
+                ln1=W(l, "ln1.weight"), ln2=W(l, "ln2.weight"),
+                rope=[W(l, "attn.%s" % n) for n in ("rope_q.cos", "rope_q.sin", "rope.cos", "rope.sin")]))
+        self.bytes = stack_bytes(cfg, pos)
+
+    def call(self, kind, l):
+        hip, r, st, w = self.hip, self.rina, self.st, self.lay[l % self.L]
+        if kind == "qkv":
+            return hip.rina_hip_linear_fused(w["qkv"], 3, r.QT_Q4_0F, self.h.data_ptr(), 1, self.d, r.EPI_STORE,
+                                             r.PRO_RMSNORM, w["ln1"], 1e-5, st)
+        if kind == "attn":
+            c = w["rope"]
+            return hip.rina_hip_gqa_decode_attention(
+                self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), c[0], c[1], c[2], c[3],
+                self.kc[l % self.L].data_ptr(), self.vc[l % self.L].data_ptr(), 0, self.H, self.Hkv, self.dh,
+                self.pos, None, self.msq, self.a.data_ptr(), None, self.ws.data_ptr(), self.wsb, st)
+        if kind == "wo":
+            return hip.rina_hip_linear_fused(C.byref(w["wo"]), 1, r.QT_Q4_0F, self.a.data_ptr(), 1, self.H * self.dh,
+                                             r.EPI_ADD, r.PRO_NONE, None, 0.0, st)
+        if kind == "w13":
+            return hip.rina_hip_linear_fused(C.byref(w["w13"]), 1, r.QT_Q4_0F, self.h.data_ptr(), 1, self.d,
+                                             r.EPI_SWIGLU, r.PRO_RMSNORM, w["ln2"], 1e-5, st)
+        return hip.rina_hip_linear_fused(C.byref(w["w2"]), 1, r.QT_Q4_0F, self.g.data_ptr(), 1, self.hd, r.EPI_ADD,
+                                         r.PRO_NONE, None, 0.0, st)
+
+    def token(self, i=0):
+        for l in range(self.L):
+            for kind in STACK_KINDS:
+                self.rina.check(self.call(kind, l), kind)
+        return 0
+
+    def bytes_per_token(self):
+        return self.L * sum(self.bytes.values())
+
+
+def layer_stack_roofline(torch, hip, rina, sm, cfg, pos, st, iters):
+    """The headline roofline: config 2's decode layer stack (the quant
+    matvecs and decode attention of all 16 layers) as one graph replay per
+    token, its algorithmic bytes per token over its device time per token;
+    plus each launch class timed on its own over the 16 layers."""
+    ls = LayerStack(torch, hip, rina, sm, cfg, pos, st)
+    t_tok = time_kernel(torch, ls.token, max(2, iters // 8))
+    per = {}
+    for kind in STACK_KINDS:
+        t = time_kernel(torch, lambda i=0, k=kind: ls.call(k, i), ls.L * max(1, iters // 8))
+        b = ls.bytes[kind]
+        per[kind] = {"bytes_per_launch": b, "avg_us": round(t * 1e6, 3), "frac": round(b / t / HBM_PEAK, 4),
+                     "note": STACK_NOTES[kind]}
+    tb = ls.bytes_per_token()
+    traffic, detail = committed_traffic(STACK_TRAFFIC_FILE)
+    roof = roofline(tb, t_tok, traffic)
+    roof.update({"kernel": "config-2 decode layer stack: 16 x [q/k/v + ln1, RoPE + KV append + attention "
+                           "(split + combine), W_o + residual, W1/W3 + ln2 + SiLU*up, W2 + residual], Q4_0F, fp32 "
+                           "KV at position %d" % pos,
+                 "bytes_per_token": tb, "us_per_token": round(t_tok * 1e6, 2),
+                 "launches_per_token": 6 * ls.L, "per_launch": per})
+    if detail:
+        roof["traffic_detail"] = detail
+    log("layer stack at position %d: %.1f us per token, %.0f GB/s (%.3f of peak)" %
+        (pos, t_tok * 1e6, tb / t_tok / 1e9, tb / t_tok / HBM_PEAK))
+    for kind in STACK_KINDS:
+        log("  %-5s %7.2f us  %.3f" % (kind, per[kind]["avg_us"], per[kind]["frac"]))
+    del ls
+    return roof
 
 
 def config4_kernel_roofs(torch, hip, rina, synth, st, pos, iters):
@@ -300,11 +485,15 @@ def main():
     ap.add_argument("--no-config3", action="store_true", help="skip the context-4096 quantized-KV (config 3) line")
     ap.add_argument("--config3-steps", type=int, default=8)
     ap.add_argument("--traffic-probe", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--traffic-probe-stack", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--measure-traffic", action="store_true",
                     help="run the two rocprofv3 --pmc passes for the LM head's HBM traffic and write them to profiles/")
     args = ap.parse_args()
     if args.traffic_probe:
         traffic_probe(args.traffic_probe)
+        return
+    if args.traffic_probe_stack:
+        traffic_probe_stack(args.traffic_probe_stack)
         return
     if args.measure_traffic:
         measure_traffic()
@@ -392,6 +581,11 @@ def main():
                            plain_read_time(torch, hip, st, lm_bytes, max(4, args.kernel_iters // 5)))
     log("lm_head fp32 GEMV: %.1f us, %.0f GB/s (plain read %.1f us)" %
         (t_lm * 1e6, lm_bytes / t_lm / 1e9, lm_roof["plain_read_us"]))
+
+    # ---- headline roofline: the metric's kernels, config 2's quant matvecs
+    # and decode attention over all 16 layers, at the timed run's middle position
+    stack_roof = layer_stack_roofline(torch, hip, rina, sm, cfg, args.prompt + 1 + args.warmup + args.steps // 2, st,
+                                      args.kernel_iters)
 
     # ---- Q4_0F SwiGLU matvec over the model's own layers (ring > MALL)
     hd = cfg["hidden_dim"]
@@ -523,37 +717,45 @@ def main():
         torch.cuda.empty_cache()
         attn_roofs.update(config4_kernel_roofs(torch, hip, rina, synth, st, p4, args.kernel_iters))
 
-    # ---- config 5: RINA Gen6 Jamba hybrid, 64-token prompt then 128 greedy steps
-    cfg5 = None
+    # ---- config 5: RINA Gen6 Jamba hybrid at context 2048, 1900-token prompt
+    # then 128 greedy steps: with its q2 K / q1 V RINA-MLA cache (the
+    # config's stated cache, rina_mla_kv_mode "q2k_q1v"), and with the fp32
+    # cache (the reference engine's RINA-MLA numerics)
+    cfg5 = {}
     if not args.no_config5:
         p5, s5 = 1900, 128   # context 2048: steps at positions 1901..2028
-        jm = synth.SynthJamba(seed=1, max_seq=2048)
-        inf5 = jm.infer()
-        pr5 = np.random.default_rng(5).integers(0, jm.cfg["vocab_size"], p5).astype(np.int32)
-        # two generated tokens: the second step captures the decode graph
-        # outside the timed region (as for config 4)
-        first5 = (C.c_int * 2)()
-        rina.check(eng.rina_infer_generate(inf5, pr5.ctypes.data_as(C.POINTER(C.c_int)), p5, 2, first5, 1, st, None),
-                   "config 5 prefill")
-        out5 = (C.c_int * s5)()
-        torch.cuda.synchronize()
-        tq = time.perf_counter()
-        rina.check(eng.rina_infer_decode(inf5, s5, out5, 1, st, None), "config 5 decode")
-        torch.cuda.synchronize()
-        w5 = time.perf_counter() - tq
-        eng.rina_infer_destroy(inf5)
-        b5 = jm.bytes_per_token(p5 + 1 + s5 // 2)
-        cfg5 = {"workload": "RINA Gen6 Jamba hybrid at random init: 640d, 16 layers (12 InertiaWave SSM + 4 RINA-MLA), "
+        for key, kvm in (("config5_rina_jamba", "q2k_q1v"), ("config5_rina_jamba_fp32_cache", "fp32")):
+            jm = synth.SynthJamba(seed=1, max_seq=2048, kv_mode=kvm)
+            inf5 = jm.infer()
+            pr5 = np.random.default_rng(5).integers(0, jm.cfg["vocab_size"], p5).astype(np.int32)
+            # two generated tokens: the second step captures the decode graph
+            # outside the timed region (as for config 4)
+            first5 = (C.c_int * 2)()
+            rina.check(eng.rina_infer_generate(inf5, pr5.ctypes.data_as(C.POINTER(C.c_int)), p5, 2, first5, 1, st,
+                                               None), "config 5 prefill")
+            out5 = (C.c_int * s5)()
+            torch.cuda.synchronize()
+            tq = time.perf_counter()
+            rina.check(eng.rina_infer_decode(inf5, s5, out5, 1, st, None), "config 5 decode")
+            torch.cuda.synchronize()
+            w5 = time.perf_counter() - tq
+            eng.rina_infer_destroy(inf5)
+            b5 = jm.bytes_per_token(p5 + 1 + s5 // 2)
+            cache = ("q2 K / q1 V RINA-MLA cache (q2_1 key content, fp32 RoPE part, q1_0 values; queries and the "
+                     "current position fp32)" if kvm == "q2k_q1v" else "fp32 RINA-MLA cache")
+            cfg5[key] = {
+                "workload": "RINA Gen6 Jamba hybrid at random init: 640d, 16 layers (12 InertiaWave SSM + 4 RINA-MLA), "
                             "10/5 heads, d_c 160, LayerNorm + SwiGLU 1536, vocab 128256, Q4_0 linears, fp32 tied LM "
-                            "head, context 2048, %d-token seeded prompt (prefill untimed), %d greedy steps at "
-                            "positions %d..%d" % (p5, s5, p5 + 1, p5 + s5),
+                            "head, %s, context 2048, %d-token seeded prompt (prefill untimed), %d greedy steps at "
+                            "positions %d..%d" % (cache, p5, s5, p5 + 1, p5 + s5),
+                "rina_mla_kv_mode": kvm,
                 "tokens_per_s": round(s5 / w5, 2), "ms_per_step": round(w5 * 1e3 / s5, 4), "steps": s5,
                 "bytes_per_token": b5, "hbm_gbps": round(b5 * s5 / w5 / 1e9, 1),
                 "hbm_frac": round(b5 * s5 / w5 / HBM_PEAK, 4), "tokens_head": list(first5) + list(out5)[:7]}
-        log("config 5: %.3f ms/step, %.1f tok/s" % (w5 * 1e3 / s5, s5 / w5))
-        jm.close()
-        del jm
-        torch.cuda.empty_cache()
+            log("config 5 (%s cache): %.3f ms/step, %.1f tok/s" % (kvm, w5 * 1e3 / s5, s5 / w5))
+            jm.close()
+            del jm
+            torch.cuda.empty_cache()
 
     # ---- config 3: the same model at context 4096, KV cache q8 / q4 / q2k_q1v.
     # A 4090-token seeded prompt is prefilled (untimed; the second generated
@@ -665,9 +867,10 @@ def main():
                                "vocab 128256, Q4_0F linears, fp32 tied LM head, fp32 KV, %d-token seeded prompt, "
                                "greedy" % (cfg["n_layers"], args.prompt),
                    "prompt": args.prompt, "kv": "fp32", "weights": "Q4_0F"},
-        "roofline": dict(lm_roof, kernel="gemv_f32_kernel (tied LM head 128256x2048 fp32)",
-                         bytes_per_launch=lm_bytes, avg_us=round(t_lm * 1e6, 2), traffic_detail=traffic_detail),
+        "roofline": stack_roof,
         "roofline_other": {
+            "lm_head_fp32": dict(lm_roof, kernel="gemv_f32_kernel (tied LM head 128256x2048 fp32)",
+                                 bytes_per_launch=lm_bytes, avg_us=round(t_lm * 1e6, 2), traffic_detail=traffic_detail),
             "q4_0f_swiglu_w1w3": dict(sw_roof, bytes_per_launch=sw_bytes, avg_us=round(t_sw * 1e6, 2)),
             "config1_q4_0_gemv_8192x2048": dict(q4_roof, bytes_per_launch=q4_bytes, avg_us=round(t_q4 * 1e6, 3)),
             "prefill_q4_0f_swiglu_m%d" % Mp: dict(swp_roof, flop_per_launch=swp_flop, avg_us=round(t_swp * 1e6, 2),
@@ -680,7 +883,8 @@ def main():
         "prefill_config2": prefill,
         "config3_ctx4096_quant_kv": cfg3,
         "config4_deepseek_mla_moe": cfg4,
-        "config5_rina_jamba": cfg5,
+        "config5_rina_jamba": cfg5.get("config5_rina_jamba"),
+        "config5_rina_jamba_fp32_cache": cfg5.get("config5_rina_jamba_fp32_cache"),
         "cpu_baseline": cpu,
         "tokens_head": tokens[:8],
     }

@@ -1276,24 +1276,52 @@ static void rope_hf_row(float* row, const float* ct, const float* st, int d, int
 /* one RINA-MLA layer on token rows [T, d] at positions start_pos.. (rina_mla_layer.cu:65-98) */
 typedef struct {
     const float *q, *qr, *kc, *vc;
+    const float *kcur, *vcur;   /* packed cache: this call's fp32 rows [T][Hkv*dq], [T][Hkv*dh] (else NULL) */
     float* att;
     int H, Hkv, dh, dhr, T, start_pos, w, nw;
 } rmla_rows_job;
 
 /* query rows t = w, w + nw, ... of the RINA-MLA attention: every head of
- * the row over keys 0..start_pos + t (flash_fp32 semantics) */
+ * the row over keys 0..start_pos + t (flash_fp32 semantics).  With kcur set
+ * (packed cache) kc / vc hold every row of the call dequantized; the worker
+ * reads them through a private copy in which row start_pos + t holds its
+ * fp32 values while that row attends, so each row sees the earlier rows
+ * through their packs and itself in fp32, as a row-by-row append would. */
 static void* rmla_rows_worker(void* arg) {
     rmla_rows_job* j = (rmla_rows_job*)arg;
     const int H = j->H, Hkv = j->Hkv, dh = j->dh, dhr = j->dhr, dq = dh + dhr, rep = H / Hkv;
+    const size_t kr = (size_t)Hkv * dq, vr = (size_t)Hkv * dh, rows = (size_t)j->start_pos + j->T;
+    const float *kc = j->kc, *vc = j->vc;
+    float *kp = NULL, *vp = NULL;
+    if (j->kcur) {
+        kp = (float*)malloc(rows * kr * 4);
+        vp = (float*)malloc(rows * vr * 4);
+        memcpy(kp, j->kc, rows * kr * 4);
+        memcpy(vp, j->vc, rows * vr * 4);
+        kc = kp;
+        vc = vp;
+    }
     float qv[512];
-    for (int t = j->w; t < j->T; t += j->nw)
+    for (int t = j->w; t < j->T; t += j->nw) {
+        const size_t pos = (size_t)j->start_pos + t;
+        if (kp) {
+            memcpy(kp + pos * kr, j->kcur + (size_t)t * kr, kr * 4);
+            memcpy(vp + pos * vr, j->vcur + (size_t)t * vr, vr * 4);
+        }
         for (int hh = 0; hh < H; hh++) {
             const int kv = hh / rep;
             memcpy(qv, j->q + ((size_t)t * H + hh) * dh, (size_t)dh * 4);
             memcpy(qv + dh, j->qr + ((size_t)t * H + hh) * dhr, (size_t)dhr * 4);
-            orc_attn_rows(qv, dq, j->kc + (size_t)kv * dq, Hkv * dq, j->vc + (size_t)kv * dh, Hkv * dh,
-                          j->att + ((size_t)t * H + hh) * dh, dh, j->start_pos + t, 1, dq, dh);
+            orc_attn_rows(qv, dq, kc + (size_t)kv * dq, Hkv * dq, vc + (size_t)kv * dh, Hkv * dh,
+                          j->att + ((size_t)t * H + hh) * dh, dh, (int)pos, 1, dq, dh);
         }
+        if (kp) {
+            memcpy(kp + pos * kr, j->kc + pos * kr, kr * 4);
+            memcpy(vp + pos * vr, j->vc + pos * vr, vr * 4);
+        }
+    }
+    free(kp);
+    free(vp);
     return NULL;
 }
 
@@ -1323,10 +1351,13 @@ static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
     /* q2k_q1v cache: position p attends to positions < p through the packed
      * cache (key content and values dequantized; the RoPE part is kept fp32)
      * and to itself through its fp32 rows, as the GQA composition reads its
-     * quantized cache (gqa_layer.cu:203-245).  Rows go in one at a time, so a
-     * T-row call equals T single-row calls. */
+     * quantized cache (gqa_layer.cu:203-245).  A T-row call equals T
+     * single-row calls: every row is packed on append (kernels/quantize.cu:
+     * 74-185) and stored dequantized, and each query row reads its own
+     * position's fp32 values (rmla_rows_worker). */
     const int qkv = c->rmla_kv_mode == ORC_KV_Q2K_Q1V;
-    const int rep_q = H / Hkv;
+    float* kcur = qkv ? (float*)malloc((size_t)T * Hkv * dq * 4) : NULL;
+    float* vcur = qkv ? (float*)malloc((size_t)T * Hkv * dh * 4) : NULL;
     for (int t = 0; t < T; t++) {
         const int pos = start_pos + t;
         if (L->rope_q_cos)
@@ -1341,43 +1372,33 @@ static void jamba_rmla(orc_jamba* m, int l, float* h, int T, int start_pos) {
         }
         memcpy(m->vc[l] + (size_t)pos * Hkv * dh, v + (size_t)t * Hkv * dh, (size_t)Hkv * dh * 4);
         if (qkv) {
-            /* quantize-on-append of the fp32 rows (kernels/quantize.cu:74-185) */
+            memcpy(kcur + (size_t)t * Hkv * dq, krow, (size_t)Hkv * dq * 4);
+            memcpy(vcur + (size_t)t * Hkv * dh, v + (size_t)t * Hkv * dh, (size_t)Hkv * dh * 4);
             for (int hh = 0; hh < Hkv; hh++) {
                 const size_t r = (size_t)pos * Hkv + hh;
                 orc_kv_quantize(ORC_KVF_Q2_1, k + ((size_t)t * Hkv + hh) * dh, m->kq[l] + r * (dh / 32) * 10, dh);
                 orc_kv_quantize(ORC_KVF_Q1_0, v + ((size_t)t * Hkv + hh) * dh, m->vq[l] + r * (dh / 32) * 6, dh);
-            }
-            /* this row's attention: earlier rows already hold their packed
-             * values, this one its fp32 values */
-            float qv[512];
-            for (int hh = 0; hh < H; hh++) {
-                const int kv = hh / rep_q;
-                memcpy(qv, q + ((size_t)t * H + hh) * dh, (size_t)dh * 4);
-                memcpy(qv + dh, qr + ((size_t)t * H + hh) * dhr, (size_t)dhr * 4);
-                orc_attn_rows(qv, dq, m->kc[l] + (size_t)kv * dq, Hkv * dq, m->vc[l] + (size_t)kv * dh, Hkv * dh,
-                              att + ((size_t)t * H + hh) * dh, dh, pos, 1, dq, dh);
-            }
-            /* from now on the row is read through the packed cache */
-            for (int hh = 0; hh < Hkv; hh++) {
-                const size_t r = (size_t)pos * Hkv + hh;
+                /* from now on the row is read through the packed cache */
                 orc_kv_dequant(ORC_KVF_Q2_1, m->kq[l] + r * (dh / 32) * 10, m->kc[l] + r * dq, dh);
                 orc_kv_dequant(ORC_KVF_Q1_0, m->vq[l] + r * (dh / 32) * 6, m->vc[l] + r * dh, dh);
             }
         }
     }
-    if (!qkv) {   /* query rows are independent: rows t = w, w + nw, ... per worker */
+    {   /* query rows are independent: rows t = w, w + nw, ... per worker */
         rmla_rows_job jobs[64];
         pthread_t th[64];
         int nw = nt > 0 ? nt : orc_num_threads();
         if (nw > T) nw = T;
         if (nw > 64) nw = 64;
         for (int w = 0; w < nw; w++) {
-            jobs[w] = (rmla_rows_job){q, qr, m->kc[l], m->vc[l], att, H, Hkv, dh, dhr, T, start_pos, w, nw};
+            jobs[w] = (rmla_rows_job){q, qr, m->kc[l], m->vc[l], kcur, vcur, att, H, Hkv, dh, dhr, T, start_pos, w, nw};
             if (w) pthread_create(&th[w], NULL, rmla_rows_worker, &jobs[w]);
         }
         rmla_rows_worker(&jobs[0]);
         for (int w = 1; w < nw; w++) pthread_join(th[w], NULL);
     }
+    free(kcur);
+    free(vcur);
     orc_linear(L->c_proj, L->qt, att, tmp, T, d, H * dh, nt);                   /* :87 (out of place) */
     orc_add(h, h, tmp, T * d);
     free(a); free(cq); free(q); free(k); free(v); free(qr); free(kr); free(att); free(tmp);

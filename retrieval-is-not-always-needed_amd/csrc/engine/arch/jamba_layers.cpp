@@ -220,10 +220,16 @@ struct RMLAImpl {
         qt = (int)L.qt;
         ws_bytes = rina_hip_dq_attention_workspace(H, dh + dhr, max_seq);
         const size_t sc = (size_t)dc + H * dhr + Hkv * dhr + H * dh + 2 * Hkv * dh + H * dh;
-        // the model's kv_quant_mode: "fp32" (or none) or "q2k_q1v" (q2 K / q1 V,
-        // rina/model_jamba_qw2.py:175-177); other modes have no RINA-MLA form
-        const int mode = cfg.kv_quant_mode.empty() ? RINA_KV_FP32 : kv_mode_from_name(cfg.kv_quant_mode.c_str());
-        if (mode != RINA_KV_FP32 && mode != RINA_KV_Q2K_Q1V) return false;
+        // kv_quant_mode applies to GQA caches only; the reference's RINA-MLA
+        // layer keeps fp32 rows whatever it says (rina_mla_layer.cu:65-98).
+        // The packed q2 K / q1 V cache is the engine's own opt-in key,
+        // rina_mla_kv_mode "q2k_q1v" (queries and the current position stay
+        // fp32; only earlier positions are read through their packs)
+        const std::string& km = cfg.rina_mla_kv_mode;
+        int mode;
+        if (km.empty() || km == "fp32") mode = RINA_KV_FP32;
+        else if (km == "q2k_q1v") mode = RINA_KV_Q2K_Q1V;
+        else return false;
         kv_mode = mode;
         const size_t kb = rina_hip_dq_kv_region_bytes(mode, 0, max_seq, Hkv, dh, dhr, dh);
         const size_t vb = rina_hip_dq_kv_region_bytes(mode, 1, max_seq, Hkv, dh, dhr, dh);

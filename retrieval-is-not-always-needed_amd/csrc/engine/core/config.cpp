@@ -73,6 +73,7 @@ void set_field(ModelConfig& c, const std::string& k, const std::string& v) {
     else if (k == "hidden_dim" || k == "intermediate_size") I(c.hidden_dim);
     else if (k == "weight_tying") c.weight_tying = (v == "true");
     else if (k == "kv_quant_mode") c.kv_quant_mode = v;
+    else if (k == "rina_mla_kv_mode") c.rina_mla_kv_mode = v;
     else if (k == "use_pre_rope_k") c.use_pre_rope_k = (v == "true" || v == "1");
     else if (k == "kv_lora_rank") I(c.kv_lora_rank);
     else if (k == "qk_nope_head_dim") I(c.qk_nope_dim);

@@ -23,7 +23,11 @@ struct ModelConfig {
     int vocab_size = 0, max_seq_len = 0;
     int hidden_dim = 0;            // SwiGLU intermediate (0: from w1's shape)
     bool weight_tying = true;
-    std::string kv_quant_mode = "fp32";
+    std::string kv_quant_mode = "fp32";   // GQA caches only (infer_gqa.cpp), as in the reference
+    // RINA-MLA (Jamba) cache form, an engine extension with no reference key:
+    // "fp32" (the reference's numerics) or "q2k_q1v" (q2_1 key content, q1_0
+    // values, packed on append).  kv_quant_mode never changes RINA-MLA layers.
+    std::string rina_mla_kv_mode = "fp32";
     bool use_pre_rope_k = false;
     // MLA / MoE (DeepSeek-V2-Lite shape)
     int kv_lora_rank = 0, qk_nope_dim = 0, qk_rope_dim = 0, v_head_dim = 0;

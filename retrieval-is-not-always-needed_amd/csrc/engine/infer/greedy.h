@@ -20,6 +20,7 @@ struct DeviceGreedyInference : Inference {
     hipGraphExec_t graph[2] = {nullptr, nullptr};   // positions below / from graph_split()
     hipStream_t graph_stream[2] = {nullptr, nullptr};
     int pos_hint = -1;         // largest position of the next device-position run (-1: unknown)
+    int h_pos = 0;             // host source of the first position's copy: outlives any queued copy
     std::string tag = "infer";
 
     ~DeviceGreedyInference() override {
@@ -95,14 +96,20 @@ struct DeviceGreedyInference : Inference {
             }
         int rc = ensure_cap(n);
         if (rc) return rc;
-        if (hipMemcpyAsync(d_ids, prompt, sizeof(int) * n, hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
-        int p0 = n - 1;
-        if (hipMemcpyAsync(d_pos, &p0, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess) return RINA_ERR_HIP;
-        if ((rc = run(d_ids, nullptr, n, 0, lm_buffer(), true, s))) return rc;
-        if ((rc = argmax(s))) return rc;
+        // the caller's prompt is a host source of queued copies: every return
+        // below waits for the stream first, so no copy outlives it
+        auto drain = [&](int r) { (void)hipStreamSynchronize(s); return r; };
+        if (hipMemcpyAsync(d_ids, prompt, sizeof(int) * n, hipMemcpyHostToDevice, s) != hipSuccess)
+            return drain(RINA_ERR_HIP);
+        h_pos = n - 1;
+        if (hipMemcpyAsync(d_pos, &h_pos, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess)
+            return drain(RINA_ERR_HIP);
+        if ((rc = run(d_ids, nullptr, n, 0, lm_buffer(), true, s))) return drain(rc);
+        if ((rc = argmax(s))) return drain(rc);
         if (hipStreamSynchronize(s) != hipSuccess) return RINA_ERR_HIP;
         gen_len = n + 1;
-        if (hipMemcpyAsync(out, d_ids + n, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return RINA_ERR_HIP;
+        if (hipMemcpyAsync(out, d_ids + n, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess)
+            return drain(RINA_ERR_HIP);
         if (steps == 1) {
             if (decode_ms) *decode_ms = 0.f;
             return hipStreamSynchronize(s) == hipSuccess ? RINA_OK : RINA_ERR_HIP;

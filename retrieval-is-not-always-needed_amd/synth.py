@@ -414,13 +414,14 @@ class SynthJamba:
         torch = _torch()
         c = self.cfg = dict(cfg)
         self.max_seq = max_seq
+        self.kv_mode = kv_mode
         self.types = jamba_types(c["n_layers"])
         self.host, self.dev = {}, {}
         d, H, Hkv, dh, dhr, dc, hd, V = (c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["d_h_r"], c["d_c"],
                                          c["hidden_dim"], c["vocab_size"])
         header = {"name": c["name"], "dim": d, "n_layers": c["n_layers"], "n_heads": H, "n_kv_heads": Hkv,
                   "head_dim": dh, "d_h_r": dhr, "d_c": dc, "ssm_steps": c["ssm_steps"], "vocab_size": V,
-                  "max_seq_len": max_seq, "hidden_dim": hd, "kv_quant_mode": kv_mode,
+                  "max_seq_len": max_seq, "hidden_dim": hd, "rina_mla_kv_mode": kv_mode,
                   "layers": [{"type": t} for t in self.types]}
         eng = load_engine()
         self._eng = eng
@@ -485,8 +486,11 @@ class SynthJamba:
         q4 = lambda n: n // 32 * 18
         mlp = 3 * q4(hd * d)
         ssm = q4(dc * d) + c["ssm_steps"] * (q4(H * dh * dc) + q4(H * dc)) + q4(d * (d + H * dh))
+        # cache bytes per position and KV head: fp32 [k | kr] and v, or the
+        # packed form (two q2_1 blocks of k, kr in fp32, two q1_0 records of v)
+        rec = (dh + dhr + dh) * 4 if self.kv_mode != "q2k_q1v" else dh // 32 * 10 + dhr * 4 + dh // 32 * 6
         att = (q4(dc * d) + q4(H * dh * dc) + q4(Hkv * dh * dc) + q4(Hkv * dh * Hkv * dh) + q4(H * dhr * d) +
-               q4(Hkv * dhr * d) + q4(d * H * dh) + (pos + 1) * Hkv * (dh + dhr + dh) * 4)
+               q4(Hkv * dhr * d) + q4(d * H * dh) + (pos + 1) * Hkv * rec)
         n_att = sum(1 for t in self.types if t != "inertia_wave_ssm")
         n_ssm = len(self.types) - n_att
         return n_ssm * (ssm + mlp) + n_att * (att + mlp) + V * d * 4

@@ -154,16 +154,20 @@ def test_jamba_config5_shape_greedy(rina, orc):
         sm.close()
 
 
-def test_jamba_config5_full_context_128_steps(rina, orc):
+@pytest.mark.parametrize("kv_mode", ["fp32", "q2k_q1v"])
+def test_jamba_config5_full_context_128_steps(rina, orc, kv_mode):
     """Config 5 as specified: the full Jamba shape at context 2048, a
-    1900-token seeded prompt, then 128 greedy steps (positions 1900..2027).
-    The oracle runs its own 1900-token prefill and its state-carrying
-    decode (proven equal to the reference's full recompute); all 129
-    tokens must match, every step's top-2 margin must clear twice the 1e-5
+    1900-token seeded prompt, then 128 greedy steps (positions 1900..2027),
+    with the fp32 RINA-MLA cache (the reference's numerics) and with the q2 K
+    / q1 V cache (rina_mla_kv_mode "q2k_q1v": key content q2_1, values q1_0,
+    packed on append; queries and the current position fp32).  The oracle
+    runs its own 1900-token prefill in the same mode and its state-carrying
+    decode (proven equal to the reference's full recompute); all 129 tokens
+    must match, every step's top-2 margin must clear twice the 1e-5
     tolerance, and the tokens must be varied."""
     synth = importlib.import_module("rina_amd.synth")
     n_prompt, steps, max_seq = 1900, 128, 2048
-    sm = synth.SynthJamba(seed=3, max_seq=max_seq, keep_host=True)
+    sm = synth.SynthJamba(seed=3, max_seq=max_seq, keep_host=True, kv_mode=kv_mode)
     try:
         eng = rina.load_engine()
         V = sm.cfg["vocab_size"]
@@ -175,7 +179,7 @@ def test_jamba_config5_full_context_128_steps(rina, orc):
         eng.rina_infer_destroy(inf)
         got = list(out)
         m, hold = orc.jamba_from_tensors(sm.cfg, sm.host, sm.types, jt.Q4_0, max_seq,
-                                         min(os.cpu_count() or 1, 16))
+                                         min(os.cpu_count() or 1, 16), kv_mode=kv_mode)
         L = orc.load()
         lg = np.zeros(V, np.float32)
         ref, margins = [], []
@@ -189,11 +193,38 @@ def test_jamba_config5_full_context_128_steps(rina, orc):
             pos += T
             ids, T = np.array([tok], np.int32), 1
         L.orc_jamba_destroy(m)
+        print("config 5 %s: tokens %s, min top-2 margin %.2e" % (kv_mode, got[:8], min(margins)))
         assert got == ref, "first divergence at step %d" % next(i for i in range(steps + 1) if got[i] != ref[i])
         assert min(margins) > 2 * REL_TOL, "near tie at step %d (%.2e)" % (int(np.argmin(margins)), min(margins))
         assert len(set(got)) >= 16
     finally:
         sm.close()
+
+
+@pytest.mark.parametrize("mode", ["q8", "q4", "q4k_q2v", "q2", "q2k_q1v"])
+def test_jamba_kv_quant_mode_keeps_fp32_rmla(rina, tiny_jamba, mode):
+    """kv_quant_mode names the GQA cache; the reference's RINA-MLA layer keeps
+    fp32 rows whatever it says (rina_mla_layer.cu:65-98, infer_gqa.cpp).  A
+    hybrid created with each reference mode initializes and gives the
+    fp32-cache model's logits, bit for bit."""
+    import torch
+    hm, tensors, max_seq = tiny_jamba
+    eng = rina.load_engine()
+    V = jt.CFG["vocab_size"]
+    ids = np.array([5, 17, 3, 90, 42, 7], np.int32)
+    outs = []
+    for kv in (None, mode):
+        inf = hm.infer("gqa", kv_mode=kv, max_seq=max_seq)
+        lg = empty(len(ids) * V)
+        rina.check(eng.rina_infer_forward(inf, torch.from_numpy(ids).cuda().data_ptr(), lg.data_ptr(), 1, len(ids),
+                                          0, stream()), "forward")
+        x = np.array([11], np.int32)
+        l1 = empty(V)
+        rina.check(eng.rina_infer_forward(inf, torch.from_numpy(x).cuda().data_ptr(), l1.data_ptr(), 1, 1, len(ids),
+                                          stream()), "decode")
+        outs.append(np.concatenate([host(lg), host(l1)]))
+        eng.rina_infer_destroy(inf)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
 @pytest.mark.parametrize("P,use_dpos", [(0, False), (9, False), (70, True), (300, False)])
@@ -283,7 +314,7 @@ def test_jamba_q2k_q1v_cache_greedy(rina, orc, use_graph):
     qts = {n: (6 if a.dtype == np.float32 else jt.Q4_0) for n, a in tensors.items()}
     up = {n: (qts[n], shapes[n], tensors[n]) for n in tensors}
     hdr = header(max_seq)
-    hdr["kv_quant_mode"] = "q2k_q1v"
+    hdr["rina_mla_kv_mode"] = "q2k_q1v"
     hm = synth.HostModel(hdr, up)
     try:
         eng = rina.load_engine()
@@ -327,43 +358,3 @@ def test_jamba_q2k_q1v_cache_greedy(rina, orc, use_graph):
         assert far > 1e-3, far
     finally:
         hm.close()
-
-
-def test_jamba_config5_q2k_q1v_cache(rina, orc):
-    """Config 5's "q2 K / q1 V cache": the full Jamba shape with the packed
-    RINA-MLA cache, a 300-token prompt and 64 greedy steps, identical to the
-    oracle in the same mode (its own prefill), with varied tokens and every
-    step's top-2 margin above twice the 1e-5 tolerance."""
-    synth = importlib.import_module("rina_amd.synth")
-    n_prompt, steps, max_seq = 300, 64, 384
-    sm = synth.SynthJamba(seed=3, max_seq=max_seq, keep_host=True, kv_mode="q2k_q1v")
-    try:
-        eng = rina.load_engine()
-        V = sm.cfg["vocab_size"]
-        prompt = np.random.default_rng(7).integers(0, V, n_prompt).astype(np.int32)
-        inf = sm.infer()
-        out = (C.c_int * (steps + 1))()
-        rina.check(eng.rina_infer_generate(inf, prompt.ctypes.data_as(C.POINTER(C.c_int)), n_prompt, steps + 1, out,
-                                           1, stream(), None), "generate")
-        eng.rina_infer_destroy(inf)
-        got = list(out)
-        m, hold = orc.jamba_from_tensors(sm.cfg, sm.host, sm.types, jt.Q4_0, max_seq, min(os.cpu_count() or 1, 16),
-                                         kv_mode="q2k_q1v")
-        L = orc.load()
-        lg = np.zeros(V, np.float32)
-        ref, margins = [], []
-        ids, T, pos = prompt, n_prompt, 0
-        for s in range(steps + 1):
-            assert L.orc_jamba_forward(m, ids.ctypes.data, T, pos, lg.ctypes.data, 1) == 0
-            top = np.argsort(lg)[::-1][:2]
-            margins.append(float(lg[top[0]] - lg[top[1]]) / float(np.max(np.abs(lg))))
-            tok = L.orc_argmax(lg.ctypes.data, V)
-            ref.append(tok)
-            pos += T
-            ids, T = np.array([tok], np.int32), 1
-        L.orc_jamba_destroy(m)
-        assert got == ref, "first divergence at step %d" % next(i for i in range(steps + 1) if got[i] != ref[i])
-        assert min(margins) > 2 * REL_TOL
-        assert len(set(got)) >= 16
-    finally:
-        sm.close()

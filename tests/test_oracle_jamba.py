@@ -55,9 +55,9 @@ def test_tiny_jamba_greedy_matches_float64(orc):
     orc.load().orc_jamba_destroy(m)
 
 
-def _qmodel(orc, seed, kv_mode, max_seq=48):
+def _qmodel(orc, seed, kv_mode, max_seq=48, nthreads=1):
     tensors, mats, shapes = jt.build(orc, seed=seed, max_pos=max_seq)
-    m, hold = orc.jamba_from_tensors(jt.CFG, tensors, jt.TYPES, jt.Q4_0, max_seq, nthreads=1, kv_mode=kv_mode)
+    m, hold = orc.jamba_from_tensors(jt.CFG, tensors, jt.TYPES, jt.Q4_0, max_seq, nthreads=nthreads, kv_mode=kv_mode)
     return m, hold, mats
 
 
@@ -89,6 +89,12 @@ def test_q2k_q1v_rmla_cache(orc):
     for t in range(T):
         L.orc_jamba_forward(ms2, ids[t:].ctypes.data, 1, t, inc.ctypes.data, 1)
     assert np.array_equal(inc.view(np.uint32), full.view(np.uint32))
+    # the prompt's query rows split over 3 worker threads: the same logits, bit for bit
+    mt, ht, _ = _qmodel(orc, 24, "q2k_q1v", nthreads=3)
+    par = np.zeros(V, np.float32)
+    L.orc_jamba_forward(mt, ids.ctypes.data, T, 0, par.ctypes.data, 1)
+    assert np.array_equal(par.view(np.uint32), full.view(np.uint32))
+    L.orc_jamba_destroy(mt)
     rmla = [l for l, ty in enumerate(jt.TYPES) if ty not in ("inertia_wave_ssm", "ssm")]
     nb = T * Hkv * (dh // 32)
     mf, hf, _ = _qmodel(orc, 24, "fp32")
