@@ -438,6 +438,12 @@ int rina_hip_argmax_ws(const float* x, int n, int* out_idx, int* ids_out,
  * same byte count. */
 int rina_hip_read_probe(const void* src, int64_t bytes, int grid, float* sink, void* stream);
 
+/* Cache warm-up, no counterpart in the reference: one launch of `grid`
+ * 256-thread workgroups that reads bytes (rounded down to 16) of src
+ * (16-byte aligned) with cache-allocating loads and writes nothing, so a
+ * later kernel finds them in the memory-side cache. */
+int rina_hip_prefetch(const void* src, int64_t bytes, int grid, void* stream);
+
 /* Library version / self-description. */
 const char* rina_hip_version(void);
 

@@ -381,6 +381,8 @@ struct DirectBlk {
     uint32_t nib[RB][2][4];
     int seg[RB], row[RB];
     bool ok[RB];
+    float yres[RB];     // one matrix: y of the group's rows (lane 0 finishes them, one wave per row)
+    float yep;          // one matrix, 2-4 waves per row: y of the row this thread finishes
 };
 
 // Q2_K in the direct kernel: a lane's column is 32 consecutive values of a
@@ -402,6 +404,8 @@ struct DirectBlkQ2 {
     int sh[RB];             // 2g
     int seg[RB], row[RB];
     bool ok[RB];
+    float yres[RB];         // as DirectBlk
+    float yep;
 };
 
 template <int FMT, int RB>
@@ -518,17 +522,42 @@ __device__ __forceinline__ void direct_issue(const GemvArgs& a, const Segs& S, i
     }
 }
 
-template <int NMAT, typename Segs>
+// The output words a one-matrix launch's epilogue finishes, loaded with the
+// weights of their row group instead of after the row sums: the residual
+// add then costs no memory round trip at the end of the launch.  Every lane
+// loads (the finishing lanes use theirs; rows past the end read row 0 of
+// their segment), so the load counters stay exact.  Each output word is read
+// and written by one thread only, and never by another workgroup.
+template <int WPR, int NMAT, int RB, typename Segs, typename Blk>
+__device__ __forceinline__ void direct_yload(const GemvArgs& a, const Segs& S, int it, Blk& b) {
+    if constexpr (NMAT == 1) {
+        if constexpr (WPR == 1) {
+#pragma unroll
+            for (int i = 0; i < RB; i++) b.yres[i] = gld(S.out(b.seg[i]) + (b.row[i] >= 0 ? b.row[i] : 0));
+        } else {
+            constexpr int RPI = 4 / WPR;
+            const int tid = threadIdx.x;
+            const int k = tid < RPI * RB ? tid : 0;
+            const int grp = it * RPI + k / RB, vr = grp * RB + k % RB;
+            const bool ok = grp < a.total_tiles && vr < a.R;
+            const int sg = S.seg_of(ok ? vr : 0);
+            b.yep = gld(S.out(sg) + (ok ? vr - S.t0(sg) : 0));
+        }
+    }
+}
+
+template <int NMAT, bool YL, typename Segs>
 __device__ __forceinline__ void direct_epilogue(const GemvArgs& a, const Segs& S, int sg, int n,
-                                                const float (&v)[2]) {
+                                                const float (&v)[2], float yold) {
     float* y = S.out(sg) + n;
     if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
+    else if (YL) gst(y, yold + v[0]);                   // YL: exactly the residual epilogue
     else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
     else gst(y, v[0]);
 }
 
 // Row sums of one row group and their epilogue.
-template <int FMT, int WPR, int NMAT, int RB, typename Segs>
+template <int FMT, int WPR, int NMAT, int RB, bool YL, typename Segs>
 __device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S, const DCols<FMT>& xc,
                                                const DirectBlkT<FMT, RB>& cur, int it, int rs, int cp,
                                                float (*red)[RB * NMAT][WPR]) {
@@ -560,7 +589,7 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S,
             for (int i = 0; i < RB; i++)
                 if (cur.row[i] >= 0) {
                     float v[2] = {part[i][0], NMAT == 2 ? part[i][1] : 0.f};
-                    direct_epilogue<NMAT>(a, S, cur.seg[i], cur.row[i], v);
+                    direct_epilogue<NMAT, YL>(a, S, cur.seg[i], cur.row[i], v, YL ? cur.yres[i] : 0.f);
                 }
         }
     } else {
@@ -581,7 +610,7 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S,
                 for (int m = 0; m < NMAT; m++)
 #pragma unroll
                     for (int c = 0; c < WPR; c++) v[m] += red[r2][i * NMAT + m][c];
-                direct_epilogue<NMAT>(a, S, sg, vr - S.t0(sg), v);
+                direct_epilogue<NMAT, YL>(a, S, sg, vr - S.t0(sg), v, YL ? cur.yep : 0.f);
             }
         }
         __syncthreads();
@@ -590,10 +619,13 @@ __device__ __forceinline__ void direct_consume(const GemvArgs& a, const Segs& S,
 
 // GemvArgs reuse for this kernel: total_tiles = number of row groups,
 // R = number of virtual rows, seg[s].tile0 = first virtual row of segment s.
-// Workgroup iterations alternate between two register sets (A, B): the next
-// group's loads are issued before the current group is reduced, and each
-// path has its own straight-line code so the load counters stay exact.
-template <int FMT, int WPR, int NMAT, int PRO, int RB, int NS>
+// ITERS == 1: one iteration per workgroup (the grid covers every row
+// group), straight-line code.  ITERS == 0: iterations alternate between two
+// register sets (A, B), the next group's loads issued before the current
+// group is reduced; each path has its own straight-line code so the load
+// counters stay exact.  YL: residual epilogue, the old output words loaded
+// with each group's weights.
+template <int FMT, int WPR, int NMAT, int PRO, int RB, int NS, int ITERS, bool YL>
 __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
     constexpr int RPI = 4 / WPR;                 // row groups per workgroup iteration
     __shared__ float red[RPI][RB * NMAT][WPR];
@@ -612,37 +644,52 @@ __global__ __launch_bounds__(kWG) void gemv_direct_kernel(GemvArgs a) {
     PrepRaw<TPC, PRO> raw;
     const PrepSrc src{a.x, a.nw, a.K, a.eps, a.xn};
     wg_prep_load<TPC, PRO>(src, raw);
-    int it = blockIdx.x;
-    DirectBlkT<FMT, RB> A, B;
-    direct_issue<FMT, NMAT, RB>(a, S, it * RPI + rs, u, active, A);
-    DCols<FMT> xc;
-    if constexpr (WPR == 4) {
-        // u == threadIdx.x: every thread prepares its own column
-        __shared__ float red[8];
-        own_prep_x<FMT, PRO>(src, raw, red, xc);
+    auto prep_cols = [&](DCols<FMT>& xc) {
+        if constexpr (WPR == 4) {
+            // u == threadIdx.x: every thread prepares its own column
+            __shared__ float red[8];
+            own_prep_x<FMT, PRO>(src, raw, red, xc);
+        } else {
+            __shared__ PrepLds prep;
+            wg_prep_x<FMT, TPC, PRO>(src, raw, prep);
+            read_cols<FMT>(prep, u, active, xc);
+        }
+    };
+    if constexpr (ITERS == 1) {
+        DirectBlkT<FMT, RB> A;
+        direct_issue<FMT, NMAT, RB>(a, S, blockIdx.x * RPI + rs, u, active, A);
+        if constexpr (YL) direct_yload<WPR, NMAT, RB>(a, S, blockIdx.x, A);
+        DCols<FMT> xc;
+        prep_cols(xc);
+        direct_consume<FMT, WPR, NMAT, RB, YL>(a, S, xc, A, blockIdx.x, rs, cp, red);
     } else {
-        __shared__ PrepLds prep;
-        wg_prep_x<FMT, TPC, PRO>(src, raw, prep);
-        read_cols<FMT>(prep, u, active, xc);
-    }
+        int it = blockIdx.x;
+        DirectBlkT<FMT, RB> A, B;
+        direct_issue<FMT, NMAT, RB>(a, S, it * RPI + rs, u, active, A);
+        if constexpr (YL) direct_yload<WPR, NMAT, RB>(a, S, it, A);
+        DCols<FMT> xc;
+        prep_cols(xc);
 
-    for (;;) {
-        if ((it + G) * RPI < ngrp) {
-            direct_issue<FMT, NMAT, RB>(a, S, (it + G) * RPI + rs, u, active, B);
-            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, A, it, rs, cp, red);
-        } else {
-            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, A, it, rs, cp, red);
-            break;
+        for (;;) {
+            if ((it + G) * RPI < ngrp) {
+                direct_issue<FMT, NMAT, RB>(a, S, (it + G) * RPI + rs, u, active, B);
+                if constexpr (YL) direct_yload<WPR, NMAT, RB>(a, S, it + G, B);
+                direct_consume<FMT, WPR, NMAT, RB, YL>(a, S, xc, A, it, rs, cp, red);
+            } else {
+                direct_consume<FMT, WPR, NMAT, RB, YL>(a, S, xc, A, it, rs, cp, red);
+                break;
+            }
+            it += G;
+            if ((it + G) * RPI < ngrp) {
+                direct_issue<FMT, NMAT, RB>(a, S, (it + G) * RPI + rs, u, active, A);
+                if constexpr (YL) direct_yload<WPR, NMAT, RB>(a, S, it + G, A);
+                direct_consume<FMT, WPR, NMAT, RB, YL>(a, S, xc, B, it, rs, cp, red);
+            } else {
+                direct_consume<FMT, WPR, NMAT, RB, YL>(a, S, xc, B, it, rs, cp, red);
+                break;
+            }
+            it += G;
         }
-        it += G;
-        if ((it + G) * RPI < ngrp) {
-            direct_issue<FMT, NMAT, RB>(a, S, (it + G) * RPI + rs, u, active, A);
-            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, B, it, rs, cp, red);
-        } else {
-            direct_consume<FMT, WPR, NMAT, RB>(a, S, xc, B, it, rs, cp, red);
-            break;
-        }
-        it += G;
     }
 }
 
@@ -1423,7 +1470,23 @@ int launch_direct(GemvArgs& a, hipStream_t st) {
     // 8192 x 2048 at 1 row: 7.33 / 6.44 us), 8 rows take 2
     int per_cu = FMT == FMT_Q2_K ? (RB >= 4 ? (NMAT == 2 ? 2 : 5) : 4) : (RB >= 8 ? 2 : 3);
     int grid = wgs < cus * per_cu ? wgs : cus * per_cu;
-    hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB, NS>), dim3(grid), dim3(kWG), 0, st, a);
+    // one iteration per workgroup: straight-line code; more: the two-set loop.
+    // Measured on the config-2 shapes: every iteration's loads issued at
+    // entry (2-3 iterations) made the launches slower (SwiGLU 8192 x 2048
+    // 6.5 -> 7.9 us, config 1 4.4 -> 5.1 us): the activation prep then waits
+    // behind the weight stream.
+    const bool one = wgs <= grid;
+    // residual epilogue: the old output words are loaded with the weights
+    // (W_o 3.16 -> 2.99 us, W2 5.5 -> 5.2 us); a store epilogue loads none
+    // (the same loads cost the fused q/k/v 3.35 -> 3.75 us)
+    const bool yl = NMAT == 1 && a.epi == RINA_EPI_ADD;
+    if (one) {
+        if (yl) hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB, NS, 1, true>), dim3(grid), dim3(kWG), 0, st, a);
+        else hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB, NS, 1, false>), dim3(grid), dim3(kWG), 0, st, a);
+    } else {
+        if (yl) hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB, NS, 0, true>), dim3(grid), dim3(kWG), 0, st, a);
+        else hipLaunchKernelGGL((gemv_direct_kernel<FMT, WPR, NMAT, PRO, RB, NS, 0, false>), dim3(grid), dim3(kWG), 0, st, a);
+    }
     return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
 }
 
