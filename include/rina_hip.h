@@ -431,6 +431,36 @@ int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out,
 int rina_hip_argmax_ws(const float* x, int n, int* out_idx, int* ids_out,
                        int* d_pos, void* key_slot, void* stream);
 
+/* The greedy decode step's tail in fewer launches (no counterpart in the
+ * reference, whose sample() runs on the host, main.cpp:139-146, and whose
+ * next step starts with the embedding launch, ops/embedding.cu:6-230).
+ *
+ * rina_hip_linear_argmax: the fp32 LM head (rina_hip_linear_fused with one
+ * segment, M = 1, the store epilogue and the optional norm prologue; the
+ * same logits) that also writes the largest argmax key of the rows each of
+ * its workgroups stored into keys[0 .. *nkeys) (8-byte aligned device
+ * memory of max_keys keys; RINA_ERR_WORKSPACE when the launch needs more:
+ * at most 8 per compute unit).  Keys are 64-bit: the order-preserving bits
+ * of the value, then the complemented index (strict ">" from -1e10, the
+ * lowest index among equal values, -0 as +0).  Other quant types return
+ * RINA_ERR_QTYPE.
+ *
+ * rina_hip_argmax_partial: the first half of rina_hip_argmax_ws, merging
+ * x's candidates into key_slot (which must hold zero).
+ *
+ * rina_hip_argmax_embed: the winner of keys[0 .. nkeys) (cleared again when
+ * reset, as a key slot must be), then what rina_hip_argmax_ws does with it
+ * (out_idx, ids_out[*d_pos + 1], *d_pos + 1; each optional), then row id of
+ * the embedding table emb (quant type emb_qt, rows of d values, vocab rows;
+ * ids outside it clamped) into h[0 .. d): the next decode step's input,
+ * so that step needs no embedding launch. */
+int rina_hip_linear_argmax(const rina_linear_seg* seg, int quant_type, const float* input, int K,
+                           int prologue, const float* norm_weight, float eps, void* keys,
+                           int max_keys, int* nkeys, void* stream);
+int rina_hip_argmax_partial(const float* x, int n, void* key_slot, void* stream);
+int rina_hip_argmax_embed(void* keys, int nkeys, int reset, int* out_idx, int* ids_out, int* d_pos,
+                          const void* emb, int emb_qt, float* h, int d, int vocab, void* stream);
+
 /* Measurement helper, no counterpart in the reference: one launch of
  * `grid` 256-thread workgroups that stream-reads bytes (rounded down to
  * 16) of src (16-byte aligned) and writes grid floats to sink.  Its time

@@ -5,6 +5,11 @@
 // captured once as a HIP graph and replayed.  An orchestrator whose kernels
 // differ below and above some position (graph_split()) gets one graph per
 // side, each captured with the bound of the positions it replays at.
+// A decode step's tail is fused: the step's last launch (argmax + embedding)
+// also writes the next step's embedding row into h, so a step is layers ->
+// LM head -> argmax_embed (with an fp32 LM head the argmax's per-workgroup
+// keys come out of the LM head launch itself); decode_more() embeds the
+// first step's id once before its loop.
 #pragma once
 #include <hip/hip_runtime_api.h>
 #include <string>
@@ -22,12 +27,17 @@ struct DeviceGreedyInference : Inference {
     int pos_hint = -1;         // largest position of the next device-position run (-1: unknown)
     int h_pos = 0;             // host source of the first position's copy: outlives any queued copy
     std::string tag = "infer";
+    static constexpr int kMaxKeys = 8192;   // argmax keys of a fused LM head: one per workgroup (<= 8 per CU)
+    unsigned long long* d_keys = nullptr;
+    int n_keys = 0;            // keys the last fused LM head wrote (0: the LM head was not fused)
+    bool fuse_tail = false;    // set while a decode step is issued: run() skips the embedding and may fuse the argmax
 
     ~DeviceGreedyInference() override {
         for (auto& g : graph)
             if (g) (void)hipGraphExecDestroy(g);
         if (d_ids) (void)hipFree(d_ids);
         if (d_pos) (void)hipFree(d_pos);
+        if (d_keys) (void)hipFree(d_keys);
     }
 
     // embedding -> layers -> final norm -> LM head for T ids at start_pos
@@ -41,10 +51,34 @@ struct DeviceGreedyInference : Inference {
     virtual float* lm_buffer() = 0;
     // first position of the second decode graph (0: one graph for all)
     virtual int graph_split() const { return 0; }
+    // the embedding table, the activation row h and its width, for the fused tail
+    virtual const WeightTensor* emb_table() const = 0;
+    virtual float* h_buffer() = 0;
+    virtual int model_dim() const = 0;
 
     bool alloc_ids() {
         return hipMalloc(&d_ids, sizeof(int) * (max_seq + 1)) == hipSuccess &&
-               hipMalloc(&d_pos, 4 * sizeof(int)) == hipSuccess && hipMemset(d_pos, 0, 4 * sizeof(int)) == hipSuccess;
+               hipMalloc(&d_pos, 4 * sizeof(int)) == hipSuccess && hipMemset(d_pos, 0, 4 * sizeof(int)) == hipSuccess &&
+               hipMalloc(&d_keys, sizeof(unsigned long long) * kMaxKeys) == hipSuccess;
+    }
+    // LM head of a decode step with the argmax keys fused in, where the
+    // head is fp32 (otherwise the plain launch; n_keys stays 0)
+    int head_launch(const rina_linear_seg& seg, int qt, const float* x, int K, int pro, const float* nw, hipStream_t s) {
+        if (fuse_tail && qt == RINA_QT_FP32)
+            return rina_hip_linear_argmax(&seg, qt, x, K, pro, nw, 1e-5f, d_keys, kMaxKeys, &n_keys, s);
+        return rina_hip_linear_fused(&seg, 1, qt, x, 1, K, RINA_EPI_STORE, pro, nw, 1e-5f, s);
+    }
+    // argmax of the step's logits and the next step's embedding row, one
+    // launch after the fused LM head, two after a plain one
+    int argmax_embed(hipStream_t s) {
+        const WeightTensor* e = emb_table();
+        if (n_keys > 0)
+            return rina_hip_argmax_embed(d_keys, n_keys, 0, nullptr, d_ids, d_pos, e->data, (int)e->quant_type,
+                                         h_buffer(), model_dim(), vocab, s);
+        int rc = rina_hip_argmax_partial(lm_buffer(), vocab, d_pos + 2, s);
+        if (rc) return rc;
+        return rina_hip_argmax_embed(d_pos + 2, 1, 1, nullptr, d_ids, d_pos, e->data, (int)e->quant_type, h_buffer(),
+                                     model_dim(), vocab, s);
     }
     // argmax with this inference's own key slot: two inferences decoding on
     // different streams never share it
@@ -80,10 +114,15 @@ struct DeviceGreedyInference : Inference {
         return RINA_OK;
     }
 
+    // one decode step: h holds the step's embedding row (written by the
+    // previous step's tail, or by decode_more() before its first step)
     int decode_step(hipStream_t s) {
+        fuse_tail = true;
+        n_keys = 0;
         int rc = run(d_ids, d_pos, 1, 0, lm_buffer(), true, s);
+        fuse_tail = false;
         if (rc) return rc;
-        return argmax(s);
+        return argmax_embed(s);
     }
 
     int generate(const int* prompt, int n, int steps, int* out, bool use_graph, hipStream_t s,
@@ -135,6 +174,12 @@ struct DeviceGreedyInference : Inference {
         (void)hipEventCreate(&e0);
         (void)hipEventCreate(&e1);
         (void)hipEventRecord(e0, s);
+        // the first step's embedding row (every later one comes from the
+        // step before it)
+        {
+            const WeightTensor* e = emb_table();
+            rc = rina_hip_embedding(e->data, (int)e->quant_type, d_ids, d_pos, h_buffer(), 1, model_dim(), vocab, s);
+        }
         for (int i = 0; i < steps && rc == RINA_OK; i++) {
             const int pos = pos_first + i;
             if (use_graph) {

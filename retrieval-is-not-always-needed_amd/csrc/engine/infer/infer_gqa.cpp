@@ -112,7 +112,10 @@ struct GQAInference : DeviceGreedyInference {
         f.kv_cache.start_pos = start_pos;
         f.kv_cache_quant.start_pos = start_pos;
         f.d_pos = pos_dev;
-        if ((rc = rina_hip_embedding(wte->data, (int)wte->quant_type, ids, pos_dev, f.h, T, cfg.dim, cfg.vocab_size, s))) return rc;
+        // a decode step's embedding row is already in h (the previous step's tail)
+        if (!fuse_tail &&
+            (rc = rina_hip_embedding(wte->data, (int)wte->quant_type, ids, pos_dev, f.h, T, cfg.dim, cfg.vocab_size, s)))
+            return rc;
         f.status = RINA_OK;
         for (auto& l : layers)
             if ((rc = l->run(f.h, f, 1, T, s))) return rc;
@@ -123,9 +126,14 @@ struct GQAInference : DeviceGreedyInference {
         // ln_f fused as the LM head's prologue (infer_gqa.cpp:90-100)
         rina_linear_seg seg{hw->data, nullptr, logits, cfg.vocab_size};
         int pro = ln_f ? (use_rms ? RINA_PRO_RMSNORM : RINA_PRO_LAYERNORM) : RINA_PRO_NONE;
-        return rina_hip_linear_fused(&seg, 1, (int)hw->quant_type, x, M, cfg.dim, RINA_EPI_STORE, pro,
-                                     ln_f ? (const float*)ln_f->data : nullptr, 1e-5f, s);
+        const float* nw = ln_f ? (const float*)ln_f->data : nullptr;
+        if (M == 1) return head_launch(seg, (int)hw->quant_type, x, cfg.dim, pro, nw, s);
+        return rina_hip_linear_fused(&seg, 1, (int)hw->quant_type, x, M, cfg.dim, RINA_EPI_STORE, pro, nw, 1e-5f, s);
     }
+
+    const WeightTensor* emb_table() const override { return wte; }
+    float* h_buffer() override { return bufs.fwd.h; }
+    int model_dim() const override { return cfg.dim; }
 
     void forward(const int* ids, float* logits, int B, int T, int start_pos, hipStream_t s) override {
         if (B != 1) return set_status(RINA_ERR_ARG, "gqa: the KV-cache path decodes one sequence (B == 1)");

@@ -707,6 +707,7 @@ struct F32Args {
     int pro;
     const float* nw;
     float eps;
+    unsigned long long* keys;   // argmax epilogue: one key per workgroup (one segment, store epilogue)
 };
 
 // dot of one fp32 row with the LDS copy of x; 4 independent 16-byte loads
@@ -745,7 +746,8 @@ __device__ __forceinline__ float f32_row_dot(const float* w, const float* xl, in
 // their 16-byte loads (NV per lane per row, lane + 64 t) before any
 // arithmetic, so a lane keeps RPW * NV loads in flight.
 template <int NMAT, int NV>
-__device__ __forceinline__ void f32_rows_short(const F32Args& a, const float* xs_lds, int gw, int nw) {
+__device__ __forceinline__ void f32_rows_short(const F32Args& a, const float* xs_lds, int gw, int nw,
+                                               unsigned long long& best) {
     constexpr int RPW = NMAT == 2 ? 2 : 4;
     const int lane = threadIdx.x & 63;
     const int K = a.K, n4 = K >> 2;
@@ -792,6 +794,7 @@ __device__ __forceinline__ void f32_rows_short(const F32Args& a, const float* xs
                 if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
                 else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
                 else gst(y, v[0]);
+                best = umax64(best, argmax_cand(v[0], row[r]));
             }
         }
     }
@@ -803,7 +806,8 @@ __device__ __forceinline__ void f32_rows_short(const F32Args& a, const float* xs
 // issued first; the half-wave sums come from lanes 31 and 63 after the
 // row_bcast step of the wave reduction.
 template <int NMAT, int NV, int RP>
-__device__ __forceinline__ void f32_rows_half(const F32Args& a, const float* xs_lds, int gw, int nw) {
+__device__ __forceinline__ void f32_rows_half(const F32Args& a, const float* xs_lds, int gw, int nw,
+                                              unsigned long long& best) {
     constexpr int RPW = 2 * RP;
     const int lane = threadIdx.x & 63, hl = lane & 31, half = lane >> 5;
     const int n4 = a.K >> 2;
@@ -850,13 +854,46 @@ __device__ __forceinline__ void f32_rows_half(const F32Args& a, const float* xs_
                 if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
                 else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
                 else gst(y, v[0]);
+                best = umax64(best, argmax_cand(v[0], row[p]));
             }
         }
     }
 }
 
 // NV > 0: rows of K <= 2048 (f32_rows_short); HALF: the half-wave rows
-template <int NMAT, bool VEC, int NV, bool HALF = false>
+// K > 2048 or unaligned rows: one row per wave per step
+template <int NMAT, bool VEC>
+__device__ __forceinline__ void f32_rows_loop(const F32Args& a, const float* xs_lds, int gw, int nw,
+                                              unsigned long long& best) {
+    const int lane = threadIdx.x & 63;
+    const int K = a.K;
+    for (int vr = gw; vr < a.total_rows; vr += nw) {
+        int s = 0;
+        if (a.nseg > 1 && vr >= a.seg[1].tile0) s = 1;
+        if (a.nseg > 2 && vr >= a.seg[2].tile0) s = 2;
+        int row = vr - a.seg[s].tile0;
+        float v[2];
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            const float* w = (const float*)(m == 0 ? a.seg[s].w : a.seg[s].w2) + (int64_t)row * K;
+            v[m] = wave_sum(f32_row_dot<VEC>(w, xs_lds, K, lane));
+        }
+        if (lane == 0) {
+            float* y = a.seg[s].y + row;
+            if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
+            else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
+            else gst(y, v[0]);
+            best = umax64(best, argmax_cand(v[0], row));
+        }
+    }
+}
+
+// AM: also the greedy argmax's per-workgroup keys (one segment, store
+// epilogue): every workgroup writes the largest key of the rows it stored
+// to a.keys[blockIdx.x] (0 when it had none), which argmax_embed_kernel
+// reduces.  Only lanes that store a row form keys; the other lanes' keys
+// stay 0.
+template <int NMAT, bool VEC, int NV, bool HALF = false, bool AM = false>
 __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     extern __shared__ __align__(16) float xs_lds[];
     __shared__ float red[8];
@@ -888,32 +925,23 @@ __global__ __launch_bounds__(kWG) void gemv_f32_kernel(F32Args a) {
     }
     __syncthreads();
     const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
+    unsigned long long best = 0ull;
     if constexpr (HALF) {
-        f32_rows_half<NMAT, NV, NMAT == 2 ? 2 : 4>(a, xs_lds, gw, nw);
-        return;
+        f32_rows_half<NMAT, NV, NMAT == 2 ? 2 : 4>(a, xs_lds, gw, nw, best);
     } else if constexpr (NV > 0) {
-        f32_rows_short<NMAT, NV>(a, xs_lds, gw, nw);
-        return;
+        f32_rows_short<NMAT, NV>(a, xs_lds, gw, nw, best);
+    } else {
+        f32_rows_loop<NMAT, VEC>(a, xs_lds, gw, nw, best);
     }
-    for (int vr = gw; vr < a.total_rows; vr += nw) {
-        int s = 0;
-        if (a.nseg > 1 && vr >= a.seg[1].tile0) s = 1;
-        if (a.nseg > 2 && vr >= a.seg[2].tile0) s = 2;
-        int row = vr - a.seg[s].tile0;
-        float v[2];
-#pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-            const float* w = (const float*)(m == 0 ? a.seg[s].w : a.seg[s].w2) + (int64_t)row * K;
-            v[m] = wave_sum(f32_row_dot<VEC>(w, xs_lds, K, lane));
-        }
-        if (lane == 0) {
-            float* y = a.seg[s].y + row;
-            if (NMAT == 2) gst(y, silu_mul(v[0], v[1]));
-            else if (a.epi == RINA_EPI_ADD) gst(y, gld(y) + v[0]);
-            else gst(y, v[0]);
-        }
+    if constexpr (AM) {
+        __shared__ unsigned long long kred[4];
+        for (int off = 32; off > 0; off >>= 1) best = umax64(best, __shfl_xor(best, off));
+        if (lane == 0) kred[wave] = best;
+        __syncthreads();
+        if (tid == 0) gst(a.keys + blockIdx.x, umax64(umax64(kred[0], kred[1]), umax64(kred[2], kred[3])));
     }
 }
+
 
 // ---------------------------------------------------------------------------
 // M > 1 (prompt phase): 32x64 output tiles, K stepped by 32; weights are
@@ -1630,9 +1658,12 @@ int gemv_quant(const rina_linear_seg* segs, int nseg, int qt, const float* x, in
     }
 }
 
+// keys != NULL: one segment, store epilogue, and the argmax keys of every
+// workgroup into keys[0 .. *nkeys) (at most max_keys)
 int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int epi, int pro, const float* nw,
-             float eps, hipStream_t st) {
+             float eps, hipStream_t st, unsigned long long* keys = nullptr, int max_keys = 0, int* nkeys = nullptr) {
     F32Args a{};
+    a.keys = keys;
     a.pro = pro;
     a.nw = nw;
     a.eps = eps;
@@ -1671,6 +1702,32 @@ int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int e
         const int rpw = two ? 2 : 4;
         int g2 = (rows + 4 * rpw - 1) / (4 * rpw);
         if (g2 < grid) grid = g2;
+    }
+    if (keys) {
+        if (nseg != 1 || epi != RINA_EPI_STORE) return RINA_ERR_ARG;
+        if (grid > max_keys) return RINA_ERR_WORKSPACE;
+        *nkeys = grid;
+#define F32_AM(V, NVV, H) hipLaunchKernelGGL((gemv_f32_kernel<1, V, NVV, H, true>), dim3(grid), dim3(kWG), lds, st, a)
+        if (nvh > 0) {
+            switch (nvh) {
+                case 1: F32_AM(true, 1, true); break;
+                case 3: F32_AM(true, 3, true); break;
+                case 5: F32_AM(true, 5, true); break;
+                default: F32_AM(true, 7, true); break;
+            }
+        } else if (nv > 0) {
+            switch (nv <= 2 ? 2 : nv <= 4 ? 4 : 8) {
+                case 2: F32_AM(true, 2, false); break;
+                case 4: F32_AM(true, 4, false); break;
+                default: F32_AM(true, 8, false); break;
+            }
+        } else if (vec) {
+            F32_AM(true, 0, false);
+        } else {
+            F32_AM(false, 0, false);
+        }
+#undef F32_AM
+        return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
     }
 #define F32_LAUNCH(NM, V, NVV) hipLaunchKernelGGL((gemv_f32_kernel<NM, V, NVV>), dim3(grid), dim3(kWG), lds, st, a)
 #define F32_HALF(NM, NVV) hipLaunchKernelGGL((gemv_f32_kernel<NM, true, NVV, true>), dim3(grid), dim3(kWG), lds, st, a)
@@ -1861,6 +1918,18 @@ extern "C" int rina_hip_linear_fused_ex(const rina_linear_seg* segs, int nseg, i
         return RINA_OK;
     }
     return gemv_quant(segs, nseg, qt, input, K, epi, pro, nw, eps, norm_out, st);
+}
+
+extern "C" int rina_hip_linear_argmax(const rina_linear_seg* seg, int qt, const float* input, int K, int pro,
+                                      const float* nw, float eps, void* keys, int max_keys, int* nkeys, void* stream) {
+    if (!seg || !seg->weight || !seg->out || seg->N < 1 || !input || K < 1 || !keys || max_keys < 1 || !nkeys ||
+        (uintptr_t)keys % 8)
+        return RINA_ERR_ARG;
+    if (qt != RINA_QT_FP32) return RINA_ERR_QTYPE;
+    if (pro < RINA_PRO_NONE || pro > RINA_PRO_LAYERNORM || (pro != RINA_PRO_NONE && !nw)) return RINA_ERR_ARG;
+    if (K > 16384) return RINA_ERR_SHAPE;
+    return gemv_f32(seg, 1, input, K, RINA_EPI_STORE, pro, nw, eps, as_stream(stream), (unsigned long long*)keys,
+                    max_keys, nkeys);
 }
 
 extern "C" int rina_hip_linear_fused(const rina_linear_seg* segs, int nseg, int qt, const float* input, int M, int K,

@@ -136,22 +136,12 @@ __global__ void saxpy_kernel(float* d, const float* s, float p, int64_t n) {
 }
 
 // Greedy argmax (main.cpp:139-146): strict ">" from -1e10, lowest index on
-// ties.  Candidates are packed into one 64-bit key (order-preserving float
-// bits, then the complemented index) and merged with a 64-bit atomicMax
-// into a key slot that the finishing kernel reads and clears again.  -0 is
-// keyed as +0: under ">" the two are equal, so the lower index must win.
+// ties.  Candidates are packed into one 64-bit key (argmax_key) and merged
+// with a 64-bit atomicMax into a key slot that the finishing kernel reads
+// and clears again.
 __device__ unsigned long long g_argmax_key = 0ull;   // slot of rina_hip_argmax (one per device)
 
-__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
-    uint32_t b = __float_as_uint(v);
-    if (b == 0x80000000u) b = 0u;
-    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
-}
-
-__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
-
-__device__ __forceinline__ unsigned long long cand(float v, int i) { return v > -1e10f ? argmax_key(v, i) : 0ull; }
+__device__ __forceinline__ unsigned long long cand(float v, int i) { return argmax_cand(v, i); }
 
 // A few workgroups (one 64-bit atomic each, after a wave + LDS reduction)
 // cover x with 16-byte loads; many same-address atomics serialize.
@@ -180,13 +170,55 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* x, int
 __global__ void argmax_finish_kernel(int* out_idx, int* ids_out, int* d_pos, unsigned long long* key) {
     unsigned long long k = *key;
     *key = 0ull;
-    int idx = k ? (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : 0;
+    int idx = argmax_index(k);
     if (out_idx) *out_idx = idx;
     if (d_pos) {
         int p = *d_pos;
         if (ids_out) ids_out[p + 1] = idx;
         *d_pos = p + 1;
     }
+}
+
+// The greedy step's tail in one launch: the winner of nkeys argmax keys
+// (the per-workgroup keys of a fused LM head, or a key slot, cleared again
+// when `reset`), then what argmax_finish_kernel does with it (out_idx, the
+// id after the device position, the position advanced), then the
+// embedding row of that id into h: the next decode step's input
+// (ops/embedding.cu:6-230 via kvq::weight_elem, ids outside the vocabulary
+// clamped as embedding_kernel does).
+__global__ __launch_bounds__(256) void argmax_embed_kernel(unsigned long long* keys, int nkeys, int reset, int* out_idx,
+                                                           int* ids_out, int* d_pos, const uint8_t* w, int qt,
+                                                           float* h, int d, int vocab) {
+    __shared__ unsigned long long red[4];
+    __shared__ int s_id;
+    const int tid = threadIdx.x;
+    unsigned long long best = 0ull;
+    for (int i = tid; i < nkeys; i += 256) best = umax64(best, gld(keys + i));
+    for (int off = 32; off > 0; off >>= 1) best = umax64(best, __shfl_xor(best, off));
+    if ((tid & 63) == 0) red[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        const int idx = argmax_index(umax64(umax64(red[0], red[1]), umax64(red[2], red[3])));
+        if (out_idx) *out_idx = idx;
+        if (d_pos) {
+            const int p = *d_pos;
+            if (ids_out) ids_out[p + 1] = idx;
+            *d_pos = p + 1;
+        }
+        s_id = idx;
+    }
+    __syncthreads();
+    if (reset)
+        for (int i = tid; i < nkeys; i += 256) keys[i] = 0ull;
+    int id = s_id;
+    if (id < 0) id = 0;
+    if (vocab > 0 && id >= vocab) id = vocab - 1;
+    const uint8_t* row;
+    if (qt == RINA_QT_Q4_0) row = w + (int64_t)id * (d / 32) * 18;
+    else if (qt == RINA_QT_Q4_0F) row = w + (int64_t)id * (d / 32) * 20;
+    else if (qt == RINA_QT_GGML_Q2_K) row = w + (int64_t)id * ((d + 255) / 256) * 84;
+    else row = w + (int64_t)id * d * 4;
+    for (int i = tid; i < d; i += 256) h[i] = kvq::weight_elem(qt, row, i);
 }
 
 // Streaming-read probe: every lane sums 16-byte non-temporal loads of its
@@ -383,6 +415,28 @@ extern "C" int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out
         key = g_key_addr[dev];
     }
     return argmax_launch(x, n, out_idx, ids_out, d_pos, key, as_stream(stream));
+}
+
+extern "C" int rina_hip_argmax_partial(const float* x, int n, void* key_slot, void* stream) {
+    if (!x || n < 1 || !key_slot || (uintptr_t)key_slot % 8) return RINA_ERR_ARG;
+    int grid = (n + 1023) / 1024;
+    if (grid > 64) grid = 64;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(grid), dim3(256), 0, as_stream(stream), x, n,
+                       (unsigned long long*)key_slot);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_argmax_embed(void* keys, int nkeys, int reset, int* out_idx, int* ids_out, int* d_pos,
+                                     const void* emb, int emb_qt, float* h, int d, int vocab, void* stream) {
+    if (!keys || nkeys < 1 || (uintptr_t)keys % 8 || !emb || !h || d < 1 || vocab < 1) return RINA_ERR_ARG;
+    if (emb_qt != RINA_QT_FP32 && emb_qt != RINA_QT_Q4_0 && emb_qt != RINA_QT_Q4_0F && emb_qt != RINA_QT_GGML_Q2_K)
+        return RINA_ERR_QTYPE;
+    if ((emb_qt == RINA_QT_Q4_0 || emb_qt == RINA_QT_Q4_0F) && d % 32) return RINA_ERR_SHAPE;
+    hipLaunchKernelGGL(argmax_embed_kernel, dim3(1), dim3(256), 0, as_stream(stream), (unsigned long long*)keys,
+                       nkeys, reset, out_idx, ids_out, d_pos, (const uint8_t*)emb, emb_qt, h, d, vocab);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
 }
 
 extern "C" int rina_hip_argmax_ws(const float* x, int n, int* out_idx, int* ids_out, int* d_pos, void* key_slot,

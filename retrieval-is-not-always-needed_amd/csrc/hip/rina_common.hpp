@@ -148,6 +148,25 @@ __device__ __forceinline__ void stage_lds(float* dst, const float* src, int n) {
 }
 
 // ---------------------------------------------------------------------------
+// Greedy argmax keys (main.cpp:139-146: strict ">" from -1e10, lowest index
+// on ties): a candidate is one 64-bit key, the order-preserving bits of the
+// value above the complemented index, so the largest key is the largest
+// value and, among equal values, the lowest index.  -0 is keyed as +0 (under
+// ">" they are equal, so the lower index must win).  0 is "no candidate".
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    uint32_t b = __float_as_uint(v);
+    if (b == 0x80000000u) b = 0u;
+    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
+}
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+__device__ __forceinline__ unsigned long long argmax_cand(float v, int i) { return v > -1e10f ? argmax_key(v, i) : 0ull; }
+__device__ __forceinline__ int argmax_index(unsigned long long k) {
+    return k ? (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : 0;
+}
+
+// ---------------------------------------------------------------------------
 // host helpers
 // ---------------------------------------------------------------------------
 

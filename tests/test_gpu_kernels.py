@@ -715,6 +715,65 @@ def test_argmax_signed_zero_and_key_slots(rina, orc):
     assert bad == -1   # misaligned slot rejected before launch
 
 
+@pytest.mark.parametrize("N,K,pro", [(128256, 2048, 1), (128256, 640, 2), (5000, 4096, 0), (333, 1000, 1)])
+def test_linear_argmax_and_embed(rina, orc, N, K, pro):
+    """The fused decode tail: rina_hip_linear_argmax writes the same logits
+    as rina_hip_linear_fused (bit for bit: the same row arithmetic) plus
+    per-workgroup argmax keys; rina_hip_argmax_embed picks the oracle's
+    greedy id from them (strict ">", lowest index among ties, planted at
+    three indices), writes it after the device position, advances the
+    position and writes that id's embedding row (fp32 and Q4_0F tables,
+    bit-exact against the oracle's row dequant).  The keys-slot form
+    (rina_hip_argmax_partial + reset) leaves its slot zero."""
+    hip = rina.load_hip()
+    L = orc.load()
+    r = rng(N + K + pro)
+    w = (r.standard_normal(N * K) * 0.02).astype(np.float32)
+    x = (r.standard_normal(K) * 2 + 0.3).astype(np.float32)
+    nw = r.uniform(0.5, 1.5, K).astype(np.float32)
+    wd, xd, nwd = dev(w), dev(x), dev(nw)
+    y0, y1 = empty(N), empty(N)
+    s0 = rina.LinearSeg(wd.data_ptr(), None, y0.data_ptr(), N)
+    s1 = rina.LinearSeg(wd.data_ptr(), None, y1.data_ptr(), N)
+    ok(hip.rina_hip_linear_fused(C.byref(s0), 1, 6, xd.data_ptr(), 1, K, rina.EPI_STORE, pro,
+                                 nwd.data_ptr() if pro else None, 1e-5, stream()))
+    keys = empty(2 * 8192, "int32")
+    nk = C.c_int()
+    ok(hip.rina_hip_linear_argmax(C.byref(s1), 6, xd.data_ptr(), K, pro, nwd.data_ptr() if pro else None, 1e-5,
+                                  keys.data_ptr(), 8192, C.byref(nk), stream()))
+    logits = host(y1)
+    assert np.array_equal(logits.view(np.uint32), host(y0).view(np.uint32))
+    assert 1 <= nk.value <= 8192
+    want = L.orc_argmax(logits.ctypes.data, N)
+    # ties at the maximum: the lowest index must win
+    top = float(logits.max())
+    tied = logits.copy()
+    tied[[N // 3, N - 1, N // 7]] = top
+    want_tied = L.orc_argmax(tied.ctypes.data, N)
+    for qt_e in (6, 7):
+        d_e = 64
+        V = N
+        ef = (r.standard_normal(V * d_e) * 0.5).astype(np.float32)
+        emb = ef if qt_e == 6 else orc.pack(qt_e, ef)
+        ed = dev(emb)
+        ids = empty(16, "int32")
+        pos = dev(np.array([6], np.int32))
+        h = empty(d_e)
+        ok(hip.rina_hip_argmax_embed(keys.data_ptr(), nk.value, 0, None, ids.data_ptr(), pos.data_ptr(), ed.data_ptr(),
+                                     qt_e, h.data_ptr(), d_e, V, stream()))
+        assert int(host(pos)[0]) == 7 and int(host(ids)[7]) == want
+        row = ef[want * d_e:(want + 1) * d_e] if qt_e == 6 else orc.dequant(qt_e, emb, V * d_e)[want * d_e:(want + 1) * d_e]
+        assert np.array_equal(host(h), row)
+    # the key-slot form over the tied logits, then the slot is zero again
+    slot = empty(2, "int32")
+    out = empty(1, "int32")
+    ok(hip.rina_hip_argmax_partial(dev(tied).data_ptr(), N, slot.data_ptr(), stream()))
+    ok(hip.rina_hip_argmax_embed(slot.data_ptr(), 1, 1, out.data_ptr(), None, None, ed.data_ptr(), 7, h.data_ptr(),
+                                 d_e, V, stream()))
+    assert int(host(out)[0]) == want_tied
+    assert not host(slot).any()
+
+
 @pytest.mark.parametrize("qt", [7, 5, 10, 6])
 @pytest.mark.parametrize("pro", [1, 2])
 @pytest.mark.parametrize("M,K", [(1, 2048), (1, 640), (2, 2048), (1, 8192), (1, 4096)])
