@@ -179,7 +179,7 @@ def traffic_probe_stack(iters):
     print("probe done: %d tokens, %d bytes per token" % (iters, ls.bytes_per_token()), flush=True)
 
 
-STACK_KERNELS = ("gemv_direct_kernel", "attn_split_kernel", "attn_combine_kernel")
+STACK_KERNELS = ("gemv_direct_kernel", "attn_vsplit_kernel", "attn_split_kernel", "attn_combine_kernel")
 
 
 def _pmc_sum(db, counter, kernels):
