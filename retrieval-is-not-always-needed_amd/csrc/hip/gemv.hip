@@ -1503,7 +1503,9 @@ int launch_direct(GemvArgs& a, hipStream_t st) {
     // entry (2-3 iterations) made the launches slower (SwiGLU 8192 x 2048
     // 6.5 -> 7.9 us, config 1 4.4 -> 5.1 us), also with a barrier that puts
     // every wave's activation requests ahead of the weight requests
-    // (SwiGLU 7.85 us).
+    // (SwiGLU 7.85 us), and so did two groups in flight from entry in the
+    // two-set loop (SwiGLU 7.0 us, config 1 5.1 us): the activation loads of
+    // a CU's later waves then queue behind more weight requests.
     const bool one = wgs <= grid;
     // residual epilogue: the old output words are loaded with the weights
     // (W_o 3.16 -> 2.99 us, W2 5.5 -> 5.2 us); a store epilogue loads none
