@@ -216,7 +216,10 @@ int rina_hip_gqa_decode_attention(const float* q, const float* k, const float* v
  * than 62 query heads) returns RINA_ERR_WORKSPACE before launching.  All
  * calls on one device share that array: calls that overlap on one device
  * (different streams) race.  The first call on each device looks the array
- * up; make it outside graph capture. */
+ * up; make it outside graph capture.  The address is kept per device ordinal
+ * for the life of the process: after hipDeviceReset it is stale, so this
+ * entry point must not be called after a device reset in the same process
+ * (nor rina_hip_argmax, whose key slot is kept the same way). */
 size_t rina_hip_noalloc_scratch_bytes(void);
 int rina_hip_gqa_decode_attention_noalloc(const float* q, const float* k, const float* v,
                                           const float* rope_q_cos, const float* rope_q_sin,
@@ -420,7 +423,8 @@ int rina_hip_saxpy(float* d, const float* s, float p, int64_t n, void* stream);
  * ids_out[*d_pos + 1] and increments *d_pos (device-side decode loop).
  * The candidates meet in one 8-byte key slot per device that the library
  * owns: calls that overlap on two streams of one device race on it (use
- * rina_hip_argmax_ws there). */
+ * rina_hip_argmax_ws there).  The slot's address is kept per device ordinal
+ * for the life of the process: not for use after hipDeviceReset. */
 int rina_hip_argmax(const float* x, int n, int* out_idx, int* ids_out,
                     int* d_pos, void* stream);
 /* rina_hip_argmax with the caller's key slot: key_slot is 8 bytes of
@@ -467,12 +471,6 @@ int rina_hip_argmax_embed(void* keys, int nkeys, int reset, int* out_idx, int* i
  * is the plain-read ceiling the benchmark sets next to each matvec of the
  * same byte count. */
 int rina_hip_read_probe(const void* src, int64_t bytes, int grid, float* sink, void* stream);
-
-/* Cache warm-up, no counterpart in the reference: one launch of `grid`
- * 256-thread workgroups that reads bytes (rounded down to 16) of src
- * (16-byte aligned) with cache-allocating loads and writes nothing, so a
- * later kernel finds them in the memory-side cache. */
-int rina_hip_prefetch(const void* src, int64_t bytes, int grid, void* stream);
 
 /* Library version / self-description. */
 const char* rina_hip_version(void);

@@ -83,7 +83,6 @@ _HIP_SIGS = {
     "rina_hip_argmax": (I32, [VP, I32, VP, VP, VP, VP]),
     "rina_hip_argmax_ws": (I32, [VP, I32, VP, VP, VP, VP, VP]),
     "rina_hip_read_probe": (I32, [VP, I64, I32, VP, VP]),
-    "rina_hip_prefetch": (I32, [VP, I64, I32, VP]),
     "rina_hip_linear_argmax": (I32, [VP, I32, VP, I32, I32, VP, F32, VP, I32, VP, VP]),
     "rina_hip_argmax_partial": (I32, [VP, I32, VP, VP]),
     "rina_hip_argmax_embed": (I32, [VP, I32, I32, VP, VP, VP, VP, I32, VP, I32, I32, VP]),

@@ -1215,9 +1215,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // the low half)
 __device__ __forceinline__ uint32_t hi16_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
-// x0, x1 split exactly into three bf16 parts each, x = h + m + l: h is x cut
-// to its top 8 significant bits, m the remainder cut the same way, l the
-// rest (at most 8 significant bits, so exact); packed as two-value dwords
+// x0, x1 split into three bf16 parts each, x = h + m + l: h is x cut to its
+// top 8 significant bits, m the remainder cut the same way, l the rest (at
+// most 8 significant bits); packed as two-value dwords.  Exact for finite
+// |x| >= 2^-103 and for 0, where both remainders are normal fp32 values; an
+// infinite x gives NaN parts (inf - inf), and a smaller x loses low bits of
+// l (the matrix cores may also flush bf16 denormals)
 __device__ __forceinline__ void split3_pair(float x0, float x1, uint32_t& ph, uint32_t& pm, uint32_t& pl) {
     const uint32_t u0 = __float_as_uint(x0), u1 = __float_as_uint(x1);
     ph = hi16_pair(u0, u1);

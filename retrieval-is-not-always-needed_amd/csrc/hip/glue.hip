@@ -242,23 +242,6 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const f32x4* src, int64
     if (threadIdx.x == 0) sink[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// Temporal (cache-allocating) reads of n4 16-byte words, four in flight per
-// thread: the bytes land in the memory-side cache (MALL) and in this XCD's
-// L2, where a later kernel's loads of them hit.  The loaded words only feed
-// an empty asm statement, so the loads stay and nothing is written.
-__global__ __launch_bounds__(256) void prefetch_kernel(const f32x4* src, int64_t n4) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    float acc = 0.f;
-    for (; i + 3 * stride < n4; i += 4 * stride) {
-        const f32x4 a = gld(src + i), b = gld(src + i + stride), c = gld(src + i + 2 * stride),
-                    d = gld(src + i + 3 * stride);
-        acc += (a.x + b.x) + (c.x + d.x);
-    }
-    for (; i < n4; i += stride) acc += gld(src + i).x;
-    asm volatile("" ::"v"(acc));
-}
-
 unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
 struct DevState {
@@ -449,13 +432,6 @@ extern "C" int rina_hip_read_probe(const void* src, int64_t bytes, int grid, flo
     if (!src || !sink || bytes < 16 || grid < 1 || (uintptr_t)src % 16) return RINA_ERR_ARG;
     hipLaunchKernelGGL(read_probe_kernel, dim3(grid), dim3(256), 0, as_stream(stream), (const f32x4*)src, bytes / 16,
                        sink);
-    RINA_LAUNCH_CHECK();
-    return RINA_OK;
-}
-
-extern "C" int rina_hip_prefetch(const void* src, int64_t bytes, int grid, void* stream) {
-    if (!src || bytes < 16 || grid < 1 || (uintptr_t)src % 16) return RINA_ERR_ARG;
-    hipLaunchKernelGGL(prefetch_kernel, dim3(grid), dim3(256), 0, as_stream(stream), (const f32x4*)src, bytes / 16);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }
