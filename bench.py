@@ -180,7 +180,7 @@ def traffic_probe_stack(iters):
 
 
 STACK_KERNELS = ("gemv_direct_kernel", "attn_vsplit_kernel", "attn_split_kernel", "attn_combine_kernel")
-VSPLIT_MAX_POS = 640   # fp32-cache decode attention runs as one launch up to this many positions
+VSPLIT_MAX_POS = 1024   # fp32-cache decode attention runs as one launch up to this many positions
 
 
 def _pmc_sum(db, counter, kernels, ncopy):
@@ -292,7 +292,7 @@ def committed_traffic(path=TRAFFIC_FILE):
 
 STACK_KINDS = ("qkv", "attn", "wo", "w13", "w2")
 STACK_NOTES = {"qkv": "fused q/k/v Q4_0F matvec with the ln1 RMSNorm prologue (N 3072, K 2048)",
-               "attn": "RoPE + fp32 KV append + decode attention (one launch up to 640 positions, else split + merge)",
+               "attn": "RoPE + fp32 KV append + decode attention (one launch up to 1024 positions, else split + merge)",
                "wo": "W_o Q4_0F matvec + residual (N 2048, K 2048)",
                "w13": "W1/W3 Q4_0F matvec pair with the ln2 RMSNorm prologue and SiLU*up (N 8192, K 2048)",
                "w2": "W2 Q4_0F matvec + residual (N 2048, K 8192)"}

@@ -7,7 +7,7 @@
 // kernels/quantize.cu), the others from the current fp32 rows; query head h
 // reads KV head h / (H/Hkv); score = (q.k) / sqrt(dh).
 //
-// Decode (T == 1, dh == 64), fp32 cache of at most 640 positions: one
+// Decode (T == 1, dh == 64), fp32 cache of at most 1024 positions: one
 // launch (attn_vsplit_kernel, below: every workgroup scores the whole
 // context for one query head and keeps a slice of the value dims).
 // Otherwise split-sequence in two launches.  The split
@@ -375,173 +375,159 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention in one launch for short fp32 caches (positions 0..pos0,
-// pos0 < kVsMaxPos), dh == 64.  One workgroup per (REP query heads, value
-// slice): it scores every position for its query heads against the full
-// 64-dim keys of their KV head and accumulates only its 64/VS value dims,
-// so the workgroups of a head repeat the scores instead of exchanging
-// partials, and the output is written normalized: no partials and no
-// combine launch.  A workgroup is bound by what its CU streams and
-// computes (every key row of the head, its value slice, the scores), which
-// the value split and one query head per workgroup keep small.  1024
-// threads: 8 lanes per position record (8 key dims and VD/8 value dims
-// each), 128 positions per step, every step's loads issued at entry.  Each
-// 8-lane slot keeps its own online softmax; the 128 slots merge through
-// LDS.  RoPE of q and of the current k (the reference's NeoX pairs,
-// fused-multiply form) and the append at pos0 are fused; positions < pos0
-// are the only cache rows read, so the append races with nothing.
+// Decode attention in one launch for fp32 caches of up to kVsMaxPos
+// positions (pos0 < kVsMaxPos), dh == 64.  One workgroup per (query head,
+// slice of 64/VS value dims): it scores every position of the context
+// against the full 64-dim key rows of the head's KV head and accumulates
+// only its value slice, so the VS workgroups of a head repeat the scores
+// instead of exchanging partials, and the output is written normalized (no
+// partials, no combine launch).  1024 threads: 4 lanes per position record
+// (16 key dims and VD/4 value dims each), 256 positions per step, NST steps
+// (the launch's position bound), every step's loads issued at entry.  All scores first, then the wave's maximum
+// and weights; the sums of weights and weighted values are reduced over the
+// lanes of each DPP row and the 64 row partials of the workgroup merge
+// through LDS.  RoPE of q and of the current k (the reference's NeoX
+// pairs, fused-multiply form) and the append at pos0 are fused; only
+// positions < pos0 are read from the cache, so the append races with
+// nothing.
 // ---------------------------------------------------------------------------
-constexpr int kVsSteps = 5;
-constexpr int kVsMaxPos = 128 * kVsSteps;      // pos0 + 1 <= 640
+constexpr int kVsSteps = 4;
+constexpr int kVsMaxPos = 256 * kVsSteps;      // pos0 + 1 <= 1024
 
-template <int VS, int REP>
+template <int VS, int NST>
 __global__ __launch_bounds__(1024) void attn_vsplit_kernel(SplitArgs a) {
-    constexpr int DH = 64, VD = DH / VS, VL = VD / 8;   // value dims per workgroup / per lane
-    static_assert(VL >= 1 && VL <= 2 && REP * 128 <= 1024, "VS 4 or 8, REP <= 8");
+    constexpr int DH = 64, VD = DH / VS, VL = VD / 4;   // value dims per workgroup / per lane
+    static_assert(VL >= 1 && VL <= 4 && VD % 4 == 0, "VS 2, 4 or 8");
     typedef float f32x2 __attribute__((ext_vector_type(2)));
-    __shared__ __align__(16) float s_q[REP][DH];     // rotated, scaled query rows
+    __shared__ __align__(16) float s_q[DH];          // rotated query row, scaled to base-2 units
     __shared__ __align__(16) float s_k[DH], s_v[DH]; // the current (rotated) key row and value row
-    __shared__ float s_m[REP][128], s_l[REP][128], s_w[REP][128], s_mx[REP][2];
-    __shared__ __align__(16) float s_o[128][REP][VD];
+    __shared__ float s_pm[16], s_pl[64];             // per wave: maximum; per DPP row: sum of weights
+    __shared__ float s_po[VD][64];                   // per DPP row: weighted value sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos0 = read_pos(a.start_pos, a.d_pos);
-    if (pos0 < 0 || pos0 >= a.max_seq || pos0 >= kVsMaxPos) return;   // host checks host-known positions
+    if (pos0 < 0 || pos0 >= a.max_seq || pos0 >= 256 * NST) return;   // host checks host-known positions
     const int L = pos0 + 1;
-    // workgroup = (KV head, group of REP query heads of it, value slice),
-    // numbered kvh + Hkv * (...): with 8 KV heads every workgroup of a KV
-    // head runs on one XCD (workgroups go to the XCDs round-robin) and the
-    // head's key rows come into its L2 once
+    // workgroup = (KV head, query head of it, value slice), numbered
+    // kvh + Hkv * (...): with 8 KV heads every workgroup of a KV head runs
+    // on one XCD (workgroups go to the XCDs round-robin) and the head's key
+    // rows come into its L2 once
     const int kvh = blockIdx.x % a.Hkv, rest = blockIdx.x / a.Hkv;
-    const int vs = rest % VS, qg = rest / VS;
-    const int rep = a.H / a.Hkv;
-    const int qh0 = kvh * rep + qg * REP;            // first query head of this workgroup
+    const int vs = rest % VS, qh = kvh * (a.H / a.Hkv) + rest / VS;
     const int kvd = a.Hkv * DH;
-    const int slot = wave * 8 + (lane >> 3), j = lane & 7;
-    const int v0 = vs * VD + VL * j;                 // this lane's first value dim
-    // small loads first (query rows, the current rows, RoPE tables: every
+    const int g = tid >> 2, qq = tid & 3;            // position within a step, quarter of the record
+    const int v0 = vs * VD + VL * qq;                // this lane's first value dim
+    // small loads first (query row, the current rows, RoPE tables: every
     // thread loads, indices clamped), then every step's key / value loads
     // (positions past pos0 read position 0 and are masked): loads retire in
     // issue order, so the rotation below waits for the small ones alone
-    const int pr = tid < DH * (REP + 2) ? tid / DH : 0, pd = tid % DH;
-    const bool pq = pr < REP;
-    const float* psrc = pq ? a.q + (int64_t)(qh0 + pr) * DH : (pr == REP ? a.kcur : a.vcur) + (int64_t)kvh * DH;
-    const float* ptc = pq ? a.qc : a.kc;
-    const float* pts = pq ? a.qs : a.ks;
-    const bool prot = pr != REP + 1 && ptc != nullptr;
+    const int pr = tid < DH * 3 ? tid / DH : 0, pd = tid % DH;
+    const float* psrc = pr == 0 ? a.q + (int64_t)qh * DH : (pr == 1 ? a.kcur : a.vcur) + (int64_t)kvh * DH;
+    const float* ptc = pr == 0 ? a.qc : a.kc;
+    const float* pts = pr == 0 ? a.qs : a.ks;
+    const bool prot = pr != 2 && ptc != nullptr;
     const float own = gld(psrc + pd), pair = gld(psrc + (pd ^ 32));
     const int64_t toff = (int64_t)pos0 * 32 + (pd & 31);
     const float pc = gld(prot ? ptc + toff : psrc), psn = gld(prot ? pts + toff : psrc);
     __builtin_amdgcn_sched_barrier(0);
-    float kk[kVsSteps][8], vv[kVsSteps][VL];
+    float kk[NST][16], vv[NST][VL];
 #pragma unroll
-    for (int t = 0; t < kVsSteps; t++) {
-        const int p = slot + 128 * t;
+    for (int t = 0; t < NST; t++) {
+        const int p = g + 256 * t;
         const int pp = p < pos0 ? p : 0;
-        ld8f((const float*)a.ck + (int64_t)pp * kvd + kvh * DH + 8 * j, kk[t]);
+        const float* kr = (const float*)a.ck + (int64_t)pp * kvd + kvh * DH + 4 * qq;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f32x4 w = gld((const f32x4*)(kr + 16 * i));
+            kk[t][4 * i] = w.x; kk[t][4 * i + 1] = w.y; kk[t][4 * i + 2] = w.z; kk[t][4 * i + 3] = w.w;
+        }
         const float* vr = (const float*)a.cv + (int64_t)pp * kvd + kvh * DH + v0;
         if constexpr (VL == 2) {
             const f32x2 w = gld((const f32x2*)vr);
             vv[t][0] = w.x; vv[t][1] = w.y;
         } else {
-            vv[t][0] = gld(vr);
+#pragma unroll
+            for (int i = 0; i < VL; i++) vv[t][i] = gld(vr + i);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (tid < DH * (REP + 2)) {
+    if (tid < DH * 3) {
         float x = own;
         if (prot) x = pd < 32 ? fmaf(own, pc, -(pair * psn)) : fmaf(pair, psn, own * pc);
-        if (pq) s_q[pr][pd] = x * (a.scale * 1.44269504088896341f);   // scores in base-2 units
-        else if (pr == REP) s_k[pd] = x;
+        if (pr == 0) s_q[pd] = x * (a.scale * 1.44269504088896341f);   // scores in base-2 units
+        else if (pr == 1) s_k[pd] = x;
         else s_v[pd] = x;
     }
     __syncthreads();
-    float qv[REP][8];
+    float qv[16];
 #pragma unroll
-    for (int r = 0; r < REP; r++) {
-        const f32x4 a4 = *(const f32x4*)&s_q[r][8 * j], b4 = *(const f32x4*)&s_q[r][8 * j + 4];
-        qv[r][0] = a4.x; qv[r][1] = a4.y; qv[r][2] = a4.z; qv[r][3] = a4.w;
-        qv[r][4] = b4.x; qv[r][5] = b4.y; qv[r][6] = b4.z; qv[r][7] = b4.w;
+    for (int i = 0; i < 4; i++) {
+        const f32x4 w = *(const f32x4*)&s_q[16 * i + 4 * qq];
+        qv[4 * i] = w.x; qv[4 * i + 1] = w.y; qv[4 * i + 2] = w.z; qv[4 * i + 3] = w.w;
     }
-    float m_run[REP], l_run[REP], ov[REP][VL];
+    // every score first (the lane group of a position holds it after the
+    // quad sum), then the wave's maximum
+    float sc[NST];
+    float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < REP; r++) {
-        m_run[r] = -INFINITY;
-        l_run[r] = 0.f;
+    for (int t = 0; t < NST; t++) {
+        sc[t] = -INFINITY;
+        if (256 * t > pos0) continue;                // uniform: no position of this step is in the context
+        const int p = g + 256 * t;
+        if (p == pos0) {                             // the current position: its rows from LDS
 #pragma unroll
-        for (int i = 0; i < VL; i++) ov[r][i] = 0.f;
-    }
-#pragma unroll
-    for (int t = 0; t < kVsSteps; t++) {
-        if (128 * t > pos0) break;                   // uniform: no position of this step is in the context
-        const int p = slot + 128 * t;
-        const bool valid = p < L, cur = p == pos0;
-        float kx[8], vx[VL];
-#pragma unroll
-        for (int i = 0; i < 8; i++) kx[i] = cur ? s_k[8 * j + i] : kk[t][i];
-#pragma unroll
-        for (int i = 0; i < VL; i++) vx[i] = cur ? s_v[v0 + i] : vv[t][i];
-#pragma unroll
-        for (int r = 0; r < REP; r++) {
-            float d = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) d = fmaf(qv[r][i], kx[i], d);
-            const float sc = sum8(d);
-            if (valid) {
-                const float mn = fmaxf(m_run[r], sc);
-                const float al = __builtin_amdgcn_exp2f(m_run[r] - mn);   // 0 while nothing is accumulated
-                const float pe = __builtin_amdgcn_exp2f(sc - mn);
-                l_run[r] = fmaf(l_run[r], al, pe);
-#pragma unroll
-                for (int i = 0; i < VL; i++) ov[r][i] = fmaf(ov[r][i], al, pe * vx[i]);
-                m_run[r] = mn;
+            for (int i = 0; i < 4; i++) {
+                const f32x4 w = *(const f32x4*)&s_k[16 * i + 4 * qq];
+                kk[t][4 * i] = w.x; kk[t][4 * i + 1] = w.y; kk[t][4 * i + 2] = w.z; kk[t][4 * i + 3] = w.w;
             }
+#pragma unroll
+            for (int i = 0; i < VL; i++) vv[t][i] = s_v[v0 + i];
         }
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) d = fmaf(qv[i], kk[t][i], d);
+        d += dpp_f<0xB1>(d);                         // quad_perm [1,0,3,2]
+        d += dpp_f<0x4E>(d);                         // quad_perm [2,3,0,1]
+        if (p < L) { sc[t] = d; mx = fmaxf(mx, d); }
     }
-    // merge of the 128 slots: every slot's (m, l, O slice) to LDS, the slot
-    // weights 2^(m - M) once per (head, slot), then each output value sums
-    // the weighted slots (16 threads per value, 8 slots each)
-    if (j == 0) {
+    const float mw = wave_max(mx);                   // -inf: no position of this wave is in the context
+    float l = 0.f, o[VL];
 #pragma unroll
-        for (int r = 0; r < REP; r++) { s_m[r][slot] = m_run[r]; s_l[r][slot] = l_run[r]; }
+    for (int i = 0; i < VL; i++) o[i] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NST; t++) {
+        const float pe = sc[t] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[t] - mw);
+        l += pe;
+#pragma unroll
+        for (int i = 0; i < VL; i++) o[i] = fmaf(pe, vv[t][i], o[i]);
     }
+    // sums over the 4 position groups of each DPP row that share this
+    // lane's quarter (lanes qq, qq + 4, qq + 8, qq + 12 of the row)
+    l += dpp_f<0x124>(l);                            // row_ror:4
+    l += dpp_f<0x128>(l);                            // row_ror:8
 #pragma unroll
-    for (int r = 0; r < REP; r++)
+    for (int i = 0; i < VL; i++) {
+        o[i] += dpp_f<0x124>(o[i]);
+        o[i] += dpp_f<0x128>(o[i]);
+    }
+    const int rw = wave * 4 + (lane >> 4);           // DPP row of the workgroup (64)
+    if ((lane & 15) < 4) {
+        if (qq == 0) s_pl[rw] = l;
 #pragma unroll
-        for (int i = 0; i < VL; i++) s_o[slot][r][VL * j + i] = ov[r][i];
+        for (int i = 0; i < VL; i++) s_po[VL * qq + i][rw] = o[i];
+    }
+    if (lane == 0) s_pm[wave] = mw;
     __syncthreads();
-    const int mr = tid >> 7, msl = tid & 127;        // head, slot: two waves per head
-    float mo = -INFINITY;
-    if (tid < REP * 128) {
-        mo = s_m[mr][msl];
-        const float wm = wave_max(mo);
-        if (lane == 0) s_mx[mr][msl >> 6] = wm;      // the two waves' maxima
-    }
-    __syncthreads();
-    if (tid < REP * 128) {
-        const float M = fmaxf(s_mx[mr][0], s_mx[mr][1]);
-        const float w = mo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - M);
-        s_w[mr][msl] = w;
-        s_l[mr][msl] *= w;
-    }
-    __syncthreads();
-    {
-        const int o = tid >> 4, part = tid & 15;
-        const int r = o / VD, d = o % VD;
-        float num = 0.f, den = 0.f;
-        if (o < REP * VD) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int sl = part * 8 + k;
-                num = fmaf(s_w[r][sl], s_o[sl][r][d], num);
-                den += s_l[r][sl];
-            }
-        }
-        num = sum16(num);
-        den = sum16(den);
-        if (o < REP * VD && part == 0) gst(a.out + (int64_t)(qh0 + r) * DH + vs * VD + d, num / den);
+    // merge of the 64 row partials: one wave per output value (lane = row)
+    if (wave < VD) {
+        const float m = s_pm[lane >> 2];
+        const float M = wave_max(m);
+        const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+        const float num = wave_sum(w * s_po[wave][lane]);
+        const float den = wave_sum(w * s_pl[lane]);
+        if (lane == 0) gst(a.out + (int64_t)qh * DH + vs * VD + wave, num / den);
     }
     // append at pos0 by one workgroup of the KV head
-    if (vs == 0 && qg == 0 && tid < DH) {
+    if (rest == 0 && tid < DH) {
         const int64_t row = (int64_t)pos0 * kvd + (int64_t)kvh * DH;
         gst((float*)a.ck + row + tid, s_k[tid]);
         gst((float*)a.cv + row + tid, s_v[tid]);
@@ -1083,10 +1069,19 @@ int launch_split(SplitArgs a, int rep, size_t ws_bytes, void* ws, hipStream_t st
     if constexpr (FUSED && KF == 0 && VF == 0) {
         // short fp32 caches: one launch, no partials (attn_vsplit_kernel)
         if (max_pos <= kVsMaxPos) {
-            // one query head and 8 value dims per workgroup (measured at
-            // config 2's shape, position 528: 4 query heads x 16 dims 10.2 us,
-            // 1 x 16 dims 6.3 us, 1 x 8 dims 6.0 us; split + combine 6.8 us)
-            hipLaunchKernelGGL((attn_vsplit_kernel<8, 1>), dim3(a.H * 8), dim3(1024), 0, st, a);
+            // one query head and 8 value dims per workgroup, as many steps
+            // of 256 positions as the bound needs (measured at config 2's
+            // shape, position 528, caches rotated past the MALL: 7.45 us
+            // against 7.9 us for 8 lanes per position in 128-position steps
+            // and 8.2 us for split + combine; 16 value slices per head
+            // (512 workgroups) 11.1 us; 4 query heads x 16 dims per workgroup
+            // with 8 lanes per position 10.2 us)
+            const int nst = (max_pos + 255) / 256;
+            const dim3 grid(a.H * 8);
+            if (nst == 1) hipLaunchKernelGGL((attn_vsplit_kernel<8, 1>), grid, dim3(1024), 0, st, a);
+            else if (nst == 2) hipLaunchKernelGGL((attn_vsplit_kernel<8, 2>), grid, dim3(1024), 0, st, a);
+            else if (nst == 3) hipLaunchKernelGGL((attn_vsplit_kernel<8, 3>), grid, dim3(1024), 0, st, a);
+            else hipLaunchKernelGGL((attn_vsplit_kernel<8, 4>), grid, dim3(1024), 0, st, a);
             return hipGetLastError() == hipSuccess ? RINA_OK : RINA_ERR_HIP;
         }
     }

@@ -486,14 +486,16 @@ def test_decode_attention_fused_edge_blocks(rina, orc, mode, P, H, Hkv):
 @pytest.mark.parametrize("P,H,Hkv,use_dpos", [(0, 32, 8, False), (37, 32, 8, False), (543, 32, 8, True),
                                               (1500, 32, 8, False), (70, 10, 5, False), (16, 8, 8, True),
                                               (300, 32, 4, True), (1500, 32, 4, False),
-                                              (639, 32, 8, False), (631, 32, 8, True), (640, 32, 8, False)])
+                                              (1023, 32, 8, False), (1015, 32, 8, True), (1024, 32, 8, False),
+                                              (255, 32, 8, False), (256, 32, 8, False), (600, 32, 8, True)])
 def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
     """RoPE + K/V append + attention in one call == rope_append then attention
     (oracle): the rotated K row and the appended cache bytes bit-exact, the
     output within tolerance, and no other cache row touched.  fp32 caches of
-    up to 640 positions take the one-launch kernel (639, and 631 with a
-    640-row cache and a device position, are its last full step), 640 the
-    split + combine pair."""
+    up to 1024 positions take the one-launch kernel in steps of 256 positions
+    (1023, and 1015 with a 1024-row cache and a device position, fill its
+    last step; 255 / 256 end and start a step), 1024 the split + combine
+    pair."""
     hip = rina.load_hip()
     L = orc.load()
     dh = 64
