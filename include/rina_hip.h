@@ -326,6 +326,17 @@ int rina_hip_moe_block(float* h, const float* ln2, float eps, const void* gate_i
 int rina_hip_ssm_step(const float* mem, const float* dec_raw, int steps, int H, int dh,
                       float* lcs, float* wcs, float* sf_out, int reset, void* stream);
 
+/* T consecutive positions of rina_hip_ssm_step in one launch (a prompt's
+ * scan; the reference's scan kernel walks the whole sequence,
+ * kernels/ssm_kernels_fp32.cu:30-42): mem [steps][T][H*dh] and dec_raw
+ * [steps][T][H] hold the projections of each position; the sf row of
+ * position t goes to sf_out + t * sf_stride (sf_stride >= H*dh).  reset != 0
+ * starts the scan from zero at the first position.  Every element advances
+ * position by position with rina_hip_ssm_step's operations, so the rows and
+ * the final state equal T one-position calls bit for bit. */
+int rina_hip_ssm_scan(const float* mem, const float* dec_raw, int steps, int H, int dh, int T,
+                      float* lcs, float* wcs, float* sf_out, int sf_stride, int reset, void* stream);
+
 /* The SSM layer's step after cq = LN(W_dq x) in one launch: LN(cq, q_norm)
  * (LayerNorm, weight only, eps), mem_k = W_mem[k] . cq [H*dh] and
  * dec_k = W_decay[k] . cq [H] for k < steps, then rina_hip_ssm_step on them

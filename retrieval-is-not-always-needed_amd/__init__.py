@@ -65,6 +65,7 @@ _HIP_SIGS = {
     "rina_hip_moe_block": (I32, [VP, VP, F32, VP, I32, VP, VP, VP, I32, VP, VP, VP, I32, I64, I64, I32, I32, I32,
                                  I32, VP, SZ, VP]),
     "rina_hip_ssm_step": (I32, [VP, VP, I32, I32, I32, VP, VP, VP, I32, VP]),
+    "rina_hip_ssm_scan": (I32, [VP, VP, I32, I32, I32, I32, VP, VP, VP, I32, I32, VP]),
     "rina_hip_ssm_proj_step": (I32, [VP, VP, F32, C.POINTER(VP), C.POINTER(VP), I32, I32, I32, I32, I32, VP, VP,
                                      VP, I32, VP]),
     "rina_hip_dq_attention_workspace": (SZ, [I32, I32, I32]),

@@ -15,6 +15,12 @@
 // one position per token with the reference's per-position operations, so a
 // decode step equals the full recompute.  A host-position call at
 // start_pos 0 restarts the scan; calls must continue the sequence in order.
+// A prompt (T > 1 rows at host positions) runs its matvecs as T-row
+// matrix products, the SSM scan over all T positions in one launch
+// (rina_hip_ssm_scan), and the RINA-MLA attention position by position
+// (each row appends its K/V, then attends to the rows before it), with the
+// rows' intermediates in ForwardBuffers::mla (workspace_per_token floats
+// per row).
 #include <algorithm>
 #include <cstdio>
 #include <string>
@@ -66,13 +72,14 @@ struct MLPPart {
     const void *w1 = nullptr, *w2 = nullptr, *w3 = nullptr;
     const float *ln2 = nullptr;
     int hd = 0;
-    int run(float* ht, ForwardBuffers& b, int d, int qt, hipStream_t s) const {
+    // h[M, d] += MLP(h) for M rows (b.g holds M rows of hd)
+    int run(float* ht, ForwardBuffers& b, int d, int qt, hipStream_t s, int M = 1) const {
         int rc;
         rina_linear_seg up{w1, w3, b.g, hd};
-        if ((rc = rina_hip_linear_fused(&up, 1, qt, ht, 1, d, RINA_EPI_SWIGLU, RINA_PRO_LAYERNORM, ln2, 1e-5f, s)))
+        if ((rc = rina_hip_linear_fused(&up, 1, qt, ht, M, d, RINA_EPI_SWIGLU, RINA_PRO_LAYERNORM, ln2, 1e-5f, s)))
             return rc;
         rina_linear_seg down{w2, nullptr, ht, d};
-        return rina_hip_linear_fused(&down, 1, qt, b.g, 1, hd, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s);
+        return rina_hip_linear_fused(&down, 1, qt, b.g, M, hd, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s);
     }
 };
 
@@ -122,7 +129,44 @@ struct SSMImpl {
                dev_alloc(&scratch, (size_t)d + H * dh + dc + 3 * H * dh + 3 * H);
     }
 
+    // prompt rows: xln [T][d] | x2 [T][d + H*dh] | cq [T][dc] | mem [steps][T][H*dh] | dec [steps][T][H]
+    int rows_per_token() const { return 2 * d + H * dh + dc + steps * (H * dh + H); }
+
+    int forward_rows(float* h, ForwardBuffers& b, int T, hipStream_t s) {
+        const int start_pos = b.kv_cache.start_pos;
+        const int xw = d + H * dh;
+        float* xln = b.mla;
+        float* x2 = xln + (size_t)T * d;
+        float* cq = x2 + (size_t)T * xw;
+        float* mem = cq + (size_t)T * dc;
+        float* dec = mem + (size_t)steps * T * H * dh;
+        int rc;
+#define CK(x) do { if ((rc = (x)) != RINA_OK) return rc; } while (0)
+        // x = LN(h, ln1) (:93-96), kept as the first d columns of W_out's input rows
+        CK(rina_hip_layer_norm(h, xln, ln1, T, d, 1e-5f, s));
+        if (hipMemcpy2DAsync(x2, sizeof(float) * xw, xln, sizeof(float) * d, sizeof(float) * d, T,
+                             hipMemcpyDeviceToDevice, s) != hipSuccess)
+            return RINA_ERR_HIP;
+        rina_linear_seg sq{w_dq, nullptr, cq, dc};
+        CK(rina_hip_linear_fused(&sq, 1, qt, xln, T, d, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
+        // LN(cq, q_norm) and the memory / decay projections of every row (:97-101)
+        rina_linear_seg sp[6];
+        for (int k = 0; k < steps; k++) {
+            sp[k] = {w_mem[k], nullptr, mem + (size_t)k * T * H * dh, H * dh};
+            sp[steps + k] = {w_decay[k], nullptr, dec + (size_t)k * T * H, H};
+        }
+        CK(rina_hip_linear_fused(sp, 2 * steps, qt, cq, T, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
+        // the scan over the T positions (:102-109), sf into the last H*dh columns of x2
+        CK(rina_hip_ssm_scan(mem, dec, steps, H, dh, T, lcs, wcs, x2 + d, xw, start_pos == 0 ? 1 : 0, s));
+        rina_linear_seg so{w_out, nullptr, h, d};
+        CK(rina_hip_linear_fused(&so, 1, qt, x2, T, xw, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
+        CK(mlp.run(h, b, d, qt, s, T));
+#undef CK
+        return RINA_OK;
+    }
+
     int forward(float* h, ForwardBuffers& b, int T, hipStream_t s) {
+        if (T > 1 && !b.d_pos && b.mla) return forward_rows(h, b, T, s);
         const int start_pos = b.kv_cache.start_pos;
         float* x2 = scratch;
         float* cq = x2 + d + H * dh;
@@ -239,7 +283,41 @@ struct RMLAImpl {
                (!rb || dev_alloc((uint8_t**)&ckr, rb)) && dev_alloc(&scratch, sc) && dev_alloc((uint8_t**)&ws, ws_bytes);
     }
 
+    // prompt rows: cq [T][dc] | qr [T][H*dhr] | kr [T][Hkv*dhr] | q [T][H*dh] | k, v [T][Hkv*dh] | att [T][H*dh]
+    int rows_per_token() const { return dc + H * dhr + Hkv * dhr + 2 * H * dh + 2 * Hkv * dh; }
+
+    int forward_rows(float* h, ForwardBuffers& b, int T, hipStream_t s) {
+        const int start_pos = b.kv_cache.start_pos;
+        float* cq = b.mla;
+        float* qr = cq + (size_t)T * dc;
+        float* kr = qr + (size_t)T * H * dhr;
+        float* q = kr + (size_t)T * Hkv * dhr;
+        float* k = q + (size_t)T * H * dh;
+        float* v = k + (size_t)T * Hkv * dh;
+        float* att = v + (size_t)T * Hkv * dh;
+        int rc;
+#define CK(x) do { if ((rc = (x)) != RINA_OK) return rc; } while (0)
+        rina_linear_seg s1[3] = {{w_dqkv, nullptr, cq, dc}, {w_qr, nullptr, qr, H * dhr}, {w_kr, nullptr, kr, Hkv * dhr}};
+        CK(rina_hip_linear_fused(s1, 3, qt, h, T, d, RINA_EPI_STORE, RINA_PRO_LAYERNORM, ln1, 1e-5f, s));
+        rina_linear_seg s2[2] = {{w_uq, nullptr, q, H * dh}, {w_uk, nullptr, k, Hkv * dh}};
+        CK(rina_hip_linear_fused(s2, 2, qt, cq, T, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
+        rina_linear_seg s3{w_k2v, nullptr, v, Hkv * dh};
+        CK(rina_hip_linear_fused(&s3, 1, qt, k, T, Hkv * dh, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
+        // causal attention (:78-86): row t appends its K / V at start_pos + t and attends to positions <= it
+        for (int t = 0; t < T; t++)
+            CK(rina_hip_dq_decode_attention_kv(q + (size_t)t * H * dh, qr + (size_t)t * H * dhr, k + (size_t)t * Hkv * dh,
+                                               kr + (size_t)t * Hkv * dhr, v + (size_t)t * Hkv * dh, rqc, rqs, rkc, rks,
+                                               kv_mode, ck, cv, ckr, H, Hkv, dh, dhr, dh, start_pos + t, nullptr,
+                                               max_seq, att + (size_t)t * H * dh, ws, ws_bytes, s));
+        rina_linear_seg so{c_proj, nullptr, h, d};
+        CK(rina_hip_linear_fused(&so, 1, qt, att, T, H * dh, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
+        CK(mlp.run(h, b, d, qt, s, T));
+#undef CK
+        return RINA_OK;
+    }
+
     int forward(float* h, ForwardBuffers& b, int T, hipStream_t s) {
+        if (T > 1 && !b.d_pos && b.mla) return forward_rows(h, b, T, s);
         const int start_pos = b.kv_cache.start_pos;
         float* cq = scratch;
         float* qr = cq + dc;
@@ -277,14 +355,16 @@ void v_forward(void* self, float* h, ForwardBuffers& b, int B, int T, hipStream_
     (void)B;
     b.fail(((Impl*)self)->forward(h, b, T, s));
 }
-int v_ws(void*, int, int, int) { return 0; }
+// floats per prompt row the layer needs in ForwardBuffers::mla
+template <typename Impl>
+int v_ws(void* self, int, int, int) { return ((Impl*)self)->rows_per_token(); }
 template <typename Impl>
 void v_destroy(void* self) { delete (Impl*)self; }
 
-const LayerVTable kSSMVTable = {v_init<SSMImpl>, v_forward<SSMImpl>, layer_no_backward, v_ws, layer_no_saved,
+const LayerVTable kSSMVTable = {v_init<SSMImpl>, v_forward<SSMImpl>, layer_no_backward, v_ws<SSMImpl>, layer_no_saved,
                                 v_destroy<SSMImpl>};
-const LayerVTable kRMLAVTable = {v_init<RMLAImpl>, v_forward<RMLAImpl>, layer_no_backward, v_ws, layer_no_saved,
-                                 v_destroy<RMLAImpl>};
+const LayerVTable kRMLAVTable = {v_init<RMLAImpl>, v_forward<RMLAImpl>, layer_no_backward, v_ws<RMLAImpl>,
+                                 layer_no_saved, v_destroy<RMLAImpl>};
 
 }  // namespace
 

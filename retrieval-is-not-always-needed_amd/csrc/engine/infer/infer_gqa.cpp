@@ -27,6 +27,7 @@ struct GQAInference : DeviceGreedyInference {
     const WeightTensor* ln_f = nullptr;
     const WeightTensor* lm_head = nullptr;
     int hd = 0, kvd = 0;
+    int rows_ws = 0;   // floats per prompt row the layers need in ForwardBuffers::mla (the Jamba layers')
     bool use_rms = false;
 
     bool fail(const std::string& m) { err_ = m; return false; }
@@ -54,12 +55,13 @@ struct GQAInference : DeviceGreedyInference {
             if (t && t->n_dim >= 2) hd = std::max(hd, (int)t->shape[0]);
         }
         if (hd <= 0) return fail("gqa: cannot size the MLP buffer (no mlp.w1 and no hidden_dim)");
+        for (auto& l : layers) rows_ws = std::max(rows_ws, l->workspace_per_token(cfg.dim, cfg.n_heads, cfg.head_dim));
         max_seq = cfg.max_seq_len > 0 ? cfg.max_seq_len : 512;
         vocab = cfg.vocab_size;
         kvd = cfg.n_kv_heads * cfg.head_dim;
         use_rms = cfg.name.find("llama") != std::string::npos;
         int cap = std::min(max_seq, 512);
-        if (!bufs.alloc_fwd(cap, cfg.dim, cfg.n_heads * cfg.head_dim, kvd, hd, cfg.vocab_size, 0))
+        if (!bufs.alloc_fwd(cap, cfg.dim, cfg.n_heads * cfg.head_dim, kvd, hd, cfg.vocab_size, rows_ws))
             return fail("gqa: forward buffer allocation failed");
         int mode = kv_mode_from_name(cfg.kv_quant_mode.c_str());
         if (mode < 0) return fail("gqa: unknown kv_quant_mode " + cfg.kv_quant_mode);
@@ -95,7 +97,7 @@ struct GQAInference : DeviceGreedyInference {
         bufs.fwd.attn_ws = keep.attn_ws;
         bufs.fwd.attn_ws_bytes = keep.attn_ws_bytes;
         bufs.fwd.kv_tap = keep.kv_tap;
-        if (!bufs.alloc_fwd(n, cfg.dim, cfg.n_heads * cfg.head_dim, kvd, hd, cfg.vocab_size, 0)) return RINA_ERR_HIP;
+        if (!bufs.alloc_fwd(n, cfg.dim, cfg.n_heads * cfg.head_dim, kvd, hd, cfg.vocab_size, rows_ws)) return RINA_ERR_HIP;
         return RINA_OK;
     }
 

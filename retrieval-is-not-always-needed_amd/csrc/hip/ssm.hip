@@ -13,25 +13,32 @@ namespace {
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// One scan advance for element j from the step's projections (decay rows
-// pre-sigmoid) and the state l0 = lcs[j], w0 = wcs[j] (read by the caller,
-// early), shared by both kernels.
-__device__ __forceinline__ void ssm_advance(const float (&dr)[3], const float (&m)[3], int steps, float l0, float w0,
-                                            int j, float* lcs, float* wcs, float* sf, int reset) {
+// One position of the aggregation and scan for one element from the
+// step's projections (decay rows pre-sigmoid): advances the state (l, w) and
+// returns sf; every kernel below runs exactly these operations.
+__device__ __forceinline__ float ssm_update(const float (&dr)[3], const float (&m)[3], int steps, float& l, float& w) {
     float dd[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) dd[k] = k < steps ? sigmoid_f(dr[k]) : 1.0f;
     float da = dd[0] * dd[1] * dd[2];                          // ssm_agg: da
     const float ma = fmaf(m[0] * dd[1], dd[2], m[1] * dd[2]) + m[2];
     if (da <= 1e-38f) da = 1e-38f;                             // ssm_scan
-    float l = reset ? 0.f : l0;
-    float w = reset ? 0.f : w0;
     l += logf(da);
     const float ca = expf(l);
     w += ma / fmaxf(ca, 1e-30f);
+    return ca * w;
+}
+
+// One scan advance for element j with the state l0 = lcs[j], w0 = wcs[j]
+// (read by the caller, early), shared by the one-position kernels.
+__device__ __forceinline__ void ssm_advance(const float (&dr)[3], const float (&m)[3], int steps, float l0, float w0,
+                                            int j, float* lcs, float* wcs, float* sf, int reset) {
+    float l = reset ? 0.f : l0;
+    float w = reset ? 0.f : w0;
+    const float y = ssm_update(dr, m, steps, l, w);
     gst(lcs + j, l);
     gst(wcs + j, w);
-    gst(sf + j, ca * w);
+    gst(sf + j, y);
 }
 
 // grid H, block dh: thread (h, d)
@@ -47,6 +54,42 @@ __global__ __launch_bounds__(256) void ssm_step_kernel(const float* mem, const f
         m[k] = k < steps ? gld(mem + (int64_t)k * H * dh + j) : 0.0f;
     }
     ssm_advance(dr, m, steps, gld(lcs + j), gld(wcs + j), j, lcs, wcs, sf, reset);
+}
+
+// T positions of the scan in one launch (a prompt; the reference's scan
+// kernel walks the whole sequence the same way, ssm_kernels_fp32.cu:30-42).
+// grid H, block dh: thread (h, d) advances its element position by position
+// with ssm_update, so the rows and the final state equal T one-position
+// launches bit for bit.  mem [steps][T][H*dh], dec [steps][T][H]; the sf
+// row of position t at sf + t * sf_stride.  The next position's projections
+// are loaded before the current one is applied.
+__global__ __launch_bounds__(256) void ssm_scan_kernel(const float* mem, const float* dec, int steps, int H, int dh,
+                                                       int T, float* lcs, float* wcs, float* sf, int sf_stride,
+                                                       int reset) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    if (d >= dh) return;
+    const int j = h * dh + d;
+    const int64_t HD = (int64_t)H * dh;
+    float l = reset ? 0.f : gld(lcs + j);
+    float w = reset ? 0.f : gld(wcs + j);
+    float dr[3], m[3];
+    auto load = [&](int t, float (&dq)[3], float (&mq)[3]) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            dq[k] = k < steps ? gld(dec + ((int64_t)k * T + t) * H + h) : 0.0f;
+            mq[k] = k < steps ? gld(mem + ((int64_t)k * T + t) * HD + j) : 0.0f;
+        }
+    };
+    load(0, dr, m);
+    for (int t = 0; t < T; t++) {
+        float dn[3] = {0.f, 0.f, 0.f}, mn[3] = {0.f, 0.f, 0.f};
+        if (t + 1 < T) load(t + 1, dn, mn);
+        gst(sf + (int64_t)t * sf_stride + j, ssm_update(dr, m, steps, l, w));
+#pragma unroll
+        for (int k = 0; k < 3; k++) { dr[k] = dn[k]; m[k] = mn[k]; }
+    }
+    gst(lcs + j, l);
+    gst(wcs + j, w);
 }
 
 // ---------------------------------------------------------------------------
@@ -219,6 +262,18 @@ extern "C" int rina_hip_ssm_step(const float* mem, const float* dec_raw, int ste
     if (dh > 256) return RINA_ERR_SHAPE;
     hipLaunchKernelGGL(ssm_step_kernel, dim3(H), dim3(dh), 0, as_stream(stream), mem, dec_raw, steps, H, dh, lcs, wcs,
                        sf_out, reset);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
+}
+
+extern "C" int rina_hip_ssm_scan(const float* mem, const float* dec_raw, int steps, int H, int dh, int T, float* lcs,
+                                 float* wcs, float* sf_out, int sf_stride, int reset, void* stream) {
+    if (!mem || !dec_raw || !lcs || !wcs || !sf_out || H < 1 || dh < 1 || T < 1 || steps < 1 || steps > 3 ||
+        sf_stride < H * dh)
+        return RINA_ERR_ARG;
+    if (dh > 256) return RINA_ERR_SHAPE;
+    hipLaunchKernelGGL(ssm_scan_kernel, dim3(H), dim3(dh), 0, as_stream(stream), mem, dec_raw, steps, H, dh, T, lcs,
+                       wcs, sf_out, sf_stride, reset);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }

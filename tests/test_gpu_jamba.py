@@ -115,6 +115,41 @@ def test_jamba_engine_forward_logits(rina, orc, tiny_jamba):
     eng.rina_infer_destroy(inf)
 
 
+def test_jamba_prompt_rows_match_single_positions(rina, orc, tiny_jamba):
+    """A prompt of T rows (the matvecs as T-row products, the SSM scan over
+    the T positions in one launch, the RINA-MLA attention row by row) against
+    the same ids fed one position at a time: every row's logits, and the
+    decode steps after the prompt (which read the caches and scan state the
+    two paths left), within tolerance."""
+    import torch
+    hm, tensors, max_seq = tiny_jamba
+    eng = rina.load_engine()
+    V = jt.CFG["vocab_size"]
+    ids = np.array([5, 17, 3, 90, 42, 7, 8, 1, 33, 64, 2, 71, 19, 4, 6, 50, 12, 99, 23], np.int32)
+    T = len(ids)
+    rows_inf, one_inf = hm.infer("gqa", max_seq=max_seq), hm.infer("gqa", max_seq=max_seq)
+    lg = empty(T * V)
+    rina.check(eng.rina_infer_forward(rows_inf, torch.from_numpy(ids).cuda().data_ptr(), lg.data_ptr(), 1, T, 0,
+                                      stream()), "prompt rows")
+    rows = host(lg).reshape(T, V)
+    one = np.zeros((T, V), np.float32)
+    l1 = empty(V)
+    for t in range(T):
+        x = torch.from_numpy(ids[t:t + 1].copy()).cuda()
+        rina.check(eng.rina_infer_forward(one_inf, x.data_ptr(), l1.data_ptr(), 1, 1, t, stream()), "position %d" % t)
+        one[t] = host(l1)
+    assert_close(rows, one, what="prompt rows vs one position at a time")
+    for t, nxt in enumerate([11, 64, 2]):
+        x = torch.from_numpy(np.array([nxt], np.int32)).cuda()
+        got = []
+        for inf in (rows_inf, one_inf):
+            rina.check(eng.rina_infer_forward(inf, x.data_ptr(), l1.data_ptr(), 1, 1, T + t, stream()), "decode")
+            got.append(host(l1))
+        assert_close(got[0], got[1], what="decode %d after the prompt" % t)
+    eng.rina_infer_destroy(rows_inf)
+    eng.rina_infer_destroy(one_inf)
+
+
 @pytest.mark.parametrize("use_graph", [True, False])
 def test_jamba_engine_greedy_identical(rina, orc, tiny_jamba, use_graph):
     hm, tensors, max_seq = tiny_jamba

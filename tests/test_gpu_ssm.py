@@ -105,6 +105,42 @@ def test_ssm_step_paths_against_reference(rina, qt, H, dh, dc, steps):
         assert_close(host(got[1]), wcs_ref, what=name + " wcs")
 
 
+@pytest.mark.parametrize("H,dh,steps,T,reset", [(4, 64, 3, 37, 1), (3, 6, 2, 5, 0), (2, 5, 1, 1, 1), (10, 64, 3, 300, 0)])
+def test_ssm_scan_equals_steps(rina, H, dh, steps, T, reset):
+    """rina_hip_ssm_scan over T positions (a prompt's scan in one launch)
+    equals T calls of rina_hip_ssm_step, bit for bit: every sf row (written
+    with a row stride wider than H*dh, the gaps untouched) and the final
+    state, from a zero start (reset) and from a carried state.  The step
+    kernel is pinned against the float64 scan above."""
+    hip = rina.load_hip()
+    r = rng(7 * H + dh + 11 * steps + T + reset)
+    n = H * dh
+    mem = (r.standard_normal((steps, T, n)) * 0.7).astype(np.float32)
+    dec = (r.standard_normal((steps, T, H)) * 1.5 + 1.0).astype(np.float32)
+    l0 = r.uniform(-3.0, 0.0, n).astype(np.float32)
+    w0 = r.standard_normal(n).astype(np.float32)
+    # T one-position launches
+    lcs1, wcs1 = dev(l0), dev(w0)
+    sf1 = np.zeros((T, n), np.float32)
+    out = empty(n)
+    for t in range(T):
+        md, dd = dev(np.ascontiguousarray(mem[:, t, :])), dev(np.ascontiguousarray(dec[:, t, :]))
+        ok(hip.rina_hip_ssm_step(md.data_ptr(), dd.data_ptr(), steps, H, dh, lcs1.data_ptr(), wcs1.data_ptr(),
+                                 out.data_ptr(), reset if t == 0 else 0, stream()), "ssm_step")
+        sf1[t] = host(out)
+    # one scan launch
+    stride = n + 7
+    lcs2, wcs2 = dev(l0), dev(w0)
+    sf2 = dev(np.full(T * stride, 123.0, np.float32))
+    ok(hip.rina_hip_ssm_scan(dev(mem).data_ptr(), dev(dec).data_ptr(), steps, H, dh, T, lcs2.data_ptr(),
+                             wcs2.data_ptr(), sf2.data_ptr(), stride, reset, stream()), "ssm_scan")
+    got = host(sf2).reshape(T, stride)
+    assert np.array_equal(got[:, :n].view(np.uint32), sf1.view(np.uint32))
+    assert np.all(got[:, n:] == 123.0)
+    assert np.array_equal(host(lcs2).view(np.uint32), host(lcs1).view(np.uint32))
+    assert np.array_equal(host(wcs2).view(np.uint32), host(wcs1).view(np.uint32))
+
+
 def test_ssm_proj_step_rejects(rina):
     hip = rina.load_hip()
     buf = empty(1 << 16)
