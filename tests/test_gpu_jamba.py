@@ -11,7 +11,7 @@ import pytest
 
 import _jamba_tiny as jt
 import _numpy_ref as nr
-from _util import REL_TOL, assert_close, dev, empty, host, ok, rng, stream
+from _util import REL_TOL, assert_close, assert_close_elem, dev, empty, host, ok, rng, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -60,7 +60,7 @@ def test_dq_decode_attention(rina, P, use_dpos, H, Hkv, da, db):
                                         cd.data_ptr(), sd.data_ptr(), ckd.data_ptr(), cvd.data_ptr(), H, Hkv, da, db,
                                         dv, 0 if use_dpos else P, pos.data_ptr() if use_dpos else None, max_seq,
                                         od.data_ptr(), ws.data_ptr(), wsb, stream()), "dq attention")
-    assert_close(host(od), ref, what="dq attention P %d" % P)
+    assert_close_elem(host(od), ref, what="dq attention P %d" % P)
     gk = host(ckd).reshape(max_seq, Hkv, dq)
     assert np.max(np.abs(gk[P] - kn)) <= 2e-6 * np.max(np.abs(kn))          # appended K row (rotated)
     assert np.array_equal(host(cvd).reshape(max_seq, Hkv, dv)[P], v)
@@ -322,7 +322,7 @@ def test_dq_decode_attention_q2k_q1v(rina, orc, P, use_dpos, H, Hkv, db):
                                            krd.data_ptr(), H, Hkv, da, db, dv, 0 if use_dpos else P,
                                            pos.data_ptr() if use_dpos else None, max_seq, od.data_ptr(),
                                            ws.data_ptr(), wsb, stream()), "dq attention q2k_q1v")
-    assert_close(host(od), ref, what="dq attention q2k_q1v P %d" % P)
+    assert_close_elem(host(od), ref, what="dq attention q2k_q1v P %d" % P)
     gk, gv, gr = host(ckd), host(cvd), host(krd).reshape(max_seq, Hkv, db)
     kbytes, vbytes = Hkv * (da // 32) * 10, Hkv * (dv // 32) * 6
     assert np.array_equal(gk[P * kbytes:(P + 1) * kbytes], orc.kv_quantize(3, ka.reshape(-1)))

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import _numpy_ref as nr
-from _util import REL_TOL, assert_close, dev, empty, host, ok, rng, stream
+from _util import REL_TOL, assert_close, assert_close_elem, dev, empty, host, ok, rng, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -355,19 +355,19 @@ def attention_case(rina, orc, mode, P, T, H=32, Hkv=8, dh=64, pre_rope=0, use_dp
 @pytest.mark.parametrize("P", [0, 1, 31, 32, 33, 100, 543, 1000])
 def test_attention_decode(rina, orc, mode, P):
     got, ref = attention_case(rina, orc, mode, P, 1)
-    assert_close(got, ref, what="decode mode %d pos %d" % (mode, P))
+    assert_close_elem(got, ref, what="decode mode %d pos %d" % (mode, P))
 
 
 @pytest.mark.parametrize("mode", [0, 1, 5])
 def test_attention_decode_device_pos(rina, orc, mode):
     got, ref = attention_case(rina, orc, mode, 70, 1, use_dpos=True)
-    assert_close(got, ref, what="d_pos mode %d" % mode)
+    assert_close_elem(got, ref, what="d_pos mode %d" % mode)
 
 
 @pytest.mark.parametrize("mode,P,T", [(0, 0, 7), (0, 5, 4), (2, 9, 3), (5, 0, 33), (1, 40, 2)])
 def test_attention_multi_row(rina, orc, mode, P, T):
     got, ref = attention_case(rina, orc, mode, P, T)
-    assert_close(got, ref, what="rows mode %d P %d T %d" % (mode, P, T))
+    assert_close_elem(got, ref, what="rows mode %d P %d T %d" % (mode, P, T))
 
 
 @pytest.mark.parametrize("T,H,Hkv", [(100, 32, 8), (300, 32, 8), (512, 32, 8), (17, 8, 2), (250, 16, 2),
@@ -378,13 +378,13 @@ def test_attention_prompt_from_zero(rina, orc, T, H, Hkv):
     matrix-core kernel (config 2's 512 x 32 / 8 among them), the others the
     one-wave block kernel."""
     got, ref = attention_case(rina, orc, 0, 0, T, H=H, Hkv=Hkv)
-    assert_close(got, ref, what="prompt T %d H %d/%d" % (T, H, Hkv))
+    assert_close_elem(got, ref, what="prompt T %d H %d/%d" % (T, H, Hkv))
 
 
 @pytest.mark.parametrize("H,Hkv,dh", [(10, 5, 64), (16, 16, 128), (4, 2, 32)])
 def test_attention_other_shapes(rina, orc, H, Hkv, dh):
     got, ref = attention_case(rina, orc, 0, 20, 1, H=H, Hkv=Hkv, dh=dh)
-    assert_close(got, ref, what="shape %s" % ((H, Hkv, dh),))
+    assert_close_elem(got, ref, what="shape %s" % ((H, Hkv, dh),))
 
 
 def edge_row(r, n, t):
@@ -535,7 +535,7 @@ def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
                                          pos.data_ptr() if use_dpos else None, max_seq, od.data_ptr(),
                                          krot.data_ptr(), ws.data_ptr(), ws_bytes, stream()), "decode attention")
     assert np.array_equal(host(krot).view(np.uint32), kr.view(np.uint32))
-    assert_close(host(od), ref, what="fused decode mode %d P %d" % (mode, P))
+    assert_close_elem(host(od), ref, what="fused decode mode %d P %d" % (mode, P))
     gk, gv = host(ckd), host(cvd)
     if mode == 0:
         want_k = kc.copy(); want_k[P] = kr
@@ -583,14 +583,14 @@ def test_decode_attention_sequence(rina, orc):
         ref = np.zeros(H * dh, np.float32)
         L.orc_gqa_attention(qr.ctypes.data, kr.ctypes.data, v.ctypes.data, kc.ctypes.data, vc.ctypes.data, None,
                             None, 0, 0, None, None, 1, P, H, Hkv, dh, ref.ctypes.data)
-        assert_close(host(od), ref, what="decode call %d (P %d)" % (i, P))
+        assert_close_elem(host(od), ref, what="decode call %d (P %d)" % (i, P))
         kc[P], vc[P] = kr, v
 
 
 @pytest.mark.parametrize("mode", [0, 2])
 def test_attention_pre_rope(rina, orc, mode):
     got, ref = attention_case(rina, orc, mode, 12, 1, pre_rope=1)
-    assert_close(got, ref, what="pre_rope mode %d" % mode)
+    assert_close_elem(got, ref, what="pre_rope mode %d" % mode)
 
 
 @pytest.mark.parametrize("d", [64, 102, 640, 2048, 3000, 8192, 10000])
@@ -608,9 +608,9 @@ def test_rms_norm_shapes(rina, orc, d):
     L.orc_rms_norm(ref.ctypes.data, w.ctypes.data, n, d, np.float32(1e-5))
     xd, od, wd = dev(x), empty(n * d), dev(w)
     ok(hip.rina_hip_rms_norm(xd.data_ptr(), od.data_ptr(), wd.data_ptr(), n, d, np.float32(1e-5), stream()))
-    assert_close(host(od).reshape(n, d), ref, what="rms_norm d %d" % d)
+    assert_close_elem(host(od).reshape(n, d), ref, what="rms_norm d %d" % d)
     ok(hip.rina_hip_rms_norm(xd.data_ptr(), xd.data_ptr(), wd.data_ptr(), n, d, np.float32(1e-5), stream()))
-    assert_close(host(xd).reshape(n, d), ref, what="rms_norm in place d %d" % d)
+    assert_close_elem(host(xd).reshape(n, d), ref, what="rms_norm in place d %d" % d)
 
 
 def test_glue(rina, orc):
@@ -625,7 +625,7 @@ def test_glue(rina, orc):
         ok(fn_h(xd.data_ptr(), od.data_ptr(), dev(w).data_ptr(), n, d, np.float32(1e-5), stream()))
         ref = x.copy()
         fn_o(ref.ctypes.data, w.ctypes.data, n, d, np.float32(1e-5))
-        assert_close(host(od).reshape(n, d), ref, what="norm")
+        assert_close_elem(host(od).reshape(n, d), ref, what="norm")
     T, H, hd = 3, 4, 64
     cos, sin = rope_tables(hd, 64)
     xr = r.standard_normal((T, H, hd)).astype(np.float32)
@@ -641,12 +641,12 @@ def test_glue(rina, orc):
     ok(hip.rina_hip_silu_mul(od.data_ptr(), dev(g).data_ptr(), dev(u).data_ptr(), 5000, stream()))
     ref = np.zeros(5000, np.float32)
     L.orc_silu_mul(ref.ctypes.data, g.ctypes.data, u.ctypes.data, 5000)
-    assert_close(host(od), ref, what="silu")
+    assert_close_elem(host(od), ref, what="silu")
     ok(hip.rina_hip_add(od.data_ptr(), dev(g).data_ptr(), dev(u).data_ptr(), 5000, stream()))
     assert np.array_equal(host(od), g + u)
     dd = dev(g)
     ok(hip.rina_hip_saxpy(dd.data_ptr(), dev(u).data_ptr(), np.float32(0.5), 5000, stream()))
-    assert_close(host(dd), g + np.float32(0.5) * u, what="saxpy")
+    assert_close_elem(host(dd), g + np.float32(0.5) * u, what="saxpy")
 
 
 @pytest.mark.parametrize("qt", [6, 5, 7, 10])

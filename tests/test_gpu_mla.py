@@ -10,7 +10,7 @@ import pytest
 
 import _mla_tiny as mt
 import _numpy_ref as nr
-from _util import assert_close, dev, empty, host, ok, rng, stream
+from _util import assert_close, assert_close_elem, dev, empty, host, ok, rng, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -90,7 +90,7 @@ def test_mla_decode_attention(rina, orc, shape, qt, P, use_dpos, hint, min_seq):
                                             dev(wkvb).data_ptr(), qt, cd.data_ptr(), H, nope, rope, vd, dc,
                                             0 if use_dpos else P, pos.data_ptr() if use_dpos else None, max_seq,
                                             hint, od.data_ptr(), ws.data_ptr(), ws_bytes, stream()), "mla attention")
-    assert_close(host(od), ref, what="mla %s qt %d P %d" % (shape, qt, P))
+    assert_close_elem(host(od), ref, what="mla %s qt %d P %d" % (shape, qt, P))
     gc = host(cd).reshape(max_seq, R)
     assert np.array_equal(gc[P, dc:].view(np.uint32), kpe.view(np.uint32))     # RoPE: same fma form
     assert np.max(np.abs(gc[P, :dc] - c)) <= 1e-6 * np.max(np.abs(c))          # norm: sum order differs
