@@ -270,6 +270,24 @@ int rina_hip_mla_decode_attention_ex(const float* q, const float* kva, const flo
                                      const int* d_pos, int max_seq, int pos_hint, float* out,
                                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* A prompt of T rows at positions 0..T-1 in one call: the prefill's causal
+ * attention over all prompt rows (deepseek_mla_layer.cu:180-217, the
+ * reference's expanded form: per head K = [W_kb c | RoPE(k_pe)],
+ * V = W_vb c, scale 1/sqrt(nope + rope)).  q [T, H*(nope+rope)] and kva
+ * [T, dc+rope] are the rows rina_hip_mla_decode_attention takes one at a
+ * time; the T latent records are appended at positions 0..T-1 exactly as
+ * T decode calls append them; out [T, H*v_dim].  dc <= 512,
+ * nope + rope <= 256 and v_dim <= nope + rope (else RINA_ERR_SHAPE, before
+ * any launch); w_kv_b Q2_K, Q4_0, Q4_0F or fp32.  The workspace (16-byte
+ * aligned) holds rina_hip_mla_prompt_workspace() bytes of intermediate
+ * rows. */
+size_t rina_hip_mla_prompt_workspace(int T, int H, int nope, int rope, int v_dim, int dc);
+int rina_hip_mla_prompt_attention(const float* q, const float* kva, const float* k_norm,
+                                  float eps, const float* rope_cos, const float* rope_sin,
+                                  const void* w_kv_b, int qt_kv_b, float* cache, int H,
+                                  int nope, int rope, int v_dim, int dc, int T, int max_seq,
+                                  float* out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Router top-k of deepseek_mla_layer.cu:310-326 on the device: softmax of
  * the E logits, insertion top-k kept ascending (strict ">", the earlier
  * expert wins ties).  ids/probs [k] in that order.  E <= 256, k <= 16. */

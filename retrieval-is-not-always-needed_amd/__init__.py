@@ -58,6 +58,9 @@ _HIP_SIGS = {
     "rina_hip_mla_fused_positions": (I32, []),
     "rina_hip_mla_decode_attention_ex": (I32, [VP, VP, VP, F32, VP, VP, VP, I32, VP, I32, I32, I32, I32, I32, I32,
                                                VP, I32, I32, VP, VP, SZ, VP]),
+    "rina_hip_mla_prompt_workspace": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "rina_hip_mla_prompt_attention": (I32, [VP, VP, VP, F32, VP, VP, VP, I32, VP, I32, I32, I32, I32, I32, I32, I32,
+                                            VP, VP, SZ, VP]),
     "rina_hip_moe_topk": (I32, [VP, I32, I32, VP, VP, VP]),
     "rina_hip_moe_workspace": (SZ, [I32, I32]),
     "rina_hip_moe_ffn": (I32, [VP, VP, VP, VP, I32, I64, I64, I32, VP, VP, I32, I32, I32, VP, VP, VP, SZ, VP]),

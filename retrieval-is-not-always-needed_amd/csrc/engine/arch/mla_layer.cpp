@@ -121,9 +121,12 @@ struct MLAImpl {
         return ok;
     }
 
-    // activation floats per token in ForwardBuffers::mla:
-    // a2 [d] | acc [d] | logits [E] | ids [K] | probs [K] | G [K*F]
-    int scratch_per_token() const { return is_moe ? 2 * d + E + 2 * K + K * F : 0; }
+    // activation floats per token in ForwardBuffers::mla: the MoE rows
+    // (a2 [d] | acc [d] | logits [E] | ids [K] | probs [K] | G [K*F]), and a
+    // prompt's attention rows (rina_hip_mla_prompt_workspace per row, plus
+    // the alignment of its parts); the two are used one after the other
+    int prompt_per_token() const { return dc + H * nope + H * vd + 4 * H * (nope + rope) + 32; }
+    int scratch_per_token() const { return std::max(is_moe ? 2 * d + E + 2 * K + K * F : 0, prompt_per_token()); }
     int ffn_width() const { return is_moe ? std::max(S, F) : hd; }
 
     int forward(float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
@@ -144,7 +147,17 @@ struct MLAImpl {
             CK(rina_hip_linear_fused(&s2, 1, (int)w_kv_a.qt, h, n, d, RINA_EPI_STORE, RINA_PRO_RMSNORM, ln1, 1e-5f, s));
         }
         float* cache = b.mla_cache.layer(layer);
-        for (int t = 0; t < n; t++)
+        // a prompt from position 0: one causal attention over its rows in the
+        // reference prefill's expanded form (deepseek_mla_layer.cu:180-217)
+        const size_t pws = n > 1 ? rina_hip_mla_prompt_workspace(n, H, nope, rope, vd, dc) : 0;
+        bool batched = false;
+        if (n > 1 && start_pos == 0 && !b.d_pos && b.mla && pws && pws <= sizeof(float) * (size_t)n * prompt_per_token()) {
+            rc = rina_hip_mla_prompt_attention(q, kva, k_norm, 1e-5f, rope_c, rope_s, w_kv_b.data, (int)w_kv_b.qt,
+                                               cache, H, nope, rope, vd, dc, n, b.mla_cache.max_seq, att, b.mla, pws, s);
+            if (rc != RINA_OK && rc != RINA_ERR_SHAPE && rc != RINA_ERR_QTYPE) return rc;   // those two launch nothing
+            batched = rc == RINA_OK;
+        }
+        for (int t = 0; t < n && !batched; t++)
             CK(rina_hip_mla_decode_attention_ex(q + (size_t)t * qd, kva + (size_t)t * kvw, k_norm, 1e-5f, rope_c,
                                                 rope_s, w_kv_b.data, (int)w_kv_b.qt, cache, H, nope, rope, vd, dc,
                                                 start_pos + t, b.d_pos, b.mla_cache.max_seq, b.pos_hint,

@@ -1002,6 +1002,83 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// A prompt from position 0 in the expanded form of the reference's prefill
+// (deepseek_mla_layer.cu:180-217: one causal attention over all prompt rows
+// with K = [W_kb c | RoPE(k_pe)] and V = W_vb c per head):
+//   mla_rows_kernel:   each row's latent record into the cache (the same
+//                      operations as the decode kernels' append), its
+//                      normalized c into a contiguous matrix and its query
+//                      [q_nope | RoPE(q_rope)] per head;
+//   one T-row product of the two halves of w_kv_b (K_nope, V);
+//   mla_expand_kernel: per row and head, K = [K_nope | RoPE(k_pe)] and V
+//                      padded with zeros to the key width;
+//   causal attention over the T rows (rina_hip_gqa_attention with H KV
+//   heads of width nope + rope: scale 1/sqrt(nope + rope)), then the value
+//   columns of each head's output.
+// ---------------------------------------------------------------------------
+
+// grid T, 256 threads: row t at position start_pos + t (dc <= 512, rope / 2 <= 256)
+__global__ __launch_bounds__(256) void mla_rows_kernel(MlaArgs a, float* c_rows, float* q_full) {
+    __shared__ float s_red[4];
+    const int tid = threadIdx.x, t = blockIdx.x;
+    const int pos = a.start_pos + (int)t;
+    const int R = a.dc + a.rope, hr = a.rope / 2, D = a.nope + a.rope;
+    const float* kva = a.kva + (int64_t)t * R;
+    const int k0 = tid < a.dc ? tid : 0, k1 = tid + 256 < a.dc ? tid + 256 : 0, jr = tid < hr ? tid : 0;
+    const float x0 = gld(kva + k0), x1 = gld(kva + k1);
+    const float n0 = gld(a.k_norm + k0), n1 = gld(a.k_norm + k1);
+    float p0 = gld(kva + a.dc + jr), p1 = gld(kva + a.dc + (hr ? jr + hr : 0));
+    const float* tc = a.rc ? a.rc : kva;
+    const float* ts = a.rs ? a.rs : kva;
+    const float cc = gld(tc + (a.rc ? (int64_t)pos * hr + jr : 0)), sn = gld(ts + (a.rs ? (int64_t)pos * hr + jr : 0));
+    float ss = (tid < a.dc ? x0 * x0 : 0.f);
+    ss = fmaf(tid + 256 < a.dc ? x1 : 0.f, tid + 256 < a.dc ? x1 : 0.f, ss);
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+    // the query rows of every head: q_nope as it is, q_rope rotated at pos
+    const float* q = a.q + (int64_t)t * a.H * D;
+    float* qo = q_full + (int64_t)t * a.H * D;
+    for (int i = tid; i < a.H * D; i += 256) {
+        const int h = i / D, e = i % D;
+        float v;
+        if (e < a.nope) {
+            v = gld(q + (int64_t)h * a.nope + e);
+        } else {
+            const int j = e - a.nope, jj = j < hr ? j : j - hr;
+            const float* qr = q + (int64_t)a.H * a.nope + (int64_t)h * a.rope;
+            float y0 = gld(qr + jj), y1 = gld(qr + jj + hr);
+            if (a.rc) rope_pair(y0, y1, gld(a.rc + (int64_t)pos * hr + jj), gld(a.rs + (int64_t)pos * hr + jj), y0, y1);
+            v = j < hr ? y0 : y1;
+        }
+        gst(qo + i, v);
+    }
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)a.dc + a.eps);
+    float* rec = a.cache + (int64_t)pos * R;
+    float* cr = c_rows + (int64_t)t * a.dc;
+    if (tid < a.dc) { const float v = x0 * inv * n0; gst(rec + tid, v); gst(cr + tid, v); }
+    if (tid + 256 < a.dc) { const float v = x1 * inv * n1; gst(rec + tid + 256, v); gst(cr + tid + 256, v); }
+    if (tid < hr) {
+        if (a.rc) rope_pair(p0, p1, cc, sn, p0, p1);
+        gst(rec + a.dc + tid, p0);
+        gst(rec + a.dc + tid + hr, p1);
+    }
+}
+
+// grid (T, H), 256 threads (nope + rope <= 256): K and V rows of head h at row t
+__global__ __launch_bounds__(256) void mla_expand_kernel(MlaArgs a, const float* k_nope, const float* v_rows,
+                                                         float* k_full, float* v_full) {
+    const int tid = threadIdx.x, t = blockIdx.x, h = blockIdx.y;
+    const int D = a.nope + a.rope;
+    if (tid >= D) return;
+    const int64_t o = ((int64_t)t * a.H + h) * D + tid;
+    const float kv = tid < a.nope ? gld(k_nope + ((int64_t)t * a.H + h) * a.nope + tid)
+                                  : gld(a.cache + (int64_t)(a.start_pos + t) * (a.dc + a.rope) + a.dc + (tid - a.nope));
+    gst(k_full + o, kv);
+    gst(v_full + o, tid < a.v ? gld(v_rows + ((int64_t)t * a.H + h) * a.v + tid) : 0.f);
+}
+
+// ---------------------------------------------------------------------------
 // MoE
 // ---------------------------------------------------------------------------
 
@@ -1255,6 +1332,65 @@ extern "C" int rina_hip_mla_decode_attention(const float* q, const float* kva, c
     return rina_hip_mla_decode_attention_ex(q, kva, k_norm, eps, rope_cos, rope_sin, w_kv_b, qt_kv_b, cache, H, nope,
                                             rope, v_dim, dc, start_pos, d_pos, max_seq, -1, out, workspace, ws_bytes,
                                             stream);
+}
+
+extern "C" size_t rina_hip_mla_prompt_workspace(int T, int H, int nope, int rope, int v_dim, int dc) {
+    if (T < 1 || H < 1 || nope < 1 || v_dim < 1 || dc < 1 || rope < 0) return 0;
+    const size_t D = (size_t)nope + rope, t = (size_t)T;
+    // c rows | K_nope | V | K, V, Q, O at width nope + rope (16-byte aligned parts)
+    auto up4 = [](size_t n) { return (n + 3) / 4 * 4; };
+    return sizeof(float) * (up4(t * dc) + up4(t * H * nope) + up4(t * H * v_dim) + 4 * up4(t * H * D));
+}
+
+extern "C" int rina_hip_mla_prompt_attention(const float* q, const float* kva, const float* k_norm, float eps,
+                                             const float* rope_cos, const float* rope_sin, const void* w_kv_b,
+                                             int qt_kv_b, float* cache, int H, int nope, int rope, int v_dim, int dc,
+                                             int T, int max_seq, float* out, void* workspace, size_t ws_bytes,
+                                             void* stream) {
+    if (!q || !kva || !k_norm || !w_kv_b || !cache || !out || H < 1 || nope < 1 || v_dim < 1 || dc < 1 || T < 1 ||
+        max_seq < 1 || rope < 0 || rope % 2)
+        return RINA_ERR_ARG;
+    if (T > max_seq) return RINA_ERR_RANGE;
+    if (dc > 512 || rope / 2 > 256 || nope + rope > 256 || v_dim > nope + rope) return RINA_ERR_SHAPE;
+    int64_t vb_off;   // byte offset of the W_vb rows (after the H*nope W_kb rows)
+    const int64_t nkb = (int64_t)H * nope * dc;
+    if (qt_kv_b == RINA_QT_GGML_Q2_K) { if (nkb % 256) return RINA_ERR_SHAPE; vb_off = nkb / 256 * 84; }
+    else if (qt_kv_b == RINA_QT_Q4_0) { if (nkb % 32) return RINA_ERR_SHAPE; vb_off = nkb / 32 * 18; }
+    else if (qt_kv_b == RINA_QT_Q4_0F) { if (nkb % 32) return RINA_ERR_SHAPE; vb_off = nkb / 32 * 20; }
+    else if (qt_kv_b == RINA_QT_FP32) vb_off = nkb * 4;
+    else return RINA_ERR_QTYPE;
+    const size_t need = rina_hip_mla_prompt_workspace(T, H, nope, rope, v_dim, dc);
+    if (!workspace || ws_bytes < need || (uintptr_t)workspace % 16) return RINA_ERR_WORKSPACE;
+    const int D = nope + rope;
+    auto up4 = [](size_t n) { return (n + 3) / 4 * 4; };
+    float* c_rows = (float*)workspace;
+    float* k_nope = c_rows + up4((size_t)T * dc);
+    float* v_rows = k_nope + up4((size_t)T * H * nope);
+    float* k_full = v_rows + up4((size_t)T * H * v_dim);
+    float* v_full = k_full + up4((size_t)T * H * D);
+    float* q_full = v_full + up4((size_t)T * H * D);
+    float* o_full = q_full + up4((size_t)T * H * D);
+    MlaArgs a{};
+    a.q = q; a.kva = kva; a.k_norm = k_norm; a.eps = eps; a.rc = rope_cos; a.rs = rope_sin;
+    a.wkvb = (const uint8_t*)w_kv_b; a.qt = qt_kv_b; a.cache = cache; a.out = out;
+    a.H = H; a.nope = nope; a.rope = rope; a.v = v_dim; a.dc = dc; a.start_pos = 0; a.max_seq = max_seq;
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(mla_rows_kernel, dim3(T), dim3(256), 0, st, a, c_rows, q_full);
+    RINA_LAUNCH_CHECK();
+    rina_linear_seg segs[2] = {{w_kv_b, nullptr, k_nope, H * nope},
+                               {(const uint8_t*)w_kv_b + vb_off, nullptr, v_rows, H * v_dim}};
+    int rc = rina_hip_linear_fused(segs, 2, qt_kv_b, c_rows, T, dc, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(mla_expand_kernel, dim3(T, H), dim3(256), 0, st, a, k_nope, v_rows, k_full, v_full);
+    RINA_LAUNCH_CHECK();
+    rc = rina_hip_gqa_attention(q_full, k_full, v_full, k_full, v_full, RINA_KV_FP32, 0, nullptr, nullptr, T, H, H, D,
+                                0, nullptr, max_seq, o_full, nullptr, 0, stream);
+    if (rc) return rc;
+    // the value columns of every (row, head)
+    if (hipMemcpy2DAsync(out, sizeof(float) * v_dim, o_full, sizeof(float) * D, sizeof(float) * v_dim, (size_t)T * H,
+                         hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return RINA_ERR_HIP;
+    return RINA_OK;
 }
 
 extern "C" int rina_hip_moe_topk(const float* logits, int n_experts, int k, int* ids, float* probs, void* stream) {

@@ -34,6 +34,83 @@ def weight(orc, qt, rows, cols, r):
     return w, nr.dequant_q4(w, rows * cols, qt == Q4F).reshape(rows, cols).astype(np.float64)
 
 
+@pytest.mark.parametrize("shape,T", [("tiny", 2), ("tiny", 37), ("dsv2lite", 17), ("dsv2lite", 300)])
+@pytest.mark.parametrize("qt", [Q2K, Q4F, Q40])
+def test_mla_prompt_attention_matches_decode_rows(rina, orc, shape, T, qt):
+    """A prompt of T rows from position 0 in one call (the prefill's causal
+    attention in the expanded form: T-row products of W_kb / W_vb, one causal
+    attention over the rows) against the same rows fed to the decode
+    attention one position at a time: the T appended latent records bit for
+    bit, every output row within tolerance, and row T-1 against the float64
+    expanded form."""
+    hip = rina.load_hip()
+    H, nope, rope, vd, dc = (4, 32, 16, 32, 64) if shape == "tiny" else (16, 128, 64, 128, 512)
+    R = dc + rope
+    max_seq = T + 5
+    r = rng(T * 7 + H + qt)
+    wkvb, W = weight(orc, qt, H * (nope + vd), dc, r)
+    q = r.standard_normal((T, H * (nope + rope))).astype(np.float32)
+    kva = r.standard_normal((T, R)).astype(np.float32)
+    knorm = r.uniform(0.8, 1.2, dc).astype(np.float32)
+    cos, sin = rope_tables(rope, max_seq)
+    qd, kd, nd, cdv, sdv, wd = dev(q), dev(kva), dev(knorm), dev(cos), dev(sin), dev(wkvb)
+    # one position at a time
+    c1 = dev(np.zeros((max_seq, R), np.float32))
+    ws_bytes = hip.rina_hip_mla_attention_workspace(H, dc, rope, max_seq)
+    ws = empty(ws_bytes, "uint8")
+    o1 = np.zeros((T, H * vd), np.float32)
+    od = empty(H * vd)
+    for t in range(T):
+        ok(hip.rina_hip_mla_decode_attention_ex(qd.data_ptr() + 4 * t * q.shape[1], kd.data_ptr() + 4 * t * R,
+                                                nd.data_ptr(), np.float32(1e-5), cdv.data_ptr(), sdv.data_ptr(),
+                                                wd.data_ptr(), qt, c1.data_ptr(), H, nope, rope, vd, dc, t, None,
+                                                max_seq, -1, od.data_ptr(), ws.data_ptr(), ws_bytes, stream()),
+           "decode row %d" % t)
+        o1[t] = host(od)
+    # the prompt in one call
+    c2 = dev(np.zeros((max_seq, R), np.float32))
+    pws = hip.rina_hip_mla_prompt_workspace(T, H, nope, rope, vd, dc)
+    pw = empty(pws, "uint8")
+    o2 = empty(T * H * vd)
+    ok(hip.rina_hip_mla_prompt_attention(qd.data_ptr(), kd.data_ptr(), nd.data_ptr(), np.float32(1e-5),
+                                         cdv.data_ptr(), sdv.data_ptr(), wd.data_ptr(), qt, c2.data_ptr(), H, nope,
+                                         rope, vd, dc, T, max_seq, o2.data_ptr(), pw.data_ptr(), pws, stream()),
+       "prompt attention")
+    assert np.array_equal(host(c2).view(np.uint32), host(c1).view(np.uint32))
+    got = host(o2).reshape(T, H * vd)
+    for t in range(T):
+        assert_close_elem(got[t], o1[t], what="prompt row %d vs decode row" % t)
+    # row T-1 against the float64 expanded form over the appended records
+    allc = host(c2).reshape(max_seq, R).astype(np.float64)
+    L = orc.load()
+    qr = q[T - 1].copy()
+    L.orc_rope_neox(qr[H * nope:].ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, H, rope, T - 1)
+    ref = np.zeros(H * vd)
+    for hh in range(H):
+        Kn = allc[:T, :dc] @ W[hh * nope:(hh + 1) * nope].T
+        K = np.concatenate([Kn, allc[:T, dc:]], axis=1)
+        V = allc[:T, :dc] @ W[H * nope + hh * vd: H * nope + (hh + 1) * vd].T
+        qh = np.concatenate([qr[hh * nope:(hh + 1) * nope], qr[H * nope + hh * rope: H * nope + (hh + 1) * rope]])
+        ref[hh * vd:(hh + 1) * vd] = nr.softmax_attn(qh.astype(np.float64), K, V, 1 / np.sqrt(nope + rope))
+    assert_close_elem(got[T - 1], ref, what="prompt last row vs float64")
+
+
+def test_mla_prompt_attention_rejects(rina):
+    """Shapes the prompt path does not take return before any launch."""
+    hip = rina.load_hip()
+    buf = empty(1 << 16)
+    p = buf.data_ptr()
+    ws = hip.rina_hip_mla_prompt_workspace(4, 2, 32, 16, 32, 64)
+    assert hip.rina_hip_mla_prompt_attention(p, p, p, np.float32(1e-5), p, p, p, FP32, p, 2, 32, 16, 32, 1024, 4, 8,
+                                             p, p, 1 << 18, stream()) == -3        # RINA_ERR_SHAPE: dc > 512
+    assert hip.rina_hip_mla_prompt_attention(p, p, p, np.float32(1e-5), p, p, p, FP32, p, 2, 32, 16, 64, 64, 4, 8,
+                                             p, p, 1 << 18, stream()) == -3        # v_dim > nope + rope
+    assert hip.rina_hip_mla_prompt_attention(p, p, p, np.float32(1e-5), p, p, p, FP32, p, 2, 32, 16, 32, 64, 9, 8,
+                                             p, p, 1 << 18, stream()) == -4        # RINA_ERR_RANGE: T > max_seq
+    assert hip.rina_hip_mla_prompt_attention(p, p, p, np.float32(1e-5), p, p, p, FP32, p, 2, 32, 16, 32, 64, 4, 8,
+                                             p, p, ws - 4, stream()) == -6   # RINA_ERR_WORKSPACE
+
+
 @pytest.mark.parametrize("shape", ["tiny", "dsv2lite"])
 @pytest.mark.parametrize("qt", [Q2K, Q4F, Q40])
 # (position, device position, pos_hint, minimum max_seq).  At the
