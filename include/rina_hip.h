@@ -308,6 +308,22 @@ int rina_hip_moe_ffn(const float* x, const void* gate_exps, const void* up_exps,
                      int d, int ffn, const float* shared_out, float* h, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* The MoE block over a prompt's T rows in one call (forward_moe,
+ * deepseek_mla_layer.cu:291-350, for every row): h[T, d] += shared experts
+ * + sum over each row's top-k of p_j * expert_j(RMSNorm(h_row, ln2)).  The
+ * norm, the fp32 router logits and the shared experts run as T-row
+ * products; the rows are then grouped by selected expert (the selection is
+ * read back to the host once: the call synchronizes the stream) and each
+ * expert runs as one product over its rows.  gate_sh / up_sh / down_sh may
+ * be NULL with S == 0.  Any quant type rina_hip_linear_fused takes; the
+ * workspace (16-byte aligned) holds rina_hip_moe_rows_workspace() bytes. */
+size_t rina_hip_moe_rows_workspace(int T, int d, int n_experts, int k, int ffn, int shared_ffn);
+int rina_hip_moe_rows(float* h, int T, const float* ln2, float eps, const void* gate_inp, int qt_inp,
+                      const void* gate_sh, const void* up_sh, const void* down_sh, int shared_ffn, int qt_sh,
+                      const void* gate_exps, const void* up_exps, const void* down_exps, int qt_exps,
+                      int64_t stride_gu, int64_t stride_dn, int n_experts, int k, int d, int ffn,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* The whole MoE MLP block of one token (forward_moe,
  * deepseek_mla_layer.cu:291-350) for Q2_K experts and shared experts with an
  * fp32 router, in three launches and without the reference's host round

@@ -63,6 +63,9 @@ _HIP_SIGS = {
                                             VP, VP, SZ, VP]),
     "rina_hip_moe_topk": (I32, [VP, I32, I32, VP, VP, VP]),
     "rina_hip_moe_workspace": (SZ, [I32, I32]),
+    "rina_hip_moe_rows_workspace": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "rina_hip_moe_rows": (I32, [VP, I32, VP, F32, VP, I32, VP, VP, VP, I32, I32, VP, VP, VP, I32, I64, I64, I32, I32,
+                                I32, I32, VP, SZ, VP]),
     "rina_hip_moe_ffn": (I32, [VP, VP, VP, VP, I32, I64, I64, I32, VP, VP, I32, I32, I32, VP, VP, VP, SZ, VP]),
     "rina_hip_moe_block_workspace": (SZ, [I32, I32, I32, I32, I32]),
     "rina_hip_moe_block": (I32, [VP, VP, F32, VP, I32, VP, VP, VP, I32, VP, VP, VP, I32, I64, I64, I32, I32, I32,

@@ -126,8 +126,23 @@ struct MLAImpl {
     // prompt's attention rows (rina_hip_mla_prompt_workspace per row, plus
     // the alignment of its parts); the two are used one after the other
     int prompt_per_token() const { return dc + H * nope + H * vd + 4 * H * (nope + rope) + 32; }
-    int scratch_per_token() const { return std::max(is_moe ? 2 * d + E + 2 * K + K * F : 0, prompt_per_token()); }
+    // a prompt's MoE rows (rina_hip_moe_rows_workspace per row, plus alignment)
+    int moe_rows_per_token() const { return is_moe ? d + E + 4 * K + S + K * (2 * d + F) + 48 : 0; }
+    int scratch_per_token() const {
+        return std::max({is_moe ? 2 * d + E + 2 * K + K * F : 0, prompt_per_token(), moe_rows_per_token()});
+    }
     int ffn_width() const { return is_moe ? std::max(S, F) : hd; }
+
+    // the products of rina_hip_moe_rows take these shapes (Q4 rows need K % 32)
+    bool moe_rows_ok() const {
+        auto fits = [](QuantType qt, int k) {
+            return qt == QuantType::GGML_Q2_K || qt == QuantType::FP32 ||
+                   ((qt == QuantType::Q4_0 || qt == QuantType::Q4_0F) && k % 32 == 0);
+        };
+        return is_moe && E <= 256 && K <= 16 && gate_inp.qt == QuantType::FP32 && fits(gate_sh.qt, d) &&
+               fits(down_sh.qt, S) && fits(gate_exps.qt, d) && fits(down_exps.qt, F) && gate_sh.qt == up_sh.qt &&
+               gate_sh.qt == down_sh.qt;
+    }
 
     int forward(float* h, ForwardBuffers& b, int B, int T, hipStream_t s) {
         (void)B;
@@ -171,7 +186,16 @@ struct MLAImpl {
             CK(rina_hip_linear_fused(&down, 1, (int)w2.qt, b.g, n, hd, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, s));
             return RINA_OK;
         }
-        // forward_moe (:291-350), one token at a time
+        // forward_moe (:291-350) over a prompt's rows at once
+        if (n > 1 && !b.d_pos && b.mla && moe_rows_ok()) {
+            const size_t mws = rina_hip_moe_rows_workspace(n, d, E, K, F, S);
+            if (mws && mws <= sizeof(float) * (size_t)n * moe_rows_per_token())
+                return rina_hip_moe_rows(h, n, ln2, 1e-5f, gate_inp.data, (int)gate_inp.qt, gate_sh.data, up_sh.data,
+                                         down_sh.data, S, (int)gate_sh.qt, gate_exps.data, up_exps.data,
+                                         down_exps.data, (int)gate_exps.qt, stride_gu, stride_dn, E, K, d, F, b.mla,
+                                         mws, s);
+        }
+        // forward_moe, one token at a time
         if (moe_block) {
             for (int t = 0; t < n; t++) {
                 rc = rina_hip_moe_block(h + (size_t)t * d, ln2, 1e-5f, gate_inp.data, (int)gate_inp.qt, gate_sh.data,

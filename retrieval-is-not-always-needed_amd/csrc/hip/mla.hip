@@ -23,6 +23,7 @@
 // the reference's ascending order onto the shared-expert output and adds the
 // residual.
 #include <algorithm>
+#include <vector>
 #include "rina_common.hpp"
 
 namespace {
@@ -1088,11 +1089,15 @@ __global__ __launch_bounds__(256) void mla_expand_kernel(MlaArgs a, const float*
 // ">" (of equal values the earlier expert stays) in ascending order, equal
 // values ending up later-expert first.  Here every expert computes its rank
 // against the others in parallel, which gives the same set and order.
+// grid = rows: workgroup r selects from logits row r into ids / probs row r
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float* lg, int E, int k, int* ids, float* probs) {
     __shared__ float s_p[256];
     __shared__ float s_red[4];
     __shared__ float s_inv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    lg += (int64_t)blockIdx.x * E;
+    ids += (int64_t)blockIdx.x * k;
+    probs += (int64_t)blockIdx.x * k;
     const float x = tid < E ? gld(lg + tid) : -INFINITY;
     const float wm = wave_max(x);
     if (lane == 0) s_red[wave] = wm;
@@ -1122,6 +1127,22 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* lg, int E, i
             gst(probs + (k - 1 - above), p);
         }
     }
+}
+
+// prompt rows of the MoE block, grouped by expert: X[i] = a2[idx[i]]
+__global__ __launch_bounds__(256) void moe_gather_kernel(const float* a2, const int* idx, int d, float* X) {
+    const float* src = a2 + (int64_t)gld(idx + blockIdx.x) * d;
+    float* dst = X + (int64_t)blockIdx.x * d;
+    for (int c = threadIdx.x; c < d; c += 256) gst(dst + c, gld(src + c));
+}
+
+// h[idx[i]] += pr[i] * Y[i]: one expert's rows (distinct rows within a launch)
+__global__ __launch_bounds__(256) void moe_scatter_kernel(float* h, const int* idx, const float* pr, const float* Y,
+                                                          int d) {
+    float* dst = h + (int64_t)gld(idx + blockIdx.x) * d;
+    const float* src = Y + (int64_t)blockIdx.x * d;
+    const float p = gld(pr + blockIdx.x);
+    for (int c = threadIdx.x; c < d; c += 256) gst(dst + c, fmaf(p, gld(src + c), gld(dst + c)));
 }
 
 struct MoeArgs {
@@ -1402,6 +1423,113 @@ extern "C" int rina_hip_moe_topk(const float* logits, int n_experts, int k, int*
 }
 
 extern "C" size_t rina_hip_moe_workspace(int k, int ffn) { return (size_t)k * ffn * sizeof(float); }
+
+// ---------------------------------------------------------------------------
+// The MoE block over a prompt's T rows (forward_moe, deepseek_mla_layer.cu:
+// 291-350, for every row at once): the rows' ln2 norm and fp32 router
+// logits as T-row products, the top-k of every row, the shared experts as
+// T-row products added to h, then one expert at a time (ascending id) its
+// selected rows gathered, its gate/up (SiLU * up) and down products over
+// them, and h[row] += p * y.  The selection comes to the host once to group
+// the rows (the stream is synchronized there).
+// ---------------------------------------------------------------------------
+namespace {
+size_t up4f(size_t n) { return (n + 3) / 4 * 4; }
+}
+
+extern "C" size_t rina_hip_moe_rows_workspace(int T, int d, int E, int k, int F, int S) {
+    if (T < 1 || d < 1 || E < 1 || k < 1 || F < 1 || S < 0) return 0;
+    const size_t t = (size_t)T, tk = t * k;
+    // a2 | logits | probs | ids | G_shared | X | G | Y | idx | pr
+    return sizeof(float) * (up4f(t * d) + up4f(t * E) + 2 * up4f(tk) + up4f(t * S) + up4f(tk * d) + up4f(tk * F) +
+                            up4f(tk * d) + 2 * up4f(tk));
+}
+
+extern "C" int rina_hip_moe_rows(float* h, int T, const float* ln2, float eps, const void* gate_inp, int qt_inp,
+                                 const void* gate_sh, const void* up_sh, const void* down_sh, int S, int qt_sh,
+                                 const void* gate_exps, const void* up_exps, const void* down_exps, int qt_exps,
+                                 int64_t stride_gu, int64_t stride_dn, int E, int k, int d, int F, void* workspace,
+                                 size_t ws_bytes, void* stream) {
+    if (!h || !ln2 || !gate_inp || !gate_exps || !up_exps || !down_exps || T < 1 || E < 1 || E > 256 || k < 1 ||
+        k > 16 || k > E || d < 1 || F < 1 || S < 0 || (S > 0 && (!gate_sh || !up_sh || !down_sh)))
+        return RINA_ERR_ARG;
+    const size_t need = rina_hip_moe_rows_workspace(T, d, E, k, F, S);
+    if (!workspace || ws_bytes < need || (uintptr_t)workspace % 16) return RINA_ERR_WORKSPACE;
+    hipStream_t st = as_stream(stream);
+    const size_t t = (size_t)T, tk = t * k;
+    float* a2 = (float*)workspace;
+    float* logits = a2 + up4f(t * d);
+    float* probs = logits + up4f(t * E);
+    int* ids = (int*)(probs + up4f(tk));
+    float* gsh = (float*)ids + up4f(tk);
+    float* X = gsh + up4f(t * S);
+    float* G = X + up4f(tk * d);
+    float* Y = G + up4f(tk * F);
+    int* idx = (int*)(Y + up4f(tk * d));
+    float* pr = (float*)idx + up4f(tk);
+    int rc;
+    if ((rc = rina_hip_rms_norm(h, a2, ln2, T, d, eps, stream))) return rc;
+    rina_linear_seg sr{gate_inp, nullptr, logits, E};
+    if ((rc = rina_hip_linear_fused(&sr, 1, qt_inp, a2, T, d, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, stream)))
+        return rc;
+    hipLaunchKernelGGL(moe_topk_kernel, dim3(T), dim3(256), 0, st, logits, E, k, ids, probs);
+    RINA_LAUNCH_CHECK();
+    if (S > 0) {
+        rina_linear_seg su{gate_sh, up_sh, gsh, S};
+        if ((rc = rina_hip_linear_fused(&su, 1, qt_sh, a2, T, d, RINA_EPI_SWIGLU, RINA_PRO_NONE, nullptr, 0.f, stream)))
+            return rc;
+        rina_linear_seg sd{down_sh, nullptr, h, d};
+        if ((rc = rina_hip_linear_fused(&sd, 1, qt_sh, gsh, T, S, RINA_EPI_ADD, RINA_PRO_NONE, nullptr, 0.f, stream)))
+            return rc;
+    }
+    // the selection on the host: rows grouped by expert, ascending
+    std::vector<int> hid(tk);
+    std::vector<float> hpr(tk);
+    if (hipMemcpyAsync(hid.data(), ids, tk * sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipMemcpyAsync(hpr.data(), probs, tk * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return RINA_ERR_HIP;
+    std::vector<int> cnt(E + 1, 0), gi(tk), off(E + 1, 0);
+    std::vector<float> gp(tk);
+    for (size_t i = 0; i < tk; i++)
+        if (hid[i] >= 0 && hid[i] < E) cnt[hid[i]]++;
+    for (int e = 0; e < E; e++) off[e + 1] = off[e] + cnt[e];
+    std::vector<int> fill(off.begin(), off.end() - 1);
+    for (size_t i = 0; i < tk; i++) {
+        const int e = hid[i];
+        if (e < 0 || e >= E) continue;
+        gi[fill[e]] = (int)(i / k);
+        gp[fill[e]++] = hpr[i];
+    }
+    const int n_sel = off[E];
+    if (n_sel > 0 &&
+        (hipMemcpyAsync(idx, gi.data(), sizeof(int) * n_sel, hipMemcpyHostToDevice, st) != hipSuccess ||
+         hipMemcpyAsync(pr, gp.data(), sizeof(float) * n_sel, hipMemcpyHostToDevice, st) != hipSuccess)) {
+        (void)hipStreamSynchronize(st);
+        return RINA_ERR_HIP;
+    }
+    for (int e = 0; e < E && rc == RINA_OK; e++) {
+        const int n = cnt[e];
+        if (!n) continue;
+        const int o = off[e];
+        float* Xe = X + (size_t)o * d;
+        float* Ge = G + (size_t)o * F;
+        float* Ye = Y + (size_t)o * d;
+        hipLaunchKernelGGL(moe_gather_kernel, dim3(n), dim3(256), 0, st, a2, idx + o, d, Xe);
+        if (hipGetLastError() != hipSuccess) { rc = RINA_ERR_HIP; break; }
+        rina_linear_seg sg{(const uint8_t*)gate_exps + e * stride_gu, (const uint8_t*)up_exps + e * stride_gu, Ge, F};
+        if ((rc = rina_hip_linear_fused(&sg, 1, qt_exps, Xe, n, d, RINA_EPI_SWIGLU, RINA_PRO_NONE, nullptr, 0.f, stream)))
+            break;
+        rina_linear_seg sd{(const uint8_t*)down_exps + e * stride_dn, nullptr, Ye, d};
+        if ((rc = rina_hip_linear_fused(&sd, 1, qt_exps, Ge, n, F, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, stream)))
+            break;
+        hipLaunchKernelGGL(moe_scatter_kernel, dim3(n), dim3(256), 0, st, h, idx + o, pr + o, Ye, d);
+        if (hipGetLastError() != hipSuccess) rc = RINA_ERR_HIP;
+    }
+    // the host lists are sources of queued copies: wait before they go
+    if (hipStreamSynchronize(st) != hipSuccess && rc == RINA_OK) rc = RINA_ERR_HIP;
+    return rc;
+}
 
 extern "C" int rina_hip_moe_ffn(const float* x, const void* gate_exps, const void* up_exps, const void* down_exps,
                                 int qt, int64_t stride_gu, int64_t stride_dn, int n_experts, const int* ids,

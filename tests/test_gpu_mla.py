@@ -301,6 +301,64 @@ def test_moe_block_vs_float64(rina, orc, d, F, S, E, k):
     assert np.all(np.isfinite(host(hd)))
 
 
+@pytest.mark.parametrize("d,F,S,E,k,T", [(2048, 1408, 2816, 64, 6, 40), (256, 64, 128, 8, 3, 1), (256, 64, 128, 8, 3, 33),
+                                         (512, 96, 192, 16, 4, 17)])
+def test_moe_rows_matches_block_rows(rina, orc, d, F, S, E, k, T):
+    """The MoE block over a prompt's T rows in one call (T-row products, rows
+    grouped by expert) against the fused single-row block applied to each
+    row, within tolerance; row 0 against a float64 restatement of
+    forward_moe."""
+    hip = rina.load_hip()
+    r = rng(d + F + S + k + T)
+    parts = {nm: [packed_only(orc, Q2K, *shp, r) for _ in range(E)] for nm, shp in
+             (("g", (F, d)), ("u", (F, d)), ("dn", (d, F)))}
+    gate, up, down = (np.concatenate(parts[nm]) for nm in ("g", "u", "dn"))
+    sgu, sdn = gate.nbytes // E, down.nbytes // E
+    sg, sg64 = weight(orc, Q2K, S, d, r)
+    su, su64 = weight(orc, Q2K, S, d, r)
+    sd, sd64 = weight(orc, Q2K, d, S, r)
+    wr = (r.standard_normal((E, d)) * 0.05).astype(np.float32)
+    ln2 = r.uniform(0.8, 1.2, d).astype(np.float32)
+    h0 = (r.standard_normal((T, d)) * 2).astype(np.float32)
+    keep = [dev(t) for t in (ln2, wr, sg, su, sd, gate, up, down)]
+    # one row at a time through the fused block
+    hb = dev(h0)
+    wsb = hip.rina_hip_moe_block_workspace(d, E, k, F, S)
+    ws = empty(wsb // 4 + 4)
+    for t in range(T):
+        ok(hip.rina_hip_moe_block(hb.data_ptr() + 4 * t * d, keep[0].data_ptr(), np.float32(1e-5), keep[1].data_ptr(),
+                                  FP32, keep[2].data_ptr(), keep[3].data_ptr(), keep[4].data_ptr(), S,
+                                  keep[5].data_ptr(), keep[6].data_ptr(), keep[7].data_ptr(), Q2K, sgu, sdn, E, k, d, F,
+                                  ws.data_ptr(), wsb, stream()), "moe block row %d" % t)
+    # all rows at once
+    hr = dev(h0)
+    mwb = hip.rina_hip_moe_rows_workspace(T, d, E, k, F, S)
+    mws = empty(mwb // 4 + 4)
+    ok(hip.rina_hip_moe_rows(hr.data_ptr(), T, keep[0].data_ptr(), np.float32(1e-5), keep[1].data_ptr(), FP32,
+                             keep[2].data_ptr(), keep[3].data_ptr(), keep[4].data_ptr(), S, Q2K, keep[5].data_ptr(),
+                             keep[6].data_ptr(), keep[7].data_ptr(), Q2K, sgu, sdn, E, k, d, F, mws.data_ptr(), mwb,
+                             stream()), "moe rows")
+    got, want = host(hr).reshape(T, d), host(hb).reshape(T, d)
+    for t in range(T):
+        assert_close(got[t], want[t], what="moe rows, row %d" % t)
+    # row 0 against float64 forward_moe (skipped at a router near tie)
+    h64 = h0[0].astype(np.float64)
+    a2 = h64 / np.sqrt((h64 ** 2).mean() + 1e-5) * ln2
+    lg = wr.astype(np.float64) @ a2
+    p = np.exp(lg - lg.max())
+    p /= p.sum()
+    order = np.argsort(-p, kind="stable")
+    if p[order[k - 1]] - p[order[k]] > 1e-4:
+        def silu(v):
+            return v / (1 + np.exp(-v))
+        acc = sd64 @ (silu(sg64 @ a2) * (su64 @ a2))
+        for e in order[:k]:
+            g = as_f64(Q2K, parts["g"][e], F, d) @ a2
+            u = as_f64(Q2K, parts["u"][e], F, d) @ a2
+            acc = acc + p[e] * (as_f64(Q2K, parts["dn"][e], d, F) @ (silu(g) * u))
+        assert_close(got[0], h64 + acc, what="moe rows, row 0 vs float64")
+
+
 def test_moe_block_rejects_unsupported(rina):
     hip = rina.load_hip()
     buf = empty(1 << 16)
