@@ -403,6 +403,23 @@ int rina_hip_dq_decode_attention(const float* qa, const float* qb, const float* 
                                  const int* d_pos, int max_seq, float* out, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* A prompt's T rows at positions 0..T-1 of the RINA-MLA attention over the
+ * fp32 caches in one call: every row's key [ka | HF-RoPE(kb)] and value
+ * appended as rina_hip_dq_decode_attention appends them (bit for bit), then
+ * one causal attention over the rows (rina_mla_layer.cu:78-86 over the
+ * whole prompt; scale 1/sqrt(da + db)).  qa [T, H*da], qb [T, H*db],
+ * ka [T, Hkv*da], kb [T, Hkv*db], v [T, Hkv*dv]; out [T, H*dv].
+ * da + db <= 256 and dv <= da + db (else RINA_ERR_SHAPE, before any
+ * launch); the workspace (16-byte aligned) holds
+ * rina_hip_dq_prompt_workspace() bytes. */
+size_t rina_hip_dq_prompt_workspace(int T, int H, int Hkv, int da, int db, int dv);
+int rina_hip_dq_prompt_attention(const float* qa, const float* qb, const float* ka, const float* kb,
+                                 const float* v, const float* rope_q_cos, const float* rope_q_sin,
+                                 const float* rope_k_cos, const float* rope_k_sin, float* cache_k,
+                                 float* cache_v, int H, int Hkv, int da, int db, int dv, int T,
+                                 int max_seq, float* out, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* rina_hip_dq_decode_attention with the cache form chosen by kv_mode:
  *   RINA_KV_FP32     cache_k [max_seq][Hkv][da+db] fp32, cache_v
  *                    [max_seq][Hkv][dv] fp32, cache_kr unused;

@@ -77,6 +77,9 @@ _HIP_SIGS = {
     "rina_hip_dq_attention_workspace": (SZ, [I32, I32, I32]),
     "rina_hip_dq_decode_attention": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, I32, I32, I32, VP,
                                            I32, VP, VP, SZ, VP]),
+    "rina_hip_dq_prompt_workspace": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "rina_hip_dq_prompt_attention": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, I32, I32, I32, I32,
+                                           VP, VP, SZ, VP]),
     "rina_hip_dq_kv_region_bytes": (SZ, [I32, I32, I32, I32, I32, I32, I32]),
     "rina_hip_dq_decode_attention_kv": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, VP, VP, VP, I32, I32, I32, I32,
                                               I32, I32, VP, I32, VP, VP, SZ, VP]),

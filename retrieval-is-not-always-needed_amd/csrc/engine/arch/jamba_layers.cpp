@@ -284,7 +284,11 @@ struct RMLAImpl {
     }
 
     // prompt rows: cq [T][dc] | qr [T][H*dhr] | kr [T][Hkv*dhr] | q [T][H*dh] | k, v [T][Hkv*dh] | att [T][H*dh]
-    int rows_per_token() const { return dc + H * dhr + Hkv * dhr + 2 * H * dh + 2 * Hkv * dh; }
+    // | the fp32-cache prompt attention's rows (rina_hip_dq_prompt_workspace per row)
+    int attn_rows_per_token() const { return 2 * (H + Hkv) * (dh + dhr); }
+    int rows_per_token() const {
+        return dc + H * dhr + Hkv * dhr + 2 * H * dh + 2 * Hkv * dh + attn_rows_per_token();
+    }
 
     int forward_rows(float* h, ForwardBuffers& b, int T, hipStream_t s) {
         const int start_pos = b.kv_cache.start_pos;
@@ -303,8 +307,22 @@ struct RMLAImpl {
         CK(rina_hip_linear_fused(s2, 2, qt, cq, T, dc, RINA_EPI_STORE, RINA_PRO_LAYERNORM, q_norm, 1e-5f, s));
         rina_linear_seg s3{w_k2v, nullptr, v, Hkv * dh};
         CK(rina_hip_linear_fused(&s3, 1, qt, k, T, Hkv * dh, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
-        // causal attention (:78-86): row t appends its K / V at start_pos + t and attends to positions <= it
-        for (int t = 0; t < T; t++)
+        // causal attention (:78-86): row t appends its K / V at start_pos + t and
+        // attends to positions <= it.  fp32 caches from position 0: one call
+        // over all rows; the q2k_q1v cache reads the rows before t through
+        // their packs, so it goes row by row
+        bool batched = false;
+        if (kv_mode == RINA_KV_FP32 && start_pos == 0) {
+            float* aws = att + (size_t)T * H * dh;
+            const size_t need = rina_hip_dq_prompt_workspace(T, H, Hkv, dh, dhr, dh);
+            if (need && need <= sizeof(float) * (size_t)T * attn_rows_per_token() && (uintptr_t)aws % 16 == 0) {
+                rc = rina_hip_dq_prompt_attention(q, qr, k, kr, v, rqc, rqs, rkc, rks, (float*)ck, (float*)cv, H, Hkv,
+                                                  dh, dhr, dh, T, max_seq, att, aws, need, s);
+                if (rc != RINA_OK && rc != RINA_ERR_SHAPE) return rc;   // a shape it does not take launches nothing
+                batched = rc == RINA_OK;
+            }
+        }
+        for (int t = 0; t < T && !batched; t++)
             CK(rina_hip_dq_decode_attention_kv(q + (size_t)t * H * dh, qr + (size_t)t * H * dhr, k + (size_t)t * Hkv * dh,
                                                kr + (size_t)t * Hkv * dhr, v + (size_t)t * Hkv * dh, rqc, rqs, rkc, rks,
                                                kv_mode, ck, cv, ckr, H, Hkv, dh, dhr, dh, start_pos + t, nullptr,

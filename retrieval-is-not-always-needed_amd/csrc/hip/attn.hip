@@ -639,6 +639,34 @@ __device__ __forceinline__ float dq_dim(const float* xa, const float* xb, const 
     return i < da ? va : vb;
 }
 
+// A prompt's rows for the RINA-MLA attention over fp32 caches: grid
+// (T, H + Hkv), one workgroup per (row, head).  Query heads: [qa | HF-RoPE(qb)]
+// of row t at position t into q_full [T][H][da+db]; KV heads: the key row
+// [ka | HF-RoPE(kb)] into k_full [T][Hkv][da+db] and the cache, the value
+// row into the cache and, zero-padded to da + db, into v_full.  The rows
+// are the ones the decode kernel appends (dq_dim).
+__global__ __launch_bounds__(256) void dq_rows_kernel(DqArgs a, float* q_full, float* k_full, float* v_full) {
+    const int i = threadIdx.x, t = blockIdx.x, y = blockIdx.y;
+    const int dq = a.da + a.db;
+    if (i >= dq) return;
+    if (y < a.H) {
+        const float* qa = a.qa + ((int64_t)t * a.H + y) * a.da;
+        const float* qb = a.qb + ((int64_t)t * a.H + y) * a.db;
+        gst(q_full + ((int64_t)t * a.H + y) * dq + i, dq_dim(qa, qb, a.qc, a.qs, a.da, a.db, t, i));
+        return;
+    }
+    const int kvh = y - a.H;
+    const float* ka = a.ka + ((int64_t)t * a.Hkv + kvh) * a.da;
+    const float* kb = a.kb + ((int64_t)t * a.Hkv + kvh) * a.db;
+    const float kv = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, t, i);
+    const int64_t o = ((int64_t)t * a.Hkv + kvh) * dq + i;
+    gst(k_full + o, kv);
+    gst(a.ck + o, kv);
+    const float vv = i < a.dv ? gld(a.v + ((int64_t)t * a.Hkv + kvh) * a.dv + i) : 0.f;
+    gst(v_full + o, vv);
+    if (i < a.dv) gst(a.cv + ((int64_t)t * a.Hkv + kvh) * a.dv + i, vv);
+}
+
 // QKV: 0 = fp32 caches; 1 = the q2k_q1v cache (key content q2_1, key RoPE
 // part fp32, values q1_0; da == 64, dv == 64)
 template <int QKV>
@@ -1335,6 +1363,48 @@ extern "C" int rina_hip_dq_decode_attention(const float* qa, const float* qb, co
     return dq_attention(qa, qb, ka, kb, v, rope_q_cos, rope_q_sin, rope_k_cos, rope_k_sin, RINA_KV_FP32, cache_k,
                         cache_v, nullptr, nullptr, nullptr, H, Hkv, da, db, dv, start_pos, d_pos, max_seq, out,
                         workspace, ws_bytes, as_stream(stream));
+}
+
+extern "C" size_t rina_hip_dq_prompt_workspace(int T, int H, int Hkv, int da, int db, int dv) {
+    if (T < 1 || H < 1 || Hkv < 1 || da < 1 || db < 0 || dv < 1) return 0;
+    const size_t dq = (size_t)da + db, t = (size_t)T;
+    return sizeof(float) * (2 * t * H * dq + 2 * t * Hkv * dq);
+}
+
+extern "C" int rina_hip_dq_prompt_attention(const float* qa, const float* qb, const float* ka, const float* kb,
+                                            const float* v, const float* rope_q_cos, const float* rope_q_sin,
+                                            const float* rope_k_cos, const float* rope_k_sin, float* cache_k,
+                                            float* cache_v, int H, int Hkv, int da, int db, int dv, int T,
+                                            int max_seq, float* out, void* workspace, size_t ws_bytes,
+                                            void* stream) {
+    if (!qa || !ka || !v || !cache_k || !cache_v || !out || H < 1 || Hkv < 1 || da < 1 || db < 0 || dv < 1 ||
+        T < 1 || max_seq < 1 || (db > 0 && (!qb || !kb)) || db % 2)
+        return RINA_ERR_ARG;
+    if (H % Hkv || da + db > 256 || dv > da + db) return RINA_ERR_SHAPE;
+    if (T > max_seq) return RINA_ERR_RANGE;
+    const size_t need = rina_hip_dq_prompt_workspace(T, H, Hkv, da, db, dv);
+    if (!workspace || ws_bytes < need || (uintptr_t)workspace % 16) return RINA_ERR_WORKSPACE;
+    const int dq = da + db;
+    float* q_full = (float*)workspace;
+    float* o_full = q_full + (size_t)T * H * dq;
+    float* k_full = o_full + (size_t)T * H * dq;
+    float* v_full = k_full + (size_t)T * Hkv * dq;
+    DqArgs a{};
+    a.qa = qa; a.qb = qb; a.ka = ka; a.kb = kb; a.v = v;
+    a.qc = rope_q_cos; a.qs = rope_q_sin; a.kc = rope_k_cos; a.ks = rope_k_sin;
+    a.ck = cache_k; a.cv = cache_v;
+    a.H = H; a.Hkv = Hkv; a.da = da; a.db = db; a.dv = dv; a.start_pos = 0; a.max_seq = max_seq;
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(dq_rows_kernel, dim3(T, H + Hkv), dim3(256), 0, st, a, q_full, k_full, v_full);
+    RINA_LAUNCH_CHECK();
+    // causal attention over the rows, scale 1/sqrt(da + db)
+    int rc = rina_hip_gqa_attention(q_full, k_full, v_full, k_full, v_full, RINA_KV_FP32, 0, nullptr, nullptr, T, H,
+                                    Hkv, dq, 0, nullptr, max_seq, o_full, nullptr, 0, stream);
+    if (rc) return rc;
+    if (hipMemcpy2DAsync(out, sizeof(float) * dv, o_full, sizeof(float) * dq, sizeof(float) * dv, (size_t)T * H,
+                         hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return RINA_ERR_HIP;
+    return RINA_OK;
 }
 
 extern "C" size_t rina_hip_dq_kv_region_bytes(int kv_mode, int part, int max_seq, int Hkv, int da, int db, int dv) {

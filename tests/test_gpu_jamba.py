@@ -69,6 +69,53 @@ def test_dq_decode_attention(rina, P, use_dpos, H, Hkv, da, db):
     assert np.array_equal(gk[keep], ck[keep])
 
 
+@pytest.mark.parametrize("T", [2, 19, 300])
+@pytest.mark.parametrize("H,Hkv,da,db", [(10, 5, 64, 32), (4, 2, 64, 16)])
+def test_dq_prompt_attention_matches_decode_rows(rina, T, H, Hkv, da, db):
+    """A prompt of T rows from position 0 in one call (every row's key and
+    value appended, then one causal attention over the rows) against the
+    same rows fed to the fp32-cache decode attention one position at a
+    time: both caches bit for bit, every output row within tolerance."""
+    hip = rina.load_hip()
+    dq, dv = da + db, 64
+    max_seq = T + 4
+    r = rng(T + H + db)
+    qa = r.standard_normal((T, H * da)).astype(np.float32)
+    qb = r.standard_normal((T, H * db)).astype(np.float32)
+    ka = r.standard_normal((T, Hkv * da)).astype(np.float32)
+    kb = r.standard_normal((T, Hkv * db)).astype(np.float32)
+    v = r.standard_normal((T, Hkv * dv)).astype(np.float32)
+    ang = np.outer(np.arange(max_seq), 1.0 / 10000 ** (np.arange(0, db, 2) / db)).astype(np.float32)
+    cd, sd = dev(np.cos(ang).astype(np.float32)), dev(np.sin(ang).astype(np.float32))
+    qad, qbd, kad, kbd, vd = dev(qa), dev(qb), dev(ka), dev(kb), dev(v)
+    ck1, cv1 = dev(np.zeros((max_seq, Hkv, dq), np.float32)), dev(np.zeros((max_seq, Hkv, dv), np.float32))
+    wsb = hip.rina_hip_dq_attention_workspace(H, dq, max_seq)
+    ws = empty(wsb, "uint8")
+    od = empty(H * dv)
+    one = np.zeros((T, H * dv), np.float32)
+    for t in range(T):
+        ok(hip.rina_hip_dq_decode_attention(qad.data_ptr() + 4 * t * H * da, qbd.data_ptr() + 4 * t * H * db,
+                                            kad.data_ptr() + 4 * t * Hkv * da, kbd.data_ptr() + 4 * t * Hkv * db,
+                                            vd.data_ptr() + 4 * t * Hkv * dv, cd.data_ptr(), sd.data_ptr(),
+                                            cd.data_ptr(), sd.data_ptr(), ck1.data_ptr(), cv1.data_ptr(), H, Hkv, da,
+                                            db, dv, t, None, max_seq, od.data_ptr(), ws.data_ptr(), wsb, stream()),
+           "decode row %d" % t)
+        one[t] = host(od)
+    ck2, cv2 = dev(np.zeros((max_seq, Hkv, dq), np.float32)), dev(np.zeros((max_seq, Hkv, dv), np.float32))
+    pwb = hip.rina_hip_dq_prompt_workspace(T, H, Hkv, da, db, dv)
+    pw = empty(pwb, "uint8")
+    o2 = empty(T * H * dv)
+    ok(hip.rina_hip_dq_prompt_attention(qad.data_ptr(), qbd.data_ptr(), kad.data_ptr(), kbd.data_ptr(), vd.data_ptr(),
+                                        cd.data_ptr(), sd.data_ptr(), cd.data_ptr(), sd.data_ptr(), ck2.data_ptr(),
+                                        cv2.data_ptr(), H, Hkv, da, db, dv, T, max_seq, o2.data_ptr(), pw.data_ptr(),
+                                        pwb, stream()), "prompt attention")
+    assert np.array_equal(host(ck2).view(np.uint32), host(ck1).view(np.uint32))
+    assert np.array_equal(host(cv2).view(np.uint32), host(cv1).view(np.uint32))
+    got = host(o2).reshape(T, H * dv)
+    for t in range(T):
+        assert_close_elem(got[t], one[t], what="prompt row %d vs decode row" % t)
+
+
 def header(max_seq, cfg=jt.CFG, types=jt.TYPES):
     c = cfg
     return {"name": c["name"], "dim": c["dim"], "n_layers": c["n_layers"], "n_heads": c["n_heads"],
