@@ -180,7 +180,6 @@ def traffic_probe_stack(iters):
 
 
 STACK_KERNELS = ("gemv_direct_kernel", "attn_vsplit_kernel", "attn_split_kernel", "attn_combine_kernel")
-VSPLIT_MAX_POS = 1024   # fp32-cache decode attention runs as one launch up to this many positions
 
 
 def _pmc_sum(db, counter, kernels, ncopy):
@@ -292,7 +291,8 @@ def committed_traffic(path=TRAFFIC_FILE):
 
 STACK_KINDS = ("qkv", "attn", "wo", "w13", "w2")
 STACK_NOTES = {"qkv": "fused q/k/v Q4_0F matvec with the ln1 RMSNorm prologue (N 3072, K 2048)",
-               "attn": "RoPE + fp32 KV append + decode attention (one launch up to 1024 positions, else split + merge)",
+               "attn": "RoPE + fp32 KV append + decode attention (one launch up to rina_hip_gqa_one_launch_positions(), "
+                       "else split + merge)",
                "wo": "W_o Q4_0F matvec + residual (N 2048, K 2048)",
                "w13": "W1/W3 Q4_0F matvec pair with the ln2 RMSNorm prologue and SiLU*up (N 8192, K 2048)",
                "w2": "W2 Q4_0F matvec + residual (N 2048, K 8192)"}
@@ -396,7 +396,7 @@ def layer_stack_roofline(torch, hip, rina, sm, cfg, pos, st, iters):
     tb = ls.bytes_per_token()
     traffic, detail = committed_traffic(STACK_TRAFFIC_FILE)
     roof = roofline(tb, t_tok, traffic)
-    one = pos + 1 <= VSPLIT_MAX_POS
+    one = pos + 1 <= hip.rina_hip_gqa_one_launch_positions()
     roof.update({"kernel": "config-2 decode layer stack: 16 x [q/k/v + ln1, RoPE + KV append + attention "
                            "(%s), W_o + residual, W1/W3 + ln2 + SiLU*up, W2 + residual], Q4_0F, fp32 "
                            "KV at position %d" % ("one launch" if one else "split + merge", pos),
@@ -690,7 +690,8 @@ def main():
         attn_roofs[name] = dict(with_ceiling(roofline(at_bytes, t_at), t_at,
                                              plain_read_time(torch, hip, st, at_bytes, args.kernel_iters)),
                                 bytes_per_launch=at_bytes, avg_us=round(t_at * 1e6, 3),
-                                note="RoPE + append + attention: one launch" if mode == 0 and pos + 1 <= VSPLIT_MAX_POS
+                                note="RoPE + append + attention: one launch"
+                                if mode == 0 and pos + 1 <= hip.rina_hip_gqa_one_launch_positions()
                                 else "RoPE + append + split-sequence attention + chunk merge, two launches")
         log("%s: %.2f us, %.0f GB/s" % (name, t_at * 1e6, at_bytes / t_at / 1e9))
         del kc, vc

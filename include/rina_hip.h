@@ -180,6 +180,10 @@ int rina_hip_rope_append(float* q, float* k, const float* v,
  * (gqa_layer.cu:236-238).  `workspace` holds split-sequence partials;
  * rina_hip_gqa_attention_workspace() gives its size. */
 size_t rina_hip_gqa_attention_workspace(int T, int H, int dh, int max_pos);
+/* The position count up to which rina_hip_gqa_decode_attention over an fp32
+ * cache with dh == 64 is one launch (1024; beyond it, or with a packed
+ * cache, split + combine). */
+int rina_hip_gqa_one_launch_positions(void);
 int rina_hip_gqa_attention(const float* q, const float* kcur, const float* vcur,
                            const void* cache_k, const void* cache_v, int mode,
                            int pre_rope, const float* rope_k_cos,

@@ -56,6 +56,7 @@ _HIP_SIGS = {
     "rina_hip_mla_decode_attention": (I32, [VP, VP, VP, F32, VP, VP, VP, I32, VP, I32, I32, I32, I32, I32, I32, VP,
                                             I32, VP, VP, SZ, VP]),
     "rina_hip_mla_fused_positions": (I32, []),
+    "rina_hip_gqa_one_launch_positions": (I32, []),
     "rina_hip_mla_decode_attention_ex": (I32, [VP, VP, VP, F32, VP, VP, VP, I32, VP, I32, I32, I32, I32, I32, I32,
                                                VP, I32, I32, VP, VP, SZ, VP]),
     "rina_hip_mla_prompt_workspace": (SZ, [I32, I32, I32, I32, I32, I32]),

@@ -1166,6 +1166,8 @@ bool rep_ok(int rep) { return rep == 1 || rep == 2 || rep == 4 || rep == 8; }
 
 }  // namespace
 
+extern "C" int rina_hip_gqa_one_launch_positions(void) { return kVsMaxPos; }
+
 extern "C" size_t rina_hip_gqa_attention_workspace(int T, int H, int dh, int max_pos) {
     (void)T;
     (void)dh;
