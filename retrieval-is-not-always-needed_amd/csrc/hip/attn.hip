@@ -112,6 +112,74 @@ __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o
     }
 }
 
+// The raw words of load8's 8 values, loaded now and converted later by
+// cvt_raw8 with load8's operations (the same values, bit for bit): loads
+// can then be issued well before their values are needed without the
+// conversion making the wave wait for them at issue.
+struct Raw8 {
+    float f[8];      // fp32 records
+    uint32_t h[4];   // packed records: the 16-bit words load8 reads
+    uint32_t s;      // packed records: the fp16 scale
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_raw8(const uint8_t* base, int64_t v0, Raw8& r) {
+    if (FMT == 0) {
+        const f32x4* p = (const f32x4*)((const float*)base + v0);
+        const f32x4 a = gld(p), b = gld(p + 1);
+        r.f[0] = a.x; r.f[1] = a.y; r.f[2] = a.z; r.f[3] = a.w;
+        r.f[4] = b.x; r.f[5] = b.y; r.f[6] = b.z; r.f[7] = b.w;
+        return;
+    }
+    constexpr int BB = kvq::block_bytes_c(FMT);
+    const uint8_t* blk = base + (v0 >> 5) * BB;
+    const int w = (int)(v0 & 31);
+    r.s = gld((const uint16_t*)blk);
+    if (FMT == RINA_KVF_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.h[i] = gld((const uint16_t*)(blk + 2 + w + 2 * i));
+    } else if (FMT == RINA_KVF_Q4_0) {
+        r.h[0] = gld((const uint16_t*)(blk + 2 + w / 2));
+        r.h[1] = gld((const uint16_t*)(blk + 4 + w / 2));
+    } else if (FMT == RINA_KVF_Q2_1) {
+        r.h[0] = gld((const uint16_t*)(blk + 2 + w / 4));
+    } else {
+        r.h[0] = gld((const uint16_t*)(blk + 2));
+        r.h[1] = gld((const uint16_t*)(blk + 4));
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void cvt_raw8(const Raw8& r, int64_t v0, float (&o)[8]) {
+    if (FMT == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = r.f[i];
+        return;
+    }
+    const int w = (int)(v0 & 31);
+    const float s = f16_to_f32(r.s);
+    if (FMT == RINA_KVF_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const uint32_t two = r.h[i / 2];
+            o[i] = (float)(int8_t)(two & 0xFF) * s;
+            o[i + 1] = (float)(int8_t)(two >> 8) * s;
+        }
+    } else if (FMT == RINA_KVF_Q4_0) {
+        const uint32_t n = r.h[0] | (r.h[1] << 16);
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (4 * i)) & 0xF) - 7) * s;
+    } else if (FMT == RINA_KVF_Q2_1) {
+        const uint32_t n = r.h[0];
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (2 * i)) & 3) - 1) * s;
+    } else {
+        const uint32_t bits = (r.h[0] | (r.h[1] << 16)) >> w;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = ((bits >> i) & 1u) ? s : -s;
+    }
+}
+
 __device__ __forceinline__ void ld8f(const float* p, float (&o)[8]) {
     const f32x4* v = (const f32x4*)p;
     f32x4 a = gld(v), b = gld(v + 1);
@@ -134,6 +202,8 @@ __device__ __forceinline__ void rope8(int dim0, const float (&own)[8], const flo
         for (int i = 0; i < 8; i++) o[i] = fmaf(pair[i], s[i], own[i] * c[i]);
     }
 }
+
+constexpr int kSplitEntrySteps = 5;   // steps a split workgroup loads at entry (80 positions)
 
 template <int KF, int VF, int HG, int REP, bool FUSED, int QS>
 __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
@@ -275,6 +345,31 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
             }
         }
     };
+    // chunks of up to kSplitEntrySteps steps: every step's raw words are
+    // issued now, so the chunk costs one memory round trip (measured at q8
+    // position 4095, 5 steps: 11.8 -> 10.7 us per call over caches rotated
+    // past the MALL, the loop 5.0 -> 3.4 us); longer chunks keep one step in
+    // flight ahead of the one consumed
+    if (nsteps <= kSplitEntrySteps) {
+        Raw8 kr[kSplitEntrySteps - 1], vr[kSplitEntrySteps - 1];
+#pragma unroll
+        for (int st = 1; st < kSplitEntrySteps; st++) {
+            if (st >= nsteps) break;                // uniform
+            const int jl = st * GS + wslot;
+            const int j = j0 + (jl < ncv ? jl : 0);
+            load_raw8<KF>(a.ck + (int64_t)j * KREC, voff, kr[st - 1]);
+            load_raw8<VF>(a.cv + (int64_t)j * VREC, voff, vr[st - 1]);
+        }
+        consume(0, kA, vA);
+#pragma unroll
+        for (int st = 1; st < kSplitEntrySteps; st++) {
+            if (st >= nsteps) break;
+            float kk[8], vv[8];
+            cvt_raw8<KF>(kr[st - 1], voff, kk);
+            cvt_raw8<VF>(vr[st - 1], voff, vv);
+            consume(st, kk, vv);
+        }
+    } else
     for (int st = 0;;) {
         if (st + 1 < nsteps) {
             issue(st + 1, kB, vB);
