@@ -113,9 +113,8 @@ __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o
 }
 
 // The raw words of load8's 8 values, loaded now and converted later by
-// cvt_raw8 with load8's operations (the same values, bit for bit): loads
-// can then be issued well before their values are needed without the
-// conversion making the wave wait for them at issue.
+// codes_raw8: loads can then be issued well before their values are needed
+// without the conversion making the wave wait for them at issue.
 struct Raw8 {
     float f[8];      // fp32 records
     uint32_t h[4];   // packed records: the 16-bit words load8 reads
@@ -149,35 +148,38 @@ __device__ __forceinline__ void load_raw8(const uint8_t* base, int64_t v0, Raw8&
     }
 }
 
+// The 8 values of a Raw8 as load8 would give them, without the block scale:
+// the integer codes as floats (exact), the scale returned apart (1 for fp32
+// records), so a consumer applies it once per lane instead of once per value
 template <int FMT>
-__device__ __forceinline__ void cvt_raw8(const Raw8& r, int64_t v0, float (&o)[8]) {
+__device__ __forceinline__ float codes_raw8(const Raw8& r, int64_t v0, float (&o)[8]) {
     if (FMT == 0) {
 #pragma unroll
         for (int i = 0; i < 8; i++) o[i] = r.f[i];
-        return;
+        return 1.0f;
     }
     const int w = (int)(v0 & 31);
-    const float s = f16_to_f32(r.s);
     if (FMT == RINA_KVF_Q8_0) {
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
             const uint32_t two = r.h[i / 2];
-            o[i] = (float)(int8_t)(two & 0xFF) * s;
-            o[i + 1] = (float)(int8_t)(two >> 8) * s;
+            o[i] = (float)(int8_t)(two & 0xFF);
+            o[i + 1] = (float)(int8_t)(two >> 8);
         }
     } else if (FMT == RINA_KVF_Q4_0) {
         const uint32_t n = r.h[0] | (r.h[1] << 16);
 #pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (4 * i)) & 0xF) - 7) * s;
+        for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (4 * i)) & 0xF) - 7);
     } else if (FMT == RINA_KVF_Q2_1) {
         const uint32_t n = r.h[0];
 #pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (2 * i)) & 3) - 1) * s;
+        for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (2 * i)) & 3) - 1);
     } else {
         const uint32_t bits = (r.h[0] | (r.h[1] << 16)) >> w;
 #pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = ((bits >> i) & 1u) ? s : -s;
+        for (int i = 0; i < 8; i++) o[i] = ((bits >> i) & 1u) ? 1.0f : -1.0f;
     }
+    return f16_to_f32(r.s);
 }
 
 __device__ __forceinline__ void ld8f(const float* p, float (&o)[8]) {
@@ -321,12 +323,19 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
     auto consume = [&](int st, const float (&kk)[8], const float (&vv)[8]) {
         const int jl = st * GS + wslot;
         const bool valid = jl < ncv;
-        const bool cur = has_cur && (j0 + jl == pos0);
         float kx[8], vx[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            kx[i] = cur ? kcur[i] : kk[i];
-            vx[i] = cur ? vcur[i] : vv[i];
+            kx[i] = kk[i];
+            vx[i] = vv[i];
+        }
+        if (has_cur) {                              // uniform: the workgroup holding pos0
+            const bool cur = j0 + jl == pos0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                kx[i] = cur ? kcur[i] : kx[i];
+                vx[i] = cur ? vcur[i] : vx[i];
+            }
         }
 #pragma unroll
         for (int r = 0; r < RL; r++) {
@@ -346,28 +355,94 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
         }
     };
     // chunks of up to kSplitEntrySteps steps: every step's raw words are
-    // issued now, so the chunk costs one memory round trip (measured at q8
-    // position 4095, 5 steps: 11.8 -> 10.7 us per call over caches rotated
-    // past the MALL, the loop 5.0 -> 3.4 us); longer chunks keep one step in
-    // flight ahead of the one consumed
+    // issued now, so the chunk costs one memory round trip, and the softmax
+    // runs scores first: every step's score (block scales applied once per
+    // lane), one maximum per slot, then one exp2 and 8 FMAs per position, no
+    // rescaling chain.  Measured at q8 position 4095 (5 steps), split +
+    // combine over caches rotated past the MALL: 11.9 us per call with one
+    // step in flight, 10.8 with the loads at entry, 10.1 scores first.
+    // Longer chunks keep one step in flight ahead of the one consumed, with
+    // the running softmax.
     if (nsteps <= kSplitEntrySteps) {
-        Raw8 kr[kSplitEntrySteps - 1], vr[kSplitEntrySteps - 1];
+        constexpr int NE = kSplitEntrySteps;
+        Raw8 kr[NE - 1], vr[NE - 1];
 #pragma unroll
-        for (int st = 1; st < kSplitEntrySteps; st++) {
+        for (int st = 1; st < NE; st++) {
             if (st >= nsteps) break;                // uniform
             const int jl = st * GS + wslot;
             const int j = j0 + (jl < ncv ? jl : 0);
             load_raw8<KF>(a.ck + (int64_t)j * KREC, voff, kr[st - 1]);
             load_raw8<VF>(a.cv + (int64_t)j * VREC, voff, vr[st - 1]);
         }
-        consume(0, kA, vA);
+        // the current position's record replaces the cache's (uniform branch)
+        auto is_cur = [&](int st) { return has_cur && j0 + st * GS + wslot == pos0; };
+        float sc[NE][RL];
 #pragma unroll
-        for (int st = 1; st < kSplitEntrySteps; st++) {
+        for (int st = 0; st < NE; st++) {
+#pragma unroll
+            for (int r = 0; r < RL; r++) sc[st][r] = -INFINITY;
+            if (st >= nsteps) continue;
+            float kk[8];
+            float ks = 1.0f;
+            if (st == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) kk[i] = kA[i];
+            } else {
+                ks = codes_raw8<KF>(kr[st - 1], voff, kk);
+            }
+            if (has_cur) {
+                const bool cur = is_cur(st);
+#pragma unroll
+                for (int i = 0; i < 8; i++) kk[i] = cur ? kcur[i] : kk[i];
+                ks = cur ? 1.0f : ks;
+            }
+            const bool valid = st * GS + wslot < ncv;
+#pragma unroll
+            for (int r = 0; r < RL; r++) {
+                float p = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) p = fmaf(qv[r][i], kk[i], p);
+                const float t = sum8(p * ks);
+                sc[st][r] = valid ? t : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RL; r++) {
+            float mx = sc[0][r];
+#pragma unroll
+            for (int st = 1; st < NE; st++) mx = fmaxf(mx, sc[st][r]);
+            m_run[r] = mx;
+        }
+#pragma unroll
+        for (int st = 0; st < NE; st++) {
             if (st >= nsteps) break;
-            float kk[8], vv[8];
-            cvt_raw8<KF>(kr[st - 1], voff, kk);
-            cvt_raw8<VF>(vr[st - 1], voff, vv);
-            consume(st, kk, vv);
+            float vv[8];
+            float vs = 1.0f;
+            if (st == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) vv[i] = vA[i];
+            } else {
+                vs = codes_raw8<VF>(vr[st - 1], voff, vv);
+            }
+            if (has_cur) {
+                const bool cur = is_cur(st);
+#pragma unroll
+                for (int i = 0; i < 8; i++) vv[i] = cur ? vcur[i] : vv[i];
+                vs = cur ? 1.0f : vs;
+            }
+#pragma unroll
+            for (int r = 0; r < RL; r++) {
+                // masked positions (their records are not this step's and
+                // may hold anything) add nothing; a slot with none valid
+                // keeps m = -inf, l = 0, O = 0
+                if (sc[st][r] != -INFINITY) {
+                    const float pe = __builtin_amdgcn_exp2f(sc[st][r] - m_run[r]);
+                    l_run[r] += pe;
+                    const float pv = pe * vs;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) ov[r][i] = fmaf(pv, vv[i], ov[r][i]);
+                }
+            }
         }
     } else
     for (int st = 0;;) {
