@@ -83,13 +83,13 @@ def plain_read_time(torch, hip, st, nbytes, iters):
     rina_hip_read_probe kernel over a ring of buffers larger than the
     256 MB MALL, best of four grid sizes.  A kernel's ceiling_frac is this
     time over its own at the same byte count."""
-    n = min(64, max(2, -(-640_000_000 // nbytes)))
+    n = min(64, max(2, -(-640_000_000 // nbytes)))   # every entry read once per graph replay
     ring = [torch.empty(nbytes // 4 + 4, device="cuda") for _ in range(n)]
     sink = torch.empty(8192, device="cuda")
     best = None
     for grid in (256, 512, 1024, 2048):
         t = time_kernel(torch, lambda i=0: hip.rina_hip_read_probe(ring[i % n].data_ptr(), nbytes, grid,
-                                                                   sink.data_ptr(), st), iters)
+                                                                   sink.data_ptr(), st), max(iters, n))
         best = t if best is None else min(best, t)
     del ring
     return best
@@ -439,7 +439,7 @@ def config4_kernel_roofs(torch, hip, rina, synth, st, pos, iters):
     t = time_kernel(torch, lambda i=0: hip.rina_hip_mla_decode_attention_ex(
         q.data_ptr(), kva.data_ptr(), kn.data_ptr(), 1e-5, cd.data_ptr(), sd.data_ptr(), wkvb[i % nr].data_ptr(),
         rina.QT_Q2_K, caches[i % nr].data_ptr(), H, nope, rope, vd, dc, 0, pd.data_ptr(), ms, ms - 1,
-        o.data_ptr(), ws.data_ptr(), wsb, st), iters)
+        o.data_ptr(), ws.data_ptr(), wsb, st), max(iters, nr))   # every ring entry once per replay
     nb = (pos + 1) * R * 4 + q2b(H * (nope + vd) * dc) + (H * (nope + rope) + R + H * vd) * 4
     out["decode_mla_latent_p%d" % pos] = dict(
         with_ceiling(roofline(nb, t), t, plain_read_time(torch, hip, st, nb, iters)), bytes_per_launch=nb,
@@ -685,7 +685,7 @@ def main():
         t_at = time_kernel(torch, lambda i=0: hip.rina_hip_gqa_decode_attention(
             qa.data_ptr(), ka.data_ptr(), va.data_ptr(), cd.data_ptr(), sd.data_ptr(), cd.data_ptr(), sd.data_ptr(),
             kc[i % nring].data_ptr(), vc[i % nring].data_ptr(), mode, H, Hkv, dh, pos, None, msq, oa.data_ptr(), None,
-            wsa.data_ptr(), wsb, st), args.kernel_iters)
+            wsa.data_ptr(), wsb, st), max(args.kernel_iters, nring))   # every ring entry once per replay
         at_bytes = int(pos * kvd * (kb + vb)) + (2 * H * dh + 2 * kvd) * 4
         attn_roofs[name] = dict(with_ceiling(roofline(at_bytes, t_at), t_at,
                                              plain_read_time(torch, hip, st, at_bytes, args.kernel_iters)),

@@ -74,6 +74,39 @@ struct SplitArgs {
     float scale;
 };
 
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+
+// q8_0 slices in one load.  A lane's 8 values of a 34-byte block (scale,
+// 32 codes) start at w = v0 % 32 in {0, 8, 16, 24}; with 2-byte aligned
+// records the 12 bytes from the dword at or below block + w hold its codes
+// at byte 2 + sh, sh = (block + w) % 4 in {0, 2}, and for w == 0 the block
+// scale at byte sh.  The other lanes of the block (w 8, 16, 24: the next
+// three lanes of the quad, by the kernels' lane layout) take the scale from
+// the quad's first lane.  The window ends at most 2 bytes past the block
+// (sh 0, w 24), inside the next block of the record or the next record: the
+// callers read only records below the last one written (positions < pos0)
+// or, for masked lanes, the query row (at least 4 * 64 bytes per KV head,
+// more than the 68 of a q8 head-record).
+__device__ __forceinline__ int q8_shift(const uint8_t* base, int64_t v0) {
+    return (int)(((uintptr_t)(base + (v0 >> 5) * 34 + (v0 & 31))) & 3);
+}
+__device__ __forceinline__ u32x3 q8_window(const uint8_t* base, int64_t v0) {
+    const uintptr_t st = (uintptr_t)(base + (v0 >> 5) * 34 + (v0 & 31));
+    return gld((const u32x3*)(st & ~(uintptr_t)3));
+}
+// codes (as floats, exact) and the fp16 scale bits of a window
+__device__ __forceinline__ uint32_t q8_unpack(const u32x3& x, int sh, float (&o)[8]) {
+    const uint32_t lo = sh ? x.y : __builtin_amdgcn_alignbyte(x.y, x.x, 2);
+    const uint32_t hi = sh ? x.z : __builtin_amdgcn_alignbyte(x.z, x.y, 2);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        o[i] = (float)(int8_t)(lo >> (8 * i));
+        o[4 + i] = (float)(int8_t)(hi >> (8 * i));
+    }
+    const uint32_t own = (x.x >> (8 * sh)) & 0xFFFF;   // the scale in the w == 0 lane
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)own, 0x00, 0xf, 0xf, false);   // quad_perm [0,0,0,0]
+}
+
 // 8 consecutive values [v0, v0+8) of one position's record, v0 % 8 == 0.
 template <int FMT>
 __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o)[8]) {
@@ -84,19 +117,17 @@ __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o
         o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
         return;
     }
+    if (FMT == RINA_KVF_Q8_0) {
+        const float s = f16_to_f32(q8_unpack(q8_window(base, v0), q8_shift(base, v0), o));
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] *= s;
+        return;
+    }
     constexpr int BB = kvq::block_bytes_c(FMT);
     const uint8_t* blk = base + (v0 >> 5) * BB;
     const int w = (int)(v0 & 31);
     float s = f16_to_f32(gld((const uint16_t*)blk));
-    if (FMT == RINA_KVF_Q8_0) {
-        const uint8_t* d = blk + 2 + w;
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            uint32_t two = gld((const uint16_t*)(d + i));
-            o[i] = (float)(int8_t)(two & 0xFF) * s;
-            o[i + 1] = (float)(int8_t)(two >> 8) * s;
-        }
-    } else if (FMT == RINA_KVF_Q4_0) {
+    if (FMT == RINA_KVF_Q4_0) {
         uint32_t n = (uint32_t)gld((const uint16_t*)(blk + 2 + w / 2)) |
                      ((uint32_t)gld((const uint16_t*)(blk + 4 + w / 2)) << 16);
 #pragma unroll
@@ -117,8 +148,9 @@ __device__ __forceinline__ void load8(const uint8_t* base, int64_t v0, float (&o
 // without the conversion making the wave wait for them at issue.
 struct Raw8 {
     float f[8];      // fp32 records
-    uint32_t h[4];   // packed records: the 16-bit words load8 reads
-    uint32_t s;      // packed records: the fp16 scale
+    u32x3 x;         // q8_0 records: the 12-byte window (q8_window)
+    uint32_t h[4];   // other packed records: the 16-bit words load8 reads
+    uint32_t s;      // other packed records: the fp16 scale
 };
 
 template <int FMT>
@@ -130,14 +162,15 @@ __device__ __forceinline__ void load_raw8(const uint8_t* base, int64_t v0, Raw8&
         r.f[4] = b.x; r.f[5] = b.y; r.f[6] = b.z; r.f[7] = b.w;
         return;
     }
+    if (FMT == RINA_KVF_Q8_0) {
+        r.x = q8_window(base, v0);
+        return;
+    }
     constexpr int BB = kvq::block_bytes_c(FMT);
     const uint8_t* blk = base + (v0 >> 5) * BB;
     const int w = (int)(v0 & 31);
     r.s = gld((const uint16_t*)blk);
-    if (FMT == RINA_KVF_Q8_0) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) r.h[i] = gld((const uint16_t*)(blk + 2 + w + 2 * i));
-    } else if (FMT == RINA_KVF_Q4_0) {
+    if (FMT == RINA_KVF_Q4_0) {
         r.h[0] = gld((const uint16_t*)(blk + 2 + w / 2));
         r.h[1] = gld((const uint16_t*)(blk + 4 + w / 2));
     } else if (FMT == RINA_KVF_Q2_1) {
@@ -151,22 +184,17 @@ __device__ __forceinline__ void load_raw8(const uint8_t* base, int64_t v0, Raw8&
 // The 8 values of a Raw8 as load8 would give them, without the block scale:
 // the integer codes as floats (exact), the scale returned apart (1 for fp32
 // records), so a consumer applies it once per lane instead of once per value
+// (sh: q8_shift of the record's lane slice; q8_0 only)
 template <int FMT>
-__device__ __forceinline__ float codes_raw8(const Raw8& r, int64_t v0, float (&o)[8]) {
+__device__ __forceinline__ float codes_raw8(const Raw8& r, int64_t v0, int sh, float (&o)[8]) {
     if (FMT == 0) {
 #pragma unroll
         for (int i = 0; i < 8; i++) o[i] = r.f[i];
         return 1.0f;
     }
+    if (FMT == RINA_KVF_Q8_0) return f16_to_f32(q8_unpack(r.x, sh, o));
     const int w = (int)(v0 & 31);
-    if (FMT == RINA_KVF_Q8_0) {
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            const uint32_t two = r.h[i / 2];
-            o[i] = (float)(int8_t)(two & 0xFF);
-            o[i + 1] = (float)(int8_t)(two >> 8);
-        }
-    } else if (FMT == RINA_KVF_Q4_0) {
+    if (FMT == RINA_KVF_Q4_0) {
         const uint32_t n = r.h[0] | (r.h[1] << 16);
 #pragma unroll
         for (int i = 0; i < 8; i++) o[i] = (float)((int)((n >> (4 * i)) & 0xF) - 7);
@@ -246,12 +274,12 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
     const int64_t voff = (int64_t)kvh * DH + dim0;  // value offset inside a position record
     const int wslot = wave * PPW + slot;
 
-    // query rows (and the current K/V row) first: cache hits, consumed while
-    // the chunk's K/V loads are in flight.  The query-side loads sit under no
+    // query rows (and the current K/V row) first: cache hits, rotated before
+    // the chunk's K/V loads are issued.  The query-side loads sit under no
     // branch (without RoPE tables the query rows stand in for them, unused):
     // loads under a branch can leave register copies at the join that wait
-    // for them there, before the cache loads are issued.  The current row is
-    // read by the workgroup that holds it only (a uniform branch).
+    // for them there.  The current row is read by the workgroup that holds
+    // it only (a uniform branch).
     float qraw[RL][8], qpair[RL][8], tc[8], ts[8];
     float kown[8], kpair[8], kc8[8], ks8[8], vcur[8];
     const bool qrope = FUSED && a.qc, krope = FUSED && a.kc;
@@ -278,18 +306,32 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
         }
     }
 
-    // K/V of step st: every lane loads (positions past the chunk end read
-    // the chunk's first position and are masked), so the load counters stay
-    // exact across the pipelined steps
+    // K/V of step st: every lane loads, so the load counters stay exact
+    // across the pipelined steps.  Lanes of positions past the chunk, and of
+    // the current position (its rows come from kcur / vcur), read the query
+    // row instead: in bounds, ignored, and no read reaches a cache record at
+    // or past pos0 (the q8 windows may end 2 bytes into the next record).
     const int nsteps = (ncv + GS - 1) / GS;
-    auto issue = [&](int st, float (&kk)[8], float (&vv)[8]) {
+    auto kv_rec = [&](int st, const uint8_t*& kb, const uint8_t*& vb) {
         const int jl = st * GS + wslot;
-        const int j = j0 + (jl < ncv ? jl : 0);
-        load8<KF>(a.ck + (int64_t)j * KREC, voff, kk);
-        load8<VF>(a.cv + (int64_t)j * VREC, voff, vv);
+        const bool rd = jl < ncv && j0 + jl < pos0;
+        kb = rd ? a.ck + (int64_t)(j0 + jl) * KREC : (const uint8_t*)a.q;
+        vb = rd ? a.cv + (int64_t)(j0 + jl) * VREC : (const uint8_t*)a.q;
+    };
+    auto issue = [&](int st, float (&kk)[8], float (&vv)[8]) {
+        const uint8_t *kb, *vb;
+        kv_rec(st, kb, vb);
+        load8<KF>(kb, voff, kk);
+        load8<VF>(vb, voff, vv);
     };
     float kA[8], vA[8], kB[8], vB[8];
-    issue(0, kA, vA);
+    // fp32 records with 4 query heads per wave: 3 entry steps (5 spill)
+    constexpr int NE = (KF == 0 && VF == 0 && RL >= 4) ? 3 : kSplitEntrySteps;
+    Raw8 kr[NE - 1], vr[NE - 1];
+    // q8 windows: the lane's byte offset inside its dword (the same in every
+    // record, whose length is a multiple of 4 bytes)
+    const int ksh = KF == RINA_KVF_Q8_0 ? q8_shift(a.ck, voff) : 0;
+    const int vsh = VF == RINA_KVF_Q8_0 ? q8_shift(a.cv, voff) : 0;
 
     // scores in base-2 units: log2 e and the scale folded into q, so the
     // softmax weights are hardware exp2 values
@@ -354,26 +396,32 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
             }
         }
     };
-    // chunks of up to kSplitEntrySteps steps: every step's raw words are
-    // issued now, so the chunk costs one memory round trip, and the softmax
-    // runs scores first: every step's score (block scales applied once per
+    // The first NE steps' loads are issued together, after the
+    // query rotation (cache loads issued before it delay the query's round
+    // trip, and with it the whole chain), every key first, then every value:
+    // loads retire in issue order, so the scores wait for the keys alone.
+    // Steps past 0 stay raw words until consumed.  Chunks of up to NE
+    // steps then cost one memory round trip and run the
+    // softmax scores first: every step's score (block scales applied once per
     // lane), one maximum per slot, then one exp2 and 8 FMAs per position, no
-    // rescaling chain.  Measured at q8 position 4095 (5 steps), split +
-    // combine over caches rotated past the MALL: 11.9 us per call with one
-    // step in flight, 10.8 with the loads at entry, 10.1 scores first.
-    // Longer chunks keep one step in flight ahead of the one consumed, with
-    // the running softmax.
-    if (nsteps <= kSplitEntrySteps) {
-        constexpr int NE = kSplitEntrySteps;
-        Raw8 kr[NE - 1], vr[NE - 1];
+    // rescaling chain.  Longer chunks go on with one step in flight ahead of
+    // the one consumed and the running softmax.  Measured at q8 (H 32 / Hkv
+    // 8, 80-position chunks, split + combine per call, graph replay over 128
+    // caches of 4104 positions, 572 MB): at positions 1000 / 2047 / 4095,
+    // one step in flight 8.93 / 9.66 / 10.15 us, scores first 8.57 / 9.45 /
+    // 9.81, these loads (12-byte q8 windows) 8.55 / 9.22 / 9.46.
+    {
+        const uint8_t *kb[NE], *vb[NE];
 #pragma unroll
-        for (int st = 1; st < NE; st++) {
-            if (st >= nsteps) break;                // uniform
-            const int jl = st * GS + wslot;
-            const int j = j0 + (jl < ncv ? jl : 0);
-            load_raw8<KF>(a.ck + (int64_t)j * KREC, voff, kr[st - 1]);
-            load_raw8<VF>(a.cv + (int64_t)j * VREC, voff, vr[st - 1]);
-        }
+        for (int st = 0; st < NE; st++) kv_rec(st, kb[st], vb[st]);
+        load8<KF>(kb[0], voff, kA);
+#pragma unroll
+        for (int st = 1; st < NE; st++) load_raw8<KF>(kb[st], voff, kr[st - 1]);
+        load8<VF>(vb[0], voff, vA);
+#pragma unroll
+        for (int st = 1; st < NE; st++) load_raw8<VF>(vb[st], voff, vr[st - 1]);
+    }
+    if (nsteps <= NE) {
         // the current position's record replaces the cache's (uniform branch)
         auto is_cur = [&](int st) { return has_cur && j0 + st * GS + wslot == pos0; };
         float sc[NE][RL];
@@ -388,7 +436,7 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) kk[i] = kA[i];
             } else {
-                ks = codes_raw8<KF>(kr[st - 1], voff, kk);
+                ks = codes_raw8<KF>(kr[st - 1], voff, ksh, kk);
             }
             if (has_cur) {
                 const bool cur = is_cur(st);
@@ -422,7 +470,7 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) vv[i] = vA[i];
             } else {
-                vs = codes_raw8<VF>(vr[st - 1], voff, vv);
+                vs = codes_raw8<VF>(vr[st - 1], voff, vsh, vv);
             }
             if (has_cur) {
                 const bool cur = is_cur(st);
@@ -444,24 +492,41 @@ __global__ __launch_bounds__(256 * QS) void attn_split_kernel(SplitArgs a) {
                 }
             }
         }
-    } else
-    for (int st = 0;;) {
-        if (st + 1 < nsteps) {
-            issue(st + 1, kB, vB);
-            consume(st, kA, vA);
-        } else {
-            consume(st, kA, vA);
-            break;
+    } else {
+        // the entry steps with the running softmax, step NE's loads in
+        // flight meanwhile, then one step in flight ahead of the one consumed
+        issue(NE, kB, vB);
+        consume(0, kA, vA);
+#pragma unroll
+        for (int st = 1; st < NE; st++) {
+            float kk[8], vv[8];
+            const float ks = codes_raw8<KF>(kr[st - 1], voff, ksh, kk);
+            const float vs = codes_raw8<VF>(vr[st - 1], voff, vsh, vv);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                kk[i] *= ks;
+                vv[i] *= vs;
+            }
+            consume(st, kk, vv);
         }
-        st++;
-        if (st + 1 < nsteps) {
-            issue(st + 1, kA, vA);
-            consume(st, kB, vB);
-        } else {
-            consume(st, kB, vB);
-            break;
+        for (int st = NE;;) {
+            if (st + 1 < nsteps) {
+                issue(st + 1, kA, vA);
+                consume(st, kB, vB);
+            } else {
+                consume(st, kB, vB);
+                break;
+            }
+            st++;
+            if (st + 1 < nsteps) {
+                issue(st + 1, kB, vB);
+                consume(st, kA, vA);
+            } else {
+                consume(st, kA, vA);
+                break;
+            }
+            st++;
         }
-        st++;
     }
 
     // merge of the NS slots through LDS: every slot's (m, l, O) is written,

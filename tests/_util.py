@@ -45,6 +45,35 @@ def assert_close_elem(got, ref, tol=REL_TOL, what=""):
         what, idx.size, tol, ELEM_FLOOR, idx[0], g[idx[0]], r[idx[0]])
 
 
+def attention_f64(q, K, V, H, Hkv, dh):
+    """Softmax attention of one query row (scale 1/sqrt(dh)) in float64 over
+    K, V [n][Hkv * dh]: the outputs, and per output element the weighted
+    mean magnitude sum_p w_p |v_p,i| of the values it averages."""
+    q = np.asarray(q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    out, mag = np.zeros(H * dh), np.zeros(H * dh)
+    for h in range(H):
+        g = h // (H // Hkv)
+        s = K[:, g * dh:(g + 1) * dh] @ q[h * dh:(h + 1) * dh] / np.sqrt(dh)
+        w = np.exp(s - s.max())
+        w /= w.sum()
+        out[h * dh:(h + 1) * dh] = w @ V[:, g * dh:(g + 1) * dh]
+        mag[h * dh:(h + 1) * dh] = w @ np.abs(V[:, g * dh:(g + 1) * dh])
+    return out, mag
+
+
+# Per-element form for long-context attention against the float64 result:
+# an output averaging n values carries fp32 rounding of the size of the
+# values it averages (mag_i above), not of the output, which cancels to
+# about mag / sqrt(n).  |got - ref| <= tol |ref| + ELEM_FLOOR mag_i.
+def assert_close_attn(got, ref64, mag, tol=REL_TOL, what=""):
+    got = np.asarray(got, np.float64).reshape(-1)
+    bad = np.flatnonzero(~(np.abs(got - ref64) <= tol * np.abs(ref64) + ELEM_FLOOR * mag))
+    assert bad.size == 0, "%s: %d elements outside %.0e |ref| + %.0e mag (first at %d: %.9g against %.9g, mag %.3g)" % (
+        what, bad.size, tol, ELEM_FLOOR, bad[0], got[bad[0]], ref64[bad[0]], mag[bad[0]])
+
+
 def torch():
     import torch as t
     return t

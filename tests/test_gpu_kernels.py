@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 
 import _numpy_ref as nr
-from _util import REL_TOL, assert_close, assert_close_elem, dev, empty, host, ok, rng, stream
+from _util import (REL_TOL, assert_close, assert_close_attn, assert_close_elem, attention_f64, dev, empty, host, ok, rng,
+                   stream)
 
 pytestmark = pytest.mark.gpu
 
@@ -487,7 +488,8 @@ def test_decode_attention_fused_edge_blocks(rina, orc, mode, P, H, Hkv):
                                               (1500, 32, 8, False), (70, 10, 5, False), (16, 8, 8, True),
                                               (300, 32, 4, True), (1500, 32, 4, False),
                                               (1023, 32, 8, False), (1015, 32, 8, True), (1024, 32, 8, False),
-                                              (255, 32, 8, False), (256, 32, 8, False), (600, 32, 8, True)])
+                                              (255, 32, 8, False), (256, 32, 8, False), (600, 32, 8, True),
+                                              (4095, 32, 8, True), (6000, 32, 8, False), (8200, 32, 4, True)])
 def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
     """RoPE + K/V append + attention in one call == rope_append then attention
     (oracle): the rotated K row and the appended cache bytes bit-exact, the
@@ -495,7 +497,17 @@ def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
     up to 1024 positions take the one-launch kernel in steps of 256 positions
     (1023, and 1015 with a 1024-row cache and a device position, fill its
     last step; 255 / 256 end and start a step), 1024 the split + combine
-    pair."""
+    pair.  On split + combine, chunks of up to 5 steps of 16 positions run
+    scores first (4095: 5 steps), longer ones the running softmax after the
+    5 entry steps (6000: 6 steps per chunk, 8200: 9).
+
+    Past 2048 positions the per-element check is against float64 attention
+    over the same (dequantized) rows, with the floor set by the magnitude
+    of the values each output averages (assert_close_attn): the fp32
+    oracle itself misses 1e-6 max|out| by one element in most of these
+    cases (its error is at most 6.9e-7 of that magnitude, while the flat
+    softmax over 4k-8k random rows leaves max|out| near 0.08).  The oracle
+    still bounds the output normwise."""
     hip = rina.load_hip()
     L = orc.load()
     dh = 64
@@ -535,7 +547,17 @@ def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
                                          pos.data_ptr() if use_dpos else None, max_seq, od.data_ptr(),
                                          krot.data_ptr(), ws.data_ptr(), ws_bytes, stream()), "decode attention")
     assert np.array_equal(host(krot).view(np.uint32), kr.view(np.uint32))
-    assert_close_elem(host(od), ref, what="fused decode mode %d P %d" % (mode, P))
+    if P <= 2048:
+        assert_close_elem(host(od), ref, what="fused decode mode %d P %d" % (mode, P))
+    else:
+        assert_close(host(od), ref, what="fused decode mode %d P %d" % (mode, P))
+        if mode == 0:
+            Kh, Vh = kc[:P], vc[:P]
+        else:
+            Kh = orc.kv_dequant(kf, ckb, max_seq * kvd).reshape(max_seq, kvd)[:P]
+            Vh = orc.kv_dequant(vf, cvb, max_seq * kvd).reshape(max_seq, kvd)[:P]
+        o64, mag = attention_f64(qr, np.vstack([Kh, kr[None]]), np.vstack([Vh, v[None]]), H, Hkv, dh)
+        assert_close_attn(host(od), o64, mag, what="fused decode mode %d P %d vs float64" % (mode, P))
     gk, gv = host(ckd), host(cvd)
     if mode == 0:
         want_k = kc.copy(); want_k[P] = kr
