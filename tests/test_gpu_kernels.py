@@ -499,7 +499,8 @@ def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
     last step; 255 / 256 end and start a step), 1024 the split + combine
     pair.  On split + combine, chunks of up to 5 steps of 16 positions run
     scores first (4095: 5 steps), longer ones the running softmax after the
-    5 entry steps (6000: 6 steps per chunk, 8200: 9).
+    5 entry steps (6000: 6 steps per chunk; 8200 with 4 KV heads: 9 steps,
+    3 entry steps for fp32).
 
     Past 2048 positions the per-element check is against float64 attention
     over the same (dequantized) rows, with the floor set by the magnitude
