@@ -1430,8 +1430,8 @@ extern "C" int rina_hip_gqa_attention(const float* q, const float* kcur, const f
     int rep = H / Hkv;
     bool fast = T == 1 && dh == 64 && !pre_rope && rep_ok(rep) && cache_k && cache_v &&
                 ((uintptr_t)q % 16 == 0) && ((uintptr_t)kcur % 16 == 0) && ((uintptr_t)vcur % 16 == 0) &&
-                (mode != RINA_KV_FP32 || (((uintptr_t)cache_k | (uintptr_t)cache_v) % 16 == 0));
-    if (fast) {
+                (((uintptr_t)cache_k | (uintptr_t)cache_v) % (mode == RINA_KV_FP32 ? 16 : 2) == 0);
+    if (fast) {   // (the split kernel's q8 windows assume 2-byte aligned records)
         SplitArgs sa{};
         sa.q = q; sa.kcur = kcur; sa.vcur = vcur;
         sa.ck = (uint8_t*)cache_k; sa.cv = (uint8_t*)cache_v;
