@@ -572,6 +572,66 @@ def test_decode_attention_fused(rina, orc, mode, P, H, Hkv, use_dpos):
         assert np.array_equal(gv, orc.kv_quantize(vf, want_v))
 
 
+@pytest.mark.parametrize("mode", [1, 2, 5])
+@pytest.mark.parametrize("P,max_seq", [(100, 109), (1200, 1201), (4095, 4096)])
+def test_decode_attention_cache_at_2_mod_4(rina, orc, mode, P, max_seq):
+    """Packed caches whose base lies 2 bytes past a 4-byte boundary (the
+    entry point asks for 2-byte alignment): the q8 slices are read as
+    12-byte windows from the dword at or below them, whose offset then
+    flips between the even and odd blocks of a record.  Output against the
+    oracle (per element below 2048 positions, else against float64 with
+    the averaged values' magnitude as floor), appended bytes bit-exact, the
+    bytes around the cache untouched; P = max_seq - 1 writes the last row
+    and reads every row before it."""
+    hip = rina.load_hip()
+    L = orc.load()
+    H, Hkv, dh = 32, 8, 64
+    kvd = Hkv * dh
+    r = rng(77 + mode + P)
+    kc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    vc = r.standard_normal((max_seq, kvd)).astype(np.float32)
+    q = r.standard_normal(H * dh).astype(np.float32)
+    k = r.standard_normal(kvd).astype(np.float32)
+    v = r.standard_normal(kvd).astype(np.float32)
+    cos, sin = rope_tables(dh, max_seq)
+    qr, kr = q.copy(), k.copy()
+    L.orc_rope_neox(qr.ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, H, dh, P)
+    L.orc_rope_neox(kr.ctypes.data, cos.ctypes.data, sin.ctypes.data, 1, Hkv, dh, P)
+    kf, vf = orc.kv_mode_formats(mode)
+    ckb, cvb = orc.kv_quantize(kf, kc), orc.kv_quantize(vf, vc)
+    ref = np.zeros(H * dh, np.float32)
+    L.orc_gqa_attention(qr.ctypes.data, kr.ctypes.data, v.ctypes.data, None, None, ckb.ctypes.data,
+                        cvb.ctypes.data, mode, 0, None, None, 1, P, H, Hkv, dh, ref.ctypes.data)
+    guard = np.arange(16, dtype=np.uint8) + 200
+    kbuf = dev(np.concatenate([guard[:2], ckb, guard]))     # cache at base + 2
+    vbuf = dev(np.concatenate([guard[:2], cvb, guard]))
+    assert kbuf.data_ptr() % 4 == 0
+    ws_bytes = hip.rina_hip_gqa_attention_workspace(1, H, dh, max_seq)
+    ws = empty(ws_bytes, "uint8")
+    od = empty(H * dh)
+    cd, sd = dev(cos), dev(sin)
+    ok(hip.rina_hip_gqa_decode_attention(dev(q).data_ptr(), dev(k).data_ptr(), dev(v).data_ptr(), cd.data_ptr(),
+                                         sd.data_ptr(), cd.data_ptr(), sd.data_ptr(), kbuf.data_ptr() + 2,
+                                         vbuf.data_ptr() + 2, mode, H, Hkv, dh, P, None, max_seq, od.data_ptr(),
+                                         None, ws.data_ptr(), ws_bytes, stream()), "decode attention")
+    got = host(od)
+    if P <= 2048:
+        assert_close_elem(got, ref, what="cache at 2 mod 4, mode %d P %d" % (mode, P))
+    else:
+        assert_close(got, ref, what="cache at 2 mod 4, mode %d P %d" % (mode, P))
+        Kh = orc.kv_dequant(kf, ckb, max_seq * kvd).reshape(max_seq, kvd)[:P]
+        Vh = orc.kv_dequant(vf, cvb, max_seq * kvd).reshape(max_seq, kvd)[:P]
+        o64, mag = attention_f64(qr, np.vstack([Kh, kr[None]]), np.vstack([Vh, v[None]]), H, Hkv, dh)
+        assert_close_attn(got, o64, mag, what="cache at 2 mod 4, mode %d P %d vs float64" % (mode, P))
+    gk, gv = host(kbuf), host(vbuf)
+    want_k, want_v = kc.copy(), vc.copy()
+    want_k[P], want_v[P] = kr, v
+    assert np.array_equal(gk[2:2 + ckb.size], orc.kv_quantize(kf, want_k))
+    assert np.array_equal(gv[2:2 + cvb.size], orc.kv_quantize(vf, want_v))
+    assert np.array_equal(gk[:2], guard[:2]) and np.array_equal(gk[2 + ckb.size:], guard)
+    assert np.array_equal(gv[:2], guard[:2]) and np.array_equal(gv[2 + cvb.size:], guard)
+
+
 def test_decode_attention_sequence(rina, orc):
     """40 consecutive decode calls at a device position (the decode loop):
     every output against the oracle over the cache as it grows, so each call
