@@ -200,7 +200,9 @@ int rina_hip_gqa_attention(const float* q, const float* kcur, const float* vcur,
  * k_rot_out (optional, [Hkv*dh]) receives the rotated K row.  Same
  * workspace as rina_hip_gqa_attention.  Fuses gqa_layer.cu:147-270 for the
  * decode step (no counterpart as one reference call); RINA_ERR_SHAPE for
- * shapes it does not cover (the caller then uses the two-call form). */
+ * shapes it does not cover (the caller then uses the two-call form): q, k,
+ * v, the RoPE tables and k_rot_out must be 16-byte aligned, fp32 caches
+ * 16-byte aligned, packed caches 2-byte aligned. */
 int rina_hip_gqa_decode_attention(const float* q, const float* k, const float* v,
                                   const float* rope_q_cos, const float* rope_q_sin,
                                   const float* rope_k_cos, const float* rope_k_sin,
