@@ -1533,6 +1533,21 @@ int direct_rb(GemvArgs& a, int rb, hipStream_t st) {
         }
         return RINA_ERR_ARG;
     }
+    // one matrix in one segment: no per-row segment selection (graph
+    // replays over weight rings past the MALL: W_o 2048 x 2048 3.05 -> 2.92
+    // us, W2 2048 x 8192 5.50 -> 5.25, the Q2_K LM head 102400 x 2048 31.5
+    // -> 29.2, whose 3-segment form spilled scalar registers; the SwiGLU
+    // pair 8192 x 2048 measured slower in this form, 6.80 -> 7.03)
+    if constexpr (NMAT == 1) {
+        if (a.nseg == 1) {
+            switch (rb) {
+                case 1: return launch_direct<FMT, WPR, 1, PRO, 1, 1>(a, st);
+                case 2: return launch_direct<FMT, WPR, 1, PRO, 2, 1>(a, st);
+                case 4: return launch_direct<FMT, WPR, 1, PRO, 4, 1>(a, st);
+                default: return launch_direct<FMT, WPR, 1, PRO, (FMT == FMT_Q2_K ? 4 : 8), 1>(a, st);
+            }
+        }
+    }
     switch (rb) {
         case 1: return launch_direct<FMT, WPR, NMAT, PRO, 1, 3>(a, st);
         case 2: return launch_direct<FMT, WPR, NMAT, PRO, 2, 3>(a, st);
