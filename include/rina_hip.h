@@ -452,6 +452,28 @@ int rina_hip_dq_decode_attention_kv(const float* qa, const float* qb, const floa
                                     float* out, void* workspace, size_t workspace_bytes,
                                     void* stream);
 
+/* A prompt's T rows at positions start_pos .. start_pos + T - 1 of the
+ * RINA-MLA attention over the q2k_q1v cache in one call (the whole-sequence
+ * forward of rina_mla_layer.cu:65-98 with the cache of
+ * rina/model_jamba_qw2.py:175-177): every row's key content and value are
+ * packed and its RoPE'd key part stored as rina_hip_dq_decode_attention_kv
+ * appends them (the same bytes), then row t attends to the positions
+ * before it through the cache and to its own position through its fp32
+ * rows, as T decode calls at those positions would (outputs equal within
+ * float rounding).  qa [T, H*da], qb [T, H*db], ka [T, Hkv*da],
+ * kb [T, Hkv*db], v [T, Hkv*dv]; out [T, H*dv].  kv_mode must be
+ * RINA_KV_Q2K_Q1V (else RINA_ERR_QTYPE; fp32 caches take
+ * rina_hip_dq_prompt_attention), da == 64, dv == 64, db <= 64 and even,
+ * caches 2-byte aligned (else RINA_ERR_SHAPE), start_pos + T <= max_seq
+ * (else RINA_ERR_RANGE).  No workspace. */
+int rina_hip_dq_prompt_attention_kv(const float* qa, const float* qb, const float* ka,
+                                    const float* kb, const float* v, const float* rope_q_cos,
+                                    const float* rope_q_sin, const float* rope_k_cos,
+                                    const float* rope_k_sin, int kv_mode, void* cache_k,
+                                    void* cache_v, float* cache_kr, int H, int Hkv, int da,
+                                    int db, int dv, int start_pos, int T, int max_seq, float* out,
+                                    void* stream);
+
 /* ====================================================================== */
 /* Per-token glue                                                          */
 /* ====================================================================== */

@@ -84,6 +84,8 @@ _HIP_SIGS = {
     "rina_hip_dq_kv_region_bytes": (SZ, [I32, I32, I32, I32, I32, I32, I32]),
     "rina_hip_dq_decode_attention_kv": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, VP, VP, VP, I32, I32, I32, I32,
                                               I32, I32, VP, I32, VP, VP, SZ, VP]),
+    "rina_hip_dq_prompt_attention_kv": (I32, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I32, VP, VP, VP, I32, I32, I32, I32,
+                                              I32, I32, I32, I32, VP, VP]),
     "rina_hip_rms_norm": (I32, [VP, VP, VP, I32, I32, F32, VP]),
     "rina_hip_layer_norm": (I32, [VP, VP, VP, I32, I32, F32, VP]),
     "rina_hip_rope": (I32, [VP, VP, VP, I32, I32, I32, I32, VP, I32, VP]),

@@ -831,6 +831,7 @@ struct DqArgs {
     uint8_t* ckq;                       // q2k_q1v: key content, q2_1 blocks [max_seq][Hkv][da/32]
     float* ckr;                         // q2k_q1v: key RoPE part, fp32 [max_seq][Hkv][db]
     uint8_t* cvq;                       // q2k_q1v: values, q1_0 records [max_seq][Hkv][dv/32]
+    float* out;                         // dq_prompt_kv_kernel: [T][H][dv]
     int H, Hkv, da, db, dv, start_pos, max_seq;
     const int* d_pos;
     float scale;
@@ -1004,6 +1005,121 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
             gst(p.ws_m + (int64_t)c * a.H + h, M);
             gst(p.ws_l + (int64_t)c * a.H + h, lt);
         }
+    }
+}
+
+// A prompt's T rows over the q2k_q1v cache (rows at positions start_pos + t).
+// dq_pack_rows_kernel, grid (T, Hkv), one wave per (row, KV head): the row's
+// key content and value packed and its RoPE'd key part stored, the bytes
+// dq_split_kernel<1> appends for that row at its position (the same dims,
+// lanes and block codec).  dq_prompt_kv_kernel, grid (T, H), four waves per
+// (row, query head), after it: row t reads the positions before it from the
+// cache (dequantized as dq_split_kernel<1> reads them) and its own position
+// from its fp32 rows, as the decode step of that row would; each wave takes
+// every fourth position of each 32-position chunk with the running softmax
+// (the next chunk's loads issued before the current chunk is scored), then
+// the four waves merge and the row is normalized.
+__global__ __launch_bounds__(64) void dq_pack_rows_kernel(DqArgs a) {
+    const int lane = threadIdx.x, t = blockIdx.x, kvh = blockIdx.y;
+    const int pos = a.start_pos + t, dq = a.da + a.db;
+    const int i1 = lane + 64 < dq ? lane + 64 : dq - 1;
+    const float* ka = a.ka + ((int64_t)t * a.Hkv + kvh) * a.da;
+    const float* kb = a.kb + ((int64_t)t * a.Hkv + kvh) * a.db;
+    const float kc0 = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, pos, lane);
+    const float kc1 = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, pos, i1);
+    const float vc = gld(a.v + ((int64_t)t * a.Hkv + kvh) * a.dv + lane);
+    const int64_t row = (int64_t)pos * a.Hkv + kvh;
+    const int b = lane >> 5;
+    if (lane < a.db) gst(a.ckr + row * a.db + lane, kc1);
+    kvq::quantize_block_lanes(RINA_KVF_Q2_1, kc0, a.ckq + row * 20 + 10 * b);
+    kvq::quantize_block_lanes(RINA_KVF_Q1_0, vc, a.cvq + row * 12 + 6 * b);
+}
+
+__global__ __launch_bounds__(256) void dq_prompt_kv_kernel(DqArgs a) {
+    constexpr int PW = kDqChunk / 4;
+    __shared__ float s_o[4][64];
+    __shared__ float s_m[4], s_l[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = blockIdx.x, h = blockIdx.y;
+    const int pos0 = a.start_pos + t, L = pos0 + 1;
+    const int dq = a.da + a.db, kvh = h / (a.H / a.Hkv);
+    const int i1 = lane + 64 < dq ? lane + 64 : dq - 1;
+    const bool hi = lane + 64 < dq;
+    const float* qa = a.qa + ((int64_t)t * a.H + h) * a.da;
+    const float* qb = a.qb + ((int64_t)t * a.H + h) * a.db;
+    const float* ka = a.ka + ((int64_t)t * a.Hkv + kvh) * a.da;
+    const float* kb = a.kb + ((int64_t)t * a.Hkv + kvh) * a.db;
+    const float q0 = dq_dim(qa, qb, a.qc, a.qs, a.da, a.db, pos0, lane);
+    const float q1v = dq_dim(qa, qb, a.qc, a.qs, a.da, a.db, pos0, i1);
+    const float kc0 = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, pos0, lane);
+    const float kc1v = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, pos0, i1);
+    const float vc = gld(a.v + ((int64_t)t * a.Hkv + kvh) * a.dv + lane);
+    const float q1 = hi ? q1v : 0.f, kc1 = hi ? kc1v : 0.f;
+    // the wave's positions j0 + wave + 4 i of a chunk; positions at or past
+    // pos0 read position 0's record (in the cache, never used)
+    auto load = [&](int j0, float (&x0)[PW], float (&x1)[PW], float (&xv)[PW]) {
+#pragma unroll
+        for (int i = 0; i < PW; i++) {
+            const int p = j0 + wave + 4 * i;
+            const int64_t r = (int64_t)(p < pos0 ? p : 0) * a.Hkv + kvh;
+            x0[i] = q2_1_dim(a.ckq + r * 20, lane);
+            x1[i] = lane < a.db ? gld(a.ckr + r * a.db + lane) : 0.f;
+            xv[i] = q1_0_dim(a.cvq + r * 12, lane);
+        }
+    };
+    const float sc2 = a.scale * 1.44269504088896341f;   // scores in base-2 units
+    float m = -INFINITY, l = 0.f, o = 0.f;
+    auto consume = [&](int j0, const float (&x0)[PW], const float (&x1)[PW], const float (&xv)[PW]) {
+#pragma unroll
+        for (int i = 0; i < PW; i++) {
+            const int p = j0 + wave + 4 * i;
+            const bool cur = p == pos0;                  // wave-uniform
+            const float kk0 = cur ? kc0 : x0[i], kk1 = cur ? kc1 : x1[i], vx = cur ? vc : xv[i];
+            const float sc = wave_sum(fmaf(q0, kk0, q1 * kk1)) * sc2;
+            if (p < L) {
+                const float mn = fmaxf(m, sc);
+                const float al = __builtin_amdgcn_exp2f(m - mn), pe = __builtin_amdgcn_exp2f(sc - mn);
+                l = fmaf(l, al, pe);
+                o = fmaf(o, al, pe * vx);
+                m = mn;
+            }
+        }
+    };
+    float kA[PW], rA[PW], vA[PW], kB[PW], rB[PW], vB[PW];
+    load(0, kA, rA, vA);
+    for (int j0 = 0;;) {
+        if (j0 + kDqChunk < L) {
+            load(j0 + kDqChunk, kB, rB, vB);
+            consume(j0, kA, rA, vA);
+        } else {
+            consume(j0, kA, rA, vA);
+            break;
+        }
+        j0 += kDqChunk;
+        if (j0 + kDqChunk < L) {
+            load(j0 + kDqChunk, kA, rA, vA);
+            consume(j0, kB, rB, vB);
+        } else {
+            consume(j0, kB, rB, vB);
+            break;
+        }
+        j0 += kDqChunk;
+    }
+    s_o[wave][lane] = o;
+    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+    __syncthreads();
+    if (wave == 0) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w]);
+        float ot = 0.f, lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float aw = s_m[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w] - M);
+            ot = fmaf(s_o[w][lane], aw, ot);
+            lt = fmaf(s_l[w], aw, lt);
+        }
+        gst(a.out + ((int64_t)t * a.H + h) * 64 + lane, ot / lt);   // pos0 itself is always counted: lt > 0
     }
 }
 
@@ -1665,4 +1781,33 @@ extern "C" int rina_hip_dq_decode_attention_kv(const float* qa, const float* qb,
     return dq_attention(qa, qb, ka, kb, v, rope_q_cos, rope_q_sin, rope_k_cos, rope_k_sin, kv_mode, nullptr, nullptr,
                         (uint8_t*)cache_k, cache_kr, (uint8_t*)cache_v, H, Hkv, da, db, dv, start_pos, d_pos, max_seq,
                         out, workspace, ws_bytes, as_stream(stream));
+}
+
+extern "C" int rina_hip_dq_prompt_attention_kv(const float* qa, const float* qb, const float* ka, const float* kb,
+                                               const float* v, const float* rope_q_cos, const float* rope_q_sin,
+                                               const float* rope_k_cos, const float* rope_k_sin, int kv_mode,
+                                               void* cache_k, void* cache_v, float* cache_kr, int H, int Hkv,
+                                               int da, int db, int dv, int start_pos, int T, int max_seq,
+                                               float* out, void* stream) {
+    if (!qa || !ka || !v || !out || H < 1 || Hkv < 1 || da < 1 || db < 0 || dv < 1 || T < 1 || max_seq < 1)
+        return RINA_ERR_ARG;
+    if (db > 0 && (!qb || !kb)) return RINA_ERR_ARG;
+    if ((!rope_q_cos) != (!rope_q_sin) || (!rope_k_cos) != (!rope_k_sin)) return RINA_ERR_ARG;
+    if (kv_mode != RINA_KV_Q2K_Q1V) return RINA_ERR_QTYPE;
+    if (!cache_k || !cache_v || (db > 0 && !cache_kr)) return RINA_ERR_ARG;
+    if (H % Hkv || da != 64 || dv != 64 || db > 64 || db % 2 || ((uintptr_t)cache_k | (uintptr_t)cache_v) % 2)
+        return RINA_ERR_SHAPE;
+    if (start_pos < 0 || (int64_t)start_pos + T > max_seq) return RINA_ERR_RANGE;
+    DqArgs a{};
+    a.qa = qa; a.qb = qb; a.ka = ka; a.kb = kb; a.v = v;
+    a.qc = rope_q_cos; a.qs = rope_q_sin; a.kc = rope_k_cos; a.ks = rope_k_sin;
+    a.ckq = (uint8_t*)cache_k; a.ckr = cache_kr; a.cvq = (uint8_t*)cache_v; a.out = out;
+    a.H = H; a.Hkv = Hkv; a.da = da; a.db = db; a.dv = dv; a.start_pos = start_pos; a.max_seq = max_seq;
+    a.scale = 1.0f / sqrtf((float)(da + db));
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(dq_pack_rows_kernel, dim3(T, Hkv), dim3(64), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(dq_prompt_kv_kernel, dim3(T, H), dim3(256), 0, st, a);
+    RINA_LAUNCH_CHECK();
+    return RINA_OK;
 }
