@@ -888,6 +888,52 @@ def test_linear_norm_prologue(rina, orc, qt, pro, M, K):
     assert_close(host(y).reshape(M, N), orc.linear(w, qt, xn, N, K), what="prologue %d qt %d" % (pro, qt))
 
 
+@pytest.mark.parametrize("qt", [5, 7, 10])
+@pytest.mark.parametrize("N,K,epi,pro", [(2048, 8192, 1, 0),    # W2 + residual: 8 rows per wave, 4 waves per row
+                                         (2048, 2048, 1, 0),    # W_o + residual: 2 rows per wave
+                                         (640, 1536, 1, 0),     # Jamba W2 + residual
+                                         (4100, 2048, 0, 1),    # Q2_K LM-head form: 4 rows per wave, loops
+                                         (2049, 2048, 1, 2)])   # ragged last row group, LayerNorm prologue
+def test_linear_single_segment_decode_shapes(rina, orc, qt, N, K, epi, pro):
+    """One matrix in one segment at the decode step's shapes (the direct
+    kernel without a segment table): the residual-add epilogue, with the old
+    output words loaded with the weights, and the norm prologues.  Normwise
+    against the oracle's norm and matvec, and per element against float64
+    products of the dequantized weights with the oracle's normalized row,
+    within 1e-5 of the element's magnitude scale sum_k |w_ik x_k| (the
+    bound fp32 accumulation of a K-term sum is held to) plus the rounding of
+    the final residual add."""
+    hip = rina.load_hip()
+    L = orc.load()
+    r = rng(qt * 7 + N + K + epi * 3 + pro)
+    if qt == 10:
+        w = q2k_blocks(N + K, N * K)
+    else:
+        w = orc.pack(qt, (r.standard_normal(N * K) * 0.02).astype(np.float32))
+    x = (r.standard_normal(K) * 2 + 0.3).astype(np.float32)
+    nw = r.uniform(0.5, 1.5, K).astype(np.float32)
+    base = r.standard_normal(N).astype(np.float32)
+    yd = dev(base)
+    seg = rina.LinearSeg(dev(w).data_ptr(), None, yd.data_ptr(), N)
+    ok(hip.rina_hip_linear_fused(C.byref(seg), 1, qt, dev(x).data_ptr(), 1, K, epi, pro,
+                                 dev(nw).data_ptr() if pro else None, np.float32(1e-5), stream()), "single segment")
+    xn = x.copy()
+    if pro:
+        (L.orc_rms_norm if pro == 1 else L.orc_layer_norm)(xn.ctypes.data, nw.ctypes.data, 1, K, np.float32(1e-5))
+    ref = orc.linear(w, qt, xn, N, K)[0]
+    if epi == 1:
+        ref = base + ref
+    got = host(yd)
+    assert_close(got, ref, what="single segment qt %d N %d K %d" % (qt, N, K))
+    W = orc.dequant(qt, w, N * K).reshape(N, K).astype(np.float64)
+    ref64 = W @ xn.astype(np.float64) + (base.astype(np.float64) if epi == 1 else 0.0)
+    scale = np.abs(W) @ np.abs(xn.astype(np.float64))
+    err = np.abs(got.astype(np.float64) - ref64) - 1.2e-7 * np.abs(ref64)
+    worst = int(np.argmax(err / scale))
+    assert err[worst] <= REL_TOL * scale[worst], "element %d: %.9g against %.9g (scale %.3g)" % (
+        worst, got[worst], ref64[worst], scale[worst])
+
+
 def _prefill_weights(orc, qt, r, n):
     if qt == 10:   # zero-mean Q2_K blocks (flat element order; rows may straddle blocks)
         import importlib
