@@ -453,19 +453,19 @@ int rina_hip_dq_decode_attention_kv(const float* qa, const float* qb, const floa
                                     void* stream);
 
 /* A prompt's T rows at positions start_pos .. start_pos + T - 1 of the
- * RINA-MLA attention over the q2k_q1v cache in one call (the whole-sequence
- * forward of rina_mla_layer.cu:65-98 with the cache of
- * rina/model_jamba_qw2.py:175-177): every row's key content and value are
- * packed and its RoPE'd key part stored as rina_hip_dq_decode_attention_kv
- * appends them (the same bytes), then row t attends to the positions
- * before it through the cache and to its own position through its fp32
- * rows, as T decode calls at those positions would (outputs equal within
- * float rounding).  qa [T, H*da], qb [T, H*db], ka [T, Hkv*da],
- * kb [T, Hkv*db], v [T, Hkv*dv]; out [T, H*dv].  kv_mode must be
- * RINA_KV_Q2K_Q1V (else RINA_ERR_QTYPE; fp32 caches take
- * rina_hip_dq_prompt_attention), da == 64, dv == 64, db <= 64 and even,
- * caches 2-byte aligned (else RINA_ERR_SHAPE), start_pos + T <= max_seq
- * (else RINA_ERR_RANGE).  No workspace. */
+ * RINA-MLA attention in one call (the whole-sequence forward of
+ * rina_mla_layer.cu:65-98), over the caches kv_mode selects as in
+ * rina_hip_dq_decode_attention_kv (RINA_KV_FP32, or RINA_KV_Q2K_Q1V, the
+ * cache of rina/model_jamba_qw2.py:175-177; else RINA_ERR_QTYPE): every
+ * row's key and value are appended as rina_hip_dq_decode_attention_kv
+ * appends them (the same bytes), then row t attends to the positions before
+ * it through the cache and to its own position through its fp32 rows, as T
+ * decode calls at those positions would (outputs equal within float
+ * rounding).  qa [T, H*da], qb [T, H*db], ka [T, Hkv*da], kb [T, Hkv*db],
+ * v [T, Hkv*dv]; out [T, H*dv].  dv == 64, 64 <= da + db <= 128, db even;
+ * q2k_q1v: da == 64, caches 2-byte aligned; fp32: caches 4-byte aligned
+ * (else RINA_ERR_SHAPE); start_pos + T <= max_seq (else RINA_ERR_RANGE).
+ * No workspace. */
 int rina_hip_dq_prompt_attention_kv(const float* qa, const float* qb, const float* ka,
                                     const float* kb, const float* v, const float* rope_q_cos,
                                     const float* rope_q_sin, const float* rope_k_cos,

@@ -308,17 +308,16 @@ struct RMLAImpl {
         rina_linear_seg s3{w_k2v, nullptr, v, Hkv * dh};
         CK(rina_hip_linear_fused(&s3, 1, qt, k, T, Hkv * dh, RINA_EPI_STORE, RINA_PRO_NONE, nullptr, 0.f, s));
         // causal attention (:78-86): row t appends its K / V at start_pos + t and
-        // attends to positions <= it.  fp32 caches from position 0: one call
-        // over all rows; the q2k_q1v cache: one call that packs every row,
-        // then each row reads the rows before it through their packs; other
-        // cases row by row
+        // attends to positions <= it.  One call appends every row, then each
+        // row reads the rows before it through the cache; shapes it does not
+        // take: fp32 caches from position 0 as one causal pass over the
+        // expanded rows, else row by row
         bool batched = false;
-        if (kv_mode == RINA_KV_Q2K_Q1V) {
-            rc = rina_hip_dq_prompt_attention_kv(q, qr, k, kr, v, rqc, rqs, rkc, rks, kv_mode, ck, cv, ckr, H, Hkv, dh,
-                                                 dhr, dh, start_pos, T, max_seq, att, s);
-            if (rc != RINA_OK && rc != RINA_ERR_SHAPE) return rc;   // a shape it does not take launches nothing
-            batched = rc == RINA_OK;
-        } else if (kv_mode == RINA_KV_FP32 && start_pos == 0) {
+        rc = rina_hip_dq_prompt_attention_kv(q, qr, k, kr, v, rqc, rqs, rkc, rks, kv_mode, ck, cv, ckr, H, Hkv, dh, dhr,
+                                             dh, start_pos, T, max_seq, att, s);
+        if (rc != RINA_OK && rc != RINA_ERR_SHAPE) return rc;   // a shape it does not take launches nothing
+        batched = rc == RINA_OK;
+        if (!batched && kv_mode == RINA_KV_FP32 && start_pos == 0) {
             float* aws = att + (size_t)T * H * dh;
             const size_t need = rina_hip_dq_prompt_workspace(T, H, Hkv, dh, dhr, dh);
             if (need && need <= sizeof(float) * (size_t)T * attn_rows_per_token() && (uintptr_t)aws % 16 == 0) {

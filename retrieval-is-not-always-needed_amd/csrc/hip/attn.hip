@@ -1008,17 +1008,18 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, SplitArgs p) {
     }
 }
 
-// A prompt's T rows over the q2k_q1v cache (rows at positions start_pos + t).
-// dq_pack_rows_kernel, grid (T, Hkv), one wave per (row, KV head): the row's
-// key content and value packed and its RoPE'd key part stored, the bytes
-// dq_split_kernel<1> appends for that row at its position (the same dims,
-// lanes and block codec).  dq_prompt_kv_kernel, grid (T, H), four waves per
-// (row, query head), after it: row t reads the positions before it from the
-// cache (dequantized as dq_split_kernel<1> reads them) and its own position
-// from its fp32 rows, as the decode step of that row would; each wave takes
-// every fourth position of each 32-position chunk with the running softmax
-// (the next chunk's loads issued before the current chunk is scored), then
-// the four waves merge and the row is normalized.
+// A prompt's T rows (rows at positions start_pos + t) over the fp32 caches
+// (QKV 0) or the q2k_q1v cache (QKV 1).  dq_pack_rows_kernel, grid (T, Hkv),
+// one wave per (row, KV head): the row's key and value as
+// dq_split_kernel<QKV> appends them at its position (the same dims, lanes
+// and, packed, block codec).  dq_prompt_kv_kernel, grid (T, H), four waves
+// per (row, query head), after it: row t reads the positions before it from
+// the cache (as dq_split_kernel<QKV> reads them) and its own position from
+// its fp32 rows, as the decode step of that row would; each wave takes every
+// fourth position of each 32-position chunk with the running softmax (the
+// next chunk's loads issued before the current chunk is scored), then the
+// four waves merge and the row is normalized.
+template <int QKV>
 __global__ __launch_bounds__(64) void dq_pack_rows_kernel(DqArgs a) {
     const int lane = threadIdx.x, t = blockIdx.x, kvh = blockIdx.y;
     const int pos = a.start_pos + t, dq = a.da + a.db;
@@ -1029,12 +1030,20 @@ __global__ __launch_bounds__(64) void dq_pack_rows_kernel(DqArgs a) {
     const float kc1 = dq_dim(ka, kb, a.kc, a.ks, a.da, a.db, pos, i1);
     const float vc = gld(a.v + ((int64_t)t * a.Hkv + kvh) * a.dv + lane);
     const int64_t row = (int64_t)pos * a.Hkv + kvh;
-    const int b = lane >> 5;
-    if (lane < a.db) gst(a.ckr + row * a.db + lane, kc1);
-    kvq::quantize_block_lanes(RINA_KVF_Q2_1, kc0, a.ckq + row * 20 + 10 * b);
-    kvq::quantize_block_lanes(RINA_KVF_Q1_0, vc, a.cvq + row * 12 + 6 * b);
+    if (QKV == 0) {
+        float* kd = a.ck + row * dq;
+        gst(kd + lane, kc0);
+        if (lane + 64 < dq) gst(kd + lane + 64, kc1);
+        gst(a.cv + row * a.dv + lane, vc);
+    } else {
+        const int b = lane >> 5;
+        if (lane < a.db) gst(a.ckr + row * a.db + lane, kc1);
+        kvq::quantize_block_lanes(RINA_KVF_Q2_1, kc0, a.ckq + row * 20 + 10 * b);
+        kvq::quantize_block_lanes(RINA_KVF_Q1_0, vc, a.cvq + row * 12 + 6 * b);
+    }
 }
 
+template <int QKV>
 __global__ __launch_bounds__(256) void dq_prompt_kv_kernel(DqArgs a) {
     constexpr int PW = kDqChunk / 4;
     __shared__ float s_o[4][64];
@@ -1062,9 +1071,15 @@ __global__ __launch_bounds__(256) void dq_prompt_kv_kernel(DqArgs a) {
         for (int i = 0; i < PW; i++) {
             const int p = j0 + wave + 4 * i;
             const int64_t r = (int64_t)(p < pos0 ? p : 0) * a.Hkv + kvh;
-            x0[i] = q2_1_dim(a.ckq + r * 20, lane);
-            x1[i] = lane < a.db ? gld(a.ckr + r * a.db + lane) : 0.f;
-            xv[i] = q1_0_dim(a.cvq + r * 12, lane);
+            if (QKV == 0) {
+                x0[i] = gld(a.ck + r * dq + lane);
+                x1[i] = lane + 64 < dq ? gld(a.ck + r * dq + lane + 64) : 0.f;
+                xv[i] = gld(a.cv + r * a.dv + lane);
+            } else {
+                x0[i] = q2_1_dim(a.ckq + r * 20, lane);
+                x1[i] = lane < a.db ? gld(a.ckr + r * a.db + lane) : 0.f;
+                xv[i] = q1_0_dim(a.cvq + r * 12, lane);
+            }
         }
     };
     const float sc2 = a.scale * 1.44269504088896341f;   // scores in base-2 units
@@ -1793,21 +1808,27 @@ extern "C" int rina_hip_dq_prompt_attention_kv(const float* qa, const float* qb,
         return RINA_ERR_ARG;
     if (db > 0 && (!qb || !kb)) return RINA_ERR_ARG;
     if ((!rope_q_cos) != (!rope_q_sin) || (!rope_k_cos) != (!rope_k_sin)) return RINA_ERR_ARG;
-    if (kv_mode != RINA_KV_Q2K_Q1V) return RINA_ERR_QTYPE;
-    if (!cache_k || !cache_v || (db > 0 && !cache_kr)) return RINA_ERR_ARG;
-    if (H % Hkv || da != 64 || dv != 64 || db > 64 || db % 2 || ((uintptr_t)cache_k | (uintptr_t)cache_v) % 2)
-        return RINA_ERR_SHAPE;
+    if (kv_mode != RINA_KV_FP32 && kv_mode != RINA_KV_Q2K_Q1V) return RINA_ERR_QTYPE;
+    const bool packed = kv_mode == RINA_KV_Q2K_Q1V;
+    if (!cache_k || !cache_v || (packed && db > 0 && !cache_kr)) return RINA_ERR_ARG;
+    if (H % Hkv || dv != 64 || da + db > 128 || da + db < 64 || db % 2) return RINA_ERR_SHAPE;
+    if (packed && (da != 64 || db > 64 || ((uintptr_t)cache_k | (uintptr_t)cache_v) % 2)) return RINA_ERR_SHAPE;
+    if (!packed && ((uintptr_t)cache_k | (uintptr_t)cache_v) % 4) return RINA_ERR_SHAPE;
     if (start_pos < 0 || (int64_t)start_pos + T > max_seq) return RINA_ERR_RANGE;
     DqArgs a{};
     a.qa = qa; a.qb = qb; a.ka = ka; a.kb = kb; a.v = v;
     a.qc = rope_q_cos; a.qs = rope_q_sin; a.kc = rope_k_cos; a.ks = rope_k_sin;
-    a.ckq = (uint8_t*)cache_k; a.ckr = cache_kr; a.cvq = (uint8_t*)cache_v; a.out = out;
+    if (packed) { a.ckq = (uint8_t*)cache_k; a.ckr = cache_kr; a.cvq = (uint8_t*)cache_v; }
+    else { a.ck = (float*)cache_k; a.cv = (float*)cache_v; }
+    a.out = out;
     a.H = H; a.Hkv = Hkv; a.da = da; a.db = db; a.dv = dv; a.start_pos = start_pos; a.max_seq = max_seq;
     a.scale = 1.0f / sqrtf((float)(da + db));
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(dq_pack_rows_kernel, dim3(T, Hkv), dim3(64), 0, st, a);
+    if (packed) hipLaunchKernelGGL(dq_pack_rows_kernel<1>, dim3(T, Hkv), dim3(64), 0, st, a);
+    else hipLaunchKernelGGL(dq_pack_rows_kernel<0>, dim3(T, Hkv), dim3(64), 0, st, a);
     RINA_LAUNCH_CHECK();
-    hipLaunchKernelGGL(dq_prompt_kv_kernel, dim3(T, H), dim3(256), 0, st, a);
+    if (packed) hipLaunchKernelGGL(dq_prompt_kv_kernel<1>, dim3(T, H), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(dq_prompt_kv_kernel<0>, dim3(T, H), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }

@@ -116,14 +116,16 @@ def test_dq_prompt_attention_matches_decode_rows(rina, T, H, Hkv, da, db):
         assert_close_elem(got[t], one[t], what="prompt row %d vs decode row" % t)
 
 
+@pytest.mark.parametrize("mode", [5, 0])
 @pytest.mark.parametrize("T,start", [(1, 0), (2, 0), (19, 0), (300, 0), (40, 37), (260, 700)])
 @pytest.mark.parametrize("H,Hkv,da,db", [(10, 5, 64, 32), (4, 2, 64, 16), (4, 1, 64, 0)])
-def test_dq_prompt_attention_kv_matches_decode_rows(rina, T, start, H, Hkv, da, db):
-    """A prompt of T rows at positions start .. start+T-1 over the q2k_q1v
-    cache in one call (every row packed, then each row reads the rows before
-    it through their packs) against the same rows fed to the q2k_q1v decode
-    attention one position at a time: the packed key content, the RoPE'd key
-    part and the packed values bit for bit over the whole cache, every
+def test_dq_prompt_attention_kv_matches_decode_rows(rina, T, start, H, Hkv, da, db, mode):
+    """A prompt of T rows at positions start .. start+T-1 in one call (every
+    row appended, then each row reads the rows before it through the cache)
+    against the same rows fed to the decode attention of the same cache one
+    position at a time: over the q2k_q1v cache (mode 5) the packed key
+    content, the RoPE'd key part and the packed values, over fp32 caches
+    (mode 0) the key and value rows, bit for bit over the whole cache; every
     output row within tolerance.  Rows before start come from decode calls
     in both runs (a prompt that continues a cache); 260 rows from 700 take
     32-position chunks on both sides of a chunk boundary."""
@@ -143,8 +145,8 @@ def test_dq_prompt_attention_kv_matches_decode_rows(rina, T, start, H, Hkv, da, 
     qad, kad, vd = dev(qa), dev(ka), dev(v)
     qbd = dev(qb) if db else None
     kbd = dev(kb) if db else None
-    sizes = [hip.rina_hip_dq_kv_region_bytes(5, part, max_seq, Hkv, da, db, dv) for part in range(3)]
-    assert sizes[0] > 0 and sizes[1] > 0 and (sizes[2] > 0) == (db > 0)
+    sizes = [hip.rina_hip_dq_kv_region_bytes(mode, part, max_seq, Hkv, da, db, dv) for part in range(3)]
+    assert sizes[0] > 0 and sizes[1] > 0 and (sizes[2] > 0) == (mode == 5 and db > 0)
 
     def caches():
         return [dev(np.zeros(max(sz, 4), np.uint8)) for sz in sizes]
@@ -158,8 +160,9 @@ def test_dq_prompt_attention_kv_matches_decode_rows(rina, T, start, H, Hkv, da, 
         ok(hip.rina_hip_dq_decode_attention_kv(ptr(qad, 4 * t * H * da), ptr(qbd, 4 * t * H * db),
                                                ptr(kad, 4 * t * Hkv * da), ptr(kbd, 4 * t * Hkv * db),
                                                ptr(vd, 4 * t * Hkv * dv), cd.data_ptr(), sd.data_ptr(), cd.data_ptr(),
-                                               sd.data_ptr(), 5, c[0].data_ptr(), c[1].data_ptr(),
-                                               c[2].data_ptr() if db else None, H, Hkv, da, db, dv, t, None, max_seq,
+                                               sd.data_ptr(), mode, c[0].data_ptr(), c[1].data_ptr(),
+                                               c[2].data_ptr() if sizes[2] else None, H, Hkv, da, db, dv, t, None,
+                                               max_seq,
                                                od.data_ptr(), ws.data_ptr(), wsb, stream()), "decode row %d" % t)
         return host(od)
 
@@ -172,9 +175,9 @@ def test_dq_prompt_attention_kv_matches_decode_rows(rina, T, start, H, Hkv, da, 
     ok(hip.rina_hip_dq_prompt_attention_kv(ptr(qad, 4 * start * H * da), ptr(qbd, 4 * start * H * db),
                                            ptr(kad, 4 * start * Hkv * da), ptr(kbd, 4 * start * Hkv * db),
                                            ptr(vd, 4 * start * Hkv * dv), cd.data_ptr(), sd.data_ptr(), cd.data_ptr(),
-                                           sd.data_ptr(), 5, c2[0].data_ptr(), c2[1].data_ptr(),
-                                           c2[2].data_ptr() if db else None, H, Hkv, da, db, dv, start, T, max_seq,
-                                           o2.data_ptr(), stream()), "prompt attention q2k_q1v")
+                                           sd.data_ptr(), mode, c2[0].data_ptr(), c2[1].data_ptr(),
+                                           c2[2].data_ptr() if sizes[2] else None, H, Hkv, da, db, dv, start, T,
+                                           max_seq, o2.data_ptr(), stream()), "prompt attention mode %d" % mode)
     for part in range(3):
         if sizes[part]:
             assert np.array_equal(host(c2[part]), host(c1[part])), "cache part %d" % part
@@ -184,16 +187,16 @@ def test_dq_prompt_attention_kv_matches_decode_rows(rina, T, start, H, Hkv, da, 
 
 
 def test_dq_prompt_attention_kv_rejects(rina):
-    """Argument checks of the batched q2k_q1v prompt entry, before any launch:
-    another cache mode (-2, RINA_ERR_QTYPE), head sizes other than 64 (-3,
-    RINA_ERR_SHAPE), rows past the cache (-4, RINA_ERR_RANGE), no rows (-1,
-    RINA_ERR_ARG)."""
+    """Argument checks of the batched prompt entry, before any launch: a GQA
+    cache mode (-2, RINA_ERR_QTYPE), q2k_q1v key content or values other than
+    64 wide (-3, RINA_ERR_SHAPE), rows past the cache (-4, RINA_ERR_RANGE),
+    no rows (-1, RINA_ERR_ARG)."""
     hip = rina.load_hip()
     buf = empty(1 << 16, "uint8")
     p = buf.data_ptr()
     call = lambda mode, da, dv, start, T, max_seq: hip.rina_hip_dq_prompt_attention_kv(
         p, p, p, p, p, None, None, None, None, mode, p, p, p, 4, 2, da, 16, dv, start, T, max_seq, p, stream())
-    assert call(0, 64, 64, 0, 4, 8) == -2
+    assert call(1, 64, 64, 0, 4, 8) == -2
     assert call(5, 32, 64, 0, 4, 8) == -3
     assert call(5, 64, 32, 0, 4, 8) == -3
     assert call(5, 64, 64, 6, 4, 8) == -4
