@@ -1723,6 +1723,11 @@ int gemv_f32(const rina_linear_seg* segs, int nseg, const float* x, int K, int e
         const int rpw = two ? 2 : 4;
         int g2 = (rows + 4 * rpw - 1) / (4 * rpw);
         if (g2 < grid) grid = g2;
+        // 4 workgroups per CU (the LM head 128256 x 2048 over copies past
+        // the MALL: 155.0-155.9 us against 156.3-159.2 at 8 and 156.5-157.6
+        // at 2; the half-wave rows above keep 8: K 640 49.9-50.2 us against
+        // 50.5-50.9 at 4)
+        if (grid > cus * 4) grid = cus * 4;
     }
     if (keys) {
         if (nseg != 1 || epi != RINA_EPI_STORE) return RINA_ERR_ARG;
