@@ -942,10 +942,11 @@ __global__ __launch_bounds__(1024) void mla_chunk_kernel(MlaArgs a) {
 // grid (H, v/16), 256 threads: the chunk merge of head h,
 // o_lat = sum_c 2^(M_c - M) partial_c / sum_c 2^(M_c - M) l_c over the
 // chunks holding positions 0..pos0 (at most kChunkTarget), then 16 rows of
-// out_h = W_vb_h o_lat, 4 per wave.  Thread = (float4 column tid & 127,
-// chunk parity tid >> 7): 8 16-byte partial loads, the chunk maxima / sums
-// and four W_vb units per thread, all issued at entry (one round trip).
-// Every workgroup of the head repeats the small merge.
+// out_h = W_vb_h o_lat, 4 per wave, 2 per half wave (a row's 32 units over
+// the half's 32 lanes).  Thread = (float4 column tid & 127, chunk parity
+// tid >> 7): 8 16-byte partial loads, the chunk maxima / sums and two W_vb
+// units per thread, all issued at entry (one round trip).  Every workgroup
+// of the head repeats the small merge.
 template <int QT>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
     __shared__ float s_w[kChunkTarget];
@@ -961,10 +962,10 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
     const int i0 = 16 * blockIdx.y + 4 * wave;
     const bool rows_ok = i0 < a.v;
     const int64_t row0 = (int64_t)a.H * a.nope + (int64_t)h * a.v + (rows_ok ? i0 : 0);
-    const int ul = lane & (kFusedNcu - 1);                     // lanes 32..63 repeat lanes 0..31's unit, summed as 0
-    RawUnit wv[4];
+    const int ul = lane & (kFusedNcu - 1), hw = lane >> 5;    // unit, half wave: rows i0 + 2 r + hw
+    RawUnit wv[2];
 #pragma unroll
-    for (int r = 0; r < 4; r++) raw_issue<QT>(wv[r], a.wkvb, (row0 + r) * kFusedDc + 16 * ul);
+    for (int r = 0; r < 2; r++) raw_issue<QT>(wv[r], a.wkvb, (row0 + 2 * r + hw) * kFusedDc + 16 * ul);
     const int t4 = tid & 127, cp = tid >> 7;
     f32x4 pv[kChunkTarget / 2];
 #pragma unroll
@@ -992,14 +993,17 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
     const float inv_l = 1.0f / ((s_red[4] + s_red[5]) + (s_red[6] + s_red[7]));
     if (!cp) *(f32x4*)(s_lat + 4 * t4) = (acc + s_half[t4]) * inv_l;
     __syncthreads();
-    float o4[4];
+    float o2[2];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const float pr = raw_dot<QT>(wv[r], s_lat + 16 * ul);
-        o4[r] = wave_sum(lane < kFusedNcu ? pr : 0.f);
+    for (int r = 0; r < 2; r++) {
+        float pr = sum16(raw_dot<QT>(wv[r], s_lat + 16 * ul));
+        pr += dpp_rows<0x142, 0xA>(pr);   // row_bcast:15: lane 31 = lanes 0..31, lane 63 = lanes 32..63
+        o2[r] = pr;
     }
-    if (rows_ok && lane < 4)
-        gst(a.out + (int64_t)h * a.v + i0 + lane, lane == 0 ? o4[0] : lane == 1 ? o4[1] : lane == 2 ? o4[2] : o4[3]);
+    if (rows_ok && (lane & 31) == 31) {
+        gst(a.out + (int64_t)h * a.v + i0 + hw, o2[0]);
+        gst(a.out + (int64_t)h * a.v + i0 + 2 + hw, o2[1]);
+    }
 }
 
 // ---------------------------------------------------------------------------
