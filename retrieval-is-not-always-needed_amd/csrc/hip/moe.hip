@@ -351,7 +351,10 @@ __device__ __forceinline__ void read_rec(const uint32_t* rc, DCols<FMT_Q2_K>& xc
 // loading all 32.
 constexpr int kDnRounds = 8;   // columns per lane: (shared + k * ffn) / 32 <= 512
 
-template <bool QUAD>
+// R: the launch's rounds, ceil(columns / 64) (<= kDnRounds): every lane
+// issues R rounds of column loads, none past the last round (DeepSeek-V2-Lite:
+// 352 columns, 6 rounds, 28 weight and G loads per wave instead of 34)
+template <bool QUAD, int R>
 __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     extern __shared__ __align__(16) uint32_t s_rec[];   // [n / 32][kRec]
     const int tid = threadIdx.x, lane = tid & 63;
@@ -376,11 +379,11 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     // floor(t / fcols) for 0 <= t < 2^16 / 128: t * ceil(2^16 / fcols) >> 16,
     // then one correction step each way
     const uint32_t magic = (65536u + (uint32_t)fcols - 1u) / (uint32_t)fcols;
-    typename std::conditional<QUAD, Q2ColQ, Q2Col>::type c[kDnRounds];
-    float wt[kDnRounds];
-    int col[kDnRounds];
+    typename std::conditional<QUAD, Q2ColQ, Q2Col>::type c[R];
+    float wt[R];
+    int col[R];
 #pragma unroll
-    for (int r = 0; r < kDnRounds; r++) {
+    for (int r = 0; r < R; r++) {
         const int cc = 64 * r + lane;
         const int t = cc - scols;                  // routed column index (negative: a shared column)
         const int tt = t < 0 ? 0 : t;
@@ -414,8 +417,8 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
 
     float acc = 0.f;
 #pragma unroll
-    for (int r = 0; r < kDnRounds; r++) {
-        if (r >= rounds) break;                    // wave-uniform
+    for (int r = 0; r < R; r++) {
+        if (r >= rounds) break;                    // wave-uniform (rounds == R)
         Q2Col cx;
         if constexpr (QUAD) q2_colq_expand(c[r], cx);   // every lane of the quad takes part
         else cx = c[r];
@@ -479,11 +482,29 @@ extern "C" int rina_hip_moe_block(float* h, const float* ln2, float eps, const v
     if (g1 > cus * 3) g1 = cus * 3;
     hipLaunchKernelGGL(moe_gate_up_q2_kernel, dim3(g1), dim3(256), 0, st, a);
     RINA_LAUNCH_CHECK();
-    // quad column loads when every source's columns come in whole half pages
-    if (S % 128 == 0 && F % 128 == 0)
-        hipLaunchKernelGGL(moe_down_q2_kernel<true>, dim3((d + 7) / 8), dim3(512), lds, st, a);
-    else
-        hipLaunchKernelGGL(moe_down_q2_kernel<false>, dim3((d + 7) / 8), dim3(512), lds, st, a);
+    // quad column loads when every source's columns come in whole half pages;
+    // one instantiation per round count (n <= 16384: at most kDnRounds)
+    {
+        const bool quad = S % 128 == 0 && F % 128 == 0;
+        const int rounds = (n / 32 + 63) / 64;
+        const dim3 g3((d + 7) / 8);
+#define DN(R)                                                                             \
+    do {                                                                                  \
+        if (quad) hipLaunchKernelGGL((moe_down_q2_kernel<true, R>), g3, dim3(512), lds, st, a);   \
+        else hipLaunchKernelGGL((moe_down_q2_kernel<false, R>), g3, dim3(512), lds, st, a);       \
+    } while (0)
+        switch (rounds) {
+            case 1: DN(1); break;
+            case 2: DN(2); break;
+            case 3: DN(3); break;
+            case 4: DN(4); break;
+            case 5: DN(5); break;
+            case 6: DN(6); break;
+            case 7: DN(7); break;
+            default: DN(8); break;
+        }
+#undef DN
+    }
     RINA_LAUNCH_CHECK();
     return RINA_OK;
 }
