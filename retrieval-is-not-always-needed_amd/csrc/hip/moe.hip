@@ -269,17 +269,20 @@ constexpr int kRec = 28;
 // consumed by stage_g_digits.
 constexpr int kStageRounds = 4;                    // 512 threads x 4 rounds / 4 = 512 columns
 
+// SR rounds of 128 columns (<= kStageRounds)
+template <int SR>
 struct GStage {
-    f32x4 v[kStageRounds][2];
+    f32x4 v[SR][2];
 };
 
 // Every lane loads (columns past ncol read column 0, which stage_g_digits
 // never stores): loads under a branch leave the load-counter waits after it
 // waiting for every load in flight.
-__device__ __forceinline__ void stage_g_load(const float* G, int ncol, GStage& g) {
+template <int SR>
+__device__ __forceinline__ void stage_g_load(const float* G, int ncol, GStage<SR>& g) {
     const int tid = threadIdx.x, j = tid & 3;
 #pragma unroll
-    for (int r = 0; r < kStageRounds; r++) {
+    for (int r = 0; r < SR; r++) {
         const int c = (tid >> 2) + 128 * r;
         const f32x4* src = (const f32x4*)(G + 32 * (c < ncol ? c : 0) + 8 * j);
         g.v[r][0] = gld(src);
@@ -287,11 +290,12 @@ __device__ __forceinline__ void stage_g_load(const float* G, int ncol, GStage& g
     }
 }
 
-__device__ __forceinline__ void stage_g_digits(const GStage& g, int ncol, uint32_t* rec) {
+template <int SR>
+__device__ __forceinline__ void stage_g_digits(const GStage<SR>& g, int ncol, uint32_t* rec) {
     const int tid = threadIdx.x, j = tid & 3;
     const int rounds = (ncol + 127) / 128;         // uniform: the group shuffles see full waves
 #pragma unroll
-    for (int r = 0; r < kStageRounds; r++) {
+    for (int r = 0; r < SR; r++) {
         if (r >= rounds) break;
         const int c = (tid >> 2) + 128 * r;
         const float x[8] = {g.v[r][0].x, g.v[r][0].y, g.v[r][0].z, g.v[r][0].w,
@@ -352,8 +356,9 @@ __device__ __forceinline__ void read_rec(const uint32_t* rc, DCols<FMT_Q2_K>& xc
 constexpr int kDnRounds = 8;   // columns per lane: (shared + k * ffn) / 32 <= 512
 
 // R: the launch's rounds, ceil(columns / 64) (<= kDnRounds): every lane
-// issues R rounds of column loads, none past the last round (DeepSeek-V2-Lite:
-// 352 columns, 6 rounds, 28 weight and G loads per wave instead of 34)
+// issues R rounds of column loads and ceil(R / 2) rounds of G loads, none
+// past the last round (DeepSeek-V2-Lite: 352 columns, 6 rounds, 26 loads
+// per wave with the ids instead of 34)
 template <bool QUAD, int R>
 __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     extern __shared__ __align__(16) uint32_t s_rec[];   // [n / 32][kRec]
@@ -374,7 +379,7 @@ __global__ __launch_bounds__(512) void moe_down_q2_kernel(MoeBlkArgs a) {
     // the ids alone)
     const int my_id = lane < a.k ? gld(a.ids + lane) : -1;
     const float my_pr = lane < a.k ? gld(a.probs + lane) : 0.f;
-    GStage gs;
+    GStage<(R + 1) / 2> gs;                        // ncol <= 64 R: ceil(R / 2) rounds of 128
     stage_g_load(a.G, ncol, gs);
     // floor(t / fcols) for 0 <= t < 2^16 / 128: t * ceil(2^16 / fcols) >> 16,
     // then one correction step each way
